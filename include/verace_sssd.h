@@ -1,0 +1,121 @@
+/*
+ * verace_sssd.h -- C ABI of the MI355X (gfx950) SSSD Cayley-scan library
+ * (libverace_sssd.so, built from verace-v1_amd/csrc/).
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream
+ * (passed as void*, it is a hipStream_t; NULL = the null stream).  Nothing
+ * here allocates device memory: scratch space is passed in by the caller and
+ * sized with the matching *_workspace_bytes query.  Kernels are enqueued on
+ * the given stream; no entry point synchronises the host.  The library holds
+ * no mutable global state, so calls from several host threads are safe as
+ * long as they use disjoint output buffers.
+ *
+ * Math implemented (reference: verace_v1/modules/sssd_attention.py:144-182):
+ *   X_t   = (delta_t / 2) * (k_t v_t^T - v_t k_t^T)
+ *   R_t   = (I + X_t)^-1 (I - X_t)           (solve(right, left) order, :163-166)
+ *   Psi_t = R_t Psi_{t-1},  Psi_0 = initial state (identity if NULL)
+ *   o_t   = Psi_t q_t
+ * R_t is applied in closed form (no solve): R = I + c(-X + X^2), c = 2/(1+m^2),
+ * m^2 = (delta/2)^2 (|k|^2 |v|^2 - (k.v)^2), which is exact for any k, v and
+ * equals I exactly at delta = 0.
+ *
+ * Layouts (all contiguous, row-major, identical to the reference launcher's
+ * contract, verace_v1/serving/triton_kernels.py:612-627):
+ *   q, k, v, out : [B, T, H, D]   dtype io_dtype (out takes q's dtype)
+ *   delta        : [B, T, H]      dtype delta_dtype
+ *   psi_in       : [B, H, D, D]   float32, NULL means identity
+ *   psi_out      : [B, H, D, D]   float32
+ */
+#ifndef VERACE_SSSD_H
+#define VERACE_SSSD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type codes for io_dtype / delta_dtype. */
+enum vmi_dtype {
+  VMI_F32 = 0,
+  VMI_BF16 = 1,
+  VMI_F16 = 2
+};
+
+/* Status codes returned by every entry point (0 = success). */
+enum vmi_status {
+  VMI_OK = 0,
+  VMI_ERR_INVALID_ARG = 1,     /* null pointer where one is required, bad size */
+  VMI_ERR_UNSUPPORTED = 2,     /* head_dim / dtype combination not built */
+  VMI_ERR_WORKSPACE = 3,       /* workspace missing or too small */
+  VMI_ERR_ALIAS = 4,           /* forbidden aliasing between buffers */
+  VMI_ERR_HIP = 5              /* a HIP runtime call failed (see vmi_last_hip_error) */
+};
+
+/* Library version (major*10000 + minor*100 + patch). */
+int vmi_version(void);
+
+/* Human-readable text for a vmi_status value. */
+const char* vmi_status_string(int status);
+
+/* hipError_t of the last failing HIP call made by this thread inside the
+ * library (0 if none). */
+int vmi_last_hip_error(void);
+
+/* Bytes of device workspace vmi_sssd_scan_fwd needs for this problem.
+ * Replaces nothing in the reference (the Triton launcher allocates its
+ * outputs itself); the caller allocates `*bytes` from its own allocator. */
+int vmi_sssd_scan_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D,
+                                  int io_dtype, size_t* bytes);
+
+/* Prefill scan over T tokens.
+ * Replaces launch_sssd_triton_scan + sssd_cayley_scan_kernel
+ * (verace_v1/serving/triton_kernels.py:603-636 and :41-144), whose results
+ * must equal the eager path sssd_attention.py:144-181.
+ *   psi_in   may be NULL (identity, triton_kernels.py:621-622); it is never
+ *            written.  psi_out must not alias psi_in (the reference returns a
+ *            fresh state, triton_kernels.py:627).
+ *   out      may be NULL if only the final state is wanted.
+ * Supported: io_dtype in {F32, BF16, F16}; delta_dtype in {F32, BF16, F16};
+ * 1 <= D <= 256.  T = 0 copies psi_in (or identity) to psi_out. */
+int vmi_sssd_scan_fwd(const void* q, const void* k, const void* v,
+                      const void* delta, int io_dtype, int delta_dtype,
+                      const float* psi_in, void* out, float* psi_out,
+                      int64_t B, int64_t T, int64_t H, int64_t D,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* One decode step (T = 1) with the state updated in place:
+ *   psi <- R psi ;  out = psi q.
+ * Replaces the reference's incremental forward at seq_len 1
+ * (sssd_attention.py:103-182 called from acd_engine.py:116-121 and
+ * hyper_generate.py:59-63), which returns a fresh state; the in-place form
+ * is opt-in for callers that own the state (the reference never mutates
+ * initial_state, so tree-search branches must pass a copy).
+ * q, k, v, out: [B, 1, H, D]; delta: [B, 1, H]; psi: [B, H, D, D] float32. */
+int vmi_sssd_step_inplace(const void* q, const void* k, const void* v,
+                          const void* delta, int io_dtype, int delta_dtype,
+                          float* psi, void* out,
+                          int64_t B, int64_t H, int64_t D, void* stream);
+
+/* Newton-Schulz unitary retraction of a batch of complex matrices
+ * H = Hr + i Hi, `steps` iterations of H <- 0.5 H (3I - H^H H), both halves
+ * of every iteration computed from the pre-update H.
+ * Replaces newton_schulz_unitary_retraction / parallel_newton_schulz_retraction
+ * (verace_v1/modules/cham_memory.py:21-51 and :296-315) and the in-kernel
+ * NS loop of cham_holographic_scan_kernel (triton_kernels.py:280-292).
+ *   h_real, h_imag : [batch, n, n] float32, read;
+ *   out_real, out_imag : [batch, n, n] float32, written (may alias the inputs).
+ * Needs vmi_cham_ns_workspace_bytes(batch, n) bytes of workspace. */
+int vmi_cham_ns_workspace_bytes(int64_t batch, int64_t n, size_t* bytes);
+int vmi_cham_ns_retraction(const float* h_real, const float* h_imag,
+                           float* out_real, float* out_imag,
+                           int64_t batch, int64_t n, int steps,
+                           void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VERACE_SSSD_H */

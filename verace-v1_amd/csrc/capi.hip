@@ -1,0 +1,114 @@
+// extern "C" entry points of libverace_sssd.so (declared in include/verace_sssd.h).
+// Argument checking and dispatch only; the kernels live in sssd_*.hip / cham_*.hip.
+#include "vmi_common.h"
+#include "vmi_dispatch.h"
+
+namespace {
+
+thread_local int g_last_hip_error = 0;
+
+int hip_status(hipError_t e) {
+  if (e == hipSuccess) return VMI_OK;
+  g_last_hip_error = static_cast<int>(e);
+  return VMI_ERR_HIP;
+}
+
+bool valid_dtype(int dt) { return dt == VMI_F32 || dt == VMI_BF16 || dt == VMI_F16; }
+
+bool ranges_overlap(const void* a, size_t abytes, const void* b, size_t bbytes) {
+  const char* pa = static_cast<const char*>(a);
+  const char* pb = static_cast<const char*>(b);
+  return pa < pb + bbytes && pb < pa + abytes;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vmi_version(void) { return 100; }
+
+const char* vmi_status_string(int status) {
+  switch (status) {
+    case VMI_OK: return "ok";
+    case VMI_ERR_INVALID_ARG: return "invalid argument";
+    case VMI_ERR_UNSUPPORTED: return "unsupported head_dim/dtype combination";
+    case VMI_ERR_WORKSPACE: return "workspace missing or too small";
+    case VMI_ERR_ALIAS: return "forbidden aliasing between buffers";
+    case VMI_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+int vmi_last_hip_error(void) { return g_last_hip_error; }
+
+int vmi_sssd_scan_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int io_dtype,
+                                  size_t* bytes) {
+  if (bytes == nullptr || B < 0 || T < 0 || H < 0 || D < 1 || D > 256 || !valid_dtype(io_dtype))
+    return VMI_ERR_INVALID_ARG;
+  *bytes = vmi::scan_workspace_bytes(B, T, H, D, io_dtype);
+  return VMI_OK;
+}
+
+int vmi_sssd_scan_fwd(const void* q, const void* k, const void* v, const void* delta,
+                      int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                      float* psi_out, int64_t B, int64_t T, int64_t H, int64_t D, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  if (!valid_dtype(io_dtype) || !valid_dtype(delta_dtype)) return VMI_ERR_INVALID_ARG;
+  if (B < 0 || T < 0 || H < 0 || D < 1) return VMI_ERR_INVALID_ARG;
+  if (D > 256) return VMI_ERR_UNSUPPORTED;
+  if (B * H > INT32_MAX || B * T * H > INT32_MAX) return VMI_ERR_INVALID_ARG;
+  if (psi_out == nullptr) return VMI_ERR_INVALID_ARG;
+  if (T > 0 && (q == nullptr || k == nullptr || v == nullptr || delta == nullptr))
+    return VMI_ERR_INVALID_ARG;
+  const size_t state_bytes = static_cast<size_t>(B * H) * D * D * sizeof(float);
+  if (psi_in != nullptr && ranges_overlap(psi_in, state_bytes, psi_out, state_bytes))
+    return VMI_ERR_ALIAS;
+  const size_t need = vmi::scan_workspace_bytes(B, T, H, D, io_dtype);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return VMI_ERR_WORKSPACE;
+  if (B == 0 || H == 0) return VMI_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return hip_status(vmi::dispatch_scan(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out,
+                                       static_cast<int>(B), static_cast<int>(T),
+                                       static_cast<int>(H), static_cast<int>(D), workspace,
+                                       workspace_bytes, s));
+}
+
+int vmi_sssd_step_inplace(const void* q, const void* k, const void* v, const void* delta,
+                          int io_dtype, int delta_dtype, float* psi, void* out, int64_t B,
+                          int64_t H, int64_t D, void* stream) {
+  if (!valid_dtype(io_dtype) || !valid_dtype(delta_dtype)) return VMI_ERR_INVALID_ARG;
+  if (B < 0 || H < 0 || D < 1) return VMI_ERR_INVALID_ARG;
+  if (D > 256) return VMI_ERR_UNSUPPORTED;
+  if (B * H > INT32_MAX) return VMI_ERR_INVALID_ARG;
+  if (psi == nullptr || q == nullptr || k == nullptr || v == nullptr || delta == nullptr)
+    return VMI_ERR_INVALID_ARG;
+  if (B == 0 || H == 0) return VMI_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return hip_status(vmi::launch_sssd_seq(q, k, v, delta, io_dtype, delta_dtype, psi, out, psi,
+                                         static_cast<int>(B), 1, static_cast<int>(H),
+                                         static_cast<int>(D), s));
+}
+
+int vmi_cham_ns_workspace_bytes(int64_t batch, int64_t n, size_t* bytes) {
+  if (bytes == nullptr || batch < 0 || n < 1) return VMI_ERR_INVALID_ARG;
+  *bytes = vmi::ns_workspace_bytes(batch, n);
+  return VMI_OK;
+}
+
+int vmi_cham_ns_retraction(const float* h_real, const float* h_imag, float* out_real,
+                           float* out_imag, int64_t batch, int64_t n, int steps, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (batch < 0 || n < 1 || steps < 0) return VMI_ERR_INVALID_ARG;
+  if (batch * n * n > INT32_MAX) return VMI_ERR_INVALID_ARG;
+  if (h_real == nullptr || h_imag == nullptr || out_real == nullptr || out_imag == nullptr)
+    return VMI_ERR_INVALID_ARG;
+  const size_t need = vmi::ns_workspace_bytes(batch, n);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return VMI_ERR_WORKSPACE;
+  if (batch == 0) return VMI_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return hip_status(vmi::launch_ns_retraction(h_real, h_imag, out_real, out_imag,
+                                              static_cast<int>(batch), static_cast<int>(n), steps,
+                                              workspace, s));
+}
+
+}  // extern "C"

@@ -1,0 +1,86 @@
+// Device helpers shared by the gfx950 kernels of libverace_sssd.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "verace_sssd.h"
+
+namespace vmi {
+
+// ---------------------------------------------------------------------------
+// Element types.  bf16 is carried as raw uint16_t bits, fp16 as _Float16.
+// ---------------------------------------------------------------------------
+struct bf16_t {
+  uint16_t bits;
+};
+typedef _Float16 f16_t;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even float -> bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+template <typename T> struct io;
+template <> struct io<float> {
+  static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void store(float* p, int64_t i, float x) { p[i] = x; }
+};
+template <> struct io<bf16_t> {
+  static __device__ __forceinline__ float load(const bf16_t* p, int64_t i) {
+    return bf16_to_f32(p[i].bits);
+  }
+  static __device__ __forceinline__ void store(bf16_t* p, int64_t i, float x) {
+    p[i].bits = f32_to_bf16(x);
+  }
+};
+template <> struct io<f16_t> {
+  static __device__ __forceinline__ float load(const f16_t* p, int64_t i) {
+    return static_cast<float>(p[i]);
+  }
+  static __device__ __forceinline__ void store(f16_t* p, int64_t i, float x) {
+    p[i] = static_cast<f16_t>(x);
+  }
+};
+
+// delta is read one scalar per (token, head); its dtype is a runtime code.
+__device__ __forceinline__ float load_scalar(const void* p, int dtype, int64_t i) {
+  if (dtype == VMI_F32) return static_cast<const float*>(p)[i];
+  if (dtype == VMI_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  return static_cast<float>(static_cast<const f16_t*>(p)[i]);
+}
+
+// ---------------------------------------------------------------------------
+// Closed-form Cayley coefficients for one token.
+//   h = delta/2,  m^2 = h^2 (|k|^2 |v|^2 - (k.v)^2),  c = 2 / (1 + m^2)
+// Applied to row vectors a = k^T Psi, b = v^T Psi:
+//   alpha = c(-h b + h^2 (kv b - vv a)),  beta = c(h a + h^2 (kv a - kk b))
+// so that R Psi = Psi + k alpha + v beta.  The coefficients below are the
+// 2x2 matrix M = [[m00, m01], [m10, m11]] with alpha = m00 a + m01 b,
+// beta = m10 a + m11 b.
+// ---------------------------------------------------------------------------
+struct cayley2 {
+  float m00, m01, m10, m11;
+};
+
+__device__ __forceinline__ cayley2 cayley_coeffs(float delta, float kk, float vv, float kv) {
+  const float h = 0.5f * delta;
+  const float h2 = h * h;
+  const float gram_det = fmaxf(kk * vv - kv * kv, 0.0f);
+  const float c = 2.0f / (1.0f + h2 * gram_det);
+  cayley2 m;
+  m.m00 = -c * h2 * vv;
+  m.m01 = c * (h2 * kv - h);
+  m.m10 = c * (h2 * kv + h);
+  m.m11 = -c * h2 * kk;
+  return m;
+}
+
+}  // namespace vmi

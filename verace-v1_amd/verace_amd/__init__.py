@@ -1,0 +1,25 @@
+"""verace_amd -- MI355X (gfx950) SSSD Cayley-scan attention for Verace V1.
+
+Drop-in replacements for the reference's SSSD hot path:
+
+* ``SSSDAttention``            <- ``verace_v1.modules.sssd_attention.SSSDAttention``
+* ``launch_sssd_hip_scan``     <- ``verace_v1.serving.triton_kernels.launch_sssd_triton_scan``
+* ``sssd_step_``               -- in-place single-token decode step (opt-in)
+* ``newton_schulz_unitary_retraction`` / ``parallel_newton_schulz_retraction``
+                               <- ``verace_v1.modules.cham_memory`` (same names)
+* ``HAS_HIP``                  <- ``verace_v1.serving.triton_kernels.HAS_TRITON``
+
+All compute runs in ``libverace_sssd.so`` (C ABI: ``include/verace_sssd.h``).
+"""
+from .hip_kernels import (HAS_HIP, launch_sssd_hip_scan, newton_schulz_unitary_retraction,
+                          parallel_newton_schulz_retraction, sssd_step_)
+from .sssd_attention import SSSDAttention
+
+__all__ = [
+    "HAS_HIP",
+    "SSSDAttention",
+    "launch_sssd_hip_scan",
+    "sssd_step_",
+    "newton_schulz_unitary_retraction",
+    "parallel_newton_schulz_retraction",
+]

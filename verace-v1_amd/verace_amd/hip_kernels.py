@@ -1,0 +1,164 @@
+"""Host-side launchers of the gfx950 SSSD / CHAM-NS kernels.
+
+Mirrors the launcher API of ``verace_v1/serving/triton_kernels.py`` for this path:
+
+* :func:`launch_sssd_hip_scan` replaces ``launch_sssd_triton_scan`` (:603-636): same
+  arguments, same layouts, same return values (out in q's dtype, a fresh fp32 state).
+* :func:`sssd_step_` is the opt-in in-place single-token decode step (no reference
+  counterpart; the reference re-runs the forward at seq_len 1 and returns a new state).
+* :func:`newton_schulz_unitary_retraction` / :func:`parallel_newton_schulz_retraction`
+  replace ``cham_memory.py:21-51`` / ``:296-315`` for device tensors.
+
+Every launcher enqueues on the current HIP stream and allocates its outputs and
+workspace from torch's caching allocator.  There is no CPU path: non-device tensors,
+a missing library or a failing call raise.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+HAS_HIP = _lib.available()
+
+
+def _require_device(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"verace_amd: {name} must be a HIP device tensor (got {t.device}); "
+                           "there is no CPU path")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def launch_sssd_hip_scan(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    delta: torch.Tensor,
+    initial_state: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """SSSD Cayley scan on the GPU.
+
+    q, k, v: [batch, seq_len, num_heads, head_dim] (L2-normalised by the caller);
+    delta: [batch, seq_len, num_heads]; initial_state: optional
+    [batch, num_heads, head_dim, head_dim], identity when None (never modified).
+    Returns (out [batch, seq_len, num_heads, head_dim] in q's dtype,
+    final_state [batch, num_heads, head_dim, head_dim] float32).
+    Reference: ``triton_kernels.py:603-636``; parity target ``sssd_attention.py:144-181``.
+    """
+    _require_device(q, "q")
+    if q.dim() != 4:
+        raise RuntimeError(f"verace_amd: q must be [B, T, H, D], got {tuple(q.shape)}")
+    b, s, h, d_k = q.shape
+    for name, t in (("k", k), ("v", v)):
+        _require_device(t, name)
+        if t.shape != q.shape:
+            raise RuntimeError(f"verace_amd: {name} shape {tuple(t.shape)} != q shape {tuple(q.shape)}")
+    _require_device(delta, "delta")
+    if delta.dim() == 4 and delta.shape[-1] == 1:
+        delta = delta.squeeze(-1)
+    if tuple(delta.shape) != (b, s, h):
+        raise RuntimeError(f"verace_amd: delta must be [B, T, H] = {(b, s, h)}, got {tuple(delta.shape)}")
+    io_code = _lib.dtype_code(q.dtype)
+    q_c = q.contiguous()
+    k_c = k.to(q.dtype).contiguous()
+    v_c = v.to(q.dtype).contiguous()
+    delta_c = delta.contiguous()
+    d_code = _lib.dtype_code(delta_c.dtype)
+    psi_in = None
+    if initial_state is not None:
+        _require_device(initial_state, "initial_state")
+        if tuple(initial_state.shape) != (b, h, d_k, d_k):
+            raise RuntimeError(f"verace_amd: initial_state must be {(b, h, d_k, d_k)}, "
+                               f"got {tuple(initial_state.shape)}")
+        psi_in = initial_state.to(torch.float32).contiguous()
+    out = torch.empty_like(q_c)
+    psi_out = torch.empty(b, h, d_k, d_k, device=q.device, dtype=torch.float32)
+    lib = _lib.load()
+    ws_bytes = ctypes.c_size_t(0)
+    _lib.check(lib.vmi_sssd_scan_workspace_bytes(b, s, h, d_k, io_code, ctypes.byref(ws_bytes)),
+               "vmi_sssd_scan_workspace_bytes")
+    ws = None
+    if ws_bytes.value > 0:
+        ws = torch.empty(ws_bytes.value, device=q.device, dtype=torch.uint8)
+    _lib.check(lib.vmi_sssd_scan_fwd(_ptr(q_c), _ptr(k_c), _ptr(v_c), _ptr(delta_c), io_code,
+                                     d_code, _ptr(psi_in), _ptr(out), _ptr(psi_out), b, s, h, d_k,
+                                     _ptr(ws), ws_bytes.value, _lib.stream_handle(q.device)),
+               "vmi_sssd_scan_fwd")
+    return out, psi_out
+
+
+def sssd_step_(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    delta: torch.Tensor,
+    state: torch.Tensor,
+) -> torch.Tensor:
+    """In-place decode step: ``state <- R state``; returns ``out = state q`` in q's dtype.
+
+    q, k, v: [B, 1, H, D] or [B, H, D]; delta: [B, 1, H], [B, H] or [B, 1, H, 1];
+    state: [B, H, D, D] float32 contiguous, updated in place.  Only for callers that own
+    the state: the reference never mutates ``initial_state`` (tree-search branches share
+    it, ``hyper_generate.py:108-115``), so pass a copy where the state is shared.
+    """
+    _require_device(q, "q")
+    _require_device(state, "state")
+    if state.dtype != torch.float32 or not state.is_contiguous():
+        raise RuntimeError("verace_amd: state must be a contiguous float32 tensor")
+    B, H, D, D2 = state.shape
+    if D != D2:
+        raise RuntimeError(f"verace_amd: state must be [B, H, D, D], got {tuple(state.shape)}")
+    io_code = _lib.dtype_code(q.dtype)
+    q_c = q.reshape(B, 1, H, D).contiguous()
+    k_c = k.reshape(B, 1, H, D).to(q.dtype).contiguous()
+    v_c = v.reshape(B, 1, H, D).to(q.dtype).contiguous()
+    delta_c = delta.reshape(B, 1, H).contiguous()
+    for name, t in (("k", k_c), ("v", v_c), ("delta", delta_c)):
+        _require_device(t, name)
+    out = torch.empty_like(q_c)
+    lib = _lib.load()
+    _lib.check(lib.vmi_sssd_step_inplace(_ptr(q_c), _ptr(k_c), _ptr(v_c), _ptr(delta_c), io_code,
+                                         _lib.dtype_code(delta_c.dtype), _ptr(state), _ptr(out),
+                                         B, H, D, _lib.stream_handle(q.device)),
+               "vmi_sssd_step_inplace")
+    return out
+
+
+def _ns(H_real: torch.Tensor, H_imag: torch.Tensor, steps: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    _require_device(H_real, "H_real")
+    _require_device(H_imag, "H_imag")
+    if H_real.shape != H_imag.shape or H_real.shape[-1] != H_real.shape[-2]:
+        raise RuntimeError("verace_amd: H_real/H_imag must be matching [..., n, n] tensors")
+    shape = H_real.shape
+    n = shape[-1]
+    hr = H_real.to(torch.float32).reshape(-1, n, n).contiguous()
+    hi = H_imag.to(torch.float32).reshape(-1, n, n).contiguous()
+    batch = hr.shape[0]
+    out_r = torch.empty_like(hr)
+    out_i = torch.empty_like(hi)
+    lib = _lib.load()
+    ws_bytes = ctypes.c_size_t(0)
+    _lib.check(lib.vmi_cham_ns_workspace_bytes(batch, n, ctypes.byref(ws_bytes)),
+               "vmi_cham_ns_workspace_bytes")
+    ws = torch.empty(max(ws_bytes.value, 1), device=hr.device, dtype=torch.uint8)
+    _lib.check(lib.vmi_cham_ns_retraction(_ptr(hr), _ptr(hi), _ptr(out_r), _ptr(out_i), batch, n,
+                                          int(steps), _ptr(ws), ws_bytes.value,
+                                          _lib.stream_handle(hr.device)),
+               "vmi_cham_ns_retraction")
+    return out_r.reshape(shape), out_i.reshape(shape)
+
+
+def newton_schulz_unitary_retraction(H_real: torch.Tensor, H_imag: torch.Tensor, steps: int = 3):
+    """[b, d, d] complex NS retraction (reference ``cham_memory.py:21-51``), fp32 out."""
+    return _ns(H_real, H_imag, steps)
+
+
+def parallel_newton_schulz_retraction(H_real: torch.Tensor, H_imag: torch.Tensor, steps: int = 3):
+    """[b, s, d, d] complex NS retraction (reference ``cham_memory.py:296-315``), fp32 out."""
+    return _ns(H_real, H_imag, steps)
