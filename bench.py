@@ -1,0 +1,247 @@
+"""Benchmark of the SSSD Cayley-scan hot path on one MI355X.
+
+Workload ("OP"): prefill scan at B=8, T=4096, H=8, D=128,
+bf16 q/k/v/delta (L2-normalised q/k/v, delta = 0.1*sigmoid(z)), fp32 state from the
+identity.  One step = one scan over the batch; value = tokens (B*T) per second.  The
+decode step (configs[4], "DEC", op level: B=64, H=8, D=128, in-place state) is timed
+beside it and reported in `decode`.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Prints ONE JSON line.  Timing: W untimed steps, then K steps bracketed by
+torch.cuda.synchronize(); each step is bracketed by HIP events recorded on the stream
+the kernels are launched on.  Two input sets are rotated so a step never finds its
+inputs in the 256 MB MALL left over from the previous step.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO_ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(REPO_ROOT, "verace-v1_amd")
+for _p in (REPO_ROOT, PKG_DIR):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E spec-sheet peak, GB/s
+OP = dict(B=8, T=4096, H=8, D=128)
+DEC = dict(B=64, H=8, D=128, layers=12, steps=256)
+
+
+def algorithmic_bytes_scan(B, T, H, D, io_bytes=2, delta_bytes=2):
+    """q, k, v in + o out (io dtype), delta in, fp32 state in and out once per (b, h)."""
+    return B * T * H * (4 * D * io_bytes + delta_bytes) + B * H * 2 * D * D * 4
+
+
+def algorithmic_bytes_step(B, H, D, io_bytes=2, delta_bytes=2):
+    return B * H * (4 * D * io_bytes + delta_bytes) + B * H * 2 * D * D * 4
+
+
+def make_inputs(B, T, H, D, seed, dtype, device):
+    import torch
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(seed)
+    q = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1).to(dtype)
+    k = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1).to(dtype)
+    v = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1).to(dtype)
+    delta = (0.1 * torch.sigmoid(torch.randn(B, T, H, generator=g))).to(dtype)
+    cpu = (q, k, v, delta)
+    dev = tuple(t.to(device) for t in cpu)
+    return cpu, dev
+
+
+def bench_scan(args, device):
+    import torch
+    from verace_amd import launch_sssd_hip_scan
+    B, T, H, D = OP["B"], OP["T"], OP["H"], OP["D"]
+    sets = []
+    for s in range(2):
+        cpu, dev = make_inputs(B, T, H, D, seed=s, dtype=torch.bfloat16, device=device)
+        sets.append((cpu, dev))
+    stream = torch.cuda.current_stream(device)
+    for i in range(args.warmup):
+        launch_sssd_hip_scan(*sets[i % 2][1])
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    outs = None
+    for i in range(args.steps):
+        evs[i][0].record(stream)
+        outs = launch_sssd_hip_scan(*sets[i % 2][1])
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [a.elapsed_time(b) for a, b in evs]  # ms
+    # parity spot check of the last step against the fp64 C oracle (two (b, h) slices)
+    parity = check_scan(sets[(args.steps - 1) % 2][0], outs, B, H)
+    return per, wall, parity
+
+
+def check_scan(cpu_inputs, outs, B, H):
+    import numpy as np
+    from oracle import sssd_closed
+    q, k, v, delta = (t.float().numpy() for t in cpu_inputs)
+    o, psi = outs
+    o = o.float().cpu().numpy()
+    psi = psi.cpu().numpy()
+    res = {}
+    worst_o = worst_p = worst_n = 0.0
+    for (b, h) in [(0, 0), (B - 1, H - 1)]:
+        sl = (slice(b, b + 1), slice(None), slice(h, h + 1))
+        o64, p64 = sssd_closed.sssd_scan_closed_c(q[sl], k[sl], v[sl], delta[b:b + 1, :, h:h + 1])
+        eo = np.linalg.norm(o[b, :, h] - o64[0, :, 0]) / np.linalg.norm(o64[0, :, 0])
+        ep = np.linalg.norm(psi[b, h] - p64[0, 0]) / np.linalg.norm(p64[0, 0])
+        worst_o, worst_p = max(worst_o, eo), max(worst_p, ep)
+    nrm = np.linalg.norm(psi.reshape(B, H, -1), axis=-1) / np.sqrt(psi.shape[-1])
+    worst_n = float(np.abs(nrm - 1).max())
+    res["o_rel_vs_fp64"] = float(worst_o)
+    res["state_rel_vs_fp64"] = float(worst_p)
+    res["state_norm_drift"] = worst_n
+    res["pass"] = bool(worst_o <= 2e-2 and worst_p <= 2e-2 and worst_n <= 1e-4)
+    return res
+
+
+def bench_decode(device):
+    import torch
+    from verace_amd import sssd_step_
+    B, H, D, L, S = DEC["B"], DEC["H"], DEC["D"], DEC["layers"], DEC["steps"]
+    g = torch.Generator().manual_seed(1)
+    states = [torch.linalg.qr(torch.randn(B, H, D, D, generator=g))[0].contiguous().to(device)
+              for _ in range(L)]
+    cpu, dev = make_inputs(B, S, H, D, seed=3, dtype=torch.bfloat16, device=device)
+    q, k, v, delta = dev
+    stream = torch.cuda.current_stream(device)
+    for t in range(8):  # warm-up on a copy so the measured states start from the seed
+        tmp = states[0].clone()
+        sssd_step_(q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1], delta[:, t:t + 1], tmp)
+    torch.cuda.synchronize()
+    per_layer, per_step = [], []
+    for t in range(S):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(L + 1)]
+        e[0].record(stream)
+        for l in range(L):
+            sssd_step_(q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1], delta[:, t:t + 1], states[l])
+            e[l + 1].record(stream)
+        per_layer.append((e, ))
+    torch.cuda.synchronize()
+    for (e,) in per_layer:
+        per_step.append(e[0].elapsed_time(e[L]) * 1000.0)
+    layer_us = [e[l].elapsed_time(e[l + 1]) * 1000.0 for (e,) in per_layer for l in range(L)]
+    nbytes = algorithmic_bytes_step(B, H, D)
+    med_layer = statistics.median(layer_us)
+    return {
+        "config": "B=64 H=8 D=128 bf16 io, fp32 state in place, 12 layers x 256 steps",
+        "layer_step_us_median": round(med_layer, 3),
+        "layer_step_us_p90": round(sorted(layer_us)[int(0.9 * len(layer_us))], 3),
+        "layers12_step_us_median": round(statistics.median(per_step), 3),
+        "layers12_step_us_p90": round(sorted(per_step)[int(0.9 * len(per_step))], 3),
+        "algorithmic_bytes_per_layer": nbytes,
+        "hbm_frac_per_layer": round(nbytes / (med_layer * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+    }
+
+
+def cpu_baseline(target_seconds=12.0):
+    """The oracle's fp32 restatement of the reference's eager path (oracle/sssd_eager.py),
+    timed on the host on a bounded prefix of the OP workload, T chunked by 256."""
+    import torch
+    from oracle import sssd_eager
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    B, H, D = OP["B"], OP["H"], OP["D"]
+    (q, k, v, delta), _ = make_inputs(B, 256, H, D, seed=0, dtype=torch.bfloat16, device="cpu")
+    chunks, tokens, state = 0, 0, None
+    t0 = time.perf_counter()
+    while True:
+        _, state = sssd_eager.sssd_scan_eager(q, k, v, delta, state)
+        chunks += 1
+        tokens += B * 256
+        el = time.perf_counter() - t0
+        if el >= target_seconds or chunks >= 8:
+            break
+    return {
+        "value": round(tokens / el, 2),
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"OP shape B=8 H=8 D=128 bf16 inputs, {chunks} chunk(s) of 256 tokens "
+                  f"({tokens} tokens, {el:.1f} s) through the eager fp32 restatement "
+                  f"(linalg.solve + Blelloch scan), state carried between chunks",
+    }
+
+
+def load_traffic():
+    """HBM bytes per scan from the committed rocprofv3 --pmc summary, if present."""
+    p = os.path.join(REPO_ROOT, "profiles", "pmc_traffic_op_scan.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("hbm_bytes_per_scan")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    device = torch.device("cuda:0")
+    per, wall, parity = bench_scan(args, device)
+    B, T, H, D = OP["B"], OP["T"], OP["H"], OP["D"]
+    tokens = B * T
+    ms = statistics.median(per)
+    total_ms = sum(per)
+    nbytes = algorithmic_bytes_scan(B, T, H, D)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    result = {
+        "metric": "SSSD scan tokens/sec + % HBM roofline (B8 T4096 H8 d128 bf16); decode step us",
+        "value": round(tokens * args.steps / (total_ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_ms / args.steps, 4),
+        "ms_per_step_median": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "OP: SSSD prefill scan B=8 T=4096 H=8 D=128, bf16 q/k/v/delta, "
+                               "fp32 state from identity", "B": B, "T": T, "H": H, "D": D,
+                   "parallelism": "single GPU"},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": load_traffic(),
+            "algorithmic_bytes": nbytes,
+            "kernel": "whole scan (all launches of one vmi_sssd_scan_fwd call)",
+        },
+        "parity": parity,
+        "wall_s_timed_region": round(wall, 3),
+    }
+    if not args.no_decode:
+        result["decode"] = bench_decode(device)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

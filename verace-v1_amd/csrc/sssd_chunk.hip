@@ -1,0 +1,587 @@
+// Chunk-parallel SSSD prefill scan on bf16/fp16 MFMA, head_dim 128.
+//
+// Math (reference recurrence sssd_attention.py:160-175, regrouped per chunk).
+// For a chunk of C = 16 tokens starting from state S:
+//   U = [k_0 v_0 k_1 v_1 ...]  (D x 32, rank row rho = 2t + {0: k, 1: v})
+//   R_t = I + U_t M_t U_t^T with the closed-form 2x2 Cayley block M_t
+//   G  = U^T U                                   (Gram, 32 x 32)
+//   T~ = (I - L)^-1 blockdiag(M),  L_{t,i} = M_t G_{t,i} for i < t
+//   W  = U^T S,  Z = T~ W                        (32 x D)
+//   end state      S' = S + U Z
+//   readout        O  = S Q + U (mask o (Z Q))   (D x 16), mask: token(rho) <= t
+// T~ is computed in 8x8 blocks (4 tokens): diagonal blocks by forward
+// substitution, off-diagonal blocks by T~_gh = T~_gg sum_{m=h}^{g-1} G_gm T~_mh.
+//
+// Workgroup = 5 waves for one (batch*head, segment):
+//   waves 0-3 (consumers) each own a 32-column slab of the fp32 state, held in
+//     MFMA accumulators for the whole segment; columns evolve independently, so
+//     W, Z and the update need no cross-wave traffic.  The readout is reduced
+//     across waves through LDS.
+//   wave 4 (producer) runs one chunk ahead: global loads, LDS staging (token-
+//     major and feature-major copies of k/v), Gram on MFMA, Cayley blocks and T~.
+//
+// Long sequences are split into segments processed by independent workgroups:
+//   pass A (READOUT=false): each segment s < S-1 from the identity -> its
+//          transform P_s (the end state),
+//   pass B (sssd_carry_kernel): start_s = P_{s-1} start_{s-1}, column blocks in
+//          parallel, bf16x3 MFMA (fp32-faithful),
+//   pass C (READOUT=true): every segment from its start state, with outputs.
+#include "vmi_common.h"
+#include "vmi_dispatch.h"
+#include "vmi_mfma.h"
+
+namespace vmi {
+namespace chunk {
+
+constexpr int D = 128;
+constexpr int C = 16;           // tokens per chunk
+constexpr int R = 2 * C;        // rank rows per chunk
+constexpr int NCW = 4;          // consumer waves
+constexpr int NT = (NCW + 1) * 64;
+constexpr int TOK_LD = D + 8;   // elements per token-major row (272 B)
+constexpr int UT_LD = R + 8;    // elements per feature-major row (80 B)
+constexpr int T_LD = R + 4;     // floats per T~ / Gram row
+constexpr int PS_LD = 32 + 8;   // elements per stash row (80 B)
+constexpr int OP_LD = D + 4;    // floats per O-partial row
+
+template <typename E>
+struct Smem {
+  E tok[2][3][C * TOK_LD];      // k, v, q of the chunk, token-major (double buffered)
+  E ut[2][D * UT_LD];           // U feature-major: ut[d][rho]
+  float tt[2][R * T_LD];        // T~, row-major
+  float gram[R * T_LD];         // producer-private
+  float4 mcoef[C];              // producer-private: (m00, m01, m10, m11) per token
+  float sblk[3 * 64];           // producer-private scratch for T~ level 2
+  E ps[NCW][D * PS_LD];         // per-wave: chunk-start state slab (row-major), then O partial
+  E zs[NCW][R * PS_LD];         // per-wave: Z slab (row-major)
+};
+
+struct Args {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* delta;
+  int delta_dtype;
+  const float* psi0;    // start of segment 0 ([BH][D][D]); null = identity
+  const float* starts;  // start of segment s >= 1 at starts[(s-1)*BH + bh]; null = identity
+  void* out;            // [B][T][H][D] (READOUT only)
+  float* ends;          // see end_mode
+  int end_mode;         // 0: ends[s*BH + bh] for every segment; 1: ends[bh] for the last one
+  int T, H, BH;
+  int seg_chunks;       // chunks per segment
+  int nseg;             // segments per sequence
+};
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <typename E>
+__device__ __forceinline__ typename mfma_t<E>::v4 lds4(const E* p) {
+  return *reinterpret_cast<const typename mfma_t<E>::v4*>(p);
+}
+template <typename E>
+__device__ __forceinline__ typename mfma_t<E>::v8 lds8(const E* p) {
+  return *reinterpret_cast<const typename mfma_t<E>::v8*>(p);
+}
+template <typename E>
+__device__ __forceinline__ typename mfma_t<E>::v8 lds4x2(const E* p0, const E* p1) {
+  typedef typename mfma_t<E>::v4 V4;
+  typedef typename mfma_t<E>::v8 V8;
+  return cat8<V4, V8>(lds4<E>(p0), lds4<E>(p1));
+}
+
+template <typename E, bool READOUT, bool PREC>
+__global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
+  typedef mfma_t<E> MM;
+  typedef typename MM::v8 V8;
+  __shared__ Smem<E> sm;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int l16 = lane & 15, g4 = lane >> 4;
+
+  const int bh = blockIdx.x;
+  const int seg = blockIdx.y;
+  const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+  const int total_chunks = (a.T + C - 1) / C;
+  const int chunk0 = seg * a.seg_chunks;
+  int nch = total_chunks - chunk0;
+  if (nch > a.seg_chunks) nch = a.seg_chunks;
+  if (nch <= 0) return;  // uniform across the workgroup
+
+  const int64_t DD = static_cast<int64_t>(D) * D;
+  const int64_t tok_stride = static_cast<int64_t>(a.H) * D;
+  const int64_t tok_base = (static_cast<int64_t>(b) * a.T * a.H + h) * D;
+  const int64_t dl_base = static_cast<int64_t>(b) * a.T * a.H + h;
+  const E* gq = static_cast<const E*>(a.q);
+  const E* gk = static_cast<const E*>(a.k);
+  const E* gv = static_cast<const E*>(a.v);
+
+  // zero T~ buffers (the strictly upper blocks are never written afterwards)
+  for (int i = tid; i < 2 * R * T_LD; i += NT) (&sm.tt[0][0])[i] = 0.0f;
+  __syncthreads();
+
+  // ---------------------------------------------------------------- producer state
+  uint4 kvr[8];   // k/v of one chunk in Gram-operand order: rho = l32, features 16ks + 8g + 0..7
+  uint4 qr[4];    // q: e = lane + 64m -> token e>>4, features 8*(e&15) + 0..7
+  float dr = 0.f; // delta of token `lane` (lanes 0..15)
+
+  auto p_load = [&](int cc) {
+    const int t0 = (chunk0 + cc) * C;
+    const int rho = l32;
+    const int tk = t0 + (rho >> 1);
+    const E* src = (rho & 1) ? gv : gk;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      uint4 x = make_uint4(0, 0, 0, 0);
+      if (tk < a.T)
+        x = *reinterpret_cast<const uint4*>(src + tok_base + tk * tok_stride + 16 * ks + 8 * g);
+      kvr[ks] = x;
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int e = lane + 64 * m;
+      const int tq = t0 + (e >> 4);
+      uint4 x = make_uint4(0, 0, 0, 0);
+      if (tq < a.T)
+        x = *reinterpret_cast<const uint4*>(gq + tok_base + tq * tok_stride + 8 * (e & 15));
+      qr[m] = x;
+    }
+    dr = 0.f;
+    if (lane < C && t0 + lane < a.T)
+      dr = load_scalar(a.delta, a.delta_dtype, dl_base + static_cast<int64_t>(t0 + lane) * a.H);
+  };
+
+  // Gram, LDS staging, Cayley blocks and T~ of the chunk held in kvr/qr/dr -> buffer nb
+  auto p_prepare = [&](int nb) {
+    const int rho = l32;
+    // token-major and feature-major copies
+    E* tdst = sm.tok[nb][rho & 1] + (rho >> 1) * TOK_LD;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      *reinterpret_cast<uint4*>(tdst + 16 * ks + 8 * g) = kvr[ks];
+      const V8 x = *reinterpret_cast<const V8*>(&kvr[ks]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sm.ut[nb][(16 * ks + 8 * g + i) * UT_LD + rho] = x[i];
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int e = lane + 64 * m;
+      *reinterpret_cast<uint4*>(sm.tok[nb][2] + (e >> 4) * TOK_LD + 8 * (e & 15)) = qr[m];
+    }
+    // Gram G = U^T U (A and B operands are the same registers)
+    f32x16 gacc = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const V8 x = *reinterpret_cast<const V8*>(&kvr[ks]);
+      gacc = MM::mma32(x, x, gacc);
+    }
+    // lane holds G[8(r/4) + 4g + r%4][l32]; store row l32 (G is symmetric)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4)
+      *reinterpret_cast<float4*>(&sm.gram[l32 * T_LD + 8 * q4 + 4 * g]) =
+          make_float4(gacc[4 * q4], gacc[4 * q4 + 1], gacc[4 * q4 + 2], gacc[4 * q4 + 3]);
+    wave_sync();
+    if (lane < C) {
+      const int t = lane;
+      const float kk = sm.gram[(2 * t) * T_LD + 2 * t];
+      const float vv = sm.gram[(2 * t + 1) * T_LD + 2 * t + 1];
+      const float kv = sm.gram[(2 * t) * T_LD + 2 * t + 1];
+      const cayley2 M = cayley_coeffs(dr, kk, vv, kv);
+      sm.mcoef[t] = make_float4(M.m00, M.m01, M.m10, M.m11);
+    }
+    wave_sync();
+    float* tt = sm.tt[nb];
+    // level 1: diagonal 8x8 blocks, lane = (block gb, column c)
+    if (lane < 32) {
+      const int gb = lane >> 3, c = lane & 7;
+      float x[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = 0.f;
+#pragma unroll
+      for (int t2 = 0; t2 < 4; ++t2) {
+        const int r0 = 8 * gb + 2 * t2;
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 2 * t2; ++i) {
+          s0 = fmaf(sm.gram[r0 * T_LD + 8 * gb + i], x[i], s0);
+          s1 = fmaf(sm.gram[(r0 + 1) * T_LD + 8 * gb + i], x[i], s1);
+        }
+        const float4 M = sm.mcoef[4 * gb + t2];
+        const float e0 = (c == 2 * t2 ? 1.f : 0.f) + s0;
+        const float e1 = (c == 2 * t2 + 1 ? 1.f : 0.f) + s1;
+        x[2 * t2] = fmaf(M.x, e0, M.y * e1);
+        x[2 * t2 + 1] = fmaf(M.z, e0, M.w * e1);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) tt[(8 * gb + i) * T_LD + 8 * gb + c] = x[i];
+    }
+    wave_sync();
+    // level 2: T~_{gr,gc} = T~_{gr,gr} * sum_{m=gc}^{gr-1} G_{gr,m} T~_{m,gc}
+    const int ea = lane >> 3, eb = lane & 7;
+#pragma unroll 1
+    for (int gr = 1; gr < 4; ++gr) {
+#pragma unroll 1
+      for (int gc = 0; gc < gr; ++gc) {
+        float s = 0.f;
+#pragma unroll 1
+        for (int m = gc; m < gr; ++m)
+#pragma unroll
+          for (int c = 0; c < 8; ++c)
+            s = fmaf(sm.gram[(8 * gr + ea) * T_LD + 8 * m + c], tt[(8 * m + c) * T_LD + 8 * gc + eb], s);
+        sm.sblk[gc * 64 + ea * 8 + eb] = s;
+      }
+      wave_sync();
+#pragma unroll 1
+      for (int gc = 0; gc < gr; ++gc) {
+        float y = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          y = fmaf(tt[(8 * gr + ea) * T_LD + 8 * gr + c], sm.sblk[gc * 64 + c * 8 + eb], y);
+        tt[(8 * gr + ea) * T_LD + 8 * gc + eb] = y;
+      }
+      wave_sync();
+    }
+  };
+
+  if (wave == NCW) {
+    // ================================================ producer: runs one chunk ahead
+    p_load(0);
+    p_prepare(0);
+    if (nch > 1) p_load(1);
+    __syncthreads();
+    for (int cc = 0; cc < nch; ++cc) {
+      if (cc + 1 < nch) {
+        p_prepare((cc & 1) ^ 1);
+        if (cc + 2 < nch) p_load(cc + 2);
+      }
+      __syncthreads();            // (A) chunk cc consumed, chunk cc+1 staged
+      if (READOUT) __syncthreads();  // (B) readout partials of chunk cc reduced
+    }
+    return;
+  }
+
+  // ================================================== consumers
+  f32x16 psi[4];  // slab columns 32*wave + l32, tile rt rows 32rt + 8(r/4) + 4g + r%4
+  const int col = 32 * wave + l32;
+  {
+    const float* src = nullptr;
+    if (seg == 0)
+      src = a.psi0 ? a.psi0 + bh * DD : nullptr;
+    else if (a.starts)
+      src = a.starts + (static_cast<int64_t>(seg - 1) * a.BH + bh) * DD;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 32 * rt + 8 * (r >> 2) + 4 * g + (r & 3);
+        psi[rt][r] = src ? src[row * D + col] : (row == col ? 1.f : 0.f);
+      }
+  }
+  __syncthreads();
+
+  for (int cc = 0; cc < nch; ++cc) {
+    const int cb = cc & 1;
+    {
+      const E* tk = sm.tok[cb][0];
+      const E* tv = sm.tok[cb][1];
+      const E* tq = sm.tok[cb][2];
+      const E* ut = sm.ut[cb];
+      const float* tt = sm.tt[cb];
+
+      // W = U^T Psi_slab  (32 x 32)
+      f32x16 W = {};
+      const E* urow = ((l32 & 1) ? tv : tk) + (l32 >> 1) * TOK_LD;
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const int d0 = 32 * rt + 16 * ks + 4 * g;
+          const V8 av = lds4x2<E>(urow + d0, urow + d0 + 8);
+          float x[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[i] = psi[rt][8 * ks + i];
+          if (PREC) {
+            V8 hi, lo;
+            split8<E>(x, hi, lo);
+            W = MM::mma32(av, hi, W);
+            W = MM::mma32(av, lo, W);
+          } else {
+            W = MM::mma32(av, round8<E>(x), W);
+          }
+        }
+
+      // Z = T~ W  (bf16x3: fp32-faithful)
+      f32x16 Z = {};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const float* trow = tt + l32 * T_LD + 16 * ks + 4 * g;
+        const float4 t0 = *reinterpret_cast<const float4*>(trow);
+        const float4 t1 = *reinterpret_cast<const float4*>(trow + 8);
+        const float tv8[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+        float wv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wv[i] = W[8 * ks + i];
+        V8 thi, tlo, whi, wlo;
+        split8<E>(tv8, thi, tlo);
+        split8<E>(wv, whi, wlo);
+        Z = MM::mma32(thi, whi, Z);
+        Z = MM::mma32(thi, wlo, Z);
+        Z = MM::mma32(tlo, whi, Z);
+      }
+
+      if (READOUT) {
+        E* ps = sm.ps[wave];
+        E* zs = sm.zs[wave];
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            ps[(32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) * PS_LD + l32] = static_cast<E>(psi[rt][r]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          zs[(8 * (r >> 2) + 4 * g + (r & 3)) * PS_LD + l32] = static_cast<E>(Z[r]);
+        wave_sync();
+        // O_w = S[:, slab] Q[slab, :] + U mask(Z[:, slab] Q[slab, :])   (128 x 16)
+        const V8 bq = lds8<E>(tq + l16 * TOK_LD + 32 * wave + 8 * g4);
+        f32x4 O[8];
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+          const f32x4 zero = {};
+          O[it] = MM::mma16(lds8<E>(ps + (16 * it + l16) * PS_LD + 8 * g4), bq, zero);
+        }
+        const f32x4 zero = {};
+        const f32x4 y0 = MM::mma16(lds8<E>(zs + l16 * PS_LD + 8 * g4), bq, zero);
+        const f32x4 y1 = MM::mma16(lds8<E>(zs + (16 + l16) * PS_LD + 8 * g4), bq, zero);
+        V8 by;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          by[r] = static_cast<E>(((4 * g4 + r) >> 1) <= l16 ? y0[r] : 0.f);
+          by[4 + r] = static_cast<E>(((16 + 4 * g4 + r) >> 1) <= l16 ? y1[r] : 0.f);
+        }
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+          const E* urow2 = ut + (16 * it + l16) * UT_LD;
+          O[it] = MM::mma16(lds4x2<E>(urow2 + 4 * g4, urow2 + 16 + 4 * g4), by, O[it]);
+        }
+        wave_sync();  // every lane is done reading ps before it is reused for O
+        float* op = reinterpret_cast<float*>(ps);
+#pragma unroll
+        for (int it = 0; it < 8; ++it)
+          *reinterpret_cast<float4*>(&op[l16 * OP_LD + 16 * it + 4 * g4]) =
+              make_float4(O[it][0], O[it][1], O[it][2], O[it][3]);
+      }
+
+      // Psi_slab += U Z
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        float zv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) zv[i] = Z[8 * ks + i];
+        V8 zhi, zlo;
+        if (PREC) split8<E>(zv, zhi, zlo);
+        else zhi = round8<E>(zv);
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+          const E* urow3 = ut + (32 * rt + l32) * UT_LD + 16 * ks + 4 * g;
+          const V8 av = lds4x2<E>(urow3, urow3 + 8);
+          psi[rt] = MM::mma32(av, zhi, psi[rt]);
+          if (PREC) psi[rt] = MM::mma32(av, zlo, psi[rt]);
+        }
+      }
+    }
+    __syncthreads();  // (A)
+    if (READOUT) {
+      if (tid < 256) {
+        const int t = tid >> 4, fg = tid & 15;
+        const int tok = (chunk0 + cc) * C + t;
+        if (tok < a.T) {
+          float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int w = 0; w < NCW; ++w) {
+            const float* op = reinterpret_cast<const float*>(sm.ps[w]) + t * OP_LD + 8 * fg;
+            const float4 x0 = *reinterpret_cast<const float4*>(op);
+            const float4 x1 = *reinterpret_cast<const float4*>(op + 4);
+            acc[0] += x0.x; acc[1] += x0.y; acc[2] += x0.z; acc[3] += x0.w;
+            acc[4] += x1.x; acc[5] += x1.y; acc[6] += x1.z; acc[7] += x1.w;
+          }
+          V8 o8;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o8[i] = static_cast<E>(acc[i]);
+          if (a.out != nullptr)
+            *reinterpret_cast<V8*>(static_cast<E*>(a.out) + tok_base + tok * tok_stride + 8 * fg) = o8;
+        }
+      }
+      __syncthreads();  // (B)
+    }
+  }
+
+  // ---------------------------------------------------------------- end state
+  {
+    float* dst = nullptr;
+    if (a.end_mode == 0) dst = a.ends + (static_cast<int64_t>(seg) * a.BH + bh) * DD;
+    else if (seg == a.nseg - 1) dst = a.ends + bh * DD;
+    if (dst) {
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          dst[(32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) * D + col] = psi[rt][r];
+    }
+  }
+}
+
+// start_s = P_{s-1} start_{s-1}, s = 1 .. S-1, start_0 = psi0 (identity if null).
+// One wave per (bh, 16-column block); the column block stays in accumulators.
+// bf16x3 (hi*hi + hi*lo + lo*hi) keeps the chain fp32-faithful.
+__global__ __launch_bounds__(64) void sssd_carry_kernel(const float* psi0, const float* P,
+                                                        float* starts, int BH, int S) {
+  typedef mfma_t<__bf16> MM;
+  typedef MM::v8 V8;
+  const int bh = blockIdx.x;
+  const int cbk = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int col = 16 * cbk + l16;
+  const int64_t DD = static_cast<int64_t>(D) * D;
+  f32x4 X[8];  // X[16it + 4g4 + r][col]
+#pragma unroll
+  for (int it = 0; it < 8; ++it)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * it + 4 * g4 + r;
+      X[it][r] = psi0 ? psi0[bh * DD + row * D + col] : (row == col ? 1.f : 0.f);
+    }
+  for (int s = 1; s < S; ++s) {
+    const float* Pm = P + (static_cast<int64_t>(s - 1) * BH + bh) * DD;
+    f32x4 Y[8];
+#pragma unroll
+    for (int it = 0; it < 8; ++it) Y[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      float xb[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        xb[r] = X[2 * ks][r];
+        xb[4 + r] = X[2 * ks + 1][r];
+      }
+      V8 xhi, xlo;
+      split8<__bf16>(xb, xhi, xlo);
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const float* prow = Pm + (16 * it + l16) * D + 32 * ks + 4 * g4;
+        const float4 p0 = *reinterpret_cast<const float4*>(prow);
+        const float4 p1 = *reinterpret_cast<const float4*>(prow + 16);
+        const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        V8 phi, plo;
+        split8<__bf16>(pv, phi, plo);
+        Y[it] = MM::mma16(phi, xhi, Y[it]);
+        Y[it] = MM::mma16(phi, xlo, Y[it]);
+        Y[it] = MM::mma16(plo, xhi, Y[it]);
+      }
+    }
+    float* dst = starts + (static_cast<int64_t>(s - 1) * BH + bh) * DD;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      X[it] = Y[it];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[(16 * it + 4 * g4 + r) * D + col] = Y[it][r];
+    }
+  }
+}
+
+}  // namespace chunk
+
+// ------------------------------------------------------------------ host side
+namespace {
+
+constexpr int kTargetWorkgroups = 256;  // one 5-wave workgroup per CU (LDS-limited)
+
+struct Plan {
+  int nchunks, seg_chunks, nseg;
+};
+
+Plan make_plan(int64_t BH, int64_t T) {
+  Plan p;
+  p.nchunks = static_cast<int>((T + chunk::C - 1) / chunk::C);
+  int64_t S = (kTargetWorkgroups + BH - 1) / BH;
+  const int64_t max_by_len = p.nchunks / 4;  // keep >= 4 chunks per segment
+  if (S > max_by_len) S = max_by_len;
+  if (S < 1) S = 1;
+  p.seg_chunks = static_cast<int>((p.nchunks + S - 1) / S);
+  p.nseg = (p.nchunks + p.seg_chunks - 1) / p.seg_chunks;
+  return p;
+}
+
+bool chunk_path(int64_t T, int64_t D, int io_dtype) {
+  return D == chunk::D && (io_dtype == VMI_BF16 || io_dtype == VMI_F16) && T >= 2 * chunk::C;
+}
+
+template <typename E>
+hipError_t run_chunked(const void* q, const void* k, const void* v, const void* delta,
+                       int delta_dtype, const float* psi_in, void* out, float* psi_out, int B,
+                       int T, int H, void* workspace, hipStream_t stream) {
+  const int BH = B * H;
+  const Plan p = make_plan(BH, T);
+  const int64_t DD = static_cast<int64_t>(chunk::D) * chunk::D;
+  chunk::Args a;
+  a.q = q; a.k = k; a.v = v; a.delta = delta; a.delta_dtype = delta_dtype;
+  a.T = T; a.H = H; a.BH = BH;
+  a.seg_chunks = p.seg_chunks;
+  a.nseg = p.nseg;
+  float* P = static_cast<float*>(workspace);
+  float* starts = P ? P + static_cast<int64_t>(p.nseg - 1) * BH * DD : nullptr;
+  if (p.nseg > 1) {
+    chunk::Args pa = a;
+    pa.psi0 = nullptr;
+    pa.starts = nullptr;
+    pa.out = nullptr;
+    pa.ends = P;
+    pa.end_mode = 0;
+    hipLaunchKernelGGL((chunk::sssd_chunk_kernel<E, false, true>), dim3(BH, p.nseg - 1),
+                       dim3(chunk::NT), 0, stream, pa);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(chunk::sssd_carry_kernel, dim3(BH, chunk::D / 16), dim3(64), 0, stream,
+                       psi_in, P, starts, BH, p.nseg);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  a.psi0 = psi_in;
+  a.starts = p.nseg > 1 ? starts : nullptr;
+  a.out = out;
+  a.ends = psi_out;
+  a.end_mode = 1;
+  hipLaunchKernelGGL((chunk::sssd_chunk_kernel<E, true, true>), dim3(BH, p.nseg), dim3(chunk::NT),
+                     0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t chunk_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int io_dtype) {
+  if (!chunk_path(T, D, io_dtype)) return 0;
+  const Plan p = make_plan(B * H, T);
+  if (p.nseg <= 1) return 0;
+  return static_cast<size_t>(2) * (p.nseg - 1) * B * H * D * D * sizeof(float);
+}
+
+bool use_chunk_path(int64_t T, int64_t D, int io_dtype) { return chunk_path(T, D, io_dtype); }
+
+hipError_t launch_sssd_chunked(const void* q, const void* k, const void* v, const void* delta,
+                               int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                               float* psi_out, int B, int T, int H, void* workspace,
+                               hipStream_t stream) {
+  if (io_dtype == VMI_BF16)
+    return run_chunked<__bf16>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, B, T, H,
+                               workspace, stream);
+  return run_chunked<_Float16>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, B, T, H,
+                               workspace, stream);
+}
+
+}  // namespace vmi

@@ -19,6 +19,14 @@ hipError_t dispatch_scan(const void* q, const void* k, const void* v, const void
                          float* psi_out, int B, int T, int H, int D, void* workspace,
                          size_t workspace_bytes, hipStream_t stream);
 
+// sssd_chunk.hip: chunk-parallel MFMA scan (bf16/fp16 I/O, head_dim 128).
+bool use_chunk_path(int64_t T, int64_t D, int io_dtype);
+size_t chunk_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int io_dtype);
+hipError_t launch_sssd_chunked(const void* q, const void* k, const void* v, const void* delta,
+                               int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                               float* psi_out, int B, int T, int H, void* workspace,
+                               hipStream_t stream);
+
 // cham_ns.hip: Newton-Schulz unitary retraction.
 size_t ns_workspace_bytes(int64_t batch, int64_t n);
 hipError_t launch_ns_retraction(const float* h_real, const float* h_imag, float* out_real,

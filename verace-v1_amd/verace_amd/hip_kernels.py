@@ -31,6 +31,10 @@ def _require_device(t: torch.Tensor, name: str) -> None:
                            "there is no CPU path")
 
 
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
@@ -65,9 +69,10 @@ def launch_sssd_hip_scan(
     if tuple(delta.shape) != (b, s, h):
         raise RuntimeError(f"verace_amd: delta must be [B, T, H] = {(b, s, h)}, got {tuple(delta.shape)}")
     io_code = _lib.dtype_code(q.dtype)
-    q_c = q.contiguous()
-    k_c = k.to(q.dtype).contiguous()
-    v_c = v.to(q.dtype).contiguous()
+    # the kernels read 16-byte vectors: contiguous and 16-byte aligned
+    q_c = _aligned(q.contiguous())
+    k_c = _aligned(k.to(q.dtype).contiguous())
+    v_c = _aligned(v.to(q.dtype).contiguous())
     delta_c = delta.contiguous()
     d_code = _lib.dtype_code(delta_c.dtype)
     psi_in = None
