@@ -37,21 +37,32 @@ constexpr int D = 128;
 constexpr int C = 16;           // tokens per chunk
 constexpr int R = 2 * C;        // rank rows per chunk
 constexpr int NCW = 4;          // consumer waves
-constexpr int NT = (NCW + 1) * 64;
+constexpr int NPW = 2;          // producer waves
+constexpr int NT = (NCW + NPW) * 64;
 constexpr int TOK_LD = D + 8;   // elements per token-major row (272 B)
 constexpr int UT_LD = R + 8;    // elements per feature-major row (80 B)
-constexpr int T_LD = R + 4;     // floats per T~ / Gram row
+constexpr int T_LD = R + 4;     // floats per Gram row
+constexpr int TT_LD = R + 8;    // elements per T~ hi/lo row (80 B)
 constexpr int PS_LD = 32 + 8;   // elements per stash row (80 B)
 constexpr int OP_LD = D + 4;    // floats per O-partial row
+
+// Producer-private scratch (one per producer wave).
+struct ProdScratch {
+  float gram[R * T_LD];         // Gram matrix G = U^T U (symmetric)
+  float4 mcoef[C];              // (m00, m01, m10, m11) per token
+  float drow[4][64];            // diagonal 8x8 blocks of T~, row-major [a*8 + c]
+  float dcol[4][64];            // the same blocks, column-major [b*8 + c]
+  float ocol[2][64];            // off-diagonal blocks reused by a later level, column-major
+  float sblk[2][64];            // S = sum_m G_gm T~_mh, column-major
+};
 
 template <typename E>
 struct Smem {
   E tok[2][3][C * TOK_LD];      // k, v, q of the chunk, token-major (double buffered)
   E ut[2][D * UT_LD];           // U feature-major: ut[d][rho]
-  float tt[2][R * T_LD];        // T~, row-major
-  float gram[R * T_LD];         // producer-private
-  float4 mcoef[C];              // producer-private: (m00, m01, m10, m11) per token
-  float sblk[3 * 64];           // producer-private scratch for T~ level 2
+  E tth[2][R * TT_LD];          // T~ = hi + lo (two 16-bit parts), row-major
+  E ttl[2][R * TT_LD];
+  ProdScratch pr[NPW];
   E ps[NCW][D * PS_LD];         // per-wave: chunk-start state slab (row-major), then O partial
   E zs[NCW][R * PS_LD];         // per-wave: Z slab (row-major)
 };
@@ -71,6 +82,19 @@ struct Args {
   int seg_chunks;       // chunks per segment
   int nseg;             // segments per sequence
 };
+
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for every
+// outstanding global load (its release fence), which would stall the whole
+// workgroup on the producers' prefetch of the chunk after next at every barrier.
+// Only LDS carries data between waves here, so waiting for this wave's LDS
+// operations (lgkmcnt(0)) before s_barrier is sufficient.  The empty asm
+// statements keep the compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt(63) expcnt(7) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -93,7 +117,7 @@ __device__ __forceinline__ typename mfma_t<E>::v8 lds4x2(const E* p0, const E* p
   return cat8<V4, V8>(lds4<E>(p0), lds4<E>(p1));
 }
 
-template <typename E, bool READOUT, bool PREC>
+template <typename E, typename DT, bool READOUT, bool PREC>
 __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
   typedef mfma_t<E> MM;
   typedef typename MM::v8 V8;
@@ -123,13 +147,22 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
   const E* gv = static_cast<const E*>(a.v);
 
   // zero T~ buffers (the strictly upper blocks are never written afterwards)
-  for (int i = tid; i < 2 * R * T_LD; i += NT) (&sm.tt[0][0])[i] = 0.0f;
+  for (int i = tid; i < 2 * R * TT_LD; i += NT) {
+    (&sm.tth[0][0])[i] = E(0.0f);
+    (&sm.ttl[0][0])[i] = E(0.0f);
+  }
   __syncthreads();
 
-  // ---------------------------------------------------------------- producer state
+  // ---------------------------------------------------------------- producers
+  // Two producer waves prepare chunk cc+1 while the consumers process chunk cc.
+  // Both compute the Gram matrix, the Cayley blocks and the diagonal blocks of T~;
+  // role 0 stages k/v (token- and feature-major), writes the diagonal blocks and the
+  // off-diagonal block column 0 of T~; role 1 stages q and writes block columns 1, 2.
+  const int role = wave - NCW;
   uint4 kvr[8];   // k/v of one chunk in Gram-operand order: rho = l32, features 16ks + 8g + 0..7
-  uint4 qr[4];    // q: e = lane + 64m -> token e>>4, features 8*(e&15) + 0..7
-  float dr = 0.f; // delta of token `lane` (lanes 0..15)
+  uint4 qr[4];    // q: e = lane + 64m -> token e>>4, features 8*(e&15) + 0..7 (role 1)
+  DT dr;          // raw delta of token `lane` (lanes 0..15); converted when used so the
+                 // prefetch is never waited for in the iteration that issues it
 
   auto p_load = [&](int cc) {
     const int t0 = (chunk0 + cc) * C;
@@ -143,36 +176,52 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
         x = *reinterpret_cast<const uint4*>(src + tok_base + tk * tok_stride + 16 * ks + 8 * g);
       kvr[ks] = x;
     }
+    if (role == 1) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int e = lane + 64 * m;
-      const int tq = t0 + (e >> 4);
-      uint4 x = make_uint4(0, 0, 0, 0);
-      if (tq < a.T)
-        x = *reinterpret_cast<const uint4*>(gq + tok_base + tq * tok_stride + 8 * (e & 15));
-      qr[m] = x;
+      for (int m = 0; m < 4; ++m) {
+        const int e = lane + 64 * m;
+        const int tq = t0 + (e >> 4);
+        uint4 x = make_uint4(0, 0, 0, 0);
+        if (tq < a.T)
+          x = *reinterpret_cast<const uint4*>(gq + tok_base + tq * tok_stride + 8 * (e & 15));
+        qr[m] = x;
+      }
     }
-    dr = 0.f;
+    dr = DT{};
     if (lane < C && t0 + lane < a.T)
-      dr = load_scalar(a.delta, a.delta_dtype, dl_base + static_cast<int64_t>(t0 + lane) * a.H);
+      dr = static_cast<const DT*>(a.delta)[dl_base + static_cast<int64_t>(t0 + lane) * a.H];
   };
 
-  // Gram, LDS staging, Cayley blocks and T~ of the chunk held in kvr/qr/dr -> buffer nb
+  auto dot8 = [](const float* x, const float* y) {
+    const float4 x0 = *reinterpret_cast<const float4*>(x);
+    const float4 x1 = *reinterpret_cast<const float4*>(x + 4);
+    const float4 y0 = *reinterpret_cast<const float4*>(y);
+    const float4 y1 = *reinterpret_cast<const float4*>(y + 4);
+    float s = x0.x * y0.x;
+    s = fmaf(x0.y, y0.y, s); s = fmaf(x0.z, y0.z, s); s = fmaf(x0.w, y0.w, s);
+    s = fmaf(x1.x, y1.x, s); s = fmaf(x1.y, y1.y, s); s = fmaf(x1.z, y1.z, s);
+    return fmaf(x1.w, y1.w, s);
+  };
+
+  // Stage, Gram, Cayley blocks and T~ of the chunk held in kvr/qr/dr -> buffer nb.
   auto p_prepare = [&](int nb) {
+    ProdScratch& P = sm.pr[role];
     const int rho = l32;
-    // token-major and feature-major copies
-    E* tdst = sm.tok[nb][rho & 1] + (rho >> 1) * TOK_LD;
+    if (role == 0) {
+      E* tdst = sm.tok[nb][rho & 1] + (rho >> 1) * TOK_LD;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      *reinterpret_cast<uint4*>(tdst + 16 * ks + 8 * g) = kvr[ks];
-      const V8 x = *reinterpret_cast<const V8*>(&kvr[ks]);
+      for (int ks = 0; ks < 8; ++ks) {
+        *reinterpret_cast<uint4*>(tdst + 16 * ks + 8 * g) = kvr[ks];
+        const V8 x = *reinterpret_cast<const V8*>(&kvr[ks]);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sm.ut[nb][(16 * ks + 8 * g + i) * UT_LD + rho] = x[i];
-    }
+        for (int i = 0; i < 8; ++i) sm.ut[nb][(16 * ks + 8 * g + i) * UT_LD + rho] = x[i];
+      }
+    } else {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int e = lane + 64 * m;
-      *reinterpret_cast<uint4*>(sm.tok[nb][2] + (e >> 4) * TOK_LD + 8 * (e & 15)) = qr[m];
+      for (int m = 0; m < 4; ++m) {
+        const int e = lane + 64 * m;
+        *reinterpret_cast<uint4*>(sm.tok[nb][2] + (e >> 4) * TOK_LD + 8 * (e & 15)) = qr[m];
+      }
     }
     // Gram G = U^T U (A and B operands are the same registers)
     f32x16 gacc = {};
@@ -181,76 +230,102 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
       const V8 x = *reinterpret_cast<const V8*>(&kvr[ks]);
       gacc = MM::mma32(x, x, gacc);
     }
-    // lane holds G[8(r/4) + 4g + r%4][l32]; store row l32 (G is symmetric)
+    // lane holds G[8(r/4) + 4g + r%4][l32]; G is symmetric, so store it as row l32
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4)
-      *reinterpret_cast<float4*>(&sm.gram[l32 * T_LD + 8 * q4 + 4 * g]) =
+      *reinterpret_cast<float4*>(&P.gram[l32 * T_LD + 8 * q4 + 4 * g]) =
           make_float4(gacc[4 * q4], gacc[4 * q4 + 1], gacc[4 * q4 + 2], gacc[4 * q4 + 3]);
     wave_sync();
     if (lane < C) {
       const int t = lane;
-      const float kk = sm.gram[(2 * t) * T_LD + 2 * t];
-      const float vv = sm.gram[(2 * t + 1) * T_LD + 2 * t + 1];
-      const float kv = sm.gram[(2 * t) * T_LD + 2 * t + 1];
-      const cayley2 M = cayley_coeffs(dr, kk, vv, kv);
-      sm.mcoef[t] = make_float4(M.m00, M.m01, M.m10, M.m11);
+      const float kk = P.gram[(2 * t) * T_LD + 2 * t];
+      const float vv = P.gram[(2 * t + 1) * T_LD + 2 * t + 1];
+      const float kv = P.gram[(2 * t) * T_LD + 2 * t + 1];
+      const cayley2 M = cayley_coeffs(io<DT>::to_f32(dr), kk, vv, kv);
+      P.mcoef[t] = make_float4(M.m00, M.m01, M.m10, M.m11);
     }
     wave_sync();
-    float* tt = sm.tt[nb];
-    // level 1: diagonal 8x8 blocks, lane = (block gb, column c)
+    E* tth = sm.tth[nb];
+    E* ttl = sm.ttl[nb];
+    auto tt_store = [&](int row, int col, float x) {
+      const E hpart = static_cast<E>(x);
+      tth[row * TT_LD + col] = hpart;
+      ttl[row * TT_LD + col] = static_cast<E>(x - static_cast<float>(hpart));
+    };
+    // level 1: diagonal 8x8 blocks by forward substitution, lane = (block gb, column c)
     if (lane < 32) {
       const int gb = lane >> 3, c = lane & 7;
+      float gblk[8][8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const float4 g0 = *reinterpret_cast<const float4*>(&P.gram[(8 * gb + r) * T_LD + 8 * gb]);
+        const float4 g1 = *reinterpret_cast<const float4*>(&P.gram[(8 * gb + r) * T_LD + 8 * gb + 4]);
+        gblk[r][0] = g0.x; gblk[r][1] = g0.y; gblk[r][2] = g0.z; gblk[r][3] = g0.w;
+        gblk[r][4] = g1.x; gblk[r][5] = g1.y; gblk[r][6] = g1.z; gblk[r][7] = g1.w;
+      }
       float x[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = 0.f;
-#pragma unroll
       for (int t2 = 0; t2 < 4; ++t2) {
-        const int r0 = 8 * gb + 2 * t2;
         float s0 = 0.f, s1 = 0.f;
 #pragma unroll
         for (int i = 0; i < 2 * t2; ++i) {
-          s0 = fmaf(sm.gram[r0 * T_LD + 8 * gb + i], x[i], s0);
-          s1 = fmaf(sm.gram[(r0 + 1) * T_LD + 8 * gb + i], x[i], s1);
+          s0 = fmaf(gblk[2 * t2][i], x[i], s0);
+          s1 = fmaf(gblk[2 * t2 + 1][i], x[i], s1);
         }
-        const float4 M = sm.mcoef[4 * gb + t2];
+        const float4 M = P.mcoef[4 * gb + t2];
         const float e0 = (c == 2 * t2 ? 1.f : 0.f) + s0;
         const float e1 = (c == 2 * t2 + 1 ? 1.f : 0.f) + s1;
         x[2 * t2] = fmaf(M.x, e0, M.y * e1);
         x[2 * t2 + 1] = fmaf(M.z, e0, M.w * e1);
       }
+      *reinterpret_cast<float4*>(&P.dcol[gb][c * 8]) = make_float4(x[0], x[1], x[2], x[3]);
+      *reinterpret_cast<float4*>(&P.dcol[gb][c * 8 + 4]) = make_float4(x[4], x[5], x[6], x[7]);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) tt[(8 * gb + i) * T_LD + 8 * gb + c] = x[i];
+      for (int i = 0; i < 8; ++i) P.drow[gb][i * 8 + c] = x[i];
+      if (role == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) tt_store(8 * gb + i, 8 * gb + c, x[i]);
+      }
     }
     wave_sync();
-    // level 2: T~_{gr,gc} = T~_{gr,gr} * sum_{m=gc}^{gr-1} G_{gr,m} T~_{m,gc}
+    // level 2: T~_{g,h} = T~_{g,g} S,  S = sum_{m=h}^{g-1} G_{g,m} T~_{m,h};  lane = element (ea, eb)
     const int ea = lane >> 3, eb = lane & 7;
-#pragma unroll 1
-    for (int gr = 1; gr < 4; ++gr) {
-#pragma unroll 1
-      for (int gc = 0; gc < gr; ++gc) {
-        float s = 0.f;
-#pragma unroll 1
-        for (int m = gc; m < gr; ++m)
+    if (role == 0) {
+      // block column 0: g = 1, 2, 3
 #pragma unroll
-          for (int c = 0; c < 8; ++c)
-            s = fmaf(sm.gram[(8 * gr + ea) * T_LD + 8 * m + c], tt[(8 * m + c) * T_LD + 8 * gc + eb], s);
-        sm.sblk[gc * 64 + ea * 8 + eb] = s;
+      for (int gr = 1; gr < 4; ++gr) {
+        const float* grow = &P.gram[(8 * gr + ea) * T_LD];
+        float sv = dot8(grow, &P.dcol[0][eb * 8]);
+        if (gr >= 2) sv += dot8(grow + 8, &P.ocol[0][eb * 8]);
+        if (gr >= 3) sv += dot8(grow + 16, &P.ocol[1][eb * 8]);
+        P.sblk[0][eb * 8 + ea] = sv;
+        wave_sync();
+        const float y = dot8(&P.drow[gr][ea * 8], &P.sblk[0][eb * 8]);
+        tt_store(8 * gr + ea, eb, y);
+        if (gr < 3) P.ocol[gr - 1][eb * 8 + ea] = y;
+        wave_sync();
       }
+    } else {
+      // blocks (2,1) and (3,2), then (3,1)
+      const float* g2 = &P.gram[(16 + ea) * T_LD];
+      const float* g3 = &P.gram[(24 + ea) * T_LD];
+      P.sblk[0][eb * 8 + ea] = dot8(g2 + 8, &P.dcol[1][eb * 8]);
+      P.sblk[1][eb * 8 + ea] = dot8(g3 + 16, &P.dcol[2][eb * 8]);
       wave_sync();
-#pragma unroll 1
-      for (int gc = 0; gc < gr; ++gc) {
-        float y = 0.f;
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-          y = fmaf(tt[(8 * gr + ea) * T_LD + 8 * gr + c], sm.sblk[gc * 64 + c * 8 + eb], y);
-        tt[(8 * gr + ea) * T_LD + 8 * gc + eb] = y;
-      }
+      const float y21 = dot8(&P.drow[2][ea * 8], &P.sblk[0][eb * 8]);
+      const float y32 = dot8(&P.drow[3][ea * 8], &P.sblk[1][eb * 8]);
+      tt_store(16 + ea, 8 + eb, y21);
+      tt_store(24 + ea, 16 + eb, y32);
+      P.ocol[0][eb * 8 + ea] = y21;
       wave_sync();
+      P.sblk[0][eb * 8 + ea] = dot8(g3 + 8, &P.dcol[1][eb * 8]) + dot8(g3 + 16, &P.ocol[0][eb * 8]);
+      wave_sync();
+      tt_store(24 + ea, 8 + eb, dot8(&P.drow[3][ea * 8], &P.sblk[0][eb * 8]));
     }
   };
 
-  if (wave == NCW) {
-    // ================================================ producer: runs one chunk ahead
+  if (wave >= NCW) {
+    // ================================================ producers: run one chunk ahead
     p_load(0);
     p_prepare(0);
     if (nch > 1) p_load(1);
@@ -260,8 +335,8 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
         p_prepare((cc & 1) ^ 1);
         if (cc + 2 < nch) p_load(cc + 2);
       }
-      __syncthreads();            // (A) chunk cc consumed, chunk cc+1 staged
-      if (READOUT) __syncthreads();  // (B) readout partials of chunk cc reduced
+      lds_barrier();               // (A) chunk cc consumed, chunk cc+1 staged
+      if (READOUT) lds_barrier();  // (B) readout partials of chunk cc reduced
     }
     return;
   }
@@ -275,13 +350,19 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
       src = a.psi0 ? a.psi0 + bh * DD : nullptr;
     else if (a.starts)
       src = a.starts + (static_cast<int64_t>(seg - 1) * a.BH + bh) * DD;
+    if (src) {
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+      for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = 32 * rt + 8 * (r >> 2) + 4 * g + (r & 3);
-        psi[rt][r] = src ? src[row * D + col] : (row == col ? 1.f : 0.f);
-      }
+        for (int r = 0; r < 16; ++r)
+          psi[rt][r] = src[(32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) * D + col];
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          psi[rt][r] = (32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) == col ? 1.f : 0.f;
+    }
   }
   __syncthreads();
 
@@ -292,10 +373,12 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
       const E* tv = sm.tok[cb][1];
       const E* tq = sm.tok[cb][2];
       const E* ut = sm.ut[cb];
-      const float* tt = sm.tt[cb];
-
-      // W = U^T Psi_slab  (32 x 32)
+      
+      // W = U^T Psi_slab  (32 x 32).  PREC: Psi split hi + lo (fp32-faithful);
+      // otherwise Psi rounded once to 16 bits, and the rounded values double as the
+      // readout stash below.
       f32x16 W = {};
+      V8 pb[4][2];
       const E* urow = ((l32 & 1) ? tv : tk) + (l32 >> 1) * TOK_LD;
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt)
@@ -307,32 +390,38 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) x[i] = psi[rt][8 * ks + i];
           if (PREC) {
-            V8 hi, lo;
-            split8<E>(x, hi, lo);
-            W = MM::mma32(av, hi, W);
+            V8 lo;
+            split8<E>(x, pb[rt][ks], lo);
+            W = MM::mma32(av, pb[rt][ks], W);
             W = MM::mma32(av, lo, W);
           } else {
-            W = MM::mma32(av, round8<E>(x), W);
+            pb[rt][ks] = round8<E>(x);
+            W = MM::mma32(av, pb[rt][ks], W);
           }
         }
 
-      // Z = T~ W  (bf16x3: fp32-faithful)
+      // Z = T~ W with T~ = hi + lo from the producers; PREC also splits W.
       f32x16 Z = {};
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const float* trow = tt + l32 * T_LD + 16 * ks + 4 * g;
-        const float4 t0 = *reinterpret_cast<const float4*>(trow);
-        const float4 t1 = *reinterpret_cast<const float4*>(trow + 8);
-        const float tv8[8] = {t0.x, t0.y, t0.z, t0.w, t1.x, t1.y, t1.z, t1.w};
+        const E* th = sm.tth[cb] + l32 * TT_LD + 16 * ks + 4 * g;
+        const E* tl = sm.ttl[cb] + l32 * TT_LD + 16 * ks + 4 * g;
+        const V8 ahi = lds4x2<E>(th, th + 8);
+        const V8 alo = lds4x2<E>(tl, tl + 8);
         float wv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) wv[i] = W[8 * ks + i];
-        V8 thi, tlo, whi, wlo;
-        split8<E>(tv8, thi, tlo);
-        split8<E>(wv, whi, wlo);
-        Z = MM::mma32(thi, whi, Z);
-        Z = MM::mma32(thi, wlo, Z);
-        Z = MM::mma32(tlo, whi, Z);
+        if (PREC) {
+          V8 whi, wlo;
+          split8<E>(wv, whi, wlo);
+          Z = MM::mma32(ahi, whi, Z);
+          Z = MM::mma32(ahi, wlo, Z);
+          Z = MM::mma32(alo, whi, Z);
+        } else {
+          const V8 wb = round8<E>(wv);
+          Z = MM::mma32(ahi, wb, Z);
+          Z = MM::mma32(alo, wb, Z);
+        }
       }
 
       if (READOUT) {
@@ -341,8 +430,10 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            ps[(32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) * PS_LD + l32] = static_cast<E>(psi[rt][r]);
+          for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              ps[(32 * rt + 16 * ks + 8 * (i >> 2) + 4 * g + (i & 3)) * PS_LD + l32] = pb[rt][ks][i];
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           zs[(8 * (r >> 2) + 4 * g + (r & 3)) * PS_LD + l32] = static_cast<E>(Z[r]);
@@ -395,7 +486,7 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
         }
       }
     }
-    __syncthreads();  // (A)
+    lds_barrier();  // (A)
     if (READOUT) {
       if (tid < 256) {
         const int t = tid >> 4, fg = tid & 15;
@@ -417,7 +508,7 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
             *reinterpret_cast<V8*>(static_cast<E*>(a.out) + tok_base + tok * tok_stride + 8 * fg) = o8;
         }
       }
-      __syncthreads();  // (B)
+      lds_barrier();  // (B)
     }
   }
 
@@ -522,8 +613,12 @@ bool chunk_path(int64_t T, int64_t D, int io_dtype) {
   return D == chunk::D && (io_dtype == VMI_BF16 || io_dtype == VMI_F16) && T >= 2 * chunk::C;
 }
 
-template <typename E>
-hipError_t run_chunked(const void* q, const void* k, const void* v, const void* delta,
+// PREC (the only variant dispatched): the state, W and Z enter the chunk GEMMs as
+// hi + lo 16-bit pairs, so every product is fp32-faithful and the state norm is kept
+// to ~1e-6 per 4096 tokens.  PREC=false rounds them to 16 bits once (about 6% faster
+// at the OP shape, but its norm drift grows to ~4e-5 per 4096 tokens).
+template <typename E, typename DT, bool PREC>
+hipError_t run_chunked_p(const void* q, const void* k, const void* v, const void* delta,
                        int delta_dtype, const float* psi_in, void* out, float* psi_out, int B,
                        int T, int H, void* workspace, hipStream_t stream) {
   const int BH = B * H;
@@ -543,7 +638,7 @@ hipError_t run_chunked(const void* q, const void* k, const void* v, const void* 
     pa.out = nullptr;
     pa.ends = P;
     pa.end_mode = 0;
-    hipLaunchKernelGGL((chunk::sssd_chunk_kernel<E, false, true>), dim3(BH, p.nseg - 1),
+    hipLaunchKernelGGL((chunk::sssd_chunk_kernel<E, DT, false, PREC>), dim3(BH, p.nseg - 1),
                        dim3(chunk::NT), 0, stream, pa);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -557,9 +652,17 @@ hipError_t run_chunked(const void* q, const void* k, const void* v, const void* 
   a.out = out;
   a.ends = psi_out;
   a.end_mode = 1;
-  hipLaunchKernelGGL((chunk::sssd_chunk_kernel<E, true, true>), dim3(BH, p.nseg), dim3(chunk::NT),
+  hipLaunchKernelGGL((chunk::sssd_chunk_kernel<E, DT, true, PREC>), dim3(BH, p.nseg), dim3(chunk::NT),
                      0, stream, a);
   return hipGetLastError();
+}
+
+template <typename E, typename DT>
+hipError_t run_chunked(const void* q, const void* k, const void* v, const void* delta,
+                       int delta_dtype, const float* psi_in, void* out, float* psi_out, int B,
+                       int T, int H, void* workspace, hipStream_t stream) {
+  return run_chunked_p<E, DT, true>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, B, T, H,
+                                    workspace, stream);
 }
 
 }  // namespace
@@ -577,11 +680,18 @@ hipError_t launch_sssd_chunked(const void* q, const void* k, const void* v, cons
                                int io_dtype, int delta_dtype, const float* psi_in, void* out,
                                float* psi_out, int B, int T, int H, void* workspace,
                                hipStream_t stream) {
-  if (io_dtype == VMI_BF16)
-    return run_chunked<__bf16>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, B, T, H,
-                               workspace, stream);
-  return run_chunked<_Float16>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, B, T, H,
-                               workspace, stream);
+#define VMI_RUN(E, DT) \
+  return run_chunked<E, DT>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, B, T, H, workspace, \
+                            stream)
+  if (io_dtype == VMI_BF16) {
+    if (delta_dtype == VMI_F32) VMI_RUN(__bf16, float);
+    if (delta_dtype == VMI_BF16) VMI_RUN(__bf16, bf16_t);
+    VMI_RUN(__bf16, f16_t);
+  }
+  if (delta_dtype == VMI_F32) VMI_RUN(_Float16, float);
+  if (delta_dtype == VMI_BF16) VMI_RUN(_Float16, bf16_t);
+  VMI_RUN(_Float16, f16_t);
+#undef VMI_RUN
 }
 
 }  // namespace vmi

@@ -30,10 +30,12 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 
 template <typename T> struct io;
 template <> struct io<float> {
+  static __device__ __forceinline__ float to_f32(float x) { return x; }
   static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
   static __device__ __forceinline__ void store(float* p, int64_t i, float x) { p[i] = x; }
 };
 template <> struct io<bf16_t> {
+  static __device__ __forceinline__ float to_f32(bf16_t x) { return bf16_to_f32(x.bits); }
   static __device__ __forceinline__ float load(const bf16_t* p, int64_t i) {
     return bf16_to_f32(p[i].bits);
   }
@@ -42,6 +44,7 @@ template <> struct io<bf16_t> {
   }
 };
 template <> struct io<f16_t> {
+  static __device__ __forceinline__ float to_f32(f16_t x) { return static_cast<float>(x); }
   static __device__ __forceinline__ float load(const f16_t* p, int64_t i) {
     return static_cast<float>(p[i]);
   }

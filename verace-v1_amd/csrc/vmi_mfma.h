@@ -55,8 +55,11 @@ __device__ __forceinline__ V8 cat8(V4 lo, V4 hi) {
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// fp32 -> (hi, lo) split: hi = round(x), lo = round(x - hi).  hi*b + lo*b carries
-// ~16 mantissa bits of x into an MFMA product with a 16-bit operand b.
+// fp32 -> (hi, lo) split so that hi*b + lo*b carries ~16 mantissa bits of x into an
+// MFMA product with a 16-bit operand b.
+//   fp16: hi = round(x), lo = round(x - hi).
+//   bf16: the same, with float(hi) rebuilt from the packed pair by shifts instead of a
+//         second conversion (3 VALU per value).
 template <typename E>
 __device__ __forceinline__ void split8(const float* x, typename mfma_t<E>::v8& hi,
                                        typename mfma_t<E>::v8& lo) {
@@ -65,6 +68,19 @@ __device__ __forceinline__ void split8(const float* x, typename mfma_t<E>::v8& h
     const E h = static_cast<E>(x[i]);
     hi[i] = h;
     lo[i] = static_cast<E>(x[i] - static_cast<float>(h));
+  }
+}
+
+template <>
+__device__ __forceinline__ void split8<__bf16>(const float* x, bf16x8& hi, bf16x8& lo) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) hi[i] = static_cast<__bf16>(x[i]);  // v_cvt_pk_bf16_f32 pairs
+  const u32x4 hp = __builtin_bit_cast(u32x4, hi);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lo[2 * i] = static_cast<__bf16>(x[2 * i] - __uint_as_float(hp[i] << 16));
+    lo[2 * i + 1] = static_cast<__bf16>(x[2 * i + 1] - __uint_as_float(hp[i] & 0xffff0000u));
   }
 }
 
