@@ -17,8 +17,15 @@
 //     MFMA accumulators for the whole segment; columns evolve independently, so
 //     W, Z and the update need no cross-wave traffic.  The readout is reduced
 //     across waves through LDS.
-//   wave 4 (producer) runs one chunk ahead: global loads, LDS staging (token-
-//     major and feature-major copies of k/v), Gram on MFMA, Cayley blocks and T~.
+//   waves 4-5 (producers) form a two-stage pipeline ahead of the consumers:
+//     role 0 prefetches chunk n+1 into registers and, for chunk n, stages k/v/q
+//     in LDS (token-major and feature-major), computes the Gram matrix on MFMA,
+//     the Cayley blocks and the diagonal blocks of T~;
+//     role 1 computes the off-diagonal blocks of T~ for chunk n-1 and writes the
+//     complete T~ (as 16-bit hi + lo) for the consumers.
+//   While the consumers process chunk c, role 1 works on c+1 and role 0 on c+2,
+//   so no wave waits on another inside an iteration; one LDS barrier per chunk
+//   (two with the readout) hands the buffers over.
 //
 // Long sequences are split into segments processed by independent workgroups:
 //   pass A (READOUT=false): each segment s < S-1 from the identity -> its
@@ -46,23 +53,28 @@ constexpr int TT_LD = R + 8;    // elements per T~ hi/lo row (80 B)
 constexpr int PS_LD = 32 + 8;   // elements per stash row (80 B)
 constexpr int OP_LD = D + 4;    // floats per O-partial row
 
-// Producer-private scratch (one per producer wave).
-struct ProdScratch {
+// Written by producer role 0 for chunk n, read by role 1 one iteration later.
+struct Stage0 {
   float gram[R * T_LD];         // Gram matrix G = U^T U (symmetric)
   float4 mcoef[C];              // (m00, m01, m10, m11) per token
   float drow[4][64];            // diagonal 8x8 blocks of T~, row-major [a*8 + c]
   float dcol[4][64];            // the same blocks, column-major [b*8 + c]
-  float ocol[2][64];            // off-diagonal blocks reused by a later level, column-major
-  float sblk[2][64];            // S = sum_m G_gm T~_mh, column-major
+};
+
+// Private to producer role 1.
+struct Stage1 {
+  float ocol[3][64];            // T~_10, T~_21, T~_20, column-major
+  float sblk[3][64];            // S = sum_m G_gm T~_mh, column-major
 };
 
 template <typename E>
 struct Smem {
-  E tok[2][3][C * TOK_LD];      // k, v, q of the chunk, token-major (double buffered)
-  E ut[2][D * UT_LD];           // U feature-major: ut[d][rho]
+  E tok[3][3][C * TOK_LD];      // k, v, q of a chunk, token-major (3 chunks in flight)
+  E ut[3][D * UT_LD];           // U feature-major: ut[d][rho]
   E tth[2][R * TT_LD];          // T~ = hi + lo (two 16-bit parts), row-major
   E ttl[2][R * TT_LD];
-  ProdScratch pr[NPW];
+  Stage0 s0[2];
+  Stage1 s1;
   E ps[NCW][D * PS_LD];         // per-wave: chunk-start state slab (row-major), then O partial
   E zs[NCW][R * PS_LD];         // per-wave: Z slab (row-major)
 };
@@ -154,42 +166,32 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
   __syncthreads();
 
   // ---------------------------------------------------------------- producers
-  // Two producer waves prepare chunk cc+1 while the consumers process chunk cc.
-  // Both compute the Gram matrix, the Cayley blocks and the diagonal blocks of T~;
-  // role 0 stages k/v (token- and feature-major), writes the diagonal blocks and the
-  // off-diagonal block column 0 of T~; role 1 stages q and writes block columns 1, 2.
-  const int role = wave - NCW;
-  uint4 kvr[8];   // k/v of one chunk in Gram-operand order: rho = l32, features 16ks + 8g + 0..7
-  uint4 qr[4];    // q: e = lane + 64m -> token e>>4, features 8*(e&15) + 0..7 (role 1)
-  DT dr;          // raw delta of token `lane` (lanes 0..15); converted when used so the
-                 // prefetch is never waited for in the iteration that issues it
+  // Loop index it runs from -2 to nch-1 in every wave; consumers work on chunk it,
+  // producer role 1 on chunk it+1, role 0 on chunk it+2.  Every wave executes one LDS
+  // barrier per iteration (plus one more after the readout reduction).
+  struct Regs {
+    uint4 kv[8];  // k/v in Gram-operand order: rho = l32, features 16ks + 8g + 0..7
+    uint4 q[4];   // q: e = lane + 64m -> token e>>4, features 8*(e&15) + 0..7
+    DT d;         // raw delta of token `lane` (lanes 0..15)
+  };
 
-  auto p_load = [&](int cc) {
-    const int t0 = (chunk0 + cc) * C;
-    const int rho = l32;
-    const int tk = t0 + (rho >> 1);
-    const E* src = (rho & 1) ? gv : gk;
+  // Branch-free loads: token indices are clamped to T-1 for the address and tokens
+  // past the end are zeroed when staged (p_stage), so no load is predicated and the
+  // destination registers need no initialisation while older loads are in flight.
+  auto p_load = [&](Regs& r, int n) {
+    const int t0 = (chunk0 + n) * C;
+    const int tk = min(t0 + (l32 >> 1), a.T - 1);
+    const E* src = ((l32 & 1) ? gv : gk) + tok_base + tk * tok_stride + 8 * g;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      uint4 x = make_uint4(0, 0, 0, 0);
-      if (tk < a.T)
-        x = *reinterpret_cast<const uint4*>(src + tok_base + tk * tok_stride + 16 * ks + 8 * g);
-      kvr[ks] = x;
-    }
-    if (role == 1) {
+    for (int ks = 0; ks < 8; ++ks) r.kv[ks] = *reinterpret_cast<const uint4*>(src + 16 * ks);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int e = lane + 64 * m;
-        const int tq = t0 + (e >> 4);
-        uint4 x = make_uint4(0, 0, 0, 0);
-        if (tq < a.T)
-          x = *reinterpret_cast<const uint4*>(gq + tok_base + tq * tok_stride + 8 * (e & 15));
-        qr[m] = x;
-      }
+    for (int m = 0; m < 4; ++m) {
+      const int e = lane + 64 * m;
+      const int tq = min(t0 + (e >> 4), a.T - 1);
+      r.q[m] = *reinterpret_cast<const uint4*>(gq + tok_base + tq * tok_stride + 8 * (e & 15));
     }
-    dr = DT{};
-    if (lane < C && t0 + lane < a.T)
-      dr = static_cast<const DT*>(a.delta)[dl_base + static_cast<int64_t>(t0 + lane) * a.H];
+    const int td = min(t0 + (lane & (C - 1)), a.T - 1);
+    r.d = static_cast<const DT*>(a.delta)[dl_base + static_cast<int64_t>(td) * a.H];
   };
 
   auto dot8 = [](const float* x, const float* y) {
@@ -197,37 +199,48 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     const float4 x1 = *reinterpret_cast<const float4*>(x + 4);
     const float4 y0 = *reinterpret_cast<const float4*>(y);
     const float4 y1 = *reinterpret_cast<const float4*>(y + 4);
-    float s = x0.x * y0.x;
-    s = fmaf(x0.y, y0.y, s); s = fmaf(x0.z, y0.z, s); s = fmaf(x0.w, y0.w, s);
-    s = fmaf(x1.x, y1.x, s); s = fmaf(x1.y, y1.y, s); s = fmaf(x1.z, y1.z, s);
-    return fmaf(x1.w, y1.w, s);
+    float sacc = x0.x * y0.x;
+    sacc = fmaf(x0.y, y0.y, sacc); sacc = fmaf(x0.z, y0.z, sacc); sacc = fmaf(x0.w, y0.w, sacc);
+    sacc = fmaf(x1.x, y1.x, sacc); sacc = fmaf(x1.y, y1.y, sacc); sacc = fmaf(x1.z, y1.z, sacc);
+    return fmaf(x1.w, y1.w, sacc);
   };
 
-  // Stage, Gram, Cayley blocks and T~ of the chunk held in kvr/qr/dr -> buffer nb.
-  auto p_prepare = [&](int nb) {
-    ProdScratch& P = sm.pr[role];
+  // role 0, chunk n: stage inputs, Gram, Cayley blocks, diagonal blocks of T~
+  auto p_stage = [&](const Regs& r_in, int n) {
+    const int nb = n % 3;
+    Stage0& P = sm.s0[n & 1];
     const int rho = l32;
-    if (role == 0) {
-      E* tdst = sm.tok[nb][rho & 1] + (rho >> 1) * TOK_LD;
+    const int t0 = (chunk0 + n) * C;
+    Regs r = r_in;
+    if (t0 + C > a.T) {  // last, partial chunk: zero the tokens past the end
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      if (t0 + (l32 >> 1) >= a.T) {
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        *reinterpret_cast<uint4*>(tdst + 16 * ks + 8 * g) = kvr[ks];
-        const V8 x = *reinterpret_cast<const V8*>(&kvr[ks]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) sm.ut[nb][(16 * ks + 8 * g + i) * UT_LD + rho] = x[i];
+        for (int ks = 0; ks < 8; ++ks) r.kv[ks] = z;
       }
-    } else {
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int e = lane + 64 * m;
-        *reinterpret_cast<uint4*>(sm.tok[nb][2] + (e >> 4) * TOK_LD + 8 * (e & 15)) = qr[m];
-      }
+      for (int m = 0; m < 4; ++m)
+        if (t0 + ((lane + 64 * m) >> 4) >= a.T) r.q[m] = z;
+      if (t0 + (lane & (C - 1)) >= a.T) r.d = DT{};
+    }
+    E* tdst = sm.tok[nb][rho & 1] + (rho >> 1) * TOK_LD;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      *reinterpret_cast<uint4*>(tdst + 16 * ks + 8 * g) = r.kv[ks];
+      const V8 x = *reinterpret_cast<const V8*>(&r.kv[ks]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sm.ut[nb][(16 * ks + 8 * g + i) * UT_LD + rho] = x[i];
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int e = lane + 64 * m;
+      *reinterpret_cast<uint4*>(sm.tok[nb][2] + (e >> 4) * TOK_LD + 8 * (e & 15)) = r.q[m];
     }
     // Gram G = U^T U (A and B operands are the same registers)
     f32x16 gacc = {};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      const V8 x = *reinterpret_cast<const V8*>(&kvr[ks]);
+      const V8 x = *reinterpret_cast<const V8*>(&r.kv[ks]);
       gacc = MM::mma32(x, x, gacc);
     }
     // lane holds G[8(r/4) + 4g + r%4][l32]; G is symmetric, so store it as row l32
@@ -241,27 +254,20 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
       const float kk = P.gram[(2 * t) * T_LD + 2 * t];
       const float vv = P.gram[(2 * t + 1) * T_LD + 2 * t + 1];
       const float kv = P.gram[(2 * t) * T_LD + 2 * t + 1];
-      const cayley2 M = cayley_coeffs(io<DT>::to_f32(dr), kk, vv, kv);
+      const cayley2 M = cayley_coeffs(io<DT>::to_f32(r.d), kk, vv, kv);
       P.mcoef[t] = make_float4(M.m00, M.m01, M.m10, M.m11);
     }
     wave_sync();
-    E* tth = sm.tth[nb];
-    E* ttl = sm.ttl[nb];
-    auto tt_store = [&](int row, int col, float x) {
-      const E hpart = static_cast<E>(x);
-      tth[row * TT_LD + col] = hpart;
-      ttl[row * TT_LD + col] = static_cast<E>(x - static_cast<float>(hpart));
-    };
-    // level 1: diagonal 8x8 blocks by forward substitution, lane = (block gb, column c)
+    // diagonal 8x8 blocks (4 tokens) by forward substitution, lane = (block gb, column c)
     if (lane < 32) {
       const int gb = lane >> 3, c = lane & 7;
       float gblk[8][8];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const float4 g0 = *reinterpret_cast<const float4*>(&P.gram[(8 * gb + r) * T_LD + 8 * gb]);
-        const float4 g1 = *reinterpret_cast<const float4*>(&P.gram[(8 * gb + r) * T_LD + 8 * gb + 4]);
-        gblk[r][0] = g0.x; gblk[r][1] = g0.y; gblk[r][2] = g0.z; gblk[r][3] = g0.w;
-        gblk[r][4] = g1.x; gblk[r][5] = g1.y; gblk[r][6] = g1.z; gblk[r][7] = g1.w;
+      for (int rr = 0; rr < 8; ++rr) {
+        const float4 g0 = *reinterpret_cast<const float4*>(&P.gram[(8 * gb + rr) * T_LD + 8 * gb]);
+        const float4 g1 = *reinterpret_cast<const float4*>(&P.gram[(8 * gb + rr) * T_LD + 8 * gb + 4]);
+        gblk[rr][0] = g0.x; gblk[rr][1] = g0.y; gblk[rr][2] = g0.z; gblk[rr][3] = g0.w;
+        gblk[rr][4] = g1.x; gblk[rr][5] = g1.y; gblk[rr][6] = g1.z; gblk[rr][7] = g1.w;
       }
       float x[8];
 #pragma unroll
@@ -282,61 +288,84 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
       *reinterpret_cast<float4*>(&P.dcol[gb][c * 8 + 4]) = make_float4(x[4], x[5], x[6], x[7]);
 #pragma unroll
       for (int i = 0; i < 8; ++i) P.drow[gb][i * 8 + c] = x[i];
-      if (role == 0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) tt_store(8 * gb + i, 8 * gb + c, x[i]);
-      }
-    }
-    wave_sync();
-    // level 2: T~_{g,h} = T~_{g,g} S,  S = sum_{m=h}^{g-1} G_{g,m} T~_{m,h};  lane = element (ea, eb)
-    const int ea = lane >> 3, eb = lane & 7;
-    if (role == 0) {
-      // block column 0: g = 1, 2, 3
-#pragma unroll
-      for (int gr = 1; gr < 4; ++gr) {
-        const float* grow = &P.gram[(8 * gr + ea) * T_LD];
-        float sv = dot8(grow, &P.dcol[0][eb * 8]);
-        if (gr >= 2) sv += dot8(grow + 8, &P.ocol[0][eb * 8]);
-        if (gr >= 3) sv += dot8(grow + 16, &P.ocol[1][eb * 8]);
-        P.sblk[0][eb * 8 + ea] = sv;
-        wave_sync();
-        const float y = dot8(&P.drow[gr][ea * 8], &P.sblk[0][eb * 8]);
-        tt_store(8 * gr + ea, eb, y);
-        if (gr < 3) P.ocol[gr - 1][eb * 8 + ea] = y;
-        wave_sync();
-      }
-    } else {
-      // blocks (2,1) and (3,2), then (3,1)
-      const float* g2 = &P.gram[(16 + ea) * T_LD];
-      const float* g3 = &P.gram[(24 + ea) * T_LD];
-      P.sblk[0][eb * 8 + ea] = dot8(g2 + 8, &P.dcol[1][eb * 8]);
-      P.sblk[1][eb * 8 + ea] = dot8(g3 + 16, &P.dcol[2][eb * 8]);
-      wave_sync();
-      const float y21 = dot8(&P.drow[2][ea * 8], &P.sblk[0][eb * 8]);
-      const float y32 = dot8(&P.drow[3][ea * 8], &P.sblk[1][eb * 8]);
-      tt_store(16 + ea, 8 + eb, y21);
-      tt_store(24 + ea, 16 + eb, y32);
-      P.ocol[0][eb * 8 + ea] = y21;
-      wave_sync();
-      P.sblk[0][eb * 8 + ea] = dot8(g3 + 8, &P.dcol[1][eb * 8]) + dot8(g3 + 16, &P.ocol[0][eb * 8]);
-      wave_sync();
-      tt_store(24 + ea, 8 + eb, dot8(&P.drow[3][ea * 8], &P.sblk[0][eb * 8]));
     }
   };
 
-  if (wave >= NCW) {
-    // ================================================ producers: run one chunk ahead
-    p_load(0);
-    p_prepare(0);
-    if (nch > 1) p_load(1);
-    __syncthreads();
-    for (int cc = 0; cc < nch; ++cc) {
-      if (cc + 1 < nch) {
-        p_prepare((cc & 1) ^ 1);
-        if (cc + 2 < nch) p_load(cc + 2);
-      }
-      lds_barrier();               // (A) chunk cc consumed, chunk cc+1 staged
-      if (READOUT) lds_barrier();  // (B) readout partials of chunk cc reduced
+  // role 1, chunk n: off-diagonal blocks T~_{g,h} = T~_{g,g} S, S = sum_{m=h}^{g-1} G_{g,m} T~_{m,h};
+  // writes all of T~ (hi + lo) for the consumers.  lane = element (ea, eb) of an 8x8 block.
+  auto p_offdiag = [&](int n) {
+    const Stage0& P = sm.s0[n & 1];
+    Stage1& Q = sm.s1;
+    E* tth = sm.tth[n & 1];
+    E* ttl = sm.ttl[n & 1];
+    auto tt_store = [&](int row, int col, float x) {
+      const E hpart = static_cast<E>(x);
+      tth[row * TT_LD + col] = hpart;
+      ttl[row * TT_LD + col] = static_cast<E>(x - static_cast<float>(hpart));
+    };
+    const int ea = lane >> 3, eb = lane & 7;
+    const float* g1 = &P.gram[(8 + ea) * T_LD];
+    const float* g2 = &P.gram[(16 + ea) * T_LD];
+    const float* g3 = &P.gram[(24 + ea) * T_LD];
+#pragma unroll
+    for (int gb = 0; gb < 4; ++gb) tt_store(8 * gb + ea, 8 * gb + eb, P.drow[gb][ea * 8 + eb]);
+    // round 1: (1,0), (2,1), (3,2)
+    Q.sblk[0][eb * 8 + ea] = dot8(g1, &P.dcol[0][eb * 8]);
+    Q.sblk[1][eb * 8 + ea] = dot8(g2 + 8, &P.dcol[1][eb * 8]);
+    Q.sblk[2][eb * 8 + ea] = dot8(g3 + 16, &P.dcol[2][eb * 8]);
+    wave_sync();
+    const float y10 = dot8(&P.drow[1][ea * 8], &Q.sblk[0][eb * 8]);
+    const float y21 = dot8(&P.drow[2][ea * 8], &Q.sblk[1][eb * 8]);
+    const float y32 = dot8(&P.drow[3][ea * 8], &Q.sblk[2][eb * 8]);
+    tt_store(8 + ea, eb, y10);
+    tt_store(16 + ea, 8 + eb, y21);
+    tt_store(24 + ea, 16 + eb, y32);
+    Q.ocol[0][eb * 8 + ea] = y10;
+    Q.ocol[1][eb * 8 + ea] = y21;
+    wave_sync();
+    // round 2: (2,0), (3,1)
+    Q.sblk[0][eb * 8 + ea] = dot8(g2, &P.dcol[0][eb * 8]) + dot8(g2 + 8, &Q.ocol[0][eb * 8]);
+    Q.sblk[1][eb * 8 + ea] = dot8(g3 + 8, &P.dcol[1][eb * 8]) + dot8(g3 + 16, &Q.ocol[1][eb * 8]);
+    wave_sync();
+    const float y20 = dot8(&P.drow[2][ea * 8], &Q.sblk[0][eb * 8]);
+    const float y31 = dot8(&P.drow[3][ea * 8], &Q.sblk[1][eb * 8]);
+    tt_store(16 + ea, eb, y20);
+    tt_store(24 + ea, 8 + eb, y31);
+    Q.ocol[2][eb * 8 + ea] = y20;
+    wave_sync();
+    // round 3: (3,0)
+    Q.sblk[2][eb * 8 + ea] = dot8(g3, &P.dcol[0][eb * 8]) + dot8(g3 + 8, &Q.ocol[0][eb * 8]) +
+                             dot8(g3 + 16, &Q.ocol[2][eb * 8]);
+    wave_sync();
+    tt_store(24 + ea, eb, dot8(&P.drow[3][ea * 8], &Q.sblk[2][eb * 8]));
+  };
+
+  if (wave == NCW) {
+    // ================================================ producer role 0
+    Regs ra, rb;
+    p_load(ra, 0);
+    auto step0 = [&](const Regs& cur, Regs& nxt, int it) {
+      const int n = it + 2;
+      // issued unconditionally (clamped to the last chunk): a conditional prefetch
+      // would make the compiler wait for it before using `cur`
+      p_load(nxt, min(n + 1, nch - 1));
+      if (n < nch) p_stage(cur, n);
+      lds_barrier();
+      if (READOUT && it >= 0) lds_barrier();
+    };
+    for (int it = -2; it < nch; it += 2) {
+      step0(ra, rb, it);
+      if (it + 1 < nch) step0(rb, ra, it + 1);
+    }
+    return;
+  }
+  if (wave == NCW + 1) {
+    // ================================================ producer role 1
+    for (int it = -2; it < nch; ++it) {
+      const int n = it + 1;
+      if (n >= 0 && n < nch) p_offdiag(n);
+      lds_barrier();
+      if (READOUT && it >= 0) lds_barrier();
     }
     return;
   }
@@ -364,20 +393,20 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
           psi[rt][r] = (32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) == col ? 1.f : 0.f;
     }
   }
-  __syncthreads();
 
-  for (int cc = 0; cc < nch; ++cc) {
-    const int cb = cc & 1;
-    {
-      const E* tk = sm.tok[cb][0];
-      const E* tv = sm.tok[cb][1];
-      const E* tq = sm.tok[cb][2];
-      const E* ut = sm.ut[cb];
+  for (int cc = -2; cc < nch; ++cc) {
+    const int cb = cc & 1;  // T~ buffer
+    if (cc >= 0) {
+      const int nb = cc % 3;
+      const E* tk = sm.tok[nb][0];
+      const E* tv = sm.tok[nb][1];
+      const E* tq = sm.tok[nb][2];
+      const E* ut = sm.ut[nb];
       
       // W = U^T Psi_slab  (32 x 32).  PREC: Psi split hi + lo (fp32-faithful);
       // otherwise Psi rounded once to 16 bits, and the rounded values double as the
       // readout stash below.
-      f32x16 W = {};
+      f32x16 Wa = {}, Wb = {};  // two independent MFMA chains (row tiles 0-1 and 2-3)
       V8 pb[4][2];
       const E* urow = ((l32 & 1) ? tv : tk) + (l32 >> 1) * TOK_LD;
 #pragma unroll
@@ -389,16 +418,18 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
           float x[8];
 #pragma unroll
           for (int i = 0; i < 8; ++i) x[i] = psi[rt][8 * ks + i];
+          f32x16& Wr = rt < 2 ? Wa : Wb;
           if (PREC) {
             V8 lo;
             split8<E>(x, pb[rt][ks], lo);
-            W = MM::mma32(av, pb[rt][ks], W);
-            W = MM::mma32(av, lo, W);
+            Wr = MM::mma32(av, pb[rt][ks], Wr);
+            Wr = MM::mma32(av, lo, Wr);
           } else {
             pb[rt][ks] = round8<E>(x);
-            W = MM::mma32(av, pb[rt][ks], W);
+            Wr = MM::mma32(av, pb[rt][ks], Wr);
           }
         }
+      const f32x16 W = Wa + Wb;
 
       // Z = T~ W with T~ = hi + lo from the producers; PREC also splits W.
       f32x16 Z = {};
@@ -487,7 +518,7 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
       }
     }
     lds_barrier();  // (A)
-    if (READOUT) {
+    if (READOUT && cc >= 0) {
       if (tid < 256) {
         const int t = tid >> 4, fg = tid & 15;
         const int tok = (chunk0 + cc) * C + t;
@@ -528,17 +559,27 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
 }
 
 // start_s = P_{s-1} start_{s-1}, s = 1 .. S-1, start_0 = psi0 (identity if null).
-// One wave per (bh, 16-column block); the column block stays in accumulators.
-// bf16x3 (hi*hi + hi*lo + lo*hi) keeps the chain fp32-faithful.
-__global__ __launch_bounds__(64) void sssd_carry_kernel(const float* psi0, const float* P,
-                                                        float* starts, int BH, int S) {
+// One workgroup of 8 waves per (b, h); wave w owns the 16-column block w of the
+// running start state (in MFMA accumulators).  Each P_{s-1} is staged once in LDS
+// as a 16-bit hi + lo pair, shared by the 8 waves; the next P is prefetched into
+// registers while the current product runs.  bf16x3 (hi*hi + hi*lo + lo*hi) keeps
+// the chain fp32-faithful.
+constexpr int CARRY_WAVES = D / 16;
+constexpr int CARRY_NT = CARRY_WAVES * 64;
+constexpr int CP_LD = D + 8;  // elements per staged P row (272 B)
+constexpr int CARRY_F4 = D * D / 4 / CARRY_NT;  // float4 of P per thread
+
+__global__ __launch_bounds__(CARRY_NT) void sssd_carry_kernel(const float* psi0, const float* P,
+                                                              float* starts, int BH, int S) {
   typedef mfma_t<__bf16> MM;
   typedef MM::v8 V8;
+  __shared__ __bf16 phi[D * CP_LD];
+  __shared__ __bf16 plo[D * CP_LD];
   const int bh = blockIdx.x;
-  const int cbk = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, g4 = lane >> 4;
-  const int col = 16 * cbk + l16;
+  const int col = 16 * wave + l16;
   const int64_t DD = static_cast<int64_t>(D) * D;
   f32x4 X[8];  // X[16it + 4g4 + r][col]
 #pragma unroll
@@ -548,8 +589,29 @@ __global__ __launch_bounds__(64) void sssd_carry_kernel(const float* psi0, const
       const int row = 16 * it + 4 * g4 + r;
       X[it][r] = psi0 ? psi0[bh * DD + row * D + col] : (row == col ? 1.f : 0.f);
     }
+  float4 pf[CARRY_F4];  // this thread's share of the next P (element e = tid + NT*m)
+  auto fetch = [&](int s) {
+    const float4* src = reinterpret_cast<const float4*>(P + (static_cast<int64_t>(s - 1) * BH + bh) * DD);
+#pragma unroll
+    for (int m = 0; m < CARRY_F4; ++m) pf[m] = src[tid + CARRY_NT * m];
+  };
+  if (S > 1) fetch(1);
   for (int s = 1; s < S; ++s) {
-    const float* Pm = P + (static_cast<int64_t>(s - 1) * BH + bh) * DD;
+    // stage P_{s-1} as hi + lo
+#pragma unroll
+    for (int m = 0; m < CARRY_F4; ++m) {
+      const int e = 4 * (tid + CARRY_NT * m);
+      const int row = e / D, c0 = e - row * D;
+      const float xv[4] = {pf[m].x, pf[m].y, pf[m].z, pf[m].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const __bf16 hv = static_cast<__bf16>(xv[i]);
+        phi[row * CP_LD + c0 + i] = hv;
+        plo[row * CP_LD + c0 + i] = static_cast<__bf16>(xv[i] - static_cast<float>(hv));
+      }
+    }
+    __syncthreads();
+    if (s + 1 < S) fetch(s + 1);
     f32x4 Y[8];
 #pragma unroll
     for (int it = 0; it < 8; ++it) Y[it] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -565,15 +627,14 @@ __global__ __launch_bounds__(64) void sssd_carry_kernel(const float* psi0, const
       split8<__bf16>(xb, xhi, xlo);
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
-        const float* prow = Pm + (16 * it + l16) * D + 32 * ks + 4 * g4;
-        const float4 p0 = *reinterpret_cast<const float4*>(prow);
-        const float4 p1 = *reinterpret_cast<const float4*>(prow + 16);
-        const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-        V8 phi, plo;
-        split8<__bf16>(pv, phi, plo);
-        Y[it] = MM::mma16(phi, xhi, Y[it]);
-        Y[it] = MM::mma16(phi, xlo, Y[it]);
-        Y[it] = MM::mma16(plo, xhi, Y[it]);
+        const int off = (16 * it + l16) * CP_LD + 32 * ks + 4 * g4;
+        const V8 ahi = cat8<bf16x4, V8>(*reinterpret_cast<const bf16x4*>(&phi[off]),
+                                         *reinterpret_cast<const bf16x4*>(&phi[off + 16]));
+        const V8 alo = cat8<bf16x4, V8>(*reinterpret_cast<const bf16x4*>(&plo[off]),
+                                         *reinterpret_cast<const bf16x4*>(&plo[off + 16]));
+        Y[it] = MM::mma16(ahi, xhi, Y[it]);
+        Y[it] = MM::mma16(ahi, xlo, Y[it]);
+        Y[it] = MM::mma16(alo, xhi, Y[it]);
       }
     }
     float* dst = starts + (static_cast<int64_t>(s - 1) * BH + bh) * DD;
@@ -583,6 +644,7 @@ __global__ __launch_bounds__(64) void sssd_carry_kernel(const float* psi0, const
 #pragma unroll
       for (int r = 0; r < 4; ++r) dst[(16 * it + 4 * g4 + r) * D + col] = Y[it][r];
     }
+    __syncthreads();  // the staged P is read by every wave before it is replaced
   }
 }
 
@@ -642,7 +704,7 @@ hipError_t run_chunked_p(const void* q, const void* k, const void* v, const void
                        dim3(chunk::NT), 0, stream, pa);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(chunk::sssd_carry_kernel, dim3(BH, chunk::D / 16), dim3(64), 0, stream,
+    hipLaunchKernelGGL(chunk::sssd_carry_kernel, dim3(BH), dim3(chunk::CARRY_NT), 0, stream,
                        psi_in, P, starts, BH, p.nseg);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
