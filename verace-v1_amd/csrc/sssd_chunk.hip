@@ -15,11 +15,13 @@
 // Workgroup = 5 waves for one (batch*head, segment):
 //   waves 0-3 (consumers) each own a 32-column slab of the fp32 state, held in
 //     MFMA accumulators for the whole segment; columns evolve independently, so
-//     W, Z and the update need no cross-wave traffic.  The readout is reduced
-//     across waves through LDS.
+//     W, Z and the update need no cross-wave traffic.  For the readout every wave
+//     stashes its slab of S and Z (16-bit, transposed) in LDS; after the chunk's
+//     barrier each wave computes 32 complete output rows from the shared stashes
+//     (read back with transposing LDS loads) and stores them, with no reduction.
 //   waves 4-5 (producers) form a two-stage pipeline ahead of the consumers:
 //     role 0 prefetches chunk n+1 into registers and, for chunk n, stages k/v/q
-//     in LDS (token-major and feature-major), computes the Gram matrix on MFMA,
+//     in LDS (token-major), computes the Gram matrix on MFMA,
 //     the Cayley blocks and the diagonal blocks of T~;
 //     role 1 computes the off-diagonal blocks of T~ for chunk n-1 and writes the
 //     complete T~ (as 16-bit hi + lo) for the consumers.
@@ -33,6 +35,8 @@
 //   pass B (sssd_carry_kernel): start_s = P_{s-1} start_{s-1}, column blocks in
 //          parallel, bf16x3 MFMA (fp32-faithful),
 //   pass C (READOUT=true): every segment from its start state, with outputs.
+#include <type_traits>
+
 #include "vmi_common.h"
 #include "vmi_dispatch.h"
 #include "vmi_mfma.h"
@@ -44,39 +48,44 @@ constexpr int D = 128;
 constexpr int C = 16;           // tokens per chunk
 constexpr int R = 2 * C;        // rank rows per chunk
 constexpr int NCW = 4;          // consumer waves
-constexpr int NPW = 2;          // producer waves
+constexpr int NPW = 4;          // producer waves
 constexpr int NT = (NCW + NPW) * 64;
-constexpr int TOK_LD = D + 8;   // elements per token-major row (272 B)
-constexpr int UT_LD = R + 8;    // elements per feature-major row (80 B)
+// One chunk of inputs in LDS, token-major: arrays k, v, q of C rows each.  The row
+// pitch (304 B) and the 128-B shift between the arrays make every access below free
+// of bank conflicts (16 lanes per clock over 64 banks): the producer's 16-B row
+// writes, the W operand reads (rows rho), the transposing reads of U for the update
+// and the readout (4 consecutive rho = alternating k/v rows), and the q reads.
+constexpr int TOK_LD = D + 24;            // elements per token row
+constexpr int TOK_ARR = C * TOK_LD + 64;  // elements per array (k, v, q) incl. shift
 constexpr int T_LD = R + 4;     // floats per Gram row
 constexpr int TT_LD = R + 8;    // elements per T~ hi/lo row (80 B)
-constexpr int PS_LD = 32 + 8;   // elements per stash row (80 B)
-constexpr int OP_LD = D + 4;    // floats per O-partial row
 
-// Written by producer role 0 for chunk n, read by role 1 one iteration later.
-struct Stage0 {
+// Readout stashes (shared by the consumer waves), row-padded so that both the 8-byte
+// row writes (16 rows per clock) and the transposing reads (4 rows x 32 B per clock)
+// are free of LDS bank conflicts while every offset stays additive:
+//   pst: chunk-start state, transposed: element (j, d) = Psi_s[d][j] at j*PST_LD + d
+//   zst: Z transposed:                   element (j, rho) = Z[rho][j] at j*ZST_LD + rho
+constexpr int PST_LD = D + 20;  // 296 B = 74 dwords (10 mod 64)
+constexpr int ZST_LD = R + 4;   // 72 B = 18 dwords
+
+// Private scratch of one producer wave.
+struct PScratch {
   float gram[R * T_LD];         // Gram matrix G = U^T U (symmetric)
   float4 mcoef[C];              // (m00, m01, m10, m11) per token
   float drow[4][64];            // diagonal 8x8 blocks of T~, row-major [a*8 + c]
   float dcol[4][64];            // the same blocks, column-major [b*8 + c]
-};
-
-// Private to producer role 1.
-struct Stage1 {
   float ocol[3][64];            // T~_10, T~_21, T~_20, column-major
   float sblk[3][64];            // S = sum_m G_gm T~_mh, column-major
 };
 
 template <typename E>
 struct Smem {
-  E tok[3][3][C * TOK_LD];      // k, v, q of a chunk, token-major (3 chunks in flight)
-  E ut[3][D * UT_LD];           // U feature-major: ut[d][rho]
+  E tok[3][3 * TOK_ARR];        // k, v, q of a chunk, token-major (3 chunks in flight)
   E tth[2][R * TT_LD];          // T~ = hi + lo (two 16-bit parts), row-major
   E ttl[2][R * TT_LD];
-  Stage0 s0[2];
-  Stage1 s1;
-  E ps[NCW][D * PS_LD];         // per-wave: chunk-start state slab (row-major), then O partial
-  E zs[NCW][R * PS_LD];         // per-wave: Z slab (row-major)
+  E pst[D * PST_LD];            // readout stash: chunk-start state (hi part), transposed
+  E zst[D * ZST_LD];            // readout stash: Z (hi part), transposed
+  PScratch pscr[NPW];           // one per producer wave
 };
 
 struct Args {
@@ -129,6 +138,24 @@ __device__ __forceinline__ typename mfma_t<E>::v8 lds4x2(const E* p0, const E* p
   return cat8<V4, V8>(lds4<E>(p0), lds4<E>(p1));
 }
 
+// Transposing LDS read (ds_read_b64_tr_b16).  Within each 16-lane group, lane 4i + r
+// supplies the address of 4 consecutive 16-bit elements X[k0 + i][n0 + 4r .. 4r + 3]
+// of a row-major block; lane n of the group receives X[k0 + 0..3][n0 + n], i.e. a
+// 4-deep k-slice of column n (measured on gfx950).
+template <typename E>
+__device__ __forceinline__ typename mfma_t<E>::v4 lds_tr4(const E* p) {
+  typedef short i16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  return __builtin_bit_cast(typename mfma_t<E>::v4, r);
+}
+template <typename E>
+__device__ __forceinline__ typename mfma_t<E>::v8 lds_tr4x2(const E* p0, const E* p1) {
+  typedef typename mfma_t<E>::v4 V4;
+  typedef typename mfma_t<E>::v8 V8;
+  return cat8<V4, V8>(lds_tr4<E>(p0), lds_tr4<E>(p1));
+}
+
 template <typename E, typename DT, bool READOUT, bool PREC>
 __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
   typedef mfma_t<E> MM;
@@ -166,9 +193,18 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
   __syncthreads();
 
   // ---------------------------------------------------------------- producers
-  // Loop index it runs from -2 to nch-1 in every wave; consumers work on chunk it,
-  // producer role 1 on chunk it+1, role 0 on chunk it+2.  Every wave executes one LDS
-  // barrier per iteration (plus one more after the readout reduction).
+  // Every wave runs iterations it = -4 .. last with the same barriers.  Consumers
+  // process chunk it in iteration it (and read out chunk it-1).  Producer p owns the
+  // chunks n = p (mod 4) and spends four iterations on each, one phase per iteration:
+  //   it = n-4  phase 0: global loads of k, v, q, delta into registers
+  //   it = n-3  phase 1: Gram matrix (MFMA), Cayley blocks, diagonal blocks of T~
+  //   it = n-2  phase 2: off-diagonal blocks of T~ (kept in registers)
+  //   it = n-1  phase 3: k, v, q rows -> tok[n % 3], T~ (hi + lo) -> tt[n & 1]
+  // tok[n % 3] last held chunk n-3, whose readout ended in iteration n-2, and tt[n & 1]
+  // last held chunk n-2, so phase 3 overwrites nothing still in use.  Phases 1-2 only
+  // touch the producer's private scratch.  Each phase is a short dependent chain, and
+  // four of them are in flight per workgroup, so their latency stays off the
+  // consumers' critical path.
   struct Regs {
     uint4 kv[8];  // k/v in Gram-operand order: rho = l32, features 16ks + 8g + 0..7
     uint4 q[4];   // q: e = lane + 64m -> token e>>4, features 8*(e&15) + 0..7
@@ -176,8 +212,7 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
   };
 
   // Branch-free loads: token indices are clamped to T-1 for the address and tokens
-  // past the end are zeroed when staged (p_stage), so no load is predicated and the
-  // destination registers need no initialisation while older loads are in flight.
+  // past the end are zeroed in phase 1, so no load is predicated.
   auto p_load = [&](Regs& r, int n) {
     const int t0 = (chunk0 + n) * C;
     const int tk = min(t0 + (l32 >> 1), a.T - 1);
@@ -205,14 +240,10 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     return fmaf(x1.w, y1.w, sacc);
   };
 
-  // role 0, chunk n: stage inputs, Gram, Cayley blocks, diagonal blocks of T~
-  auto p_stage = [&](const Regs& r_in, int n) {
-    const int nb = n % 3;
-    Stage0& P = sm.s0[n & 1];
-    const int rho = l32;
+  // phase 1: zero the tokens past the end, Gram, Cayley blocks, diagonal blocks of T~
+  auto p_gram = [&](Regs& r, int n, PScratch& P) {
     const int t0 = (chunk0 + n) * C;
-    Regs r = r_in;
-    if (t0 + C > a.T) {  // last, partial chunk: zero the tokens past the end
+    if (t0 + C > a.T) {  // last, partial chunk
       const uint4 z = make_uint4(0, 0, 0, 0);
       if (t0 + (l32 >> 1) >= a.T) {
 #pragma unroll
@@ -223,20 +254,7 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
         if (t0 + ((lane + 64 * m) >> 4) >= a.T) r.q[m] = z;
       if (t0 + (lane & (C - 1)) >= a.T) r.d = DT{};
     }
-    E* tdst = sm.tok[nb][rho & 1] + (rho >> 1) * TOK_LD;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      *reinterpret_cast<uint4*>(tdst + 16 * ks + 8 * g) = r.kv[ks];
-      const V8 x = *reinterpret_cast<const V8*>(&r.kv[ks]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) sm.ut[nb][(16 * ks + 8 * g + i) * UT_LD + rho] = x[i];
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int e = lane + 64 * m;
-      *reinterpret_cast<uint4*>(sm.tok[nb][2] + (e >> 4) * TOK_LD + 8 * (e & 15)) = r.q[m];
-    }
-    // Gram G = U^T U (A and B operands are the same registers)
+    // G = U^T U (A and B operands are the same registers)
     f32x16 gacc = {};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
@@ -291,81 +309,87 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     }
   };
 
-  // role 1, chunk n: off-diagonal blocks T~_{g,h} = T~_{g,g} S, S = sum_{m=h}^{g-1} G_{g,m} T~_{m,h};
-  // writes all of T~ (hi + lo) for the consumers.  lane = element (ea, eb) of an 8x8 block.
-  auto p_offdiag = [&](int n) {
-    const Stage0& P = sm.s0[n & 1];
-    Stage1& Q = sm.s1;
-    E* tth = sm.tth[n & 1];
-    E* ttl = sm.ttl[n & 1];
-    auto tt_store = [&](int row, int col, float x) {
-      const E hpart = static_cast<E>(x);
-      tth[row * TT_LD + col] = hpart;
-      ttl[row * TT_LD + col] = static_cast<E>(x - static_cast<float>(hpart));
-    };
+  // phase 2: off-diagonal blocks T~_{g,h} = T~_{g,g} S, S = sum_{m=h}^{g-1} G_{g,m} T~_{m,h}.
+  // lane = element (ea, eb) of an 8x8 block; tv[] receives this lane's element of the
+  // blocks 00, 11, 22, 33, 10, 21, 32, 20, 31, 30.
+  auto p_offdiag = [&](PScratch& P, float* tv) {
     const int ea = lane >> 3, eb = lane & 7;
     const float* g1 = &P.gram[(8 + ea) * T_LD];
     const float* g2 = &P.gram[(16 + ea) * T_LD];
     const float* g3 = &P.gram[(24 + ea) * T_LD];
 #pragma unroll
-    for (int gb = 0; gb < 4; ++gb) tt_store(8 * gb + ea, 8 * gb + eb, P.drow[gb][ea * 8 + eb]);
+    for (int gb = 0; gb < 4; ++gb) tv[gb] = P.drow[gb][ea * 8 + eb];
     // round 1: (1,0), (2,1), (3,2)
-    Q.sblk[0][eb * 8 + ea] = dot8(g1, &P.dcol[0][eb * 8]);
-    Q.sblk[1][eb * 8 + ea] = dot8(g2 + 8, &P.dcol[1][eb * 8]);
-    Q.sblk[2][eb * 8 + ea] = dot8(g3 + 16, &P.dcol[2][eb * 8]);
+    P.sblk[0][eb * 8 + ea] = dot8(g1, &P.dcol[0][eb * 8]);
+    P.sblk[1][eb * 8 + ea] = dot8(g2 + 8, &P.dcol[1][eb * 8]);
+    P.sblk[2][eb * 8 + ea] = dot8(g3 + 16, &P.dcol[2][eb * 8]);
     wave_sync();
-    const float y10 = dot8(&P.drow[1][ea * 8], &Q.sblk[0][eb * 8]);
-    const float y21 = dot8(&P.drow[2][ea * 8], &Q.sblk[1][eb * 8]);
-    const float y32 = dot8(&P.drow[3][ea * 8], &Q.sblk[2][eb * 8]);
-    tt_store(8 + ea, eb, y10);
-    tt_store(16 + ea, 8 + eb, y21);
-    tt_store(24 + ea, 16 + eb, y32);
-    Q.ocol[0][eb * 8 + ea] = y10;
-    Q.ocol[1][eb * 8 + ea] = y21;
+    tv[4] = dot8(&P.drow[1][ea * 8], &P.sblk[0][eb * 8]);
+    tv[5] = dot8(&P.drow[2][ea * 8], &P.sblk[1][eb * 8]);
+    tv[6] = dot8(&P.drow[3][ea * 8], &P.sblk[2][eb * 8]);
+    P.ocol[0][eb * 8 + ea] = tv[4];
+    P.ocol[1][eb * 8 + ea] = tv[5];
     wave_sync();
     // round 2: (2,0), (3,1)
-    Q.sblk[0][eb * 8 + ea] = dot8(g2, &P.dcol[0][eb * 8]) + dot8(g2 + 8, &Q.ocol[0][eb * 8]);
-    Q.sblk[1][eb * 8 + ea] = dot8(g3 + 8, &P.dcol[1][eb * 8]) + dot8(g3 + 16, &Q.ocol[1][eb * 8]);
+    P.sblk[0][eb * 8 + ea] = dot8(g2, &P.dcol[0][eb * 8]) + dot8(g2 + 8, &P.ocol[0][eb * 8]);
+    P.sblk[1][eb * 8 + ea] = dot8(g3 + 8, &P.dcol[1][eb * 8]) + dot8(g3 + 16, &P.ocol[1][eb * 8]);
     wave_sync();
-    const float y20 = dot8(&P.drow[2][ea * 8], &Q.sblk[0][eb * 8]);
-    const float y31 = dot8(&P.drow[3][ea * 8], &Q.sblk[1][eb * 8]);
-    tt_store(16 + ea, eb, y20);
-    tt_store(24 + ea, 8 + eb, y31);
-    Q.ocol[2][eb * 8 + ea] = y20;
+    tv[7] = dot8(&P.drow[2][ea * 8], &P.sblk[0][eb * 8]);
+    tv[8] = dot8(&P.drow[3][ea * 8], &P.sblk[1][eb * 8]);
+    P.ocol[2][eb * 8 + ea] = tv[7];
     wave_sync();
     // round 3: (3,0)
-    Q.sblk[2][eb * 8 + ea] = dot8(g3, &P.dcol[0][eb * 8]) + dot8(g3 + 8, &Q.ocol[0][eb * 8]) +
-                             dot8(g3 + 16, &Q.ocol[2][eb * 8]);
+    P.sblk[2][eb * 8 + ea] = dot8(g3, &P.dcol[0][eb * 8]) + dot8(g3 + 8, &P.ocol[0][eb * 8]) +
+                             dot8(g3 + 16, &P.ocol[2][eb * 8]);
     wave_sync();
-    tt_store(24 + ea, eb, dot8(&P.drow[3][ea * 8], &Q.sblk[2][eb * 8]));
+    tv[9] = dot8(&P.drow[3][ea * 8], &P.sblk[2][eb * 8]);
   };
 
-  if (wave == NCW) {
-    // ================================================ producer role 0
-    Regs ra, rb;
-    p_load(ra, 0);
-    auto step0 = [&](const Regs& cur, Regs& nxt, int it) {
-      const int n = it + 2;
-      // issued unconditionally (clamped to the last chunk): a conditional prefetch
-      // would make the compiler wait for it before using `cur`
-      p_load(nxt, min(n + 1, nch - 1));
-      if (n < nch) p_stage(cur, n);
-      lds_barrier();
-      if (READOUT && it >= 0) lds_barrier();
-    };
-    for (int it = -2; it < nch; it += 2) {
-      step0(ra, rb, it);
-      if (it + 1 < nch) step0(rb, ra, it + 1);
+  // phase 3: token-major k/v/q rows and T~ (16-bit hi + lo) for the consumers
+  auto p_write = [&](const Regs& r, int n, const float* tv) {
+    E* tb = sm.tok[n % 3];
+    E* tdst = tb + (l32 & 1) * TOK_ARR + (l32 >> 1) * TOK_LD;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) *reinterpret_cast<uint4*>(tdst + 16 * ks + 8 * g) = r.kv[ks];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int e = lane + 64 * m;
+      *reinterpret_cast<uint4*>(tb + 2 * TOK_ARR + (e >> 4) * TOK_LD + 8 * (e & 15)) = r.q[m];
     }
-    return;
-  }
-  if (wave == NCW + 1) {
-    // ================================================ producer role 1
-    for (int it = -2; it < nch; ++it) {
-      const int n = it + 1;
-      if (n >= 0 && n < nch) p_offdiag(n);
-      lds_barrier();
-      if (READOUT && it >= 0) lds_barrier();
+    E* tth = sm.tth[n & 1];
+    E* ttl = sm.ttl[n & 1];
+    const int ea = lane >> 3, eb = lane & 7;
+    const int brow[10] = {0, 1, 2, 3, 1, 2, 3, 2, 3, 3};
+    const int bcol[10] = {0, 1, 2, 3, 0, 1, 2, 0, 1, 0};
+#pragma unroll
+    for (int i = 0; i < 10; ++i) {
+      const int o = (8 * brow[i] + ea) * TT_LD + 8 * bcol[i] + eb;
+      const E hpart = static_cast<E>(tv[i]);
+      tth[o] = hpart;
+      ttl[o] = static_cast<E>(tv[i] - static_cast<float>(hpart));
+    }
+  };
+
+  // With the readout, iteration it has two barriers: (B) in the middle, after which
+  // the consumers overwrite the readout stashes, and (A) at the end.  Without it, only (A).
+  const int last = READOUT ? nch : nch - 1;  // the readout of chunk c runs in iteration c+1
+  if (wave >= NCW) {
+    // ================================================ producers
+    const int p = wave - NCW;
+    PScratch& P = sm.pscr[p];
+    Regs r;
+    float tv[10];
+    for (int it = -4; it <= last; ++it) {
+      const int phase = (it - p + 8) & 3;
+      const int n = it + 4 - phase;
+      if (n >= 0 && n < nch) {  // uniform across the wave
+        if (phase == 0) p_load(r, n);
+        else if (phase == 1) p_gram(r, n, P);
+        else if (phase == 2) p_offdiag(P, tv);
+        else p_write(r, n, tv);
+      }
+      if (READOUT) lds_barrier();  // (B)
+      lds_barrier();               // (A)
     }
     return;
   }
@@ -394,112 +418,187 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     }
   }
 
-  for (int cc = -2; cc < nch; ++cc) {
-    const int cb = cc & 1;  // T~ buffer
-    if (cc >= 0) {
-      const int nb = cc % 3;
-      const E* tk = sm.tok[nb][0];
-      const E* tv = sm.tok[nb][1];
-      const E* tq = sm.tok[nb][2];
-      const E* ut = sm.ut[nb];
-      
-      // W = U^T Psi_slab  (32 x 32).  PREC: Psi split hi + lo (fp32-faithful);
-      // otherwise Psi rounded once to 16 bits, and the rounded values double as the
-      // readout stash below.
-      f32x16 Wa = {}, Wb = {};  // two independent MFMA chains (row tiles 0-1 and 2-3)
-      V8 pb[4][2];
-      const E* urow = ((l32 & 1) ? tv : tk) + (l32 >> 1) * TOK_LD;
+  // Per-lane element offsets into a chunk buffer (constant parts are added at the use).
+  //   offW: W operand, U^T row rho = l32, features 32rt + 16ks + 4g + {0..3, 8..11}
+  //   offU: update operand via transposing reads: rows rho = 16ks + 8hh + 4g + i,
+  //         features 32rt + 16 (lane>>4 & 1) + 4r  ->  lane gets U[32rt + l32][rho..rho+3]
+  //   offO: readout operand, rows rho = 16hh + 4g4 + i, features 32 wave + 16tl + 4r
+  //   offQ: readout q, token l16, features 32ks + 8pg
+  const int pg = 2 * (g4 & 1) + (g4 >> 1);
+  const int offW = (l32 & 1) * TOK_ARR + (l32 >> 1) * TOK_LD + 4 * g;
+  const int rhoU = 4 * g + (l16 >> 2);
+  const int offU = (rhoU & 1) * TOK_ARR + (rhoU >> 1) * TOK_LD + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
+  const int rhoO = 4 * g4 + (l16 >> 2);
+  const int offO = (rhoO & 1) * TOK_ARR + (rhoO >> 1) * TOK_LD + 32 * wave + 4 * (l16 & 3);
+  const int offQ = 2 * TOK_ARR + l16 * TOK_LD + 8 * pg;
+
+  // Readout of chunk c (run in iteration c+1, after barrier (A) of iteration c, from
+  // the shared stashes): this wave computes output rows d in [32*wave, 32*wave + 32)
+  // completely, so no cross-wave reduction is needed:
+  //   O = S Q + U mask(Z Q)  restricted to those rows; S Q and Z Q contract over all
+  //   128 state columns j (k-slot group g4 covers j = 32ks + 8pg + 0..7).
+  // stash rows read by this lane's transposing loads: j = 32ks + 8pg + 4hh + (l16 >> 2)
+  const E* const pst_rd = sm.pst + (8 * pg + (l16 >> 2)) * PST_LD + 32 * wave + 4 * (l16 & 3);
+  const E* const zst_rd = sm.zst + (8 * pg + (l16 >> 2)) * ZST_LD + 4 * (l16 & 3);
+  E* const pst_wr = sm.pst + col * PST_LD + 4 * g;
+  E* const zst_wr = sm.zst + col * ZST_LD + 4 * g;
+  auto readout = [&](int c) {
+    const E* tb = sm.tok[c % 3];
+    f32x4 O[2] = {}, Y[2] = {};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const V8 bq = lds8<E>(tb + offQ + 32 * ks);
+#pragma unroll
+      for (int tl = 0; tl < 2; ++tl) {
+        const E* p = pst_rd + 32 * ks * PST_LD + 16 * tl;
+        O[tl] = MM::mma16(lds_tr4x2<E>(p, p + 4 * PST_LD), bq, O[tl]);
+      }
+#pragma unroll
+      for (int yy = 0; yy < 2; ++yy) {
+        const E* p = zst_rd + 32 * ks * ZST_LD + 16 * yy;
+        Y[yy] = MM::mma16(lds_tr4x2<E>(p, p + 4 * ZST_LD), bq, Y[yy]);
+      }
+    }
+    // Y lane (g4, t = l16) holds rho = 16yy + 4g4 + r: the B-operand layout of U mask(Y)
+    V8 by;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      by[r] = static_cast<E>(((4 * g4 + r) >> 1) <= l16 ? Y[0][r] : 0.f);
+      by[4 + r] = static_cast<E>(((16 + 4 * g4 + r) >> 1) <= l16 ? Y[1][r] : 0.f);
+    }
+#pragma unroll
+    for (int tl = 0; tl < 2; ++tl)
+      O[tl] = MM::mma16(lds_tr4x2<E>(tb + offO + 16 * tl, tb + offO + 8 * TOK_LD + 16 * tl), by, O[tl]);
+    // Keep two k-steps of operands (1 + 8 LDS reads each) in flight ahead of the MFMAs,
+    // and the U operands of the last product behind the third k-step.
+    __builtin_amdgcn_sched_group_barrier(0x100, 18, 0);  // DS reads: k-steps 0, 1
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // MFMA: k-step 0
+    __builtin_amdgcn_sched_group_barrier(0x100, 9, 0);   // DS reads: k-step 2
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // MFMA: k-step 1
+    __builtin_amdgcn_sched_group_barrier(0x100, 9, 0);   // DS reads: k-step 3
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // MFMA: k-step 2
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // DS reads: U operands
+    __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);   // MFMA: k-step 3, U mask(Y)
+    // lane (g4, t = l16) holds O[32 wave + 16 tl + 4 g4 + 0..3][t]
+    const int tok = (chunk0 + c) * C + l16;
+    if (a.out != nullptr && tok < a.T) {
+      E* dst = static_cast<E*>(a.out) + tok_base + static_cast<int64_t>(tok) * tok_stride +
+               32 * wave + 4 * g4;
+#pragma unroll
+      for (int tl = 0; tl < 2; ++tl) {
+        typename MM::v4 o4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o4[r] = static_cast<E>(O[tl][r]);
+        *reinterpret_cast<typename MM::v4*>(dst + 16 * tl) = o4;
+      }
+    }
+  };
+
+  // One iteration; HAS_READOUT / ACTIVE are compile-time so that the steady-state
+  // body is a single basic block the scheduler can overlap freely.
+  auto iteration = [&](int cc, auto has_readout, auto active) {
+    constexpr bool RO = decltype(has_readout)::value;
+    constexpr bool ACT = decltype(active)::value;
+    const E* tb = sm.tok[ACT ? cc % 3 : 0];
+    if constexpr (RO) readout(cc - 1);
+    V8 wu[4][2];  // W operands (ready since two iterations back)
+    if constexpr (ACT) {
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const int d0 = 32 * rt + 16 * ks + 4 * g;
-          const V8 av = lds4x2<E>(urow + d0, urow + d0 + 8);
-          float x[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) x[i] = psi[rt][8 * ks + i];
-          f32x16& Wr = rt < 2 ? Wa : Wb;
-          if (PREC) {
-            V8 lo;
-            split8<E>(x, pb[rt][ks], lo);
-            Wr = MM::mma32(av, pb[rt][ks], Wr);
-            Wr = MM::mma32(av, lo, Wr);
-          } else {
-            pb[rt][ks] = round8<E>(x);
-            Wr = MM::mma32(av, pb[rt][ks], Wr);
-          }
+          const E* p = tb + offW + 32 * rt + 16 * ks;
+          wu[rt][ks] = lds4x2<E>(p, p + 8);
         }
-      const f32x16 W = Wa + Wb;
+    }
+
+    // W = U^T Psi_slab  (32 x 32).  PREC: Psi split hi + lo (fp32-faithful);
+    // otherwise Psi rounded once to 16 bits.  The hi parts go to the readout stash.
+    V8 pb[4][2];
+    f32x16 W = {};
+    if constexpr (ACT) {
+      f32x16 Wa = {}, Wb = {};  // two independent MFMA chains (row tiles 0-1 and 2-3)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int rp = 0; rp < 2; ++rp)
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int rt = rp + 2 * half;  // alternate the chains: rt 0, 2, 1, 3
+            float x[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = psi[rt][8 * ks + i];
+            f32x16& Wr = half == 0 ? Wa : Wb;
+            if (PREC) {
+              V8 lo;
+              split8<E>(x, pb[rt][ks], lo);
+              Wr = MM::mma32(wu[rt][ks], pb[rt][ks], Wr);
+              Wr = MM::mma32(wu[rt][ks], lo, Wr);
+            } else {
+              pb[rt][ks] = round8<E>(x);
+              Wr = MM::mma32(wu[rt][ks], pb[rt][ks], Wr);
+            }
+          }
+      W = Wa + Wb;
+    }
+    // T~ operands and the update operands (transposing reads of U): both buffers were
+    // completed before earlier barriers, so the loads are issued here and land during
+    // barrier (B).
+    V8 ahi[2], alo[2], uu[2][4];
+    if constexpr (ACT) {
+      const int cb = cc & 1;  // T~ buffer
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const E* th = sm.tth[cb] + l32 * TT_LD + 16 * ks + 4 * g;
+        const E* tl = sm.ttl[cb] + l32 * TT_LD + 16 * ks + 4 * g;
+        ahi[ks] = lds4x2<E>(th, th + 8);
+        alo[ks] = lds4x2<E>(tl, tl + 8);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+          const E* p = tb + offU + 8 * ks * TOK_LD + 32 * rt;
+          uu[ks][rt] = lds_tr4x2<E>(p, p + 4 * TOK_LD);
+        }
+    }
+    if (READOUT) lds_barrier();  // (B): every wave is done reading the stashes of chunk cc-1
+    if constexpr (ACT) {
+      if (READOUT) {
+        // psi tile rt, ks, half hh holds rows 32rt + 16ks + 8hh + 4g + 0..3 of column col
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            typedef typename MM::v4 V4;
+            const V4 h0 = __builtin_shufflevector(pb[rt][ks], pb[rt][ks], 0, 1, 2, 3);
+            const V4 h1 = __builtin_shufflevector(pb[rt][ks], pb[rt][ks], 4, 5, 6, 7);
+            *reinterpret_cast<V4*>(pst_wr + 32 * rt + 16 * ks) = h0;
+            *reinterpret_cast<V4*>(pst_wr + 32 * rt + 16 * ks + 8) = h1;
+          }
+      }
 
       // Z = T~ W with T~ = hi + lo from the producers; PREC also splits W.
       f32x16 Z = {};
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const E* th = sm.tth[cb] + l32 * TT_LD + 16 * ks + 4 * g;
-        const E* tl = sm.ttl[cb] + l32 * TT_LD + 16 * ks + 4 * g;
-        const V8 ahi = lds4x2<E>(th, th + 8);
-        const V8 alo = lds4x2<E>(tl, tl + 8);
         float wv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) wv[i] = W[8 * ks + i];
         if (PREC) {
           V8 whi, wlo;
           split8<E>(wv, whi, wlo);
-          Z = MM::mma32(ahi, whi, Z);
-          Z = MM::mma32(ahi, wlo, Z);
-          Z = MM::mma32(alo, whi, Z);
+          Z = MM::mma32(ahi[ks], whi, Z);
+          Z = MM::mma32(ahi[ks], wlo, Z);
+          Z = MM::mma32(alo[ks], whi, Z);
         } else {
           const V8 wb = round8<E>(wv);
-          Z = MM::mma32(ahi, wb, Z);
-          Z = MM::mma32(alo, wb, Z);
+          Z = MM::mma32(ahi[ks], wb, Z);
+          Z = MM::mma32(alo[ks], wb, Z);
         }
       }
 
-      if (READOUT) {
-        E* ps = sm.ps[wave];
-        E* zs = sm.zs[wave];
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-              ps[(32 * rt + 16 * ks + 8 * (i >> 2) + 4 * g + (i & 3)) * PS_LD + l32] = pb[rt][ks][i];
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          zs[(8 * (r >> 2) + 4 * g + (r & 3)) * PS_LD + l32] = static_cast<E>(Z[r]);
-        wave_sync();
-        // O_w = S[:, slab] Q[slab, :] + U mask(Z[:, slab] Q[slab, :])   (128 x 16)
-        const V8 bq = lds8<E>(tq + l16 * TOK_LD + 32 * wave + 8 * g4);
-        f32x4 O[8];
-#pragma unroll
-        for (int it = 0; it < 8; ++it) {
-          const f32x4 zero = {};
-          O[it] = MM::mma16(lds8<E>(ps + (16 * it + l16) * PS_LD + 8 * g4), bq, zero);
-        }
-        const f32x4 zero = {};
-        const f32x4 y0 = MM::mma16(lds8<E>(zs + l16 * PS_LD + 8 * g4), bq, zero);
-        const f32x4 y1 = MM::mma16(lds8<E>(zs + (16 + l16) * PS_LD + 8 * g4), bq, zero);
-        V8 by;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          by[r] = static_cast<E>(((4 * g4 + r) >> 1) <= l16 ? y0[r] : 0.f);
-          by[4 + r] = static_cast<E>(((16 + 4 * g4 + r) >> 1) <= l16 ? y1[r] : 0.f);
-        }
-#pragma unroll
-        for (int it = 0; it < 8; ++it) {
-          const E* urow2 = ut + (16 * it + l16) * UT_LD;
-          O[it] = MM::mma16(lds4x2<E>(urow2 + 4 * g4, urow2 + 16 + 4 * g4), by, O[it]);
-        }
-        wave_sync();  // every lane is done reading ps before it is reused for O
-        float* op = reinterpret_cast<float*>(ps);
-#pragma unroll
-        for (int it = 0; it < 8; ++it)
-          *reinterpret_cast<float4*>(&op[l16 * OP_LD + 16 * it + 4 * g4]) =
-              make_float4(O[it][0], O[it][1], O[it][2], O[it][3]);
-      }
-
-      // Psi_slab += U Z
+      // Psi_slab += U Z;  Z tile ks holds rho = 16ks + 8hh + 4g + 0..3 of column col
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         float zv[8];
@@ -508,39 +607,32 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
         V8 zhi, zlo;
         if (PREC) split8<E>(zv, zhi, zlo);
         else zhi = round8<E>(zv);
+        if (READOUT) {
+          typedef typename MM::v4 V4;
+          *reinterpret_cast<V4*>(zst_wr + 16 * ks) =
+              __builtin_shufflevector(zhi, zhi, 0, 1, 2, 3);
+          *reinterpret_cast<V4*>(zst_wr + 16 * ks + 8) =
+              __builtin_shufflevector(zhi, zhi, 4, 5, 6, 7);
+        }
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
-          const E* urow3 = ut + (32 * rt + l32) * UT_LD + 16 * ks + 4 * g;
-          const V8 av = lds4x2<E>(urow3, urow3 + 8);
-          psi[rt] = MM::mma32(av, zhi, psi[rt]);
-          if (PREC) psi[rt] = MM::mma32(av, zlo, psi[rt]);
+          psi[rt] = MM::mma32(uu[ks][rt], zhi, psi[rt]);
+          if (PREC) psi[rt] = MM::mma32(uu[ks][rt], zlo, psi[rt]);
         }
       }
     }
     lds_barrier();  // (A)
-    if (READOUT && cc >= 0) {
-      if (tid < 256) {
-        const int t = tid >> 4, fg = tid & 15;
-        const int tok = (chunk0 + cc) * C + t;
-        if (tok < a.T) {
-          float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int w = 0; w < NCW; ++w) {
-            const float* op = reinterpret_cast<const float*>(sm.ps[w]) + t * OP_LD + 8 * fg;
-            const float4 x0 = *reinterpret_cast<const float4*>(op);
-            const float4 x1 = *reinterpret_cast<const float4*>(op + 4);
-            acc[0] += x0.x; acc[1] += x0.y; acc[2] += x0.z; acc[3] += x0.w;
-            acc[4] += x1.x; acc[5] += x1.y; acc[6] += x1.z; acc[7] += x1.w;
-          }
-          V8 o8;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o8[i] = static_cast<E>(acc[i]);
-          if (a.out != nullptr)
-            *reinterpret_cast<V8*>(static_cast<E*>(a.out) + tok_base + tok * tok_stride + 8 * fg) = o8;
-        }
-      }
-      lds_barrier();  // (B)
-    }
+  };
+
+  typedef std::integral_constant<bool, true> yes;
+  typedef std::integral_constant<bool, false> no;
+  for (int cc = -4; cc < 0; ++cc) iteration(cc, no{}, no{});
+  if (READOUT) {
+    iteration(0, no{}, yes{});
+    for (int cc = 1; cc < nch; ++cc) iteration(cc, std::integral_constant<bool, READOUT>{}, yes{});
+    iteration(nch, std::integral_constant<bool, READOUT>{}, no{});
+  } else {
+    for (int cc = 0; cc < nch; ++cc) iteration(cc, no{}, yes{});
   }
 
   // ---------------------------------------------------------------- end state
