@@ -169,6 +169,56 @@ def test_step_inplace_matches_oracle(device, dtype):
     assert np.abs(nrm / math.sqrt(D) - 1).max() <= 1e-4
 
 
+# head counts around the persistent decode kernel's grid (one workgroup per CU, each
+# looping over heads): fewer heads than CUs, uneven loops, several heads per workgroup
+@pytest.mark.parametrize("B,H,dtype,dscale", [(1, 7, torch.bfloat16, 0.1),
+                                             (37, 8, torch.bfloat16, 0.1),
+                                             (75, 9, torch.float16, 0.5),
+                                             (33, 24, torch.float32, 1.0)])
+def test_step_head_counts_match_oracle(device, B, H, dtype, dscale):
+    from verace_amd import sssd_step_
+    print(f"[case] step heads B={B} H={H} {dtype}", flush=True)
+    D = 128
+    g = torch.Generator().manual_seed(5 + B)
+    psi0 = torch.linalg.qr(torch.randn(B, H, D, D, generator=g))[0].contiguous()
+    state = psi0.to(device)
+    q, k, v, delta = _inputs(B, 1, H, D, seed=B, dtype=dtype, delta_scale=dscale,
+                             delta_dtype=torch.float32)
+    o = sssd_step_(q.to(device), k.to(device), v.to(device), delta.to(device), state)
+    torch.cuda.synchronize()
+    o64, psi64 = sssd_closed.sssd_scan_closed_c(q.float().numpy(), k.float().numpy(),
+                                                v.float().numpy(), delta.float().numpy(),
+                                                psi0.double().numpy())
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert _max_slice_rel(o.float().cpu(), o64, (0, 2)) <= tol
+    assert _max_slice_rel(state.cpu(), psi64, (0, 1)) <= 1e-5
+
+
+@pytest.mark.parametrize("with_state", [False, True])
+def test_scan_single_token_d128(device, with_state):
+    """T == 1 through the scan entry point (not in place): identity or given state,
+    the state argument is left untouched."""
+    print(f"[case] scan T=1 D=128 state={with_state}", flush=True)
+    B, H, D = 70, 4, 128
+    q, k, v, delta = _inputs(B, 1, H, D, seed=3, dtype=torch.bfloat16)
+    psi0 = None
+    if with_state:
+        g = torch.Generator().manual_seed(4)
+        psi0 = torch.linalg.qr(torch.randn(B, H, D, D, generator=g))[0].contiguous()
+    psi0_dev = None if psi0 is None else psi0.to(device)
+    from verace_amd import launch_sssd_hip_scan
+    o, psi = launch_sssd_hip_scan(q.to(device), k.to(device), v.to(device), delta.to(device), psi0_dev)
+    torch.cuda.synchronize()
+    init = (np.broadcast_to(np.eye(D), (B, H, D, D)) if psi0 is None else psi0.double().numpy())
+    o64, psi64 = sssd_closed.sssd_scan_closed_c(q.float().numpy(), k.float().numpy(),
+                                                v.float().numpy(), delta.float().numpy(),
+                                                np.ascontiguousarray(init))
+    assert _max_slice_rel(o.float().cpu(), o64, (0, 2)) <= 2e-2
+    assert _max_slice_rel(psi.cpu(), psi64, (0, 1)) <= 1e-5
+    if psi0 is not None:
+        assert torch.equal(psi0_dev.cpu(), psi0)
+
+
 def test_module_matches_reference_golden(device):
     """Drop-in SSSDAttention, seeded construction + forward == the reference's eager module
     outputs recorded in tests/golden (reference test shapes)."""

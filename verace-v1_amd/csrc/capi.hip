@@ -84,6 +84,9 @@ int vmi_sssd_step_inplace(const void* q, const void* k, const void* v, const voi
     return VMI_ERR_INVALID_ARG;
   if (B == 0 || H == 0) return VMI_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (vmi::use_step128(1, D))
+    return hip_status(vmi::launch_sssd_step128(q, k, v, delta, io_dtype, delta_dtype, psi, out, psi,
+                                               static_cast<int>(B * H), s));
   return hip_status(vmi::launch_sssd_seq(q, k, v, delta, io_dtype, delta_dtype, psi, out, psi,
                                          static_cast<int>(B), 1, static_cast<int>(H),
                                          static_cast<int>(D), s));

@@ -1,0 +1,237 @@
+// Single-token SSSD step (decode) for head_dim 128: Psi' = R Psi, o = Psi' q.
+//
+// The step is bound by HBM traffic: every (batch, head) state (64 KiB fp32) is read
+// once and written once, while the arithmetic is ~10 D^2 flops.  A workgroup can only
+// start writing a state after it has read all of it (a = k^T Psi and b = v^T Psi are
+// sums over every row), so one workgroup per head would read all states first and
+// write them all afterwards, leaving HBM reads and writes unoverlapped.  Here the
+// workgroups are persistent: workgroup w handles heads w, w + G, w + 2G, ... and
+// issues the loads of its next head before it reduces, updates and stores the
+// current one, so the reads of one head overlap the writes of the previous one.
+//
+// Layout (as in the token-sequential kernel): thread (rg, cg) owns rows rg + 8m
+// (m = 0..15) and columns 4cg .. 4cg+3, so every state load and store is a
+// coalesced float4.  Per head (reference recurrence sssd_attention.py:160-175 at
+// seq_len 1, closed form):
+//   a = k^T Psi, b = v^T Psi     per-thread partials over 16 rows, combined across
+//                                the two half-waves with a lane swap and across
+//                                the four waves in LDS
+//   Psi += k alpha + v beta      alpha, beta from vmi::cayley_coeffs
+//   o = Psi q                    row partials reduce-scattered over the 32 lanes
+//                                that share a row group
+#include "vmi_common.h"
+#include "vmi_dispatch.h"
+
+namespace vmi {
+namespace step {
+
+constexpr int D = 128;
+constexpr int NT = 256;
+constexpr int RPT = 16;  // rows per thread
+
+template <typename IO>
+__global__ __launch_bounds__(NT) void sssd_step128_kernel(
+    const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
+    const void* __restrict__ delta, int delta_dtype, const float* psi_in, IO* __restrict__ out,
+    float* psi_out, int BH) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int cg = tid & 31, rg = tid >> 5;
+  const int c0 = 4 * cg;
+  constexpr int64_t DD = static_cast<int64_t>(D) * D;
+
+  __shared__ float s_tok[2][3][D];   // q, k, v (fp32) of the head being processed, x2
+  __shared__ float s_delta[2];
+  __shared__ float4 s_red[2][4][2][D / 4];  // per wave: a and b partials, x2
+
+  // state of the current and the next head (double-buffered registers)
+  float4 st0[RPT], st1[RPT];
+  // this thread's share of the next head's q/k/v row (elements tid and tid + 256 of
+  // the 384-element concatenation) and its delta
+  float tk0 = 0.f, tk1 = 0.f, tdl = 0.f;
+
+  auto load_state = [&](float4* st, int bh) {
+    if (psi_in != nullptr) {
+      const float* src = psi_in + bh * DD + c0;
+#pragma unroll
+      for (int m = 0; m < RPT; ++m) st[m] = *reinterpret_cast<const float4*>(src + (rg + 8 * m) * D);
+    } else {
+#pragma unroll
+      for (int m = 0; m < RPT; ++m) {
+        const int r = rg + 8 * m;
+        st[m] = make_float4(r == c0 ? 1.f : 0.f, r == c0 + 1 ? 1.f : 0.f, r == c0 + 2 ? 1.f : 0.f,
+                            r == c0 + 3 ? 1.f : 0.f);
+      }
+    }
+  };
+  auto load_tok = [&](int bh) {
+    // element e of [q | k | v] for head bh lives at bh*D + (e % D) of array e / D
+    const int64_t base = static_cast<int64_t>(bh) * D;
+    tk0 = io<IO>::load(tid < D ? q : k, base + (tid & (D - 1)));
+    if (tid < D) tk1 = io<IO>::load(v, base + tid);
+    if (tid == 0) tdl = load_scalar(delta, delta_dtype, bh);
+  };
+  auto commit_tok = [&](int buf) {
+    (&s_tok[buf][0][0])[tid] = tk0;
+    if (tid < D) s_tok[buf][2][tid] = tk1;
+    if (tid == 0) s_delta[buf] = tdl;
+  };
+
+  // process head bh whose state is in st and whose q/k/v are in s_tok[buf]
+  auto process = [&](float4* st, int bh, int buf) {
+    float kr[RPT], vr[RPT];
+#pragma unroll
+    for (int m = 0; m < RPT; ++m) {
+      kr[m] = s_tok[buf][1][rg + 8 * m];
+      vr[m] = s_tok[buf][2][rg + 8 * m];
+    }
+    const float4 qc = *reinterpret_cast<const float4*>(&s_tok[buf][0][c0]);
+    // Gram entries, reduced by every wave over the full vectors
+    float kk, vv, kv;
+    {
+      const float k0 = s_tok[buf][1][lane], k1 = s_tok[buf][1][lane + 64];
+      const float v0 = s_tok[buf][2][lane], v1 = s_tok[buf][2][lane + 64];
+      kk = fmaf(k0, k0, k1 * k1);
+      vv = fmaf(v0, v0, v1 * v1);
+      kv = fmaf(k0, v0, k1 * v1);
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        kk += __shfl_xor(kk, off);
+        vv += __shfl_xor(vv, off);
+        kv += __shfl_xor(kv, off);
+      }
+    }
+    // column partials over this thread's 16 rows
+    float4 pa = make_float4(0.f, 0.f, 0.f, 0.f), pb = pa;
+#pragma unroll
+    for (int m = 0; m < RPT; ++m) {
+      pa.x = fmaf(kr[m], st[m].x, pa.x); pa.y = fmaf(kr[m], st[m].y, pa.y);
+      pa.z = fmaf(kr[m], st[m].z, pa.z); pa.w = fmaf(kr[m], st[m].w, pa.w);
+      pb.x = fmaf(vr[m], st[m].x, pb.x); pb.y = fmaf(vr[m], st[m].y, pb.y);
+      pb.z = fmaf(vr[m], st[m].z, pb.z); pb.w = fmaf(vr[m], st[m].w, pb.w);
+    }
+    // the two half-waves hold row groups 2w and 2w+1 of the same columns
+    pa.x += __shfl_xor(pa.x, 32); pa.y += __shfl_xor(pa.y, 32);
+    pa.z += __shfl_xor(pa.z, 32); pa.w += __shfl_xor(pa.w, 32);
+    pb.x += __shfl_xor(pb.x, 32); pb.y += __shfl_xor(pb.y, 32);
+    pb.z += __shfl_xor(pb.z, 32); pb.w += __shfl_xor(pb.w, 32);
+    if (lane < 32) {
+      s_red[buf][wave][0][cg] = pa;
+      s_red[buf][wave][1][cg] = pb;
+    }
+    __syncthreads();
+    float4 a4 = s_red[buf][0][0][cg], b4 = s_red[buf][0][1][cg];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const float4 xa = s_red[buf][w][0][cg], xb = s_red[buf][w][1][cg];
+      a4.x += xa.x; a4.y += xa.y; a4.z += xa.z; a4.w += xa.w;
+      b4.x += xb.x; b4.y += xb.y; b4.z += xb.z; b4.w += xb.w;
+    }
+    const cayley2 M = cayley_coeffs(s_delta[buf], kk, vv, kv);
+    const float4 al = make_float4(fmaf(M.m00, a4.x, M.m01 * b4.x), fmaf(M.m00, a4.y, M.m01 * b4.y),
+                                  fmaf(M.m00, a4.z, M.m01 * b4.z), fmaf(M.m00, a4.w, M.m01 * b4.w));
+    const float4 be = make_float4(fmaf(M.m10, a4.x, M.m11 * b4.x), fmaf(M.m10, a4.y, M.m11 * b4.y),
+                                  fmaf(M.m10, a4.z, M.m11 * b4.z), fmaf(M.m10, a4.w, M.m11 * b4.w));
+    // update, store, and row partials of o = Psi' q
+    float* dst = psi_out + bh * DD + c0;
+    float po[RPT];
+#pragma unroll
+    for (int m = 0; m < RPT; ++m) {
+      float4 x = st[m];
+      x.x = fmaf(kr[m], al.x, fmaf(vr[m], be.x, x.x));
+      x.y = fmaf(kr[m], al.y, fmaf(vr[m], be.y, x.y));
+      x.z = fmaf(kr[m], al.z, fmaf(vr[m], be.z, x.z));
+      x.w = fmaf(kr[m], al.w, fmaf(vr[m], be.w, x.w));
+      *reinterpret_cast<float4*>(dst + (rg + 8 * m) * D) = x;
+      po[m] = fmaf(x.x, qc.x, fmaf(x.y, qc.y, fmaf(x.z, qc.z, x.w * qc.w)));
+    }
+    // reduce-scatter po[] over the 32 lanes (cg) of this half-wave: after the
+    // halving steps lane cg holds the sum for row rg + 8*mloc, paired with lane cg^1
+    int mloc = 0;
+#pragma unroll
+    for (int off = 16, cnt = RPT; off >= 2; off >>= 1, cnt >>= 1) {
+      const int half = cnt >> 1;
+      const bool hi = (lane & off) != 0;
+#pragma unroll
+      for (int i = 0; i < RPT / 2; ++i) {
+        if (i < half) {
+          const float send = hi ? po[i] : po[i + half];
+          const float keep = hi ? po[i + half] : po[i];
+          po[i] = keep + __shfl_xor(send, off);
+        }
+      }
+      if (hi) mloc += half;
+    }
+    const float o_row = po[0] + __shfl_xor(po[0], 1);
+    if (out != nullptr && (lane & 1) == 0) io<IO>::store(out, static_cast<int64_t>(bh) * D + rg + 8 * mloc, o_row);
+  };
+
+  const int G = gridDim.x;
+  int bh = blockIdx.x;
+  if (bh >= BH) return;  // uniform
+  load_state(st0, bh);
+  load_tok(bh);
+  commit_tok(0);
+  // iterations alternate the register buffers st0 / st1 and the LDS buffers 0 / 1
+  for (;;) {
+    const int bh1 = bh + G;
+    if (bh1 < BH) {
+      load_state(st1, bh1);
+      load_tok(bh1);
+    }
+    __syncthreads();  // s_tok[0] complete; s_red[0] free
+    process(st0, bh, 0);
+    if (bh1 >= BH) break;
+    commit_tok(1);
+    const int bh2 = bh1 + G;
+    if (bh2 < BH) {
+      load_state(st0, bh2);
+      load_tok(bh2);
+    }
+    __syncthreads();  // s_tok[1] complete; s_red[1] free
+    process(st1, bh1, 1);
+    if (bh2 >= BH) break;
+    commit_tok(0);
+    bh = bh2;
+  }
+}
+
+template <typename IO>
+hipError_t launch_typed(const IO* q, const IO* k, const IO* v, const void* delta, int delta_dtype,
+                        const float* psi_in, IO* out, float* psi_out, int BH, hipStream_t stream) {
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  const int grid = BH < cus ? BH : cus;
+  hipLaunchKernelGGL(sssd_step128_kernel<IO>, dim3(grid), dim3(NT), 0, stream, q, k, v, delta,
+                     delta_dtype, psi_in, out, psi_out, BH);
+  return hipGetLastError();
+}
+
+}  // namespace step
+
+bool use_step128(int64_t T, int64_t D) { return T == 1 && D == step::D; }
+
+hipError_t launch_sssd_step128(const void* q, const void* k, const void* v, const void* delta,
+                               int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                               float* psi_out, int BH, hipStream_t stream) {
+  switch (io_dtype) {
+    case VMI_F32:
+      return step::launch_typed<float>(static_cast<const float*>(q), static_cast<const float*>(k),
+                                       static_cast<const float*>(v), delta, delta_dtype, psi_in,
+                                       static_cast<float*>(out), psi_out, BH, stream);
+    case VMI_BF16:
+      return step::launch_typed<bf16_t>(static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                                        static_cast<const bf16_t*>(v), delta, delta_dtype, psi_in,
+                                        static_cast<bf16_t*>(out), psi_out, BH, stream);
+    default:
+      return step::launch_typed<f16_t>(static_cast<const f16_t*>(q), static_cast<const f16_t*>(k),
+                                       static_cast<const f16_t*>(v), delta, delta_dtype, psi_in,
+                                       static_cast<f16_t*>(out), psi_out, BH, stream);
+  }
+}
+
+}  // namespace vmi

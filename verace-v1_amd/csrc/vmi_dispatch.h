@@ -12,6 +12,13 @@ hipError_t launch_sssd_seq(const void* q, const void* k, const void* v, const vo
                            int io_dtype, int delta_dtype, const float* psi_in, void* out,
                            float* psi_out, int B, int T, int H, int D, hipStream_t stream);
 
+// sssd_step.hip: single-token step for head_dim 128 (persistent, loads of the next
+// head overlap the update and store of the current one).  psi_in may equal psi_out.
+bool use_step128(int64_t T, int64_t D);
+hipError_t launch_sssd_step128(const void* q, const void* k, const void* v, const void* delta,
+                               int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                               float* psi_out, int BH, hipStream_t stream);
+
 // sssd_scan.hip: picks the kernel family for a prefill scan.
 size_t scan_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int io_dtype);
 hipError_t dispatch_scan(const void* q, const void* k, const void* v, const void* delta,
