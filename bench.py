@@ -192,6 +192,43 @@ def cpu_baseline(target_seconds=12.0):
     }
 
 
+COPY_PROBE_BYTES = 256 << 20  # bytes read (and written) by one calibration copy
+
+
+def pmc_summary(fetch_csv, write_csv, out_json):
+    """Turn two rocprofv3 --pmc runs of `bench.py --copy-probe` (FETCH_SIZE, then
+    WRITE_SIZE; values in KiB per dispatch) into HBM bytes per scan.  Each counter is
+    scaled so that the calibration copy (COPY_PROBE_BYTES read and written) reads
+    exactly its known size."""
+    import csv
+    import collections
+
+    def per_kernel(path):
+        vals = collections.defaultdict(list)
+        for r in csv.DictReader(open(path)):
+            vals[r["Kernel_Name"]].append(float(r["Counter_Value"]) * 1024.0)
+        return vals
+
+    res = {"copy_probe_bytes": COPY_PROBE_BYTES}
+    total = 0.0
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        vals = per_kernel(path)
+        copies = [x for k, v in vals.items() if "copyBuffer" in k for x in v]
+        scale = COPY_PROBE_BYTES / max(copies)
+        kern = {}
+        for k, v in vals.items():
+            if "sssd_chunk_kernel" in k or "sssd_carry_kernel" in k:
+                tag = ("pass C (readout)" if "Lb1ELb1E" in k else "pass A (segment transforms)"
+                       if "sssd_chunk_kernel" in k else "pass B (carry)")
+                kern[tag] = sum(v) / len(v) * scale
+        res[counter] = {"scale": scale, "bytes_per_launch": kern, "bytes_per_scan": sum(kern.values())}
+        total += sum(kern.values())
+    res["hbm_bytes_per_scan"] = total
+    with open(out_json, "w") as f:
+        json.dump(res, f, indent=1)
+    return res
+
+
 def load_traffic():
     """HBM bytes per scan from the committed rocprofv3 --pmc summary, if present."""
     p = os.path.join(REPO_ROOT, "profiles", "pmc_traffic_op_scan.json")
@@ -208,7 +245,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarise two rocprofv3 --pmc counter CSVs into "
+                         "profiles/pmc_traffic_op_scan.json and exit")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="after the scan, run torch copies of COPY_PROBE_BYTES (calibration "
+                         "kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    if args.pmc_summary:
+        out = os.path.join(REPO_ROOT, "profiles", "pmc_traffic_op_scan.json")
+        print(json.dumps(pmc_summary(args.pmc_summary[0], args.pmc_summary[1], out), indent=1))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
@@ -253,6 +300,13 @@ def main():
         "parity": parity,
         "wall_s_timed_region": round(wall, 3),
     }
+    if args.copy_probe:
+        src = torch.ones(COPY_PROBE_BYTES // 4, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_decode:
         result["decode"] = bench_decode(device)
     if not args.no_cpu_baseline:

@@ -219,11 +219,13 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     const E* src = ((l32 & 1) ? gv : gk) + tok_base + tk * tok_stride + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) r.kv[ks] = *reinterpret_cast<const uint4*>(src + 16 * ks);
+    if (READOUT) {  // q only feeds the readout
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int e = lane + 64 * m;
-      const int tq = min(t0 + (e >> 4), a.T - 1);
-      r.q[m] = *reinterpret_cast<const uint4*>(gq + tok_base + tq * tok_stride + 8 * (e & 15));
+      for (int m = 0; m < 4; ++m) {
+        const int e = lane + 64 * m;
+        const int tq = min(t0 + (e >> 4), a.T - 1);
+        r.q[m] = *reinterpret_cast<const uint4*>(gq + tok_base + tq * tok_stride + 8 * (e & 15));
+      }
     }
     const int td = min(t0 + (lane & (C - 1)), a.T - 1);
     r.d = static_cast<const DT*>(a.delta)[dl_base + static_cast<int64_t>(td) * a.H];
@@ -249,9 +251,11 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) r.kv[ks] = z;
       }
+      if (READOUT) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
-        if (t0 + ((lane + 64 * m) >> 4) >= a.T) r.q[m] = z;
+        for (int m = 0; m < 4; ++m)
+          if (t0 + ((lane + 64 * m) >> 4) >= a.T) r.q[m] = z;
+      }
       if (t0 + (lane & (C - 1)) >= a.T) r.d = DT{};
     }
     // G = U^T U (A and B operands are the same registers)
@@ -351,10 +355,12 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     E* tdst = tb + (l32 & 1) * TOK_ARR + (l32 >> 1) * TOK_LD;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) *reinterpret_cast<uint4*>(tdst + 16 * ks + 8 * g) = r.kv[ks];
+    if (READOUT) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int e = lane + 64 * m;
-      *reinterpret_cast<uint4*>(tb + 2 * TOK_ARR + (e >> 4) * TOK_LD + 8 * (e & 15)) = r.q[m];
+      for (int m = 0; m < 4; ++m) {
+        const int e = lane + 64 * m;
+        *reinterpret_cast<uint4*>(tb + 2 * TOK_ARR + (e >> 4) * TOK_LD + 8 * (e & 15)) = r.q[m];
+      }
     }
     E* tth = sm.tth[n & 1];
     E* ttl = sm.ttl[n & 1];
