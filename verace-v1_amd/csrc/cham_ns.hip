@@ -7,7 +7,7 @@
 //   Hr' = 0.5 (Hr Dr - Hi Di)
 //   Hi' = 0.5 (Hr Di + Hi Dr)
 // Each line is one launch of a batched "two products, signed sum, scale,
-// diagonal shift" fp32 GEMM.
+// diagonal shift" GEMM on the fp32 MFMA.
 #include "vmi_common.h"
 #include "vmi_dispatch.h"
 
@@ -15,97 +15,104 @@ namespace vmi {
 
 namespace {
 
-constexpr int NS_TILE = 64;
-constexpr int NS_KT = 16;
+// Out = scale * (op(A0) B0 + sign1 * op(A1) B1) + diag * I, all n x n, batched over
+// blockIdx.z; transA: op(A) = A^T.  fp32 MFMA (v_mfma_f32_32x32x2f32: exact fp32
+// products, fp32 accumulation), so the result carries fp32 matmul rounding only.
+//
+// Workgroup = 4 waves, 64 x 64 output tile; wave (wr, wc) owns the 32 x 32 sub-tile
+// (32wr, 32wc) in one accumulator.  The K dimension runs in chunks of 32 staged in
+// LDS k-major (As[k][m], Bs[k][n]); the two products are one flattened sequence of
+// chunks, and the next chunk is loaded into registers while the current one is
+// multiplied.  Within a chunk, MFMA s (s = 0..15) uses k = s for lanes 0-31 and
+// k = 16 + s for lanes 32-63 (the k-slot of a 32x32x2 operand is lane / 32).
+constexpr int NS_TM = 64;
+constexpr int NS_KT = 32;
+constexpr int NS_LD = NS_TM + 4;
 constexpr int NS_THREADS = 256;
+constexpr int NS_EPT = NS_TM * NS_KT / NS_THREADS;  // elements per thread per operand tile
 
-// Out = scale * (op(A0) B0 + sign1 * op(A1) B1) + diag * I, all n x n, batched.
-// transA: op(A) = A^T.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
 __global__ __launch_bounds__(NS_THREADS) void ns_gemm2_kernel(
     const float* __restrict__ A0, const float* __restrict__ B0, const float* __restrict__ A1,
     const float* __restrict__ B1, float* __restrict__ Out, int n, int transA, float sign1,
     float scale, float diag) {
-  __shared__ float As[NS_KT][NS_TILE + 4];
-  __shared__ float Bs[NS_KT][NS_TILE + 4];
+  __shared__ float As[2][NS_KT][NS_LD];
+  __shared__ float Bs[2][NS_KT][NS_LD];
 
   const int64_t boff = static_cast<int64_t>(blockIdx.z) * n * n;
-  const int i0 = blockIdx.y * NS_TILE;
-  const int j0 = blockIdx.x * NS_TILE;
+  const int i0 = blockIdx.y * NS_TM;
+  const int j0 = blockIdx.x * NS_TM;
   const int tid = threadIdx.x;
-  const int tx = tid % 16, ty = tid / 16;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int lm = lane & 31, g = lane >> 5;
 
-  float acc[4][4];
-#pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[a][c] = 0.f;
+  const int nk = (n + NS_KT - 1) / NS_KT;  // chunks per product
+  const int nchunks = 2 * nk;
+  float ra[NS_EPT], rb[NS_EPT];
 
-  for (int term = 0; term < 2; ++term) {
-    const float* A = (term == 0 ? A0 : A1) + boff;
-    const float* Bm = (term == 0 ? B0 : B1) + boff;
-    const float sgn = term == 0 ? 1.0f : sign1;
-    for (int k0 = 0; k0 < n; k0 += NS_KT) {
-      // A tile: op(A)[i0 .. i0+63][k0 .. k0+15] stored k-major
+  // Element e = tid + 256 s of a 64 x 32 tile.  A tile: (m, k) = (e % 64, e / 64) when
+  // op(A) = A^T (A[k][m] is contiguous in m), (e / 32, e % 32) otherwise; B tile:
+  // (k, col) = (e / 64, e % 64).  Consecutive threads read consecutive addresses.
+  auto fetch = [&](int c) {
+    const int term = c >= nk;
+    const int k0 = (c - term * nk) * NS_KT;
+    const float* A = (term ? A1 : A0) + boff;
+    const float* Bm = (term ? B1 : B0) + boff;
+    const float sgn = term ? sign1 : 1.0f;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int e = tid + s * NS_THREADS;
-        int ii, kk;
-        float x = 0.f;
-        if (transA) {  // op(A)(i, k) = A[k][i]
-          kk = e / NS_TILE;
-          ii = e % NS_TILE;
-          if (i0 + ii < n && k0 + kk < n) x = A[static_cast<int64_t>(k0 + kk) * n + i0 + ii];
-        } else {  // op(A)(i, k) = A[i][k]
-          ii = e / NS_KT;
-          kk = e % NS_KT;
-          if (i0 + ii < n && k0 + kk < n) x = A[static_cast<int64_t>(i0 + ii) * n + k0 + kk];
-        }
-        As[kk][ii] = sgn * x;
-      }
-      // B tile: B[k0 .. k0+15][j0 .. j0+63]
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int e = tid + s * NS_THREADS;
-        const int kk = e / NS_TILE, jj = e % NS_TILE;
-        float x = 0.f;
-        if (k0 + kk < n && j0 + jj < n) x = Bm[static_cast<int64_t>(k0 + kk) * n + j0 + jj];
-        Bs[kk][jj] = x;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int kk = 0; kk < NS_KT; ++kk) {
-        float a[4], b[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) a[r] = As[kk][ty + 16 * r];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) b[c] = Bs[kk][tx + 16 * c];
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(a[r], b[c], acc[r][c]);
-      }
-      __syncthreads();
+    for (int s = 0; s < NS_EPT; ++s) {
+      const int e = tid + NS_THREADS * s;
+      int m, k;
+      if (transA) { m = e % NS_TM; k = e / NS_TM; } else { m = e / NS_KT; k = e % NS_KT; }
+      const int gi = i0 + m, gk = k0 + k;
+      float x = 0.f;
+      if (gi < n && gk < n) x = transA ? A[static_cast<int64_t>(gk) * n + gi] : A[static_cast<int64_t>(gi) * n + gk];
+      ra[s] = sgn * x;
+      const int kb = e / NS_TM, jb = e % NS_TM;
+      const int gkb = k0 + kb, gj = j0 + jb;
+      rb[s] = (gkb < n && gj < n) ? Bm[static_cast<int64_t>(gkb) * n + gj] : 0.f;
     }
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int s = 0; s < NS_EPT; ++s) {
+      const int e = tid + NS_THREADS * s;
+      if (transA) As[buf][e / NS_TM][e % NS_TM] = ra[s];
+      else As[buf][e % NS_KT][e / NS_KT] = ra[s];
+      Bs[buf][e / NS_TM][e % NS_TM] = rb[s];
+    }
+  };
+
+  f32x16 acc = {};
+  fetch(0);
+  commit(0);
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const int buf = c & 1;
+    if (c + 1 < nchunks) fetch(c + 1);
+    const float* as = &As[buf][16 * g][32 * wr + lm];
+    const float* bs = &Bs[buf][16 * g][32 * wc + lm];
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(as[s * NS_LD], bs[s * NS_LD], acc, 0, 0, 0);
+    if (c + 1 < nchunks) commit(buf ^ 1);
+    __syncthreads();
   }
+  // lane holds rows 8(r/4) + 4g + r%4 of column lm in the wave's sub-tile
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int i = i0 + ty + 16 * r;
-    if (i >= n) continue;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int j = j0 + tx + 16 * c;
-      if (j >= n) continue;
-      float y = scale * acc[r][c];
-      if (i == j) y += diag;
-      Out[boff + static_cast<int64_t>(i) * n + j] = y;
-    }
+  for (int r = 0; r < 16; ++r) {
+    const int i = i0 + 32 * wr + 8 * (r >> 2) + 4 * g + (r & 3);
+    const int j = j0 + 32 * wc + lm;
+    if (i < n && j < n) Out[boff + static_cast<int64_t>(i) * n + j] = scale * acc[r] + (i == j ? diag : 0.f);
   }
 }
 
 hipError_t gemm2(const float* A0, const float* B0, const float* A1, const float* B1, float* Out,
                  int batch, int n, int transA, float sign1, float scale, float diag,
                  hipStream_t stream) {
-  const dim3 grid((n + NS_TILE - 1) / NS_TILE, (n + NS_TILE - 1) / NS_TILE, batch);
+  const dim3 grid((n + NS_TM - 1) / NS_TM, (n + NS_TM - 1) / NS_TM, batch);
   hipLaunchKernelGGL(ns_gemm2_kernel, grid, dim3(NS_THREADS), 0, stream, A0, B0, A1, B1, Out, n,
                      transA, sign1, scale, diag);
   return hipGetLastError();
