@@ -401,13 +401,8 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
   }
 
   // ================================================== consumers
-  // Wave w owns state columns 32w .. 32w+31 as two halves h of 16 columns.  Columns
-  // evolve independently, so the halves form two independent dependency chains
-  // (W -> split -> Z -> split -> update -> split -> W); the iteration runs them one
-  // step apart so that the hi/lo splits (VALU) of one half overlap the MFMAs of the
-  // other.  All products are 16x16x32 MFMAs.
-  //   psi[h][t][r] = S[16t + 4g4 + r][32w + 16h + l16]   (fp32, accumulator layout)
-  f32x4 psi[2][8];
+  f32x16 psi[4];  // slab columns 32*wave + l32, tile rt rows 32rt + 8(r/4) + 4g + r%4
+  const int col = 32 * wave + l32;
   {
     const float* src = nullptr;
     if (seg == 0)
@@ -416,48 +411,43 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
       src = a.starts + (static_cast<int64_t>(seg - 1) * a.BH + bh) * DD;
     if (src) {
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2)
+      for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            psi[h2][t][r] = src[(16 * t + 4 * g4 + r) * D + 32 * wave + 16 * h2 + l16];
+        for (int r = 0; r < 16; ++r)
+          psi[rt][r] = src[(32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) * D + col];
     } else {
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2)
+      for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            psi[h2][t][r] = (16 * t + 4 * g4 + r) == (32 * wave + 16 * h2 + l16) ? 1.f : 0.f;
+        for (int r = 0; r < 16; ++r)
+          psi[rt][r] = (32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) == col ? 1.f : 0.f;
     }
   }
 
-  // Per-lane element offsets into a chunk buffer (constant parts added at the use):
-  //   offUT: W operand, U^T row rho = l16 (+16: +8 rows), features 32s + 4g4 (+16)
-  //   offUU: transposing reads of U: rows rho = 16hh + 4g4 + (l16>>2) (+16: +8 rows),
-  //          features 16t + 4(l16&3)  ->  lane gets U[16t + l16][rho .. rho+3]
-  //   offO:  the same rows, features 32 wave + 16tl + 4(l16&3) (readout)
-  //   offQ:  readout q, token l16, features 32ks + 8pg
+  // Per-lane element offsets into a chunk buffer (constant parts are added at the use).
+  //   offW: W operand, U^T row rho = l32, features 32rt + 16ks + 4g + {0..3, 8..11}
+  //   offU: update operand via transposing reads: rows rho = 16ks + 8hh + 4g + i,
+  //         features 32rt + 16 (lane>>4 & 1) + 4r  ->  lane gets U[32rt + l32][rho..rho+3]
+  //   offO: readout operand, rows rho = 16hh + 4g4 + i, features 32 wave + 16tl + 4r
+  //   offQ: readout q, token l16, features 32ks + 8pg
   const int pg = 2 * (g4 & 1) + (g4 >> 1);
-  const int offUT = (l16 & 1) * TOK_ARR + (l16 >> 1) * TOK_LD + 4 * g4;
-  const int rhoU = 4 * g4 + (l16 >> 2);
-  const int offUU = (rhoU & 1) * TOK_ARR + (rhoU >> 1) * TOK_LD + 4 * (l16 & 3);
-  const int offO = offUU + 32 * wave;
+  const int offW = (l32 & 1) * TOK_ARR + (l32 >> 1) * TOK_LD + 4 * g;
+  const int rhoU = 4 * g + (l16 >> 2);
+  const int offU = (rhoU & 1) * TOK_ARR + (rhoU >> 1) * TOK_LD + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
+  const int rhoO = 4 * g4 + (l16 >> 2);
+  const int offO = (rhoO & 1) * TOK_ARR + (rhoO >> 1) * TOK_LD + 32 * wave + 4 * (l16 & 3);
   const int offQ = 2 * TOK_ARR + l16 * TOK_LD + 8 * pg;
-
-  // stash rows read by this lane's transposing loads: j = 32ks + 8pg + 4hh + (l16 >> 2)
-  const E* const pst_rd = sm.pst + (8 * pg + (l16 >> 2)) * PST_LD + 32 * wave + 4 * (l16 & 3);
-  const E* const zst_rd = sm.zst + (8 * pg + (l16 >> 2)) * ZST_LD + 4 * (l16 & 3);
-  // stash rows written by this lane: j = 32 wave + 16h + l16
-  E* const pst_wr = sm.pst + (32 * wave + l16) * PST_LD + 4 * g4;
-  E* const zst_wr = sm.zst + (32 * wave + l16) * ZST_LD + 4 * g4;
 
   // Readout of chunk c (run in iteration c+1, after barrier (A) of iteration c, from
   // the shared stashes): this wave computes output rows d in [32*wave, 32*wave + 32)
   // completely, so no cross-wave reduction is needed:
   //   O = S Q + U mask(Z Q)  restricted to those rows; S Q and Z Q contract over all
   //   128 state columns j (k-slot group g4 covers j = 32ks + 8pg + 0..7).
+  // stash rows read by this lane's transposing loads: j = 32ks + 8pg + 4hh + (l16 >> 2)
+  const E* const pst_rd = sm.pst + (8 * pg + (l16 >> 2)) * PST_LD + 32 * wave + 4 * (l16 & 3);
+  const E* const zst_rd = sm.zst + (8 * pg + (l16 >> 2)) * ZST_LD + 4 * (l16 & 3);
+  E* const pst_wr = sm.pst + col * PST_LD + 4 * g;
+  E* const zst_wr = sm.zst + col * ZST_LD + 4 * g;
   auto readout = [&](int c) {
     const E* tb = sm.tok[c % 3];
     f32x4 O[2] = {}, Y[2] = {};
@@ -510,33 +500,6 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     }
   };
 
-  // Split helpers.  A 16x16x32 B operand at k-step s is the pair of accumulator tiles
-  // (2s, 2s+1): k-slot (g4, i) = row 32s + 16(i>>2) + 4g4 + (i&3).
-  V8 phi[2][4], plo[2][4];  // state halves, split for W (and the stash)
-  auto split_psi = [&](int h2) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      float x[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[i] = psi[h2][2 * s][i];
-        x[4 + i] = psi[h2][2 * s + 1][i];
-      }
-      if (PREC) split8<E>(x, phi[h2][s], plo[h2][s]);
-      else phi[h2][s] = round8<E>(x);
-    }
-  };
-  auto split2 = [&](const f32x4& t0, const f32x4& t1, V8& hi, V8& lo) {
-    float x[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      x[i] = t0[i];
-      x[4 + i] = t1[i];
-    }
-    if (PREC) split8<E>(x, hi, lo);
-    else hi = round8<E>(x);
-  };
-
   // One iteration; HAS_READOUT / ACTIVE are compile-time so that the steady-state
   // body is a single basic block the scheduler can overlap freely.
   auto iteration = [&](int cc, auto has_readout, auto active) {
@@ -544,124 +507,131 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     constexpr bool ACT = decltype(active)::value;
     const E* tb = sm.tok[ACT ? cc % 3 : 0];
     if constexpr (RO) readout(cc - 1);
-
-    V8 ut[2][4];            // W operands: U^T tile rz, k-step s
-    f32x4 W[2][2];          // W[h][rz]: rows rho = 16rz + 4g4 + r, column 16h + l16
+    V8 wu[4][2];  // W operands (ready since two iterations back)
     if constexpr (ACT) {
 #pragma unroll
-      for (int rz = 0; rz < 2; ++rz)
+      for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const E* p = tb + offUT + 8 * rz * TOK_LD + 32 * s;
-          ut[rz][s] = lds4x2<E>(p, p + 16);
+        for (int ks = 0; ks < 2; ++ks) {
+          const E* p = tb + offW + 32 * rt + 16 * ks;
+          wu[rt][ks] = lds4x2<E>(p, p + 8);
         }
-      split_psi(1);  // half 1 was updated last in the previous iteration
+    }
+
+    // W = U^T Psi_slab  (32 x 32).  PREC: Psi split hi + lo (fp32-faithful);
+    // otherwise Psi rounded once to 16 bits.  The hi parts go to the readout stash.
+    V8 pb[4][2];
+    f32x16 W = {};
+    if constexpr (ACT) {
+      f32x16 Wa = {}, Wb = {};  // two independent MFMA chains (row tiles 0-1 and 2-3)
 #pragma unroll
-      for (int rz = 0; rz < 2; ++rz) {
-        W[0][rz] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          W[0][rz] = MM::mma16(ut[rz][s], phi[0][s], W[0][rz]);
-          if (PREC) W[0][rz] = MM::mma16(ut[rz][s], plo[0][s], W[0][rz]);
-        }
-      }
+        for (int rp = 0; rp < 2; ++rp)
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int rt = rp + 2 * half;  // alternate the chains: rt 0, 2, 1, 3
+            float x[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = psi[rt][8 * ks + i];
+            f32x16& Wr = half == 0 ? Wa : Wb;
+            if (PREC) {
+              V8 lo;
+              split8<E>(x, pb[rt][ks], lo);
+              Wr = MM::mma32(wu[rt][ks], pb[rt][ks], Wr);
+              Wr = MM::mma32(wu[rt][ks], lo, Wr);
+            } else {
+              pb[rt][ks] = round8<E>(x);
+              Wr = MM::mma32(wu[rt][ks], pb[rt][ks], Wr);
+            }
+          }
+      W = Wa + Wb;
     }
     // T~ operands and the update operands (transposing reads of U): both buffers were
     // completed before earlier barriers, so the loads are issued here and land during
     // barrier (B).
-    V8 ahi[2], alo[2], uu[8];
+    V8 ahi[2], alo[2], uu[2][4];
     if constexpr (ACT) {
       const int cb = cc & 1;  // T~ buffer
 #pragma unroll
-      for (int rz = 0; rz < 2; ++rz) {
-        const E* th = sm.tth[cb] + (16 * rz + l16) * TT_LD + 4 * g4;
-        const E* tl = sm.ttl[cb] + (16 * rz + l16) * TT_LD + 4 * g4;
-        ahi[rz] = lds4x2<E>(th, th + 16);
-        alo[rz] = lds4x2<E>(tl, tl + 16);
+      for (int ks = 0; ks < 2; ++ks) {
+        const E* th = sm.tth[cb] + l32 * TT_LD + 16 * ks + 4 * g;
+        const E* tl = sm.ttl[cb] + l32 * TT_LD + 16 * ks + 4 * g;
+        ahi[ks] = lds4x2<E>(th, th + 8);
+        alo[ks] = lds4x2<E>(tl, tl + 8);
       }
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const E* p = tb + offUU + 16 * t;
-        uu[t] = lds_tr4x2<E>(p, p + 8 * TOK_LD);
-      }
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+          const E* p = tb + offU + 8 * ks * TOK_LD + 32 * rt;
+          uu[ks][rt] = lds_tr4x2<E>(p, p + 4 * TOK_LD);
+        }
     }
     if (READOUT) lds_barrier();  // (B): every wave is done reading the stashes of chunk cc-1
     if constexpr (ACT) {
-      typedef typename MM::v4 V4;
       if (READOUT) {
-        // stash the chunk-start state (hi parts): lane holds rows 32s + 16(i>>2) + 4g4 + 0..3
+        // psi tile rt, ks, half hh holds rows 32rt + 16ks + 8hh + 4g + 0..3 of column col
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2)
+        for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            *reinterpret_cast<V4*>(pst_wr + 16 * h2 * PST_LD + 32 * s) =
-                __builtin_shufflevector(phi[h2][s], phi[h2][s], 0, 1, 2, 3);
-            *reinterpret_cast<V4*>(pst_wr + 16 * h2 * PST_LD + 32 * s + 16) =
-                __builtin_shufflevector(phi[h2][s], phi[h2][s], 4, 5, 6, 7);
+          for (int ks = 0; ks < 2; ++ks) {
+            typedef typename MM::v4 V4;
+            const V4 h0 = __builtin_shufflevector(pb[rt][ks], pb[rt][ks], 0, 1, 2, 3);
+            const V4 h1 = __builtin_shufflevector(pb[rt][ks], pb[rt][ks], 4, 5, 6, 7);
+            *reinterpret_cast<V4*>(pst_wr + 32 * rt + 16 * ks) = h0;
+            *reinterpret_cast<V4*>(pst_wr + 32 * rt + 16 * ks + 8) = h1;
           }
       }
-      // W half 1 | split W half 0
+
+      // Z = T~ W with T~ = hi + lo from the producers; PREC also splits W.
+      f32x16 Z = {};
 #pragma unroll
-      for (int rz = 0; rz < 2; ++rz) {
-        W[1][rz] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int ks = 0; ks < 2; ++ks) {
+        float wv[8];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          W[1][rz] = MM::mma16(ut[rz][s], phi[1][s], W[1][rz]);
-          if (PREC) W[1][rz] = MM::mma16(ut[rz][s], plo[1][s], W[1][rz]);
+        for (int i = 0; i < 8; ++i) wv[i] = W[8 * ks + i];
+        if (PREC) {
+          V8 whi, wlo;
+          split8<E>(wv, whi, wlo);
+          Z = MM::mma32(ahi[ks], whi, Z);
+          Z = MM::mma32(ahi[ks], wlo, Z);
+          Z = MM::mma32(alo[ks], whi, Z);
+        } else {
+          const V8 wb = round8<E>(wv);
+          Z = MM::mma32(ahi[ks], wb, Z);
+          Z = MM::mma32(alo[ks], wb, Z);
         }
       }
-      V8 whi[2], wlo[2];
-      split2(W[0][0], W[0][1], whi[0], wlo[0]);
-      // Z = T~ W (hi*hi + hi*lo + lo*hi): Z half 0 | split W half 1
-      f32x4 Z[2][2];
-      auto zmul = [&](int h2) {
+
+      // Psi_slab += U Z;  Z tile ks holds rho = 16ks + 8hh + 4g + 0..3 of column col
 #pragma unroll
-        for (int rz = 0; rz < 2; ++rz) {
-          Z[h2][rz] = MM::mma16(ahi[rz], whi[h2], f32x4{0.f, 0.f, 0.f, 0.f});
-          if (PREC) {
-            Z[h2][rz] = MM::mma16(ahi[rz], wlo[h2], Z[h2][rz]);
-            Z[h2][rz] = MM::mma16(alo[rz], whi[h2], Z[h2][rz]);
-          } else {
-            Z[h2][rz] = MM::mma16(alo[rz], whi[h2], Z[h2][rz]);
-          }
-        }
-      };
-      zmul(0);
-      split2(W[1][0], W[1][1], whi[1], wlo[1]);
-      // Z half 1 | split Z half 0
-      zmul(1);
-      V8 zhi[2], zlo[2];
-      auto zsplit = [&](int h2) {
-        split2(Z[h2][0], Z[h2][1], zhi[h2], zlo[h2]);
+      for (int ks = 0; ks < 2; ++ks) {
+        float zv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) zv[i] = Z[8 * ks + i];
+        V8 zhi, zlo;
+        if (PREC) split8<E>(zv, zhi, zlo);
+        else zhi = round8<E>(zv);
         if (READOUT) {
-          // Z rows rho = 16(i>>2) + 4g4 + 0..3 of column 32 wave + 16h + l16
-          *reinterpret_cast<V4*>(zst_wr + 16 * h2 * ZST_LD) =
-              __builtin_shufflevector(zhi[h2], zhi[h2], 0, 1, 2, 3);
-          *reinterpret_cast<V4*>(zst_wr + 16 * h2 * ZST_LD + 16) =
-              __builtin_shufflevector(zhi[h2], zhi[h2], 4, 5, 6, 7);
+          typedef typename MM::v4 V4;
+          *reinterpret_cast<V4*>(zst_wr + 16 * ks) =
+              __builtin_shufflevector(zhi, zhi, 0, 1, 2, 3);
+          *reinterpret_cast<V4*>(zst_wr + 16 * ks + 8) =
+              __builtin_shufflevector(zhi, zhi, 4, 5, 6, 7);
         }
-      };
-      zsplit(0);
-      // update half 0 | split Z half 1
-      auto upd = [&](int h2) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          psi[h2][t] = MM::mma16(uu[t], zhi[h2], psi[h2][t]);
-          if (PREC) psi[h2][t] = MM::mma16(uu[t], zlo[h2], psi[h2][t]);
+        for (int rt = 0; rt < 4; ++rt) {
+          psi[rt] = MM::mma32(uu[ks][rt], zhi, psi[rt]);
+          if (PREC) psi[rt] = MM::mma32(uu[ks][rt], zlo, psi[rt]);
         }
-      };
-      upd(0);
-      zsplit(1);
-      // update half 1 | split the new state of half 0 for the next iteration
-      upd(1);
-      split_psi(0);
+      }
     }
     lds_barrier();  // (A)
   };
 
   typedef std::integral_constant<bool, true> yes;
   typedef std::integral_constant<bool, false> no;
-  split_psi(0);
   for (int cc = -4; cc < 0; ++cc) iteration(cc, no{}, no{});
   if (READOUT) {
     iteration(0, no{}, yes{});
@@ -678,12 +648,10 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     else if (seg == a.nseg - 1) dst = a.ends + bh * DD;
     if (dst) {
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2)
+      for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            dst[(16 * t + 4 * g4 + r) * D + 32 * wave + 16 * h2 + l16] = psi[h2][t][r];
+        for (int r = 0; r < 16; ++r)
+          dst[(32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) * D + col] = psi[rt][r];
     }
   }
 }
