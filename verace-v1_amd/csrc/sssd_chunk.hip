@@ -12,22 +12,20 @@
 // T~ is computed in 8x8 blocks (4 tokens): diagonal blocks by forward
 // substitution, off-diagonal blocks by T~_gh = T~_gg sum_{m=h}^{g-1} G_gm T~_mh.
 //
-// Workgroup = 5 waves for one (batch*head, segment):
+// Workgroup = 8 waves for one (batch*head, segment):
 //   waves 0-3 (consumers) each own a 32-column slab of the fp32 state, held in
 //     MFMA accumulators for the whole segment; columns evolve independently, so
 //     W, Z and the update need no cross-wave traffic.  For the readout every wave
 //     stashes its slab of S and Z (16-bit, transposed) in LDS; after the chunk's
 //     barrier each wave computes 32 complete output rows from the shared stashes
 //     (read back with transposing LDS loads) and stores them, with no reduction.
-//   waves 4-5 (producers) form a two-stage pipeline ahead of the consumers:
-//     role 0 prefetches chunk n+1 into registers and, for chunk n, stages k/v/q
-//     in LDS (token-major), computes the Gram matrix on MFMA,
-//     the Cayley blocks and the diagonal blocks of T~;
-//     role 1 computes the off-diagonal blocks of T~ for chunk n-1 and writes the
-//     complete T~ (as 16-bit hi + lo) for the consumers.
-//   While the consumers process chunk c, role 1 works on c+1 and role 0 on c+2,
-//   so no wave waits on another inside an iteration; one LDS barrier per chunk
-//   (two with the readout) hands the buffers over.
+//   waves 4-7 (producers) take chunks round-robin (producer p owns chunks n = p mod 4)
+//     and run each through four phases, one per iteration, ahead of the consumers:
+//     load k/v/q/delta into registers; Gram matrix on MFMA, Cayley blocks and the
+//     diagonal 8x8 blocks of T~; off-diagonal blocks of T~; write U, q and T~
+//     (16-bit hi + lo) to LDS.  The four producers are in different phases at any
+//     time, so one chunk completes per iteration and no wave waits on another inside
+//     an iteration; one LDS barrier per chunk (two with the readout) hands over.
 //
 // Long sequences are split into segments processed by independent workgroups:
 //   pass A (READOUT=false): each segment s < S-1 from the identity -> its
@@ -50,23 +48,39 @@ constexpr int R = 2 * C;        // rank rows per chunk
 constexpr int NCW = 4;          // consumer waves
 constexpr int NPW = 4;          // producer waves
 constexpr int NT = (NCW + NPW) * 64;
-// One chunk of inputs in LDS, token-major: arrays k, v, q of C rows each.  The row
-// pitch (304 B) and the 128-B shift between the arrays make every access below free
-// of bank conflicts (16 lanes per clock over 64 banks): the producer's 16-B row
-// writes, the W operand reads (rows rho), the transposing reads of U for the update
-// and the readout (4 consecutive rho = alternating k/v rows), and the q reads.
-constexpr int TOK_LD = D + 24;            // elements per token row
-constexpr int TOK_ARR = C * TOK_LD + 64;  // elements per array (k, v, q) incl. shift
+// LDS bank model (measured on gfx950): 64 banks of 4 B; a 64-bit access (also the
+// transposing ds_read_b64_tr_b16 and each half of read2/write2_b64) is served in
+// units of 32 lanes, a 128-bit access in units of 16 lanes, and a unit is conflict-free
+// when its dwords fall in distinct banks.  Every layout below is conflict-free for all
+// the accesses made to it (checked exhaustively against this model) while keeping each
+// per-instruction offset additive, so addresses are one VGPR plus immediates.
+//
+// One chunk of inputs, token-major.  Rank row rho of U (= k_t for rho = 2t, v_t for
+// rho = 2t + 1) lives in slot rho_slot(rho) (a fixed bit permutation of rho) with a
+// pitch of 132 elements (264 B); the q rows follow with a pitch of 136 elements.
+// Accesses: the producer's 16-B row writes, the W operand (32 rows rho, one column
+// block), the transposing reads of U for the update (rows rho0 + 0..3, 32 columns)
+// and for the readout (rows 4g + 0..3, 16 columns), and the readout's q reads.
+constexpr int U_LD = D + 4;               // elements per U row slot
+constexpr int Q_LD = D + 8;               // elements per q row
+constexpr int Q_OFF = R * U_LD;           // q rows after the 32 U slots
+constexpr int CHUNK_ELEMS = Q_OFF + C * Q_LD;
+__host__ __device__ constexpr int rho_slot(int rho) {  // bits 0,1,2,3,4 -> 3,4,2,1,0
+  return ((rho & 1) << 3) | ((rho & 2) << 3) | (rho & 4) | ((rho & 8) >> 2) | ((rho & 16) >> 4);
+}
 constexpr int T_LD = R + 4;     // floats per Gram row
-constexpr int TT_LD = R + 8;    // elements per T~ hi/lo row (80 B)
+constexpr int TT_LD = R + 4;    // elements per T~ hi/lo row (72 B: 32 rows in distinct banks)
 
-// Readout stashes (shared by the consumer waves), row-padded so that both the 8-byte
-// row writes (16 rows per clock) and the transposing reads (4 rows x 32 B per clock)
-// are free of LDS bank conflicts while every offset stays additive:
-//   pst: chunk-start state, transposed: element (j, d) = Psi_s[d][j] at j*PST_LD + d
-//   zst: Z transposed:                   element (j, rho) = Z[rho][j] at j*ZST_LD + rho
-constexpr int PST_LD = D + 20;  // 296 B = 74 dwords (10 mod 64)
-constexpr int ZST_LD = R + 4;   // 72 B = 18 dwords
+// Readout stashes (shared by the consumer waves):
+//   pst: chunk-start state, transposed: element (j, d) = Psi_s[d][j], row slot j_slot(j)
+//   zst: Z transposed:                   element (j, rho) = Z[rho][j], row slot j_slot(j)
+// with j_slot a bit permutation of the low 5 bits of j (rows j = 32w + l32 are written
+// 8 bytes per lane; rows 32ks + 8pg + 4hh + 0..3 are read back with transposing loads).
+constexpr int PST_LD = D + 4;   // 264 B
+constexpr int ZST_LD = R + 4;   // 72 B
+__host__ __device__ constexpr int j_slot(int j) {  // bits 0,1,2,3,4 -> 2,3,0,1,4 (j < 32)
+  return ((j & 1) << 2) | ((j & 2) << 2) | ((j & 4) >> 2) | ((j & 8) >> 2) | (j & 16);
+}
 
 // Private scratch of one producer wave.
 struct PScratch {
@@ -80,7 +94,7 @@ struct PScratch {
 
 template <typename E>
 struct Smem {
-  E tok[3][3 * TOK_ARR];        // k, v, q of a chunk, token-major (3 chunks in flight)
+  E tok[3][CHUNK_ELEMS];        // U rows and q rows of a chunk (3 chunks in flight)
   E tth[2][R * TT_LD];          // T~ = hi + lo (two 16-bit parts), row-major
   E ttl[2][R * TT_LD];
   E pst[D * PST_LD];            // readout stash: chunk-start state (hi part), transposed
@@ -352,14 +366,14 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
   // phase 3: token-major k/v/q rows and T~ (16-bit hi + lo) for the consumers
   auto p_write = [&](const Regs& r, int n, const float* tv) {
     E* tb = sm.tok[n % 3];
-    E* tdst = tb + (l32 & 1) * TOK_ARR + (l32 >> 1) * TOK_LD;
+    E* tdst = tb + rho_slot(l32) * U_LD;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) *reinterpret_cast<uint4*>(tdst + 16 * ks + 8 * g) = r.kv[ks];
     if (READOUT) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const int e = lane + 64 * m;
-        *reinterpret_cast<uint4*>(tb + 2 * TOK_ARR + (e >> 4) * TOK_LD + 8 * (e & 15)) = r.q[m];
+        *reinterpret_cast<uint4*>(tb + Q_OFF + (e >> 4) * Q_LD + 8 * (e & 15)) = r.q[m];
       }
     }
     E* tth = sm.tth[n & 1];
@@ -430,24 +444,25 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
   //         features 32rt + 16 (lane>>4 & 1) + 4r  ->  lane gets U[32rt + l32][rho..rho+3]
   //   offO: readout operand, rows rho = 16hh + 4g4 + i, features 32 wave + 16tl + 4r
   //   offQ: readout q, token l16, features 32ks + 8pg
+  // rho_slot is linear over disjoint bits, so +16ks / +8hh / +16hh are +ks / +2hh / +hh slots.
   const int pg = 2 * (g4 & 1) + (g4 >> 1);
-  const int offW = (l32 & 1) * TOK_ARR + (l32 >> 1) * TOK_LD + 4 * g;
-  const int rhoU = 4 * g + (l16 >> 2);
-  const int offU = (rhoU & 1) * TOK_ARR + (rhoU >> 1) * TOK_LD + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
-  const int rhoO = 4 * g4 + (l16 >> 2);
-  const int offO = (rhoO & 1) * TOK_ARR + (rhoO >> 1) * TOK_LD + 32 * wave + 4 * (l16 & 3);
-  const int offQ = 2 * TOK_ARR + l16 * TOK_LD + 8 * pg;
+  const int offW = rho_slot(l32) * U_LD + 4 * g;
+  const int offU = rho_slot(4 * g + (l16 >> 2)) * U_LD + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
+  const int offO = rho_slot(4 * g4 + (l16 >> 2)) * U_LD + 32 * wave + 4 * (l16 & 3);
+  const int offQ = Q_OFF + l16 * Q_LD + 8 * pg;
+
+  // stash rows read by this lane's transposing loads: j = 32ks + 8pg + 4hh + (l16 >> 2)
+  // (j_slot(8pg + 4hh + i) = j_slot(8pg + i) + hh); rows written: j = col = 32 wave + l32
+  const E* const pst_rd = sm.pst + j_slot(8 * pg + (l16 >> 2)) * PST_LD + 32 * wave + 4 * (l16 & 3);
+  const E* const zst_rd = sm.zst + j_slot(8 * pg + (l16 >> 2)) * ZST_LD + 4 * (l16 & 3);
+  E* const pst_wr = sm.pst + (32 * wave + j_slot(l32)) * PST_LD + 4 * g;
+  E* const zst_wr = sm.zst + (32 * wave + j_slot(l32)) * ZST_LD + 4 * g;
 
   // Readout of chunk c (run in iteration c+1, after barrier (A) of iteration c, from
   // the shared stashes): this wave computes output rows d in [32*wave, 32*wave + 32)
   // completely, so no cross-wave reduction is needed:
   //   O = S Q + U mask(Z Q)  restricted to those rows; S Q and Z Q contract over all
   //   128 state columns j (k-slot group g4 covers j = 32ks + 8pg + 0..7).
-  // stash rows read by this lane's transposing loads: j = 32ks + 8pg + 4hh + (l16 >> 2)
-  const E* const pst_rd = sm.pst + (8 * pg + (l16 >> 2)) * PST_LD + 32 * wave + 4 * (l16 & 3);
-  const E* const zst_rd = sm.zst + (8 * pg + (l16 >> 2)) * ZST_LD + 4 * (l16 & 3);
-  E* const pst_wr = sm.pst + col * PST_LD + 4 * g;
-  E* const zst_wr = sm.zst + col * ZST_LD + 4 * g;
   auto readout = [&](int c) {
     const E* tb = sm.tok[c % 3];
     f32x4 O[2] = {}, Y[2] = {};
@@ -457,12 +472,12 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
 #pragma unroll
       for (int tl = 0; tl < 2; ++tl) {
         const E* p = pst_rd + 32 * ks * PST_LD + 16 * tl;
-        O[tl] = MM::mma16(lds_tr4x2<E>(p, p + 4 * PST_LD), bq, O[tl]);
+        O[tl] = MM::mma16(lds_tr4x2<E>(p, p + PST_LD), bq, O[tl]);
       }
 #pragma unroll
       for (int yy = 0; yy < 2; ++yy) {
         const E* p = zst_rd + 32 * ks * ZST_LD + 16 * yy;
-        Y[yy] = MM::mma16(lds_tr4x2<E>(p, p + 4 * ZST_LD), bq, Y[yy]);
+        Y[yy] = MM::mma16(lds_tr4x2<E>(p, p + ZST_LD), bq, Y[yy]);
       }
     }
     // Y lane (g4, t = l16) holds rho = 16yy + 4g4 + r: the B-operand layout of U mask(Y)
@@ -474,7 +489,7 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     }
 #pragma unroll
     for (int tl = 0; tl < 2; ++tl)
-      O[tl] = MM::mma16(lds_tr4x2<E>(tb + offO + 16 * tl, tb + offO + 8 * TOK_LD + 16 * tl), by, O[tl]);
+      O[tl] = MM::mma16(lds_tr4x2<E>(tb + offO + 16 * tl, tb + offO + U_LD + 16 * tl), by, O[tl]);
     // Keep two k-steps of operands (1 + 8 LDS reads each) in flight ahead of the MFMAs,
     // and the U operands of the last product behind the third k-step.
     __builtin_amdgcn_sched_group_barrier(0x100, 18, 0);  // DS reads: k-steps 0, 1
@@ -564,8 +579,8 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
-          const E* p = tb + offU + 8 * ks * TOK_LD + 32 * rt;
-          uu[ks][rt] = lds_tr4x2<E>(p, p + 4 * TOK_LD);
+          const E* p = tb + offU + ks * U_LD + 32 * rt;
+          uu[ks][rt] = lds_tr4x2<E>(p, p + 2 * U_LD);
         }
     }
     if (READOUT) lds_barrier();  // (B): every wave is done reading the stashes of chunk cc-1
