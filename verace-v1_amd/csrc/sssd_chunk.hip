@@ -100,6 +100,7 @@ struct Smem {
   E pst[D * PST_LD];            // readout stash: chunk-start state (hi part), transposed
   E zst[D * ZST_LD];            // readout stash: Z (hi part), transposed
   PScratch pscr[NPW];           // one per producer wave
+  float smax[NCW];              // per consumer wave: max |start state| of its slab
 };
 
 struct Args {
@@ -170,8 +171,25 @@ __device__ __forceinline__ typename mfma_t<E>::v8 lds_tr4x2(const E* p0, const E
   return cat8<V4, V8>(lds_tr4<E>(p0), lds_tr4<E>(p1));
 }
 
-template <typename E, typename DT, bool READOUT, bool PREC>
+// Eight 16-bit inputs (one uint4) as f16: bf16 -> f32 (a shift or a mask) -> f16 pairs
+// (v_cvt_pk_f16_f32, round to nearest even).  Exact for |x| in [2^-14, 65504]; L2-normalised
+// rows (|x| <= 1) lose at most 2^-25 absolute on entries below 2^-14.
+template <typename IO> __device__ __forceinline__ uint4 to_f16x8(uint4 x);
+template <> __device__ __forceinline__ uint4 to_f16x8<_Float16>(uint4 x) { return x; }
+template <> __device__ __forceinline__ uint4 to_f16x8<__bf16>(uint4 x) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  auto cv = [](unsigned u) {
+    h2 h;
+    h[0] = static_cast<_Float16>(__uint_as_float(u << 16));
+    h[1] = static_cast<_Float16>(__uint_as_float(u & 0xffff0000u));
+    return __builtin_bit_cast(unsigned, h);
+  };
+  return make_uint4(cv(x.x), cv(x.y), cv(x.z), cv(x.w));
+}
+
+template <typename IO, typename DT, bool READOUT>
 __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
+  typedef _Float16 E;  // MFMA operand type (inputs converted on the way into LDS)
   typedef mfma_t<E> MM;
   typedef typename MM::v8 V8;
   __shared__ Smem<E> sm;
@@ -195,14 +213,47 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
   const int64_t tok_stride = static_cast<int64_t>(a.H) * D;
   const int64_t tok_base = (static_cast<int64_t>(b) * a.T * a.H + h) * D;
   const int64_t dl_base = static_cast<int64_t>(b) * a.T * a.H + h;
-  const E* gq = static_cast<const E*>(a.q);
-  const E* gk = static_cast<const E*>(a.k);
-  const E* gv = static_cast<const E*>(a.v);
+  const IO* gq = static_cast<const IO*>(a.q);
+  const IO* gk = static_cast<const IO*>(a.k);
+  const IO* gv = static_cast<const IO*>(a.v);
 
   // zero T~ buffers (the strictly upper blocks are never written afterwards)
   for (int i = tid; i < 2 * R * TT_LD; i += NT) {
     (&sm.tth[0][0])[i] = E(0.0f);
     (&sm.ttl[0][0])[i] = E(0.0f);
+  }
+
+  // Consumers: start state slab (columns 32*wave + l32; tile rt holds rows
+  // 32rt + 8(r/4) + 4g + r%4) and its largest magnitude, for the state scale below.
+  f32x16 psi[4];
+  const int col = 32 * wave + l32;
+  if (wave < NCW) {
+    const float* src = nullptr;
+    if (seg == 0)
+      src = a.psi0 ? a.psi0 + bh * DD : nullptr;
+    else if (a.starts)
+      src = a.starts + (static_cast<int64_t>(seg - 1) * a.BH + bh) * DD;
+    if (src) {
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          psi[rt][r] = src[(32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) * D + col];
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          psi[rt][r] = (32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) == col ? 1.f : 0.f;
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) m = fmaxf(m, fabsf(psi[rt][r]));
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (lane == 0) sm.smax[wave] = m;
   }
   __syncthreads();
 
@@ -230,7 +281,7 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
   auto p_load = [&](Regs& r, int n) {
     const int t0 = (chunk0 + n) * C;
     const int tk = min(t0 + (l32 >> 1), a.T - 1);
-    const E* src = ((l32 & 1) ? gv : gk) + tok_base + tk * tok_stride + 8 * g;
+    const IO* src = ((l32 & 1) ? gv : gk) + tok_base + tk * tok_stride + 8 * g;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) r.kv[ks] = *reinterpret_cast<const uint4*>(src + 16 * ks);
     if (READOUT) {  // q only feeds the readout
@@ -272,7 +323,10 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
       }
       if (t0 + (lane & (C - 1)) >= a.T) r.d = DT{};
     }
-    // G = U^T U (A and B operands are the same registers)
+    // U as f16 (what the consumers use); G = U^T U from the same values, so every
+    // chunk factor I + U T~ U^T stays exactly consistent with its Gram matrix
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) r.kv[ks] = to_f16x8<IO>(r.kv[ks]);
     f32x16 gacc = {};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
@@ -373,7 +427,7 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const int e = lane + 64 * m;
-        *reinterpret_cast<uint4*>(tb + Q_OFF + (e >> 4) * Q_LD + 8 * (e & 15)) = r.q[m];
+        *reinterpret_cast<uint4*>(tb + Q_OFF + (e >> 4) * Q_LD + 8 * (e & 15)) = to_f16x8<IO>(r.q[m]);
       }
     }
     E* tth = sm.tth[n & 1];
@@ -415,26 +469,20 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
   }
 
   // ================================================== consumers
-  f32x16 psi[4];  // slab columns 32*wave + l32, tile rt rows 32rt + 8(r/4) + 4g + r%4
-  const int col = 32 * wave + l32;
+  // The state enters the MFMAs rounded to f16, so it is carried scaled by a power of
+  // two s (exact) that puts its largest start entry in [1, 2): every column keeps its
+  // norm under the orthogonal updates, so no later entry leaves the f16 range.  The
+  // readout and the end state are multiplied back by 1/s.
+  float inv_s = 1.f;
   {
-    const float* src = nullptr;
-    if (seg == 0)
-      src = a.psi0 ? a.psi0 + bh * DD : nullptr;
-    else if (a.starts)
-      src = a.starts + (static_cast<int64_t>(seg - 1) * a.BH + bh) * DD;
-    if (src) {
+    const float m = fmaxf(fmaxf(sm.smax[0], sm.smax[1]), fmaxf(sm.smax[2], sm.smax[3]));
+    if (m > 0.f && m <= 3.0e38f) {
+      int e;
+      (void)frexpf(m, &e);  // m = f * 2^e, f in [0.5, 1)
+      const float sc = ldexpf(1.f, 1 - e);
+      inv_s = ldexpf(1.f, e - 1);
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          psi[rt][r] = src[(32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) * D + col];
-    } else {
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          psi[rt][r] = (32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) == col ? 1.f : 0.f;
+      for (int rt = 0; rt < 4; ++rt) psi[rt] *= sc;
     }
   }
 
@@ -503,14 +551,15 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     // lane (g4, t = l16) holds O[32 wave + 16 tl + 4 g4 + 0..3][t]
     const int tok = (chunk0 + c) * C + l16;
     if (a.out != nullptr && tok < a.T) {
-      E* dst = static_cast<E*>(a.out) + tok_base + static_cast<int64_t>(tok) * tok_stride +
-               32 * wave + 4 * g4;
+      IO* dst = static_cast<IO*>(a.out) + tok_base + static_cast<int64_t>(tok) * tok_stride +
+                32 * wave + 4 * g4;
 #pragma unroll
       for (int tl = 0; tl < 2; ++tl) {
-        typename MM::v4 o4;
+        typedef IO io4 __attribute__((ext_vector_type(4)));
+        io4 o4;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o4[r] = static_cast<E>(O[tl][r]);
-        *reinterpret_cast<typename MM::v4*>(dst + 16 * tl) = o4;
+        for (int r = 0; r < 4; ++r) o4[r] = static_cast<IO>(O[tl][r] * inv_s);
+        *reinterpret_cast<io4*>(dst + 16 * tl) = o4;
       }
     }
   };
@@ -533,8 +582,8 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
         }
     }
 
-    // W = U^T Psi_slab  (32 x 32).  PREC: Psi split hi + lo (fp32-faithful);
-    // otherwise Psi rounded once to 16 bits.  The hi parts go to the readout stash.
+    // W = U^T Psi_slab  (32 x 32), the (scaled) state rounded once to f16; the same
+    // f16 values go to the readout stash.
     V8 pb[4][2];
     f32x16 W = {};
     if constexpr (ACT) {
@@ -550,15 +599,8 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) x[i] = psi[rt][8 * ks + i];
             f32x16& Wr = half == 0 ? Wa : Wb;
-            if (PREC) {
-              V8 lo;
-              split8<E>(x, pb[rt][ks], lo);
-              Wr = MM::mma32(wu[rt][ks], pb[rt][ks], Wr);
-              Wr = MM::mma32(wu[rt][ks], lo, Wr);
-            } else {
-              pb[rt][ks] = round8<E>(x);
-              Wr = MM::mma32(wu[rt][ks], pb[rt][ks], Wr);
-            }
+            pb[rt][ks] = round8<E>(x);
+            Wr = MM::mma32(wu[rt][ks], pb[rt][ks], Wr);
           }
       W = Wa + Wb;
     }
@@ -599,24 +641,16 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
           }
       }
 
-      // Z = T~ W with T~ = hi + lo from the producers; PREC also splits W.
+      // Z = T~ W with T~ = hi + lo (f16 pair) from the producers, W rounded once to f16
       f32x16 Z = {};
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         float wv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) wv[i] = W[8 * ks + i];
-        if (PREC) {
-          V8 whi, wlo;
-          split8<E>(wv, whi, wlo);
-          Z = MM::mma32(ahi[ks], whi, Z);
-          Z = MM::mma32(ahi[ks], wlo, Z);
-          Z = MM::mma32(alo[ks], whi, Z);
-        } else {
-          const V8 wb = round8<E>(wv);
-          Z = MM::mma32(ahi[ks], wb, Z);
-          Z = MM::mma32(alo[ks], wb, Z);
-        }
+        const V8 wb = round8<E>(wv);
+        Z = MM::mma32(ahi[ks], wb, Z);
+        Z = MM::mma32(alo[ks], wb, Z);
       }
 
       // Psi_slab += U Z;  Z tile ks holds rho = 16ks + 8hh + 4g + 0..3 of column col
@@ -625,21 +659,14 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
         float zv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) zv[i] = Z[8 * ks + i];
-        V8 zhi, zlo;
-        if (PREC) split8<E>(zv, zhi, zlo);
-        else zhi = round8<E>(zv);
+        const V8 zb = round8<E>(zv);
         if (READOUT) {
           typedef typename MM::v4 V4;
-          *reinterpret_cast<V4*>(zst_wr + 16 * ks) =
-              __builtin_shufflevector(zhi, zhi, 0, 1, 2, 3);
-          *reinterpret_cast<V4*>(zst_wr + 16 * ks + 8) =
-              __builtin_shufflevector(zhi, zhi, 4, 5, 6, 7);
+          *reinterpret_cast<V4*>(zst_wr + 16 * ks) = __builtin_shufflevector(zb, zb, 0, 1, 2, 3);
+          *reinterpret_cast<V4*>(zst_wr + 16 * ks + 8) = __builtin_shufflevector(zb, zb, 4, 5, 6, 7);
         }
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-          psi[rt] = MM::mma32(uu[ks][rt], zhi, psi[rt]);
-          if (PREC) psi[rt] = MM::mma32(uu[ks][rt], zlo, psi[rt]);
-        }
+        for (int rt = 0; rt < 4; ++rt) psi[rt] = MM::mma32(uu[ks][rt], zb, psi[rt]);
       }
     }
     lds_barrier();  // (A)
@@ -666,7 +693,7 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
       for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          dst[(32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) * D + col] = psi[rt][r];
+          dst[(32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) * D + col] = psi[rt][r] * inv_s;
     }
   }
 }
@@ -788,12 +815,8 @@ bool chunk_path(int64_t T, int64_t D, int io_dtype) {
   return D == chunk::D && (io_dtype == VMI_BF16 || io_dtype == VMI_F16) && T >= 2 * chunk::C;
 }
 
-// PREC (the only variant dispatched): the state, W and Z enter the chunk GEMMs as
-// hi + lo 16-bit pairs, so every product is fp32-faithful and the state norm is kept
-// to ~1e-6 per 4096 tokens.  PREC=false rounds them to 16 bits once (about 6% faster
-// at the OP shape, but its norm drift grows to ~4e-5 per 4096 tokens).
-template <typename E, typename DT, bool PREC>
-hipError_t run_chunked_p(const void* q, const void* k, const void* v, const void* delta,
+template <typename IO, typename DT>
+hipError_t run_chunked(const void* q, const void* k, const void* v, const void* delta,
                        int delta_dtype, const float* psi_in, void* out, float* psi_out, int B,
                        int T, int H, void* workspace, hipStream_t stream) {
   const int BH = B * H;
@@ -813,7 +836,7 @@ hipError_t run_chunked_p(const void* q, const void* k, const void* v, const void
     pa.out = nullptr;
     pa.ends = P;
     pa.end_mode = 0;
-    hipLaunchKernelGGL((chunk::sssd_chunk_kernel<E, DT, false, PREC>), dim3(BH, p.nseg - 1),
+    hipLaunchKernelGGL((chunk::sssd_chunk_kernel<IO, DT, false>), dim3(BH, p.nseg - 1),
                        dim3(chunk::NT), 0, stream, pa);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -827,17 +850,9 @@ hipError_t run_chunked_p(const void* q, const void* k, const void* v, const void
   a.out = out;
   a.ends = psi_out;
   a.end_mode = 1;
-  hipLaunchKernelGGL((chunk::sssd_chunk_kernel<E, DT, true, PREC>), dim3(BH, p.nseg), dim3(chunk::NT),
+  hipLaunchKernelGGL((chunk::sssd_chunk_kernel<IO, DT, true>), dim3(BH, p.nseg), dim3(chunk::NT),
                      0, stream, a);
   return hipGetLastError();
-}
-
-template <typename E, typename DT>
-hipError_t run_chunked(const void* q, const void* k, const void* v, const void* delta,
-                       int delta_dtype, const float* psi_in, void* out, float* psi_out, int B,
-                       int T, int H, void* workspace, hipStream_t stream) {
-  return run_chunked_p<E, DT, true>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, B, T, H,
-                                    workspace, stream);
 }
 
 }  // namespace
