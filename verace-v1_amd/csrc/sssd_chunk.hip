@@ -1,4 +1,4 @@
-// Chunk-parallel SSSD prefill scan on bf16/fp16 MFMA, head_dim 128.
+// Chunk-parallel SSSD prefill scan on f16 MFMA (bf16 or fp16 I/O), head_dim 128.
 //
 // Math (reference recurrence sssd_attention.py:160-175, regrouped per chunk).
 // For a chunk of C = 16 tokens starting from state S:
@@ -12,20 +12,31 @@
 // T~ is computed in 8x8 blocks (4 tokens): diagonal blocks by forward
 // substitution, off-diagonal blocks by T~_gh = T~_gg sum_{m=h}^{g-1} G_gm T~_mh.
 //
-// Workgroup = 8 waves for one (batch*head, segment):
+// Precision: every MFMA accumulates in fp32.  U and q enter as f16 (exact for the
+// L2-normalised inputs of this op); G, the Cayley blocks and T~ are fp32, and T~
+// enters as an f16 hi + lo pair, so each chunk factor I + U T~ U^T is orthogonal to
+// ~2^-22.  The state S (scaled by a power of two, see below), W and Z are rounded to
+// f16 once per chunk (11-bit significand): the rounding errors are unbiased, so the
+// state norm drifts as a random walk (~1e-6 over 65536 tokens, against 1e-4 allowed)
+// and the state stays within ~3e-4 of the exact recurrence at that length.
+//
+// Workgroup = 12 waves for one (batch*head, segment):
 //   waves 0-3 (consumers) each own a 32-column slab of the fp32 state, held in
 //     MFMA accumulators for the whole segment; columns evolve independently, so
-//     W, Z and the update need no cross-wave traffic.  For the readout every wave
-//     stashes its slab of S and Z (16-bit, transposed) in LDS; after the chunk's
-//     barrier each wave computes 32 complete output rows from the shared stashes
-//     (read back with transposing LDS loads) and stores them, with no reduction.
-//   waves 4-7 (producers) take chunks round-robin (producer p owns chunks n = p mod 4)
-//     and run each through four phases, one per iteration, ahead of the consumers:
-//     load k/v/q/delta into registers; Gram matrix on MFMA, Cayley blocks and the
-//     diagonal 8x8 blocks of T~; off-diagonal blocks of T~; write U, q and T~
-//     (16-bit hi + lo) to LDS.  The four producers are in different phases at any
+//     W, Z and the update need no cross-wave traffic.  With the readout every wave
+//     also stashes its slab of S and Z (f16, transposed) in LDS.
+//   waves 4-7 (readout, pass C only) compute, from the stashes of chunk c-1, 32
+//     complete output rows each (transposing LDS loads, no reduction) while the
+//     consumers work on chunk c.
+//   the remaining 4 (pass C) or 8 (pass A) producer waves take chunks round-robin
+//     (producer p owns chunks n = p mod NPW) and run each through NPW phases, one per
+//     iteration, ahead of the consumers: loads of k/v/q/delta; Gram matrix on MFMA and
+//     Cayley blocks; diagonal and off-diagonal 8x8 blocks of T~; the write of U, q
+//     and T~ (f16 hi + lo) to LDS.  The producers are in different phases at any
 //     time, so one chunk completes per iteration and no wave waits on another inside
-//     an iteration; one LDS barrier per chunk (two with the readout) hands over.
+//     an iteration; one LDS barrier per chunk hands the buffers over.  The readout
+//     stashes are double-buffered by chunk parity, so the stash writes of chunk c need
+//     no barrier against the readout of chunk c-1.
 //
 // Long sequences are split into segments processed by independent workgroups:
 //   pass A (READOUT=false): each segment s < S-1 from the identity -> its
@@ -46,8 +57,15 @@ constexpr int D = 128;
 constexpr int C = 16;           // tokens per chunk
 constexpr int R = 2 * C;        // rank rows per chunk
 constexpr int NCW = 4;          // consumer waves
-constexpr int NPW = 4;          // producer waves
-constexpr int NT = (NCW + NPW) * 64;
+// Twelve waves (3 per SIMD, at most 168 VGPRs each).  Pass C: 4 consumers (the state),
+// 4 readout waves and 4 producers.  Pass A (no readout): 4 consumers and 8 producers,
+// whose latency-bound phases are then split over a pipeline twice as deep.
+template <bool READOUT> struct Cfg {
+  static constexpr int NPW = READOUT ? 4 : 8;
+  static constexpr int NRW = READOUT ? 4 : 0;  // readout waves
+  static constexpr int NT = (NCW + NRW + NPW) * 64;
+  static constexpr int NSCR = READOUT ? 2 : 8;  // producer scratch slots
+};
 // LDS bank model (measured on gfx950): 64 banks of 4 B; a 64-bit access (also the
 // transposing ds_read_b64_tr_b16 and each half of read2/write2_b64) is served in
 // units of 32 lanes, a 128-bit access in units of 16 lanes, and a unit is conflict-free
@@ -82,7 +100,7 @@ __host__ __device__ constexpr int j_slot(int j) {  // bits 0,1,2,3,4 -> 2,3,0,1,
   return ((j & 1) << 2) | ((j & 2) << 2) | ((j & 4) >> 2) | ((j & 8) >> 2) | (j & 16);
 }
 
-// Private scratch of one producer wave.
+// Scratch of a producer wave during phases 1-2 of one chunk (two slots, by chunk parity).
 struct PScratch {
   float gram[R * T_LD];         // Gram matrix G = U^T U (symmetric)
   float4 mcoef[C];              // (m00, m01, m10, m11) per token
@@ -92,14 +110,14 @@ struct PScratch {
   float sblk[3][64];            // S = sum_m G_gm T~_mh, column-major
 };
 
-template <typename E>
+template <typename E, bool READOUT>
 struct Smem {
   E tok[3][CHUNK_ELEMS];        // U rows and q rows of a chunk (3 chunks in flight)
   E tth[2][R * TT_LD];          // T~ = hi + lo (two 16-bit parts), row-major
   E ttl[2][R * TT_LD];
-  E pst[D * PST_LD];            // readout stash: chunk-start state (hi part), transposed
-  E zst[D * ZST_LD];            // readout stash: Z (hi part), transposed
-  PScratch pscr[NPW];           // one per producer wave
+  E pst[2][READOUT ? D * PST_LD : 1];  // readout stash (chunk parity): chunk-start state, transposed
+  E zst[2][READOUT ? D * ZST_LD : 1];  // readout stash (chunk parity): Z, transposed
+  PScratch pscr[Cfg<READOUT>::NSCR];   // producer scratch (chunk parity / producer wave)
   float smax[NCW];              // per consumer wave: max |start state| of its slab
 };
 
@@ -188,11 +206,14 @@ template <> __device__ __forceinline__ uint4 to_f16x8<__bf16>(uint4 x) {
 }
 
 template <typename IO, typename DT, bool READOUT>
-__global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
+__global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
+  constexpr int NPW = Cfg<READOUT>::NPW;
+  constexpr int NRW = Cfg<READOUT>::NRW;
+  constexpr int NT = Cfg<READOUT>::NT;
   typedef _Float16 E;  // MFMA operand type (inputs converted on the way into LDS)
   typedef mfma_t<E> MM;
   typedef typename MM::v8 V8;
-  __shared__ Smem<E> sm;
+  __shared__ Smem<E, READOUT> sm;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -258,18 +279,22 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
   __syncthreads();
 
   // ---------------------------------------------------------------- producers
-  // Every wave runs iterations it = -4 .. last with the same barriers.  Consumers
+  // Every wave runs iterations it = -NPW .. last with the same barriers.  Consumers
   // process chunk it in iteration it (and read out chunk it-1).  Producer p owns the
-  // chunks n = p (mod 4) and spends four iterations on each, one phase per iteration:
+  // chunks n = p (mod NPW) and spends NPW iterations on each, one phase per iteration.
+  // With 4 producers:
   //   it = n-4  phase 0: global loads of k, v, q, delta into registers
   //   it = n-3  phase 1: Gram matrix (MFMA), Cayley blocks, diagonal blocks of T~
   //   it = n-2  phase 2: off-diagonal blocks of T~ (kept in registers)
   //   it = n-1  phase 3: k, v, q rows -> tok[n % 3], T~ (hi + lo) -> tt[n & 1]
+  // with 8 the same steps run as load, Gram + Cayley blocks, diagonal blocks, four
+  // off-diagonal steps and the write (it = n-8 .. n-1).
   // tok[n % 3] last held chunk n-3, whose readout ended in iteration n-2, and tt[n & 1]
-  // last held chunk n-2, so phase 3 overwrites nothing still in use.  Phases 1-2 only
-  // touch the producer's private scratch.  Each phase is a short dependent chain, and
-  // four of them are in flight per workgroup, so their latency stays off the
-  // consumers' critical path.
+  // last held chunk n-2, so the write overwrites nothing still in use.  The scratch of
+  // a chunk is pscr[n & 1] with 4 producers (chunk n+2, the next one to use it, starts
+  // its Gram in iteration n-1, after chunk n's off-diagonal blocks) and the producer's
+  // own slot with 8.  Each phase is a short dependent chain, and NPW of them are in
+  // flight per workgroup, so their latency stays off the consumers' critical path.
   struct Regs {
     uint4 kv[8];  // k/v in Gram-operand order: rho = l32, features 16ks + 8g + 0..7
     uint4 q[4];   // q: e = lane + 64m -> token e>>4, features 8*(e&15) + 0..7
@@ -307,7 +332,7 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     return fmaf(x1.w, y1.w, sacc);
   };
 
-  // phase 1: zero the tokens past the end, Gram, Cayley blocks, diagonal blocks of T~
+  // zero the tokens past the end, convert U to f16, Gram matrix, Cayley blocks
   auto p_gram = [&](Regs& r, int n, PScratch& P) {
     const int t0 = (chunk0 + n) * C;
     if (t0 + C > a.T) {  // last, partial chunk
@@ -347,8 +372,10 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
       const cayley2 M = cayley_coeffs(io<DT>::to_f32(r.d), kk, vv, kv);
       P.mcoef[t] = make_float4(M.m00, M.m01, M.m10, M.m11);
     }
-    wave_sync();
-    // diagonal 8x8 blocks (4 tokens) by forward substitution, lane = (block gb, column c)
+  };
+
+  // diagonal 8x8 blocks of T~ (4 tokens) by forward substitution, lane = (block gb, column c)
+  auto p_diag = [&](PScratch& P) {
     if (lane < 32) {
       const int gb = lane >> 3, c = lane & 7;
       float gblk[8][8];
@@ -381,36 +408,40 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     }
   };
 
-  // phase 2: off-diagonal blocks T~_{g,h} = T~_{g,g} S, S = sum_{m=h}^{g-1} G_{g,m} T~_{m,h}.
-  // lane = element (ea, eb) of an 8x8 block; tv[] receives this lane's element of the
-  // blocks 00, 11, 22, 33, 10, 21, 32, 20, 31, 30.
-  auto p_offdiag = [&](PScratch& P, float* tv) {
-    const int ea = lane >> 3, eb = lane & 7;
+  // off-diagonal blocks T~_{g,h} = T~_{g,g} S, S = sum_{m=h}^{g-1} G_{g,m} T~_{m,h}, in four
+  // steps (each ends with LDS writes that the next one reads).  lane = element (ea, eb) of
+  // an 8x8 block; tv[] receives this lane's element of the blocks 00, 11, 22, 33, 10, 21,
+  // 32, 20, 31, 30.
+  const int ea = lane >> 3, eb = lane & 7;
+  auto od_1a = [&](PScratch& P, float* tv) {  // S for (1,0), (2,1), (3,2)
     const float* g1 = &P.gram[(8 + ea) * T_LD];
     const float* g2 = &P.gram[(16 + ea) * T_LD];
     const float* g3 = &P.gram[(24 + ea) * T_LD];
 #pragma unroll
     for (int gb = 0; gb < 4; ++gb) tv[gb] = P.drow[gb][ea * 8 + eb];
-    // round 1: (1,0), (2,1), (3,2)
     P.sblk[0][eb * 8 + ea] = dot8(g1, &P.dcol[0][eb * 8]);
     P.sblk[1][eb * 8 + ea] = dot8(g2 + 8, &P.dcol[1][eb * 8]);
     P.sblk[2][eb * 8 + ea] = dot8(g3 + 16, &P.dcol[2][eb * 8]);
-    wave_sync();
+  };
+  auto od_1b = [&](PScratch& P, float* tv) {  // T~ (1,0), (2,1), (3,2)
     tv[4] = dot8(&P.drow[1][ea * 8], &P.sblk[0][eb * 8]);
     tv[5] = dot8(&P.drow[2][ea * 8], &P.sblk[1][eb * 8]);
     tv[6] = dot8(&P.drow[3][ea * 8], &P.sblk[2][eb * 8]);
     P.ocol[0][eb * 8 + ea] = tv[4];
     P.ocol[1][eb * 8 + ea] = tv[5];
-    wave_sync();
-    // round 2: (2,0), (3,1)
+  };
+  auto od_2 = [&](PScratch& P, float* tv) {  // (2,0), (3,1)
+    const float* g2 = &P.gram[(16 + ea) * T_LD];
+    const float* g3 = &P.gram[(24 + ea) * T_LD];
     P.sblk[0][eb * 8 + ea] = dot8(g2, &P.dcol[0][eb * 8]) + dot8(g2 + 8, &P.ocol[0][eb * 8]);
     P.sblk[1][eb * 8 + ea] = dot8(g3 + 8, &P.dcol[1][eb * 8]) + dot8(g3 + 16, &P.ocol[1][eb * 8]);
     wave_sync();
     tv[7] = dot8(&P.drow[2][ea * 8], &P.sblk[0][eb * 8]);
     tv[8] = dot8(&P.drow[3][ea * 8], &P.sblk[1][eb * 8]);
     P.ocol[2][eb * 8 + ea] = tv[7];
-    wave_sync();
-    // round 3: (3,0)
+  };
+  auto od_3 = [&](PScratch& P, float* tv) {  // (3,0)
+    const float* g3 = &P.gram[(24 + ea) * T_LD];
     P.sblk[2][eb * 8 + ea] = dot8(g3, &P.dcol[0][eb * 8]) + dot8(g3 + 8, &P.ocol[0][eb * 8]) +
                              dot8(g3 + 16, &P.ocol[2][eb * 8]);
     wave_sync();
@@ -444,133 +475,162 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     }
   };
 
-  // With the readout, iteration it has two barriers: (B) in the middle, after which
-  // the consumers overwrite the readout stashes, and (A) at the end.  Without it, only (A).
+  // Every iteration ends with one workgroup barrier (A).
   const int last = READOUT ? nch : nch - 1;  // the readout of chunk c runs in iteration c+1
-  if (wave >= NCW) {
+  if (wave >= NCW + NRW) {
     // ================================================ producers
-    const int p = wave - NCW;
-    PScratch& P = sm.pscr[p];
+    const int p = wave - NCW - NRW;
     Regs r;
     float tv[10];
-    for (int it = -4; it <= last; ++it) {
-      const int phase = (it - p + 8) & 3;
-      const int n = it + 4 - phase;
+    for (int it = -NPW; it <= last; ++it) {
+      const int phase = (it - p + 2 * NPW) & (NPW - 1);
+      const int n = it + NPW - phase;
       if (n >= 0 && n < nch) {  // uniform across the wave
-        if (phase == 0) p_load(r, n);
-        else if (phase == 1) p_gram(r, n, P);
-        else if (phase == 2) p_offdiag(P, tv);
-        else p_write(r, n, tv);
+        PScratch& P = sm.pscr[NPW == 8 ? p : (n & 1)];
+        if constexpr (NPW == 4) {
+          if (phase == 0) {
+            p_load(r, n);
+          } else if (phase == 1) {
+            p_gram(r, n, P);
+            wave_sync();
+            p_diag(P);
+          } else if (phase == 2) {
+            od_1a(P, tv);
+            wave_sync();
+            od_1b(P, tv);
+            wave_sync();
+            od_2(P, tv);
+            wave_sync();
+            od_3(P, tv);
+          } else {
+            p_write(r, n, tv);
+          }
+        } else {
+          if (phase == 0) p_load(r, n);
+          else if (phase == 1) p_gram(r, n, P);
+          else if (phase == 2) p_diag(P);
+          else if (phase == 3) od_1a(P, tv);
+          else if (phase == 4) od_1b(P, tv);
+          else if (phase == 5) od_2(P, tv);
+          else if (phase == 6) od_3(P, tv);
+          else p_write(r, n, tv);
+        }
       }
-      if (READOUT) lds_barrier();  // (B)
-      lds_barrier();               // (A)
+      lds_barrier();  // (A)
     }
     return;
   }
 
-  // ================================================== consumers
   // The state enters the MFMAs rounded to f16, so it is carried scaled by a power of
   // two s (exact) that puts its largest start entry in [1, 2): every column keeps its
   // norm under the orthogonal updates, so no later entry leaves the f16 range.  The
   // readout and the end state are multiplied back by 1/s.
-  float inv_s = 1.f;
+  float sc = 1.f, inv_s = 1.f;
   {
     const float m = fmaxf(fmaxf(sm.smax[0], sm.smax[1]), fmaxf(sm.smax[2], sm.smax[3]));
     if (m > 0.f && m <= 3.0e38f) {
       int e;
       (void)frexpf(m, &e);  // m = f * 2^e, f in [0.5, 1)
-      const float sc = ldexpf(1.f, 1 - e);
+      sc = ldexpf(1.f, 1 - e);
       inv_s = ldexpf(1.f, e - 1);
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt) psi[rt] *= sc;
     }
   }
+  const int pg = 2 * (g4 & 1) + (g4 >> 1);
+  constexpr int PST_BUF = D * PST_LD, ZST_BUF = D * ZST_LD;
+
+  if (READOUT && wave >= NCW) {
+    // ================================================ readout waves
+    // Readout of chunk c in iteration c+1 (after barrier (A) of iteration c, which ends
+    // the consumers' stash writes of chunk c): readout wave w computes the output rows
+    // d in [32w, 32w + 32) completely, so no cross-wave reduction is needed:
+    //   O = S Q + U mask(Z Q)  restricted to those rows; S Q and Z Q contract over all
+    //   128 state columns j (k-slot group g4 covers j = 32ks + 8pg + 0..7).
+    // Offsets: U rows rho = 16hh + 4g4 + i, features 32w + 16tl + 4r (transposing reads);
+    // q token l16, features 32ks + 8pg; stash rows j = 32ks + 8pg + 4hh + (l16 >> 2),
+    // where j_slot(8pg + 4hh + i) = j_slot(8pg + i) + hh (stashes of chunk c in buffer c & 1).
+    const int rw = wave - NCW;
+    const int offO = rho_slot(4 * g4 + (l16 >> 2)) * U_LD + 32 * rw + 4 * (l16 & 3);
+    const int offQ = Q_OFF + l16 * Q_LD + 8 * pg;
+    const E* const pst_rd = sm.pst[0] + j_slot(8 * pg + (l16 >> 2)) * PST_LD + 32 * rw + 4 * (l16 & 3);
+    const E* const zst_rd = sm.zst[0] + j_slot(8 * pg + (l16 >> 2)) * ZST_LD + 4 * (l16 & 3);
+    auto readout = [&](int c) {
+      const E* tb = sm.tok[c % 3];
+      const E* const pst_c = pst_rd + (c & 1) * PST_BUF;
+      const E* const zst_c = zst_rd + (c & 1) * ZST_BUF;
+      f32x4 O[2] = {}, Y[2] = {};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const V8 bq = lds8<E>(tb + offQ + 32 * ks);
+#pragma unroll
+        for (int tl = 0; tl < 2; ++tl) {
+          const E* p = pst_c + 32 * ks * PST_LD + 16 * tl;
+          O[tl] = MM::mma16(lds_tr4x2<E>(p, p + PST_LD), bq, O[tl]);
+        }
+#pragma unroll
+        for (int yy = 0; yy < 2; ++yy) {
+          const E* p = zst_c + 32 * ks * ZST_LD + 16 * yy;
+          Y[yy] = MM::mma16(lds_tr4x2<E>(p, p + ZST_LD), bq, Y[yy]);
+        }
+      }
+      // Y lane (g4, t = l16) holds rho = 16yy + 4g4 + r: the B-operand layout of U mask(Y)
+      V8 by;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        by[r] = static_cast<E>(((4 * g4 + r) >> 1) <= l16 ? Y[0][r] : 0.f);
+        by[4 + r] = static_cast<E>(((16 + 4 * g4 + r) >> 1) <= l16 ? Y[1][r] : 0.f);
+      }
+#pragma unroll
+      for (int tl = 0; tl < 2; ++tl)
+        O[tl] = MM::mma16(lds_tr4x2<E>(tb + offO + 16 * tl, tb + offO + U_LD + 16 * tl), by, O[tl]);
+      // lane (g4, t = l16) holds O[32 rw + 16 tl + 4 g4 + 0..3][t].  Stored through a
+      // buffer resource spanning this chunk's valid tokens: rows past the end of the
+      // sequence fall outside it and the hardware drops them, so no branch is needed.
+      const int t0 = (chunk0 + c) * C;
+      const int nvalid = a.out ? min(C, a.T - t0) : 0;
+      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+          static_cast<IO*>(a.out) + tok_base + static_cast<int64_t>(t0) * tok_stride, (short)0,
+          nvalid * static_cast<int>(tok_stride) * static_cast<int>(sizeof(IO)), 0x00020000);
+      const int ooff = (l16 * static_cast<int>(tok_stride) + 32 * rw + 4 * g4) * static_cast<int>(sizeof(IO));
+#pragma unroll
+      for (int tl = 0; tl < 2; ++tl) {
+        typedef IO io4 __attribute__((ext_vector_type(4)));
+        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+        io4 o4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o4[r] = static_cast<IO>(O[tl][r] * inv_s);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o4), orsrc,
+                                              ooff + 16 * tl * static_cast<int>(sizeof(IO)), 0, 0);
+      }
+    };
+    for (int it = -NPW; it <= last; ++it) {
+      if (it >= 1) readout(it - 1);  // it - 1 < nch since last = nch
+      lds_barrier();  // (A)
+    }
+    return;
+  }
+
+  // ================================================== consumers
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) psi[rt] *= sc;
 
   // Per-lane element offsets into a chunk buffer (constant parts are added at the use).
   //   offW: W operand, U^T row rho = l32, features 32rt + 16ks + 4g + {0..3, 8..11}
   //   offU: update operand via transposing reads: rows rho = 16ks + 8hh + 4g + i,
   //         features 32rt + 16 (lane>>4 & 1) + 4r  ->  lane gets U[32rt + l32][rho..rho+3]
-  //   offO: readout operand, rows rho = 16hh + 4g4 + i, features 32 wave + 16tl + 4r
-  //   offQ: readout q, token l16, features 32ks + 8pg
-  // rho_slot is linear over disjoint bits, so +16ks / +8hh / +16hh are +ks / +2hh / +hh slots.
-  const int pg = 2 * (g4 & 1) + (g4 >> 1);
+  // rho_slot is linear over disjoint bits, so +16ks / +8hh are +ks / +2hh slots.
   const int offW = rho_slot(l32) * U_LD + 4 * g;
   const int offU = rho_slot(4 * g + (l16 >> 2)) * U_LD + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
-  const int offO = rho_slot(4 * g4 + (l16 >> 2)) * U_LD + 32 * wave + 4 * (l16 & 3);
-  const int offQ = Q_OFF + l16 * Q_LD + 8 * pg;
+  // readout stash rows written: j = col = 32 wave + l32 (buffer 0; chunk c uses buffer c & 1)
+  E* const pst_wr = sm.pst[0] + (32 * wave + j_slot(l32)) * PST_LD + 4 * g;
+  E* const zst_wr = sm.zst[0] + (32 * wave + j_slot(l32)) * ZST_LD + 4 * g;
 
-  // stash rows read by this lane's transposing loads: j = 32ks + 8pg + 4hh + (l16 >> 2)
-  // (j_slot(8pg + 4hh + i) = j_slot(8pg + i) + hh); rows written: j = col = 32 wave + l32
-  const E* const pst_rd = sm.pst + j_slot(8 * pg + (l16 >> 2)) * PST_LD + 32 * wave + 4 * (l16 & 3);
-  const E* const zst_rd = sm.zst + j_slot(8 * pg + (l16 >> 2)) * ZST_LD + 4 * (l16 & 3);
-  E* const pst_wr = sm.pst + (32 * wave + j_slot(l32)) * PST_LD + 4 * g;
-  E* const zst_wr = sm.zst + (32 * wave + j_slot(l32)) * ZST_LD + 4 * g;
-
-  // Readout of chunk c (run in iteration c+1, after barrier (A) of iteration c, from
-  // the shared stashes): this wave computes output rows d in [32*wave, 32*wave + 32)
-  // completely, so no cross-wave reduction is needed:
-  //   O = S Q + U mask(Z Q)  restricted to those rows; S Q and Z Q contract over all
-  //   128 state columns j (k-slot group g4 covers j = 32ks + 8pg + 0..7).
-  auto readout = [&](int c) {
-    const E* tb = sm.tok[c % 3];
-    f32x4 O[2] = {}, Y[2] = {};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const V8 bq = lds8<E>(tb + offQ + 32 * ks);
-#pragma unroll
-      for (int tl = 0; tl < 2; ++tl) {
-        const E* p = pst_rd + 32 * ks * PST_LD + 16 * tl;
-        O[tl] = MM::mma16(lds_tr4x2<E>(p, p + PST_LD), bq, O[tl]);
-      }
-#pragma unroll
-      for (int yy = 0; yy < 2; ++yy) {
-        const E* p = zst_rd + 32 * ks * ZST_LD + 16 * yy;
-        Y[yy] = MM::mma16(lds_tr4x2<E>(p, p + ZST_LD), bq, Y[yy]);
-      }
-    }
-    // Y lane (g4, t = l16) holds rho = 16yy + 4g4 + r: the B-operand layout of U mask(Y)
-    V8 by;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      by[r] = static_cast<E>(((4 * g4 + r) >> 1) <= l16 ? Y[0][r] : 0.f);
-      by[4 + r] = static_cast<E>(((16 + 4 * g4 + r) >> 1) <= l16 ? Y[1][r] : 0.f);
-    }
-#pragma unroll
-    for (int tl = 0; tl < 2; ++tl)
-      O[tl] = MM::mma16(lds_tr4x2<E>(tb + offO + 16 * tl, tb + offO + U_LD + 16 * tl), by, O[tl]);
-    // Keep two k-steps of operands (1 + 8 LDS reads each) in flight ahead of the MFMAs,
-    // and the U operands of the last product behind the third k-step.
-    __builtin_amdgcn_sched_group_barrier(0x100, 18, 0);  // DS reads: k-steps 0, 1
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // MFMA: k-step 0
-    __builtin_amdgcn_sched_group_barrier(0x100, 9, 0);   // DS reads: k-step 2
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // MFMA: k-step 1
-    __builtin_amdgcn_sched_group_barrier(0x100, 9, 0);   // DS reads: k-step 3
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // MFMA: k-step 2
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // DS reads: U operands
-    __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);   // MFMA: k-step 3, U mask(Y)
-    // lane (g4, t = l16) holds O[32 wave + 16 tl + 4 g4 + 0..3][t]
-    const int tok = (chunk0 + c) * C + l16;
-    if (a.out != nullptr && tok < a.T) {
-      IO* dst = static_cast<IO*>(a.out) + tok_base + static_cast<int64_t>(tok) * tok_stride +
-                32 * wave + 4 * g4;
-#pragma unroll
-      for (int tl = 0; tl < 2; ++tl) {
-        typedef IO io4 __attribute__((ext_vector_type(4)));
-        io4 o4;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o4[r] = static_cast<IO>(O[tl][r] * inv_s);
-        *reinterpret_cast<io4*>(dst + 16 * tl) = o4;
-      }
-    }
-  };
-
-  // One iteration; HAS_READOUT / ACTIVE are compile-time so that the steady-state
-  // body is a single basic block the scheduler can overlap freely.
-  auto iteration = [&](int cc, auto has_readout, auto active) {
-    constexpr bool RO = decltype(has_readout)::value;
+  // One iteration; ACTIVE is compile-time so that the steady-state body is a single
+  // basic block the scheduler can overlap freely.
+  auto iteration = [&](int cc, auto active) {
     constexpr bool ACT = decltype(active)::value;
     const E* tb = sm.tok[ACT ? cc % 3 : 0];
-    if constexpr (RO) readout(cc - 1);
+    E* const pw = pst_wr + (cc & 1) * PST_BUF;  // this chunk's readout stashes
+    E* const zw = zst_wr + (cc & 1) * ZST_BUF;
     V8 wu[4][2];  // W operands (ready since two iterations back)
     if constexpr (ACT) {
 #pragma unroll
@@ -587,26 +647,19 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
     V8 pb[4][2];
     f32x16 W = {};
     if constexpr (ACT) {
-      f32x16 Wa = {}, Wb = {};  // two independent MFMA chains (row tiles 0-1 and 2-3)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int rp = 0; rp < 2; ++rp)
+        for (int rt = 0; rt < 4; ++rt) {
+          float x[8];
 #pragma unroll
-          for (int half = 0; half < 2; ++half) {
-            const int rt = rp + 2 * half;  // alternate the chains: rt 0, 2, 1, 3
-            float x[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) x[i] = psi[rt][8 * ks + i];
-            f32x16& Wr = half == 0 ? Wa : Wb;
-            pb[rt][ks] = round8<E>(x);
-            Wr = MM::mma32(wu[rt][ks], pb[rt][ks], Wr);
-          }
-      W = Wa + Wb;
+          for (int i = 0; i < 8; ++i) x[i] = psi[rt][8 * ks + i];
+          pb[rt][ks] = round8<E>(x);
+          W = MM::mma32(wu[rt][ks], pb[rt][ks], W);
+        }
     }
     // T~ operands and the update operands (transposing reads of U): both buffers were
-    // completed before earlier barriers, so the loads are issued here and land during
-    // barrier (B).
+    // completed before earlier barriers.
     V8 ahi[2], alo[2], uu[2][4];
     if constexpr (ACT) {
       const int cb = cc & 1;  // T~ buffer
@@ -625,7 +678,6 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
           uu[ks][rt] = lds_tr4x2<E>(p, p + 2 * U_LD);
         }
     }
-    if (READOUT) lds_barrier();  // (B): every wave is done reading the stashes of chunk cc-1
     if constexpr (ACT) {
       if (READOUT) {
         // psi tile rt, ks, half hh holds rows 32rt + 16ks + 8hh + 4g + 0..3 of column col
@@ -636,8 +688,8 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
             typedef typename MM::v4 V4;
             const V4 h0 = __builtin_shufflevector(pb[rt][ks], pb[rt][ks], 0, 1, 2, 3);
             const V4 h1 = __builtin_shufflevector(pb[rt][ks], pb[rt][ks], 4, 5, 6, 7);
-            *reinterpret_cast<V4*>(pst_wr + 32 * rt + 16 * ks) = h0;
-            *reinterpret_cast<V4*>(pst_wr + 32 * rt + 16 * ks + 8) = h1;
+            *reinterpret_cast<V4*>(pw + 32 * rt + 16 * ks) = h0;
+            *reinterpret_cast<V4*>(pw + 32 * rt + 16 * ks + 8) = h1;
           }
       }
 
@@ -662,8 +714,8 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
         const V8 zb = round8<E>(zv);
         if (READOUT) {
           typedef typename MM::v4 V4;
-          *reinterpret_cast<V4*>(zst_wr + 16 * ks) = __builtin_shufflevector(zb, zb, 0, 1, 2, 3);
-          *reinterpret_cast<V4*>(zst_wr + 16 * ks + 8) = __builtin_shufflevector(zb, zb, 4, 5, 6, 7);
+          *reinterpret_cast<V4*>(zw + 16 * ks) = __builtin_shufflevector(zb, zb, 0, 1, 2, 3);
+          *reinterpret_cast<V4*>(zw + 16 * ks + 8) = __builtin_shufflevector(zb, zb, 4, 5, 6, 7);
         }
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) psi[rt] = MM::mma32(uu[ks][rt], zb, psi[rt]);
@@ -674,14 +726,9 @@ __global__ __launch_bounds__(NT) void sssd_chunk_kernel(Args a) {
 
   typedef std::integral_constant<bool, true> yes;
   typedef std::integral_constant<bool, false> no;
-  for (int cc = -4; cc < 0; ++cc) iteration(cc, no{}, no{});
-  if (READOUT) {
-    iteration(0, no{}, yes{});
-    for (int cc = 1; cc < nch; ++cc) iteration(cc, std::integral_constant<bool, READOUT>{}, yes{});
-    iteration(nch, std::integral_constant<bool, READOUT>{}, no{});
-  } else {
-    for (int cc = 0; cc < nch; ++cc) iteration(cc, no{}, yes{});
-  }
+  for (int cc = -NPW; cc < 0; ++cc) iteration(cc, no{});
+  for (int cc = 0; cc < nch; ++cc) iteration(cc, yes{});
+  if (READOUT) iteration(nch, no{});  // the readout waves' last iteration
 
   // ---------------------------------------------------------------- end state
   {
@@ -837,7 +884,7 @@ hipError_t run_chunked(const void* q, const void* k, const void* v, const void* 
     pa.ends = P;
     pa.end_mode = 0;
     hipLaunchKernelGGL((chunk::sssd_chunk_kernel<IO, DT, false>), dim3(BH, p.nseg - 1),
-                       dim3(chunk::NT), 0, stream, pa);
+                       dim3(chunk::Cfg<false>::NT), 0, stream, pa);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(chunk::sssd_carry_kernel, dim3(BH), dim3(chunk::CARRY_NT), 0, stream,
@@ -850,7 +897,7 @@ hipError_t run_chunked(const void* q, const void* k, const void* v, const void* 
   a.out = out;
   a.ends = psi_out;
   a.end_mode = 1;
-  hipLaunchKernelGGL((chunk::sssd_chunk_kernel<IO, DT, true>), dim3(BH, p.nseg), dim3(chunk::NT),
+  hipLaunchKernelGGL((chunk::sssd_chunk_kernel<IO, DT, true>), dim3(BH, p.nseg), dim3(chunk::Cfg<true>::NT),
                      0, stream, a);
   return hipGetLastError();
 }
