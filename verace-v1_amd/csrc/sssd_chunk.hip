@@ -42,7 +42,7 @@
 //   pass A (READOUT=false): each segment s < S-1 from the identity -> its
 //          transform P_s (the end state),
 //   pass B (sssd_carry_kernel): start_s = P_{s-1} start_{s-1}, column blocks in
-//          parallel, bf16x3 MFMA (fp32-faithful),
+//          parallel workgroups, bf16x3 MFMA (fp32-faithful),
 //   pass C (READOUT=true): every segment from its start state, with outputs.
 #include <type_traits>
 
@@ -746,37 +746,42 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
 }
 
 // start_s = P_{s-1} start_{s-1}, s = 1 .. S-1, start_0 = psi0 (identity if null).
-// One workgroup of 8 waves per (b, h); wave w owns the 16-column block w of the
-// running start state (in MFMA accumulators).  Each P_{s-1} is staged once in LDS
-// as a 16-bit hi + lo pair, shared by the 8 waves; the next P is prefetched into
-// registers while the current product runs.  bf16x3 (hi*hi + hi*lo + lo*hi) keeps
-// the chain fp32-faithful.
-constexpr int CARRY_WAVES = D / 16;
+// Left products act on the columns independently, so the chain of one sequence is
+// split over CARRY_SPLIT workgroups of CARRY_COLS columns each.  Every P_{s-1} is read
+// with coalesced loads (issued one product ahead) and staged in LDS as a bf16 hi + lo
+// pair; the running columns X are kept in LDS the same way (transposed).  Wave
+// (rb, ch) produces rows 32rb .. 32rb+31 and columns 32ch .. 32ch+31 of the workgroup's
+// block with bf16x3 MFMA (hi*hi + hi*lo + lo*hi, fp32-faithful).
+constexpr int CARRY_SPLIT = 2;
+constexpr int CARRY_COLS = D / CARRY_SPLIT;         // 64
+constexpr int CARRY_WAVES = (D / 32) * (CARRY_COLS / 32);  // 8
 constexpr int CARRY_NT = CARRY_WAVES * 64;
-constexpr int CP_LD = D + 8;  // elements per staged P row (272 B)
+constexpr int CP_LD = D + 8;   // bf16 per LDS row of P and of X^T (272 B)
 constexpr int CARRY_F4 = D * D / 4 / CARRY_NT;  // float4 of P per thread
 
 __global__ __launch_bounds__(CARRY_NT) void sssd_carry_kernel(const float* psi0, const float* P,
                                                               float* starts, int BH, int S) {
   typedef mfma_t<__bf16> MM;
   typedef MM::v8 V8;
-  __shared__ __bf16 phi[D * CP_LD];
-  __shared__ __bf16 plo[D * CP_LD];
-  const int bh = blockIdx.x;
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  __shared__ __bf16 phi[D * CP_LD], plo[D * CP_LD];                    // P, row-major
+  __shared__ __bf16 xhi[CARRY_COLS * CP_LD], xlo[CARRY_COLS * CP_LD];  // X^T: [n][k]
+  const int bh = blockIdx.x, cb = blockIdx.y;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int l16 = lane & 15, g4 = lane >> 4;
-  const int col = 16 * wave + l16;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int rb = wave & 3, ch = wave >> 2;
   const int64_t DD = static_cast<int64_t>(D) * D;
-  f32x4 X[8];  // X[16it + 4g4 + r][col]
-#pragma unroll
-  for (int it = 0; it < 8; ++it)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * it + 4 * g4 + r;
-      X[it][r] = psi0 ? psi0[bh * DD + row * D + col] : (row == col ? 1.f : 0.f);
-    }
-  float4 pf[CARRY_F4];  // this thread's share of the next P (element e = tid + NT*m)
+  auto put = [](__bf16* hi, __bf16* lo, int off, float x) {
+    const __bf16 h = static_cast<__bf16>(x);
+    hi[off] = h;
+    lo[off] = static_cast<__bf16>(x - static_cast<float>(h));
+  };
+  for (int e = tid; e < CARRY_COLS * D; e += CARRY_NT) {
+    const int row = e / CARRY_COLS, n = e - row * CARRY_COLS, colg = CARRY_COLS * cb + n;
+    put(xhi, xlo, n * CP_LD + row, psi0 ? psi0[bh * DD + row * D + colg] : (row == colg ? 1.f : 0.f));
+  }
+  float4 pf[CARRY_F4];  // this thread's share of the next P: float4 index tid + NT*m
   auto fetch = [&](int s) {
     const float4* src = reinterpret_cast<const float4*>(P + (static_cast<int64_t>(s - 1) * BH + bh) * DD);
 #pragma unroll
@@ -784,54 +789,46 @@ __global__ __launch_bounds__(CARRY_NT) void sssd_carry_kernel(const float* psi0,
   };
   if (S > 1) fetch(1);
   for (int s = 1; s < S; ++s) {
-    // stage P_{s-1} as hi + lo
 #pragma unroll
-    for (int m = 0; m < CARRY_F4; ++m) {
+    for (int m = 0; m < CARRY_F4; ++m) {  // stage P_{s-1} as hi + lo (8-byte stores)
       const int e = 4 * (tid + CARRY_NT * m);
       const int row = e / D, c0 = e - row * D;
       const float xv[4] = {pf[m].x, pf[m].y, pf[m].z, pf[m].w};
+      bf16x4 h4, l4;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const __bf16 hv = static_cast<__bf16>(xv[i]);
-        phi[row * CP_LD + c0 + i] = hv;
-        plo[row * CP_LD + c0 + i] = static_cast<__bf16>(xv[i] - static_cast<float>(hv));
+        h4[i] = static_cast<__bf16>(xv[i]);
+        l4[i] = static_cast<__bf16>(xv[i] - static_cast<float>(h4[i]));
       }
+      *reinterpret_cast<bf16x4*>(&phi[row * CP_LD + c0]) = h4;
+      *reinterpret_cast<bf16x4*>(&plo[row * CP_LD + c0]) = l4;
     }
-    __syncthreads();
+    __syncthreads();  // P staged; X (initial or from the previous product) complete
     if (s + 1 < S) fetch(s + 1);
-    f32x4 Y[8];
+    // Y = P[32rb .. +31][:] X[:][32ch .. +31]; A row = l32, B column = l32, k-slots
+    // 16ks + 8g + 0..7 in both operands
+    f32x16 Y = {};
 #pragma unroll
-    for (int it = 0; it < 8; ++it) Y[it] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      float xb[8];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        xb[r] = X[2 * ks][r];
-        xb[4 + r] = X[2 * ks + 1][r];
-      }
-      V8 xhi, xlo;
-      split8<__bf16>(xb, xhi, xlo);
-#pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const int off = (16 * it + l16) * CP_LD + 32 * ks + 4 * g4;
-        const V8 ahi = cat8<bf16x4, V8>(*reinterpret_cast<const bf16x4*>(&phi[off]),
-                                         *reinterpret_cast<const bf16x4*>(&phi[off + 16]));
-        const V8 alo = cat8<bf16x4, V8>(*reinterpret_cast<const bf16x4*>(&plo[off]),
-                                         *reinterpret_cast<const bf16x4*>(&plo[off + 16]));
-        Y[it] = MM::mma16(ahi, xhi, Y[it]);
-        Y[it] = MM::mma16(ahi, xlo, Y[it]);
-        Y[it] = MM::mma16(alo, xhi, Y[it]);
-      }
+    for (int ks = 0; ks < 8; ++ks) {
+      const int ka = 16 * ks + 8 * g;
+      const V8 ah = *reinterpret_cast<const V8*>(&phi[(32 * rb + l32) * CP_LD + ka]);
+      const V8 al = *reinterpret_cast<const V8*>(&plo[(32 * rb + l32) * CP_LD + ka]);
+      const V8 bh8 = *reinterpret_cast<const V8*>(&xhi[(32 * ch + l32) * CP_LD + ka]);
+      const V8 bl8 = *reinterpret_cast<const V8*>(&xlo[(32 * ch + l32) * CP_LD + ka]);
+      Y = MM::mma32(ah, bh8, Y);
+      Y = MM::mma32(ah, bl8, Y);
+      Y = MM::mma32(al, bh8, Y);
     }
-    float* dst = starts + (static_cast<int64_t>(s - 1) * BH + bh) * DD;
+    __syncthreads();  // every wave has read P and X before they are replaced
+    // Y: lane (g, l32) holds rows 32rb + 8(r/4) + 4g + r%4 of column 32ch + l32
+    const int colw = 32 * ch + l32;
+    float* dst = starts + (static_cast<int64_t>(s - 1) * BH + bh) * DD + CARRY_COLS * cb + colw;
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      X[it] = Y[it];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dst[(16 * it + 4 * g4 + r) * D + col] = Y[it][r];
+    for (int r = 0; r < 16; ++r) {
+      const int row = 32 * rb + 8 * (r >> 2) + 4 * g + (r & 3);
+      dst[row * D] = Y[r];
+      put(xhi, xlo, colw * CP_LD + row, Y[r]);
     }
-    __syncthreads();  // the staged P is read by every wave before it is replaced
   }
 }
 
@@ -887,7 +884,8 @@ hipError_t run_chunked(const void* q, const void* k, const void* v, const void* 
                        dim3(chunk::Cfg<false>::NT), 0, stream, pa);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(chunk::sssd_carry_kernel, dim3(BH), dim3(chunk::CARRY_NT), 0, stream,
+    hipLaunchKernelGGL(chunk::sssd_carry_kernel, dim3(BH, chunk::CARRY_SPLIT),
+                       dim3(chunk::CARRY_NT), 0, stream,
                        psi_in, P, starts, BH, p.nseg);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
