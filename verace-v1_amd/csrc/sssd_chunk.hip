@@ -114,6 +114,7 @@ template <typename E, bool READOUT>
 struct Smem {
   E tok[3][CHUNK_ELEMS];        // U rows and q rows of a chunk (3 chunks in flight)
   E tth[2][R * TT_LD];          // T~ = hi + lo (two 16-bit parts), row-major
+  E ttpad[8];                   // puts ttl 4 banks after tth (conflict-light pair writes)
   E ttl[2][R * TT_LD];
   E pst[2][READOUT ? D * PST_LD : 1];  // readout stash (chunk parity): chunk-start state, transposed
   E zst[2][READOUT ? D * ZST_LD : 1];  // readout stash (chunk parity): Z, transposed
@@ -461,17 +462,24 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
         *reinterpret_cast<uint4*>(tb + Q_OFF + (e >> 4) * Q_LD + 8 * (e & 15)) = to_f16x8<IO>(r.q[m]);
       }
     }
-    E* tth = sm.tth[n & 1];
-    E* ttl = sm.ttl[n & 1];
+    // T~ element (ea, eb) of each block as f16 hi + lo.  Lanes pair up (eb, eb ^ 1):
+    // the even lane writes the two hi parts, the odd lane the two lo parts, as one
+    // 32-bit store each (DPP swaps the parts between the two lanes).
     const int ea = lane >> 3, eb = lane & 7;
+    const bool odd = eb & 1;
+    uint32_t* const tw = reinterpret_cast<uint32_t*>(odd ? sm.ttl[n & 1] : sm.tth[n & 1]);
     const int brow[10] = {0, 1, 2, 3, 1, 2, 3, 2, 3, 3};
     const int bcol[10] = {0, 1, 2, 3, 0, 1, 2, 0, 1, 0};
 #pragma unroll
     for (int i = 0; i < 10; ++i) {
-      const int o = (8 * brow[i] + ea) * TT_LD + 8 * bcol[i] + eb;
       const E hpart = static_cast<E>(tv[i]);
-      tth[o] = hpart;
-      ttl[o] = static_cast<E>(tv[i] - static_cast<float>(hpart));
+      const E lpart = static_cast<E>(tv[i] - static_cast<float>(hpart));
+      const uint32_t hb = __builtin_bit_cast(uint16_t, hpart), lb = __builtin_bit_cast(uint16_t, lpart);
+      // quad_perm(1, 0, 3, 2): each lane receives its partner's value
+      const uint32_t recv = static_cast<uint32_t>(
+          __builtin_amdgcn_mov_dpp(static_cast<int>(odd ? hb : lb), 0xB1, 0xF, 0xF, false));
+      const uint32_t word = odd ? (recv | (lb << 16)) : (hb | (recv << 16));
+      tw[((8 * brow[i] + ea) * TT_LD + 8 * bcol[i] + (eb & ~1)) >> 1] = word;
     }
   };
 
