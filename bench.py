@@ -200,8 +200,9 @@ def pmc_summary(fetch_csv, write_csv, out_json):
     WRITE_SIZE; values in KiB per dispatch) into HBM bytes per scan.  Each counter is
     scaled so that the calibration copy (COPY_PROBE_BYTES read and written) reads
     exactly its known size."""
-    import csv
     import collections
+    import csv
+    import re
 
     def per_kernel(path):
         vals = collections.defaultdict(list)
@@ -218,8 +219,10 @@ def pmc_summary(fetch_csv, write_csv, out_json):
         kern = {}
         for k, v in vals.items():
             if "sssd_chunk_kernel" in k or "sssd_carry_kernel" in k:
-                tag = ("pass C (readout)" if "Lb1ELb1E" in k else "pass A (segment transforms)"
-                       if "sssd_chunk_kernel" in k else "pass B (carry)")
+                # the READOUT flag is the kernel template's last argument (mangled Lb0E / Lb1E)
+                flags = re.findall(r"Lb([01])E", k)
+                tag = ("pass B (carry)" if "sssd_carry_kernel" in k else
+                       "pass C (readout)" if flags and flags[-1] == "1" else "pass A (segment transforms)")
                 kern[tag] = sum(v) / len(v) * scale
         res[counter] = {"scale": scale, "bytes_per_launch": kern, "bytes_per_scan": sum(kern.values())}
         total += sum(kern.values())
