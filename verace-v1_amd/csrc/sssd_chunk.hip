@@ -39,10 +39,11 @@
 //     no barrier against the readout of chunk c-1.
 //
 // Long sequences are split into segments processed by independent workgroups:
-//   pass A (READOUT=false): each segment s < S-1 from the identity -> its
-//          transform P_s (the end state),
-//   pass B (sssd_carry_kernel): start_s = P_{s-1} start_{s-1}, column blocks in
-//          parallel workgroups, bf16x3 MFMA (fp32-faithful),
+//   pass A (READOUT=false): the transforms of segments 0 .. S-2 from the identity,
+//          spread over S workgroups per sequence (so it fills as many CUs as pass C):
+//          each segment is covered by two parts, each part's transform is stored,
+//   pass B (sssd_carry_kernel): start_s = (part 2 of s-1)(part 1 of s-1) start_{s-1},
+//          column blocks in parallel workgroups, bf16x3 MFMA (fp32-faithful),
 //   pass C (READOUT=true): every segment from its start state, with outputs.
 #include <type_traits>
 
@@ -132,10 +133,17 @@ struct Args {
   const float* starts;  // start of segment s >= 1 at starts[(s-1)*BH + bh]; null = identity
   void* out;            // [B][T][H][D] (READOUT only)
   float* ends;          // see end_mode
-  int end_mode;         // 0: ends[s*BH + bh] for every segment; 1: ends[bh] for the last one
+  int end_mode;         // 0: pass A factors (see below); 1: ends[bh] for the last segment
   int T, H, BH;
   int seg_chunks;       // chunks per segment
   int nseg;             // segments per sequence
+  // Pass A with npieces > 0: workgroup (bh, a) covers chunks [c_a, c_{a+1}) of the
+  // first (nseg-1) * seg_chunks, c_a = a * that / npieces, and writes the transform of
+  // every part between segment boundaries: factor 2s is the part of segment s before
+  // the piece boundary inside it, factor 2s+1 the part after it (npieces = nseg puts
+  // exactly one piece boundary inside every segment).  Factor f of sequence bh is at
+  // ends[f * BH + bh].  With npieces = 0 the pieces are the segments, factor s = P_s.
+  int npieces;
 };
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also waits for every
@@ -226,9 +234,17 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   const int seg = blockIdx.y;
   const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
   const int total_chunks = (a.T + C - 1) / C;
-  const int chunk0 = seg * a.seg_chunks;
+  int chunk0 = seg * a.seg_chunks;
   int nch = total_chunks - chunk0;
   if (nch > a.seg_chunks) nch = a.seg_chunks;
+  int split = -1;  // pieces: chunk index (within the piece) where a segment starts
+  if (!READOUT && a.npieces > 0) {
+    const int64_t span = static_cast<int64_t>(a.nseg - 1) * a.seg_chunks;
+    chunk0 = static_cast<int>(seg * span / a.npieces);
+    nch = static_cast<int>((seg + 1) * span / a.npieces) - chunk0;
+    const int bnd = (chunk0 + a.seg_chunks - 1) / a.seg_chunks * a.seg_chunks;
+    if (bnd > chunk0 && bnd < chunk0 + nch) split = bnd - chunk0;
+  }
   if (nch <= 0) return;  // uniform across the workgroup
 
   const int64_t DD = static_cast<int64_t>(D) * D;
@@ -251,9 +267,9 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   const int col = 32 * wave + l32;
   if (wave < NCW) {
     const float* src = nullptr;
-    if (seg == 0)
+    if (READOUT && seg == 0)
       src = a.psi0 ? a.psi0 + bh * DD : nullptr;
-    else if (a.starts)
+    else if (READOUT && a.starts)
       src = a.starts + (static_cast<int64_t>(seg - 1) * a.BH + bh) * DD;
     if (src) {
 #pragma unroll
@@ -732,47 +748,62 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
     lds_barrier();  // (A)
   };
 
+  auto write_state = [&](float* dst) {
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        dst[(32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) * D + col] = psi[rt][r] * inv_s;
+  };
   typedef std::integral_constant<bool, true> yes;
   typedef std::integral_constant<bool, false> no;
   for (int cc = -NPW; cc < 0; ++cc) iteration(cc, no{});
-  for (int cc = 0; cc < nch; ++cc) iteration(cc, yes{});
-  if (READOUT) iteration(nch, no{});  // the readout waves' last iteration
-
-  // ---------------------------------------------------------------- end state
-  {
-    float* dst = nullptr;
-    if (a.end_mode == 0) dst = a.ends + (static_cast<int64_t>(seg) * a.BH + bh) * DD;
-    else if (seg == a.nseg - 1) dst = a.ends + bh * DD;
-    if (dst) {
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          dst[(32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) * D + col] = psi[rt][r] * inv_s;
-    }
+  if (READOUT) {
+    for (int cc = 0; cc < nch; ++cc) iteration(cc, yes{});
+    iteration(nch, no{});  // the readout waves' last iteration
+    if (seg == a.nseg - 1) write_state(a.ends + bh * DD);
+    return;
   }
+  // pass A: factor slots of this workgroup's parts
+  const int f0 = a.npieces > 0 ? (seg == 0 ? 0 : 2 * seg - 1) : seg;
+  const int n1 = split > 0 ? split : nch;
+  for (int cc = 0; cc < n1; ++cc) iteration(cc, yes{});
+  if (split > 0) {  // a segment starts here: store the part so far, restart from I
+    write_state(a.ends + (static_cast<int64_t>(f0) * a.BH + bh) * DD);
+    int colx = col;
+    asm volatile("" : "+v"(colx));  // keeps the identity pattern from being hoisted
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        psi[rt][r] = (32 * rt + 8 * (r >> 2) + 4 * g + (r & 3)) == colx ? 1.f : 0.f;
+    for (int cc = split; cc < nch; ++cc) iteration(cc, yes{});
+  }
+  write_state(a.ends + (static_cast<int64_t>(split > 0 ? 2 * seg : f0) * a.BH + bh) * DD);
 }
 
-// start_s = P_{s-1} start_{s-1}, s = 1 .. S-1, start_0 = psi0 (identity if null).
+// The segment start states: X = psi0 (identity if null), then X <- F_f X for the pass A
+// factors f = 0 .. nf-1 in order, storing start_s = X after every fstride-th factor
+// (fstride = 1: F_f = P_f; 2: F_2s, F_2s+1 are the two parts of segment s).
 // Left products act on the columns independently, so the chain of one sequence is
-// split over CARRY_SPLIT workgroups of CARRY_COLS columns each.  Every P_{s-1} is read
-// with coalesced loads (issued one product ahead) and staged in LDS as a bf16 hi + lo
-// pair; the running columns X are kept in LDS the same way (transposed).  Wave
-// (rb, ch) produces rows 32rb .. 32rb+31 and columns 32ch .. 32ch+31 of the workgroup's
-// block with bf16x3 MFMA (hi*hi + hi*lo + lo*hi, fp32-faithful).
+// split over CARRY_SPLIT workgroups of CARRY_COLS columns each.  Every factor is read
+// with coalesced loads two products ahead and staged in LDS as a bf16 hi + lo pair;
+// the running columns X are kept in LDS the same way (transposed).  Wave (rb, ch)
+// produces rows 32rb .. 32rb+31 and columns 32ch .. 32ch+31 of the workgroup's block
+// with bf16x3 MFMA (hi*hi + hi*lo + lo*hi, fp32-faithful).
 constexpr int CARRY_SPLIT = 2;
 constexpr int CARRY_COLS = D / CARRY_SPLIT;         // 64
 constexpr int CARRY_WAVES = (D / 32) * (CARRY_COLS / 32);  // 8
 constexpr int CARRY_NT = CARRY_WAVES * 64;
-constexpr int CP_LD = D + 8;   // bf16 per LDS row of P and of X^T (272 B)
-constexpr int CARRY_F4 = D * D / 4 / CARRY_NT;  // float4 of P per thread
+constexpr int CP_LD = D + 8;   // bf16 per LDS row of a factor and of X^T (272 B)
+constexpr int CARRY_F4 = D * D / 4 / CARRY_NT;  // float4 of a factor per thread
 
-__global__ __launch_bounds__(CARRY_NT) void sssd_carry_kernel(const float* psi0, const float* P,
-                                                              float* starts, int BH, int S) {
+__global__ __launch_bounds__(CARRY_NT) void sssd_carry_kernel(const float* psi0, const float* F,
+                                                              float* starts, int BH, int nf,
+                                                              int fstride) {
   typedef mfma_t<__bf16> MM;
   typedef MM::v8 V8;
-  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-  __shared__ __bf16 phi[D * CP_LD], plo[D * CP_LD];                    // P, row-major
+  __shared__ __bf16 phi[D * CP_LD], plo[D * CP_LD];                    // factor, row-major
   __shared__ __bf16 xhi[CARRY_COLS * CP_LD], xlo[CARRY_COLS * CP_LD];  // X^T: [n][k]
   const int bh = blockIdx.x, cb = blockIdx.y;
   const int tid = threadIdx.x;
@@ -789,16 +820,16 @@ __global__ __launch_bounds__(CARRY_NT) void sssd_carry_kernel(const float* psi0,
     const int row = e / CARRY_COLS, n = e - row * CARRY_COLS, colg = CARRY_COLS * cb + n;
     put(xhi, xlo, n * CP_LD + row, psi0 ? psi0[bh * DD + row * D + colg] : (row == colg ? 1.f : 0.f));
   }
-  float4 pf[CARRY_F4];  // this thread's share of the next P: float4 index tid + NT*m
-  auto fetch = [&](int s) {
-    const float4* src = reinterpret_cast<const float4*>(P + (static_cast<int64_t>(s - 1) * BH + bh) * DD);
+  typedef float4 Share[CARRY_F4];  // a thread's share of a factor: float4 index tid + NT*m
+  auto fetch = [&](Share& pf, int f) {
+    if (f >= nf) return;
+    const float4* src = reinterpret_cast<const float4*>(F + (static_cast<int64_t>(f) * BH + bh) * DD);
 #pragma unroll
     for (int m = 0; m < CARRY_F4; ++m) pf[m] = src[tid + CARRY_NT * m];
   };
-  if (S > 1) fetch(1);
-  for (int s = 1; s < S; ++s) {
+  auto step = [&](Share& pf, int f) {  // X <- F_f X
 #pragma unroll
-    for (int m = 0; m < CARRY_F4; ++m) {  // stage P_{s-1} as hi + lo (8-byte stores)
+    for (int m = 0; m < CARRY_F4; ++m) {  // stage F_f as hi + lo (8-byte stores)
       const int e = 4 * (tid + CARRY_NT * m);
       const int row = e / D, c0 = e - row * D;
       const float xv[4] = {pf[m].x, pf[m].y, pf[m].z, pf[m].w};
@@ -811,9 +842,9 @@ __global__ __launch_bounds__(CARRY_NT) void sssd_carry_kernel(const float* psi0,
       *reinterpret_cast<bf16x4*>(&phi[row * CP_LD + c0]) = h4;
       *reinterpret_cast<bf16x4*>(&plo[row * CP_LD + c0]) = l4;
     }
-    __syncthreads();  // P staged; X (initial or from the previous product) complete
-    if (s + 1 < S) fetch(s + 1);
-    // Y = P[32rb .. +31][:] X[:][32ch .. +31]; A row = l32, B column = l32, k-slots
+    __syncthreads();  // factor staged; X (initial or from the previous product) complete
+    fetch(pf, f + 2);
+    // Y = F[32rb .. +31][:] X[:][32ch .. +31]; A row = l32, B column = l32, k-slots
     // 16ks + 8g + 0..7 in both operands
     f32x16 Y = {};
 #pragma unroll
@@ -827,16 +858,34 @@ __global__ __launch_bounds__(CARRY_NT) void sssd_carry_kernel(const float* psi0,
       Y = MM::mma32(ah, bl8, Y);
       Y = MM::mma32(al, bh8, Y);
     }
-    __syncthreads();  // every wave has read P and X before they are replaced
+    __syncthreads();  // every wave has read the factor and X before they are replaced
     // Y: lane (g, l32) holds rows 32rb + 8(r/4) + 4g + r%4 of column 32ch + l32
     const int colw = 32 * ch + l32;
-    float* dst = starts + (static_cast<int64_t>(s - 1) * BH + bh) * DD + CARRY_COLS * cb + colw;
+    float* dst = (f + 1) % fstride == 0
+                     ? starts + (static_cast<int64_t>((f + 1) / fstride - 1) * BH + bh) * DD +
+                           CARRY_COLS * cb + colw
+                     : nullptr;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = 32 * rb + 8 * (r >> 2) + 4 * g + (r & 3);
-      dst[row * D] = Y[r];
-      put(xhi, xlo, colw * CP_LD + row, Y[r]);
+    for (int i = 0; i < 4; ++i) {  // rows 32rb + 8i + 4g + 0..3: 4 consecutive k of X^T
+      const int row0 = 32 * rb + 8 * i + 4 * g;
+      bf16x4 h4, l4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float y = Y[4 * i + r];
+        if (dst) dst[(row0 + r) * D] = y;
+        h4[r] = static_cast<__bf16>(y);
+        l4[r] = static_cast<__bf16>(y - static_cast<float>(h4[r]));
+      }
+      *reinterpret_cast<bf16x4*>(&xhi[colw * CP_LD + row0]) = h4;
+      *reinterpret_cast<bf16x4*>(&xlo[colw * CP_LD + row0]) = l4;
     }
+  };
+  Share p0, p1;
+  fetch(p0, 0);
+  fetch(p1, 1);
+  for (int f = 0; f < nf; f += 2) {
+    step(p0, f);
+    if (f + 1 < nf) step(p1, f + 1);
   }
 }
 
@@ -849,6 +898,9 @@ constexpr int kTargetWorkgroups = 256;  // one 5-wave workgroup per CU (LDS-limi
 
 struct Plan {
   int nchunks, seg_chunks, nseg;
+  int npieces;   // pass A workgroups per sequence (0: one per segment 0 .. nseg-2)
+  int nfactors;  // pass A transforms per sequence
+  int fstride;   // factors per segment
 };
 
 Plan make_plan(int64_t BH, int64_t T) {
@@ -860,6 +912,18 @@ Plan make_plan(int64_t BH, int64_t T) {
   if (S < 1) S = 1;
   p.seg_chunks = static_cast<int>((p.nchunks + S - 1) / S);
   p.nseg = (p.nchunks + p.seg_chunks - 1) / p.seg_chunks;
+  // Pass A covers segments 0 .. nseg-2.  Spread over nseg workgroups per sequence instead
+  // of nseg-1 it fills as many CUs as pass C; every segment then holds exactly one piece
+  // boundary (given seg_chunks >= 2 nseg) and contributes two factors to the carry.
+  if (p.nseg > 1 && p.seg_chunks >= 2 * p.nseg) {
+    p.npieces = p.nseg;
+    p.nfactors = 2 * (p.nseg - 1);
+    p.fstride = 2;
+  } else {
+    p.npieces = 0;
+    p.nfactors = p.nseg - 1;
+    p.fstride = 1;
+  }
   return p;
 }
 
@@ -879,8 +943,10 @@ hipError_t run_chunked(const void* q, const void* k, const void* v, const void* 
   a.T = T; a.H = H; a.BH = BH;
   a.seg_chunks = p.seg_chunks;
   a.nseg = p.nseg;
+  a.npieces = 0;
+  // workspace: pass A factors, then the segment start states
   float* P = static_cast<float*>(workspace);
-  float* starts = P ? P + static_cast<int64_t>(p.nseg - 1) * BH * DD : nullptr;
+  float* starts = P ? P + static_cast<int64_t>(p.nfactors) * BH * DD : nullptr;
   if (p.nseg > 1) {
     chunk::Args pa = a;
     pa.psi0 = nullptr;
@@ -888,13 +954,15 @@ hipError_t run_chunked(const void* q, const void* k, const void* v, const void* 
     pa.out = nullptr;
     pa.ends = P;
     pa.end_mode = 0;
-    hipLaunchKernelGGL((chunk::sssd_chunk_kernel<IO, DT, false>), dim3(BH, p.nseg - 1),
+    pa.npieces = p.npieces;
+    hipLaunchKernelGGL((chunk::sssd_chunk_kernel<IO, DT, false>),
+                       dim3(BH, p.npieces > 0 ? p.npieces : p.nseg - 1),
                        dim3(chunk::Cfg<false>::NT), 0, stream, pa);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(chunk::sssd_carry_kernel, dim3(BH, chunk::CARRY_SPLIT),
                        dim3(chunk::CARRY_NT), 0, stream,
-                       psi_in, P, starts, BH, p.nseg);
+                       psi_in, P, starts, BH, p.nfactors, p.fstride);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -914,7 +982,7 @@ size_t chunk_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int io_
   if (!chunk_path(T, D, io_dtype)) return 0;
   const Plan p = make_plan(B * H, T);
   if (p.nseg <= 1) return 0;
-  return static_cast<size_t>(2) * (p.nseg - 1) * B * H * D * D * sizeof(float);
+  return static_cast<size_t>(p.nfactors + p.nseg - 1) * B * H * D * D * sizeof(float);
 }
 
 bool use_chunk_path(int64_t T, int64_t D, int io_dtype) { return chunk_path(T, D, io_dtype); }
