@@ -20,12 +20,12 @@
 // state norm drifts as a random walk (~1e-6 over 65536 tokens, against 1e-4 allowed)
 // and the state stays within ~3e-4 of the exact recurrence at that length.
 //
-// Workgroup = 12 waves for one (batch*head, segment):
+// Workgroup = 10 (pass C) or 12 (pass A) waves for one (batch*head, segment):
 //   waves 0-3 (consumers) each own a 32-column slab of the fp32 state, held in
 //     MFMA accumulators for the whole segment; columns evolve independently, so
 //     W, Z and the update need no cross-wave traffic.  With the readout every wave
 //     also stashes its slab of S and Z (f16, transposed) in LDS.
-//   waves 4-7 (readout, pass C only) compute, from the stashes of chunk c-1, 32
+//   waves 4-5 (readout, pass C only) compute, from the stashes of chunk c-1, 64
 //     complete output rows each (transposing LDS loads, no reduction) while the
 //     consumers work on chunk c.
 //   the remaining 4 (pass C) or 8 (pass A) producer waves take chunks round-robin
@@ -58,12 +58,13 @@ constexpr int D = 128;
 constexpr int C = 16;           // tokens per chunk
 constexpr int R = 2 * C;        // rank rows per chunk
 constexpr int NCW = 4;          // consumer waves
-// Twelve waves (3 per SIMD, at most 168 VGPRs each).  Pass C: 4 consumers (the state),
-// 4 readout waves and 4 producers.  Pass A (no readout): 4 consumers and 8 producers,
-// whose latency-bound phases are then split over a pipeline twice as deep.
+// Up to 3 waves per SIMD (at most 168 VGPRs each).  Pass C: 4 consumers (the state),
+// 2 readout waves and 4 producers; two readout waves of 64 rows each compute Z Q half
+// as often as four of 32 rows and measured fastest.  Pass A (no readout): 4 consumers
+// and 8 producers, whose latency-bound phases are then split over a deeper pipeline.
 template <bool READOUT> struct Cfg {
   static constexpr int NPW = READOUT ? 4 : 8;
-  static constexpr int NRW = READOUT ? 4 : 0;  // readout waves
+  static constexpr int NRW = READOUT ? 2 : 0;  // readout waves (64 output rows each)
   static constexpr int NT = (NCW + NRW + NPW) * 64;
   static constexpr int NSCR = READOUT ? 2 : 8;  // producer scratch slots
 };
@@ -566,27 +567,29 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
     // ================================================ readout waves
     // Readout of chunk c in iteration c+1 (after barrier (A) of iteration c, which ends
     // the consumers' stash writes of chunk c): readout wave w computes the output rows
-    // d in [32w, 32w + 32) completely, so no cross-wave reduction is needed:
+    // d in [RWR w, RWR w + RWR) completely, so no cross-wave reduction is needed:
     //   O = S Q + U mask(Z Q)  restricted to those rows; S Q and Z Q contract over all
     //   128 state columns j (k-slot group g4 covers j = 32ks + 8pg + 0..7).
-    // Offsets: U rows rho = 16hh + 4g4 + i, features 32w + 16tl + 4r (transposing reads);
+    // Offsets: U rows rho = 16hh + 4g4 + i, features RWR w + 16tl + 4r (transposing reads);
     // q token l16, features 32ks + 8pg; stash rows j = 32ks + 8pg + 4hh + (l16 >> 2),
     // where j_slot(8pg + 4hh + i) = j_slot(8pg + i) + hh (stashes of chunk c in buffer c & 1).
+    constexpr int RWR = D / (NRW > 0 ? NRW : 1);  // output rows per readout wave
+    constexpr int TL = RWR / 16;                    // 16-row output tiles per readout wave
     const int rw = wave - NCW;
-    const int offO = rho_slot(4 * g4 + (l16 >> 2)) * U_LD + 32 * rw + 4 * (l16 & 3);
+    const int offO = rho_slot(4 * g4 + (l16 >> 2)) * U_LD + RWR * rw + 4 * (l16 & 3);
     const int offQ = Q_OFF + l16 * Q_LD + 8 * pg;
-    const E* const pst_rd = sm.pst[0] + j_slot(8 * pg + (l16 >> 2)) * PST_LD + 32 * rw + 4 * (l16 & 3);
+    const E* const pst_rd = sm.pst[0] + j_slot(8 * pg + (l16 >> 2)) * PST_LD + RWR * rw + 4 * (l16 & 3);
     const E* const zst_rd = sm.zst[0] + j_slot(8 * pg + (l16 >> 2)) * ZST_LD + 4 * (l16 & 3);
     auto readout = [&](int c) {
       const E* tb = sm.tok[c % 3];
       const E* const pst_c = pst_rd + (c & 1) * PST_BUF;
       const E* const zst_c = zst_rd + (c & 1) * ZST_BUF;
-      f32x4 O[2] = {}, Y[2] = {};
+      f32x4 O[TL] = {}, Y[2] = {};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const V8 bq = lds8<E>(tb + offQ + 32 * ks);
 #pragma unroll
-        for (int tl = 0; tl < 2; ++tl) {
+        for (int tl = 0; tl < TL; ++tl) {
           const E* p = pst_c + 32 * ks * PST_LD + 16 * tl;
           O[tl] = MM::mma16(lds_tr4x2<E>(p, p + PST_LD), bq, O[tl]);
         }
@@ -604,9 +607,9 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
         by[4 + r] = static_cast<E>(((16 + 4 * g4 + r) >> 1) <= l16 ? Y[1][r] : 0.f);
       }
 #pragma unroll
-      for (int tl = 0; tl < 2; ++tl)
+      for (int tl = 0; tl < TL; ++tl)
         O[tl] = MM::mma16(lds_tr4x2<E>(tb + offO + 16 * tl, tb + offO + U_LD + 16 * tl), by, O[tl]);
-      // lane (g4, t = l16) holds O[32 rw + 16 tl + 4 g4 + 0..3][t].  Stored through a
+      // lane (g4, t = l16) holds O[RWR rw + 16 tl + 4 g4 + 0..3][t].  Stored through a
       // buffer resource spanning this chunk's valid tokens: rows past the end of the
       // sequence fall outside it and the hardware drops them, so no branch is needed.
       const int t0 = (chunk0 + c) * C;
@@ -614,9 +617,9 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
       const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
           static_cast<IO*>(a.out) + tok_base + static_cast<int64_t>(t0) * tok_stride, (short)0,
           nvalid * static_cast<int>(tok_stride) * static_cast<int>(sizeof(IO)), 0x00020000);
-      const int ooff = (l16 * static_cast<int>(tok_stride) + 32 * rw + 4 * g4) * static_cast<int>(sizeof(IO));
+      const int ooff = (l16 * static_cast<int>(tok_stride) + RWR * rw + 4 * g4) * static_cast<int>(sizeof(IO));
 #pragma unroll
-      for (int tl = 0; tl < 2; ++tl) {
+      for (int tl = 0; tl < TL; ++tl) {
         typedef IO io4 __attribute__((ext_vector_type(4)));
         typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
         io4 o4;
