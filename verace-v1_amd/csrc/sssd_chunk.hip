@@ -108,8 +108,9 @@ struct PScratch {
   float4 mcoef[C];              // (m00, m01, m10, m11) per token
   float drow[4][64];            // diagonal 8x8 blocks of T~, row-major [a*8 + c]
   float dcol[4][64];            // the same blocks, column-major [b*8 + c]
-  float ocol[3][64];            // T~_10, T~_21, T~_20, column-major
-  float sblk[3][64];            // S = sum_m G_gm T~_mh, column-major
+  float ocol[64];               // T~_10, column-major
+  float orow[64];               // T~_32, row-major
+  float sblk[2][64];            // S = G_10 T~_00 and G_32 T~_22, column-major
 };
 
 template <typename E, bool READOUT>
@@ -303,10 +304,10 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   // With 4 producers:
   //   it = n-4  phase 0: global loads of k, v, q, delta into registers
   //   it = n-3  phase 1: Gram matrix (MFMA), Cayley blocks, diagonal blocks of T~
-  //   it = n-2  phase 2: off-diagonal blocks of T~ (kept in registers)
+  //   it = n-2  phase 2: off-diagonal blocks of T~ (kept in registers; the 16x16 block on MFMA)
   //   it = n-1  phase 3: k, v, q rows -> tok[n % 3], T~ (hi + lo) -> tt[n & 1]
-  // with 8 the same steps run as load, Gram + Cayley blocks, diagonal blocks, four
-  // off-diagonal steps and the write (it = n-8 .. n-1).
+  // with 8 the same steps run as load, Gram + Cayley blocks, diagonal blocks, three
+  // off-diagonal steps, an empty phase and the write (it = n-8 .. n-1).
   // tok[n % 3] last held chunk n-3, whose readout ended in iteration n-2, and tt[n & 1]
   // last held chunk n-2, so the write overwrites nothing still in use.  The scratch of
   // a chunk is pscr[n & 1] with 4 producers (chunk n+2, the next one to use it, starts
@@ -426,48 +427,60 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
     }
   };
 
-  // off-diagonal blocks T~_{g,h} = T~_{g,g} S, S = sum_{m=h}^{g-1} G_{g,m} T~_{m,h}, in four
-  // steps (each ends with LDS writes that the next one reads).  lane = element (ea, eb) of
-  // an 8x8 block; tv[] receives this lane's element of the blocks 00, 11, 22, 33, 10, 21,
-  // 32, 20, 31, 30.
+  // Off-diagonal blocks of T~, by composing the two 8-token halves.  With the 16x16
+  // diagonal blocks A = T~[0:16, 0:16] and B = T~[16:32, 16:32] (each itself
+  // [[T~_gg, 0], [T~_{g+1,g}, T~_{g+1,g+1}]] with T~_{g+1,g} = T~_{g+1,g+1} G_{g+1,g} T~_gg),
+  // the lower-left block is T~[16:32, 0:16] = B G[16:32, 0:16] A.
+  //   od_1a / od_1b: the 8x8 blocks T~_10 and T~_32 (lane = element (ea, eb); VALU dot
+  //     products through LDS); tv[] receives this lane's element of the blocks 00, 11, 22,
+  //     33, 10, 32.
+  //   od_c: the 16x16 block by two 16x16x16 products on the fp32 MFMA (exact fp32
+  //     products); cv[r] receives T~[16 + 4 g4 + r][l16].  k-slot s of lane group
+  //     kg = lane >> 4 is k = 4 kg + s in both products, so the first product's result
+  //     (lane (n, g4) holds rows 4 g4 + r of column n) is the second one's B operand as is.
   const int ea = lane >> 3, eb = lane & 7;
-  auto od_1a = [&](PScratch& P, float* tv) {  // S for (1,0), (2,1), (3,2)
+  auto od_1a = [&](PScratch& P, float* tv) {  // S for (1,0) and (3,2)
     const float* g1 = &P.gram[(8 + ea) * T_LD];
-    const float* g2 = &P.gram[(16 + ea) * T_LD];
     const float* g3 = &P.gram[(24 + ea) * T_LD];
 #pragma unroll
     for (int gb = 0; gb < 4; ++gb) tv[gb] = P.drow[gb][ea * 8 + eb];
     P.sblk[0][eb * 8 + ea] = dot8(g1, &P.dcol[0][eb * 8]);
-    P.sblk[1][eb * 8 + ea] = dot8(g2 + 8, &P.dcol[1][eb * 8]);
-    P.sblk[2][eb * 8 + ea] = dot8(g3 + 16, &P.dcol[2][eb * 8]);
+    P.sblk[1][eb * 8 + ea] = dot8(g3 + 16, &P.dcol[2][eb * 8]);
   };
-  auto od_1b = [&](PScratch& P, float* tv) {  // T~ (1,0), (2,1), (3,2)
+  auto od_1b = [&](PScratch& P, float* tv) {  // T~ (1,0) and (3,2)
     tv[4] = dot8(&P.drow[1][ea * 8], &P.sblk[0][eb * 8]);
-    tv[5] = dot8(&P.drow[2][ea * 8], &P.sblk[1][eb * 8]);
-    tv[6] = dot8(&P.drow[3][ea * 8], &P.sblk[2][eb * 8]);
-    P.ocol[0][eb * 8 + ea] = tv[4];
-    P.ocol[1][eb * 8 + ea] = tv[5];
+    tv[5] = dot8(&P.drow[3][ea * 8], &P.sblk[1][eb * 8]);
+    P.ocol[eb * 8 + ea] = tv[4];
+    P.orow[ea * 8 + eb] = tv[5];
   };
-  auto od_2 = [&](PScratch& P, float* tv) {  // (2,0), (3,1)
-    const float* g2 = &P.gram[(16 + ea) * T_LD];
-    const float* g3 = &P.gram[(24 + ea) * T_LD];
-    P.sblk[0][eb * 8 + ea] = dot8(g2, &P.dcol[0][eb * 8]) + dot8(g2 + 8, &P.ocol[0][eb * 8]);
-    P.sblk[1][eb * 8 + ea] = dot8(g3 + 8, &P.dcol[1][eb * 8]) + dot8(g3 + 16, &P.ocol[1][eb * 8]);
-    wave_sync();
-    tv[7] = dot8(&P.drow[2][ea * 8], &P.sblk[0][eb * 8]);
-    tv[8] = dot8(&P.drow[3][ea * 8], &P.sblk[1][eb * 8]);
-    P.ocol[2][eb * 8 + ea] = tv[7];
-  };
-  auto od_3 = [&](PScratch& P, float* tv) {  // (3,0)
-    const float* g3 = &P.gram[(24 + ea) * T_LD];
-    P.sblk[2][eb * 8 + ea] = dot8(g3, &P.dcol[0][eb * 8]) + dot8(g3 + 8, &P.ocol[0][eb * 8]) +
-                             dot8(g3 + 16, &P.ocol[2][eb * 8]);
-    wave_sync();
-    tv[9] = dot8(&P.drow[3][ea * 8], &P.sblk[2][eb * 8]);
+  auto od_c = [&](PScratch& P, float* cv) {
+    const int kg = g4;
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    // X = G[16:32, 0:16] A: A operand G[16 + l16][4kg + s]; B operand A[4kg + s][l16]
+    const f32x4 ga = *reinterpret_cast<const f32x4*>(&P.gram[(16 + l16) * T_LD + 4 * kg]);
+    const float* bs = kg < 2 ? &P.dcol[0][(l16 & 7) * 8 + 4 * kg]
+                             : (l16 < 8 ? &P.ocol[l16 * 8 + 4 * (kg - 2)]
+                                        : &P.dcol[1][(l16 - 8) * 8 + 4 * (kg - 2)]);
+    f32x4 bx = *reinterpret_cast<const f32x4*>(bs);
+    if (kg < 2 && l16 >= 8) bx = z4;  // upper-right block of A is zero
+    f32x4 X = z4;
+#pragma unroll
+    for (int si = 0; si < 4; ++si) X = __builtin_amdgcn_mfma_f32_16x16x4f32(ga[si], bx[si], X, 0, 0, 0);
+    // T~[16:32, 0:16] = B X: A operand B[l16][4kg + s]; B operand X (as computed)
+    const float* as = l16 < 8 ? &P.drow[2][l16 * 8 + 4 * (kg & 1)]
+                              : (kg < 2 ? &P.orow[(l16 - 8) * 8 + 4 * kg]
+                                        : &P.drow[3][(l16 - 8) * 8 + 4 * (kg - 2)]);
+    f32x4 ax = *reinterpret_cast<const f32x4*>(as);
+    if (l16 < 8 && kg >= 2) ax = z4;  // upper-right block of B is zero
+    f32x4 Cc = z4;
+#pragma unroll
+    for (int si = 0; si < 4; ++si) Cc = __builtin_amdgcn_mfma_f32_16x16x4f32(ax[si], X[si], Cc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) cv[r] = Cc[r];
   };
 
-  // phase 3: token-major k/v/q rows and T~ (16-bit hi + lo) for the consumers
-  auto p_write = [&](const Regs& r, int n, const float* tv) {
+  // the write: U and q rows, T~ (f16 hi + lo) for the consumers
+  auto p_write = [&](const Regs& r, int n, const float* tv, const float* cv) {
     E* tb = sm.tok[n % 3];
     E* tdst = tb + rho_slot(l32) * U_LD;
 #pragma unroll
@@ -479,25 +492,28 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
         *reinterpret_cast<uint4*>(tb + Q_OFF + (e >> 4) * Q_LD + 8 * (e & 15)) = to_f16x8<IO>(r.q[m]);
       }
     }
-    // T~ element (ea, eb) of each block as f16 hi + lo.  Lanes pair up (eb, eb ^ 1):
-    // the even lane writes the two hi parts, the odd lane the two lo parts, as one
-    // 32-bit store each (DPP swaps the parts between the two lanes).
-    const int ea = lane >> 3, eb = lane & 7;
-    const bool odd = eb & 1;
+    // T~ as f16 hi + lo.  Lanes pair up (lane, lane ^ 1) on adjacent columns: the even
+    // lane writes the two hi parts, the odd lane the two lo parts, as one 32-bit store
+    // each (DPP quad_perm(1, 0, 3, 2) swaps the parts between the two lanes).
+    const bool odd = lane & 1;
     uint32_t* const tw = reinterpret_cast<uint32_t*>(odd ? sm.ttl[n & 1] : sm.tth[n & 1]);
-    const int brow[10] = {0, 1, 2, 3, 1, 2, 3, 2, 3, 3};
-    const int bcol[10] = {0, 1, 2, 3, 0, 1, 2, 0, 1, 0};
-#pragma unroll
-    for (int i = 0; i < 10; ++i) {
-      const E hpart = static_cast<E>(tv[i]);
-      const E lpart = static_cast<E>(tv[i] - static_cast<float>(hpart));
+    auto put_pair = [&](float x, int row, int col_even) {
+      const E hpart = static_cast<E>(x);
+      const E lpart = static_cast<E>(x - static_cast<float>(hpart));
       const uint32_t hb = __builtin_bit_cast(uint16_t, hpart), lb = __builtin_bit_cast(uint16_t, lpart);
-      // quad_perm(1, 0, 3, 2): each lane receives its partner's value
       const uint32_t recv = static_cast<uint32_t>(
           __builtin_amdgcn_mov_dpp(static_cast<int>(odd ? hb : lb), 0xB1, 0xF, 0xF, false));
       const uint32_t word = odd ? (recv | (lb << 16)) : (hb | (recv << 16));
-      tw[((8 * brow[i] + ea) * TT_LD + 8 * bcol[i] + (eb & ~1)) >> 1] = word;
-    }
+      tw[(row * TT_LD + col_even) >> 1] = word;
+    };
+    // the 8x8 blocks 00, 11, 22, 33, 10, 32: element (ea, eb) of each
+    const int brow[6] = {0, 1, 2, 3, 1, 3};
+    const int bcol[6] = {0, 1, 2, 3, 0, 2};
+#pragma unroll
+    for (int i = 0; i < 6; ++i) put_pair(tv[i], 8 * brow[i] + ea, 8 * bcol[i] + (eb & ~1));
+    // T~[16:32, 0:16]: rows 16 + 4 g4 + r of column l16
+#pragma unroll
+    for (int r = 0; r < 4; ++r) put_pair(cv[r], 16 + 4 * g4 + r, l16 & ~1);
   };
 
   // Every iteration ends with one workgroup barrier (A).
@@ -506,7 +522,7 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
     // ================================================ producers
     const int p = wave - NCW - NRW;
     Regs r;
-    float tv[10];
+    float tv[6], cv[4];
     for (int it = -NPW; it <= last; ++it) {
       const int phase = (it - p + 2 * NPW) & (NPW - 1);
       const int n = it + NPW - phase;
@@ -524,11 +540,9 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
             wave_sync();
             od_1b(P, tv);
             wave_sync();
-            od_2(P, tv);
-            wave_sync();
-            od_3(P, tv);
+            od_c(P, cv);
           } else {
-            p_write(r, n, tv);
+            p_write(r, n, tv, cv);
           }
         } else {
           if (phase == 0) p_load(r, n);
@@ -536,9 +550,8 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
           else if (phase == 2) p_diag(P);
           else if (phase == 3) od_1a(P, tv);
           else if (phase == 4) od_1b(P, tv);
-          else if (phase == 5) od_2(P, tv);
-          else if (phase == 6) od_3(P, tv);
-          else p_write(r, n, tv);
+          else if (phase == 5) od_c(P, cv);
+          else if (phase == 7) p_write(r, n, tv, cv);
         }
       }
       lds_barrier();  // (A)
