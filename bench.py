@@ -163,6 +163,110 @@ def bench_decode(device):
     }
 
 
+def bench_decode_cache(device, branches=4, tokens=64):
+    """DEC through the decode state cache (vmi_state_cache_step, prebuilt arguments).
+
+    steady: the 12 x 256 steps of bench_decode with the states in cache slots (every
+    handle the sole holder of its slot, so in place), timed the same way.
+    tree: tree-search decoding as hyper_generate.py:97-121 does it, for all 64 sequences
+    at once: per token every sequence forks `branches` handles, the 64 * branches
+    branches step through the 12 layers (each branch reads its parent's slot and writes
+    its own: copy-on-write inside the step), one branch per sequence is kept and the
+    parents and the other branches are released.  Timed per token (12 launches of
+    64 * branches items, plus the host bookkeeping between them).
+    """
+    import ctypes
+    import numpy as np
+    import torch
+    from verace_amd import SSSDStateCache, _lib
+    B, H, D, L, S = DEC["B"], DEC["H"], DEC["D"], DEC["layers"], DEC["steps"]
+    g = torch.Generator().manual_seed(1)
+    cache = SSSDStateCache(L, B * (branches + 2), H, D, device=device)
+    seqs = cache.new(B)
+    for l in range(L):
+        cache.write(l, seqs, torch.linalg.qr(torch.randn(B, H, D, D, generator=g))[0].to(device))
+    _, dev = make_inputs(B, S, H, D, seed=3, dtype=torch.bfloat16, device=device)
+    _, dev_tree = make_inputs(B * branches, tokens, H, D, seed=4, dtype=torch.bfloat16,
+                              device=device)
+    lib = _lib.load()
+    code = _lib.dtype_code(torch.bfloat16)
+    stream = torch.cuda.current_stream(device)
+    sh = _lib.stream_handle(device)
+    vp = ctypes.c_void_p
+    i64p = ctypes.POINTER(ctypes.c_int64)
+    call = lib.vmi_state_cache_step
+    hcache = cache.table._h
+
+    def slices(src, t):
+        return tuple(x[:, t:t + 1].contiguous() for x in src)
+
+    # steady state: B handles, in place
+    hs = np.asarray(seqs, dtype=np.int64)
+    steps = [slices(dev, t) for t in range(S)]
+    outs = [torch.empty_like(steps[0][0]) for _ in range(L)]
+    args = [[(hcache, l, hs.ctypes.data_as(i64p), B, vp(qq.data_ptr()), vp(kk.data_ptr()),
+              vp(vv.data_ptr()), vp(dd.data_ptr()), code, code, vp(outs[l].data_ptr()), sh)
+             for l in range(L)] for (qq, kk, vv, dd) in steps]
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(S + 1)]
+    ev[0].record(stream)
+    for t in range(S):
+        for a in args[t]:
+            st = call(*a)
+            if st != 0:
+                raise RuntimeError(f"vmi_state_cache_step failed: {st}")
+        ev[t + 1].record(stream)
+    torch.cuda.synchronize()
+    per_step = [ev[t].elapsed_time(ev[t + 1]) * 1000.0 for t in range(S)]
+    steady = {
+        "layer_step_us_median": round(statistics.median(per_step) / L, 3),
+        "layers12_step_us_median": round(statistics.median(per_step), 3),
+    }
+
+    # tree search: fork, step all branches through the 12 layers, keep one per sequence
+    nb = B * branches
+    tok = [slices(dev_tree, t) for t in range(tokens)]
+    touts = [torch.empty_like(tok[0][0]) for _ in range(L)]
+    rng = np.random.default_rng(0)
+    live = list(seqs)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(tokens + 1)]
+    ev[0].record(stream)
+    for t in range(tokens):
+        kids = np.asarray([c for p in live for c in cache.fork(p, branches)], dtype=np.int64)
+        qq, kk, vv, dd = tok[t]
+        for l in range(L):
+            st = call(hcache, l, kids.ctypes.data_as(i64p), nb, vp(qq.data_ptr()),
+                      vp(kk.data_ptr()), vp(vv.data_ptr()), vp(dd.data_ptr()), code, code,
+                      vp(touts[l].data_ptr()), sh)
+            if st != 0:
+                raise RuntimeError(f"vmi_state_cache_step failed: {st}")
+        keep = kids.reshape(B, branches)[np.arange(B), rng.integers(0, branches, B)]
+        kept = set(keep.tolist())
+        drop = [int(h) for h in kids if int(h) not in kept] + live
+        cache.release(drop)
+        live = keep.tolist()
+        ev[t + 1].record(stream)
+    torch.cuda.synchronize()
+    per_tok = [ev[t].elapsed_time(ev[t + 1]) * 1000.0 for t in range(tokens)]
+    med = statistics.median(per_tok)
+    nrm = torch.linalg.vector_norm(cache.read(L - 1, live).reshape(B, H, -1), dim=-1)
+    drift = float((nrm / D ** 0.5 - 1).abs().max())
+    return {
+        "config": f"B=64 H=8 D=128 bf16 io, 12 layers, states in an [L, N, H, D, D] cache",
+        "steady": steady,
+        "tree": {
+            "branches": branches,
+            "items_per_launch": nb,
+            "token_us_median": round(med, 3),
+            "layer_us_median": round(med / L, 3),
+            "algorithmic_bytes_per_layer": algorithmic_bytes_step(nb, H, D),
+            "hbm_frac_per_layer": round(algorithmic_bytes_step(nb, H, D) / (med / L * 1e-6)
+                                        / (HBM_PEAK_GBS * 1e9), 4),
+            "state_norm_drift_max": drift,
+        },
+    }
+
+
 def cpu_baseline(target_seconds=12.0):
     """The oracle's fp32 restatement of the reference's eager path (oracle/sssd_eager.py),
     timed on the host on a bounded prefix of the OP workload, T chunked by 256."""
@@ -312,6 +416,7 @@ def main():
         del src, dst
     if not args.no_decode:
         result["decode"] = bench_decode(device)
+        result["decode_cache"] = bench_decode_cache(device)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

@@ -50,7 +50,8 @@ enum vmi_status {
   VMI_ERR_UNSUPPORTED = 2,     /* head_dim / dtype combination not built */
   VMI_ERR_WORKSPACE = 3,       /* workspace missing or too small */
   VMI_ERR_ALIAS = 4,           /* forbidden aliasing between buffers */
-  VMI_ERR_HIP = 5              /* a HIP runtime call failed (see vmi_last_hip_error) */
+  VMI_ERR_HIP = 5,             /* a HIP runtime call failed (see vmi_last_hip_error) */
+  VMI_ERR_FULL = 6             /* a state cache layer has no free slot left */
 };
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -97,6 +98,63 @@ int vmi_sssd_step_inplace(const void* q, const void* k, const void* v,
                           const void* delta, int io_dtype, int delta_dtype,
                           float* psi, void* out,
                           int64_t B, int64_t H, int64_t D, void* stream);
+
+/* One decode step over the slots of a state cache (copy-on-write decode):
+ *   item b reads state slot in_slot[b] (or the identity when in_slot[b] == -1),
+ *   writes R * state to slot out_slot[b], and out[b] = (R * state) q[b].
+ * Replaces the per-item incremental forward of acd_engine.py:102-126 and the
+ * branch fan-out of hyper_generate.py:97-121, which call sssd_attention.py:103-182
+ * at seq_len 1 with a state taken from layer_states[l][i] and store the fresh
+ * state back: here a branch reads its parent's slot and writes its own, so a
+ * fork costs no copy.
+ *   states: [num_slots, H, D, D] float32, one layer's pool (read and written);
+ *   in_slot, out_slot: [B] int32 device arrays;
+ *   q, k, v, out: [B, 1, H, D]; delta: [B, 1, H].
+ * Out slots must be distinct, and an out slot may be read by no item other than
+ * its own (in_slot[b] == out_slot[b] updates in place).  Indexes outside
+ * [0, num_slots) read as the identity (in) or drop the state write (out). */
+int vmi_sssd_step_slots(const void* q, const void* k, const void* v,
+                        const void* delta, int io_dtype, int delta_dtype,
+                        float* states, int64_t num_slots,
+                        const int32_t* in_slot, const int32_t* out_slot, void* out,
+                        int64_t B, int64_t H, int64_t D, void* stream);
+
+/* ---- Decode state cache (copy-on-write branches) ---------------------------
+ * Replaces the reference's per-item decode state threading: layer_states[l][i] =
+ * (sssd_state, ...) lists stepped one item at a time (acd_engine.py:85-126) and
+ * copied per tree-search branch (hyper_generate.py:97-121).  The caller allocates
+ * the device pool [num_layers, num_slots, H, D, D] float32; the cache object (host
+ * memory only) maps sequence handles to slots with reference counts:
+ *   new      handles starting from the identity (no slot until first written);
+ *   fork     handles sharing every layer's slot with a parent (no copy);
+ *   step     one batched decode step of a layer: one launch (several above 256
+ *            items); a sole holder is updated in place, a handle on a shared slot
+ *            (or none) reads it and writes a fresh slot;
+ *   plan     the same slot decisions without a launch (for whole-state writes,
+ *            e.g. prefill results, which the caller copies into dst slots);
+ *   slots    current slot of each handle (-1 = identity), for reads;
+ *   release  drops handles; slots nobody holds return to their layer's free list.
+ * Handle ids of released handles are reused.  Not thread-safe: one host thread per
+ * cache; the steps of one cache must be ordered on one stream.  A failed step
+ * (status != VMI_OK after planning) leaves the states of its handles undefined. */
+typedef struct vmi_state_cache vmi_state_cache;
+int vmi_state_cache_create(int64_t num_layers, int64_t num_slots, int64_t H, int64_t D,
+                           float* pool, vmi_state_cache** cache);
+int vmi_state_cache_destroy(vmi_state_cache* cache);
+int vmi_state_cache_new(vmi_state_cache* cache, int64_t n, int64_t* handles);
+int vmi_state_cache_fork(vmi_state_cache* cache, int64_t parent, int64_t n, int64_t* handles);
+int vmi_state_cache_release(vmi_state_cache* cache, const int64_t* handles, int64_t n);
+int vmi_state_cache_plan(vmi_state_cache* cache, int64_t layer, const int64_t* handles,
+                         int64_t n, int32_t* src_slots, int32_t* dst_slots);
+int vmi_state_cache_slots(vmi_state_cache* cache, int64_t layer, const int64_t* handles,
+                          int64_t n, int32_t* slots);
+int vmi_state_cache_refs(vmi_state_cache* cache, int64_t layer, int32_t* refs,
+                         int64_t* free_slots);
+/* q, k, v, out: [n, 1, H, D] io_dtype; delta: [n, 1, H]; item b continues handles[b]. */
+int vmi_state_cache_step(vmi_state_cache* cache, int64_t layer, const int64_t* handles,
+                         int64_t n, const void* q, const void* k, const void* v,
+                         const void* delta, int io_dtype, int delta_dtype, void* out,
+                         void* stream);
 
 /* Newton-Schulz unitary retraction of a batch of complex matrices
  * H = Hr + i Hi, `steps` iterations of H <- 0.5 H (3I - H^H H), both halves

@@ -68,4 +68,13 @@ def test_argument_errors_before_any_device_call(lib):
     assert lib.vmi_sssd_scan_fwd(big, big, big, big, 1, 1, big, None, big,
                                  1, 4, 1, 16, None, 0, None) == 4
     assert lib.vmi_sssd_step_inplace(None, None, None, None, 1, 1, None, None, 1, 1, 16, None) == 1
+    assert lib.vmi_sssd_step_slots(None, None, None, None, 1, 1, None, 4, None, None, None,
+                                   1, 1, 16, None) == 1
+    assert lib.vmi_sssd_step_slots(big, big, big, big, 1, 1, big, -1, big, big, big,
+                                   1, 1, 16, None) == 1
+    assert lib.vmi_sssd_step_slots(big, big, big, big, 1, 1, big, 4, big, big, big,
+                                   1, 1, 512, None) == 2
+    # an empty batch is a no-op that touches nothing
+    assert lib.vmi_sssd_step_slots(None, None, None, None, 1, 1, None, 0, None, None, None,
+                                   0, 8, 128, None) == 0
     assert lib.vmi_cham_ns_retraction(None, None, None, None, 1, 4, 3, None, 0, None) == 1

@@ -4,14 +4,20 @@
 #include "vmi_dispatch.h"
 
 namespace {
-
 thread_local int g_last_hip_error = 0;
+}  // namespace
 
+namespace vmi {
 int hip_status(hipError_t e) {
   if (e == hipSuccess) return VMI_OK;
   g_last_hip_error = static_cast<int>(e);
   return VMI_ERR_HIP;
 }
+}  // namespace vmi
+
+namespace {
+
+using vmi::hip_status;
 
 bool valid_dtype(int dt) { return dt == VMI_F32 || dt == VMI_BF16 || dt == VMI_F16; }
 
@@ -35,6 +41,7 @@ const char* vmi_status_string(int status) {
     case VMI_ERR_WORKSPACE: return "workspace missing or too small";
     case VMI_ERR_ALIAS: return "forbidden aliasing between buffers";
     case VMI_ERR_HIP: return "HIP runtime error";
+    case VMI_ERR_FULL: return "state cache layer full";
     default: return "unknown status";
   }
 }
@@ -86,10 +93,34 @@ int vmi_sssd_step_inplace(const void* q, const void* k, const void* v, const voi
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (vmi::use_step128(1, D))
     return hip_status(vmi::launch_sssd_step128(q, k, v, delta, io_dtype, delta_dtype, psi, out, psi,
-                                               static_cast<int>(B * H), s));
+                                               static_cast<int>(B),
+                                               static_cast<int>(H), s));
   return hip_status(vmi::launch_sssd_seq(q, k, v, delta, io_dtype, delta_dtype, psi, out, psi,
                                          static_cast<int>(B), 1, static_cast<int>(H),
                                          static_cast<int>(D), s));
+}
+
+int vmi_sssd_step_slots(const void* q, const void* k, const void* v, const void* delta,
+                        int io_dtype, int delta_dtype, float* states, int64_t num_slots,
+                        const int32_t* in_slot, const int32_t* out_slot, void* out, int64_t B,
+                        int64_t H, int64_t D, void* stream) {
+  if (!valid_dtype(io_dtype) || !valid_dtype(delta_dtype)) return VMI_ERR_INVALID_ARG;
+  if (B < 0 || H < 0 || D < 1 || num_slots < 0) return VMI_ERR_INVALID_ARG;
+  if (D > 256) return VMI_ERR_UNSUPPORTED;
+  if (B * H > INT32_MAX || num_slots > INT32_MAX) return VMI_ERR_INVALID_ARG;
+  if (B == 0 || H == 0) return VMI_OK;
+  if (states == nullptr || in_slot == nullptr || out_slot == nullptr || out == nullptr ||
+      q == nullptr || k == nullptr || v == nullptr || delta == nullptr)
+    return VMI_ERR_INVALID_ARG;
+  const vmi::StateMap map = {in_slot, out_slot, static_cast<int>(num_slots)};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (vmi::use_step128(1, D))
+    return hip_status(vmi::launch_sssd_step128(q, k, v, delta, io_dtype, delta_dtype, states, out,
+                                               states, map, static_cast<int>(B),
+                                               static_cast<int>(H), s));
+  return hip_status(vmi::launch_sssd_seq(q, k, v, delta, io_dtype, delta_dtype, states, out,
+                                         states, static_cast<int>(B), 1, static_cast<int>(H),
+                                         static_cast<int>(D), s, map));
 }
 
 int vmi_cham_ns_workspace_bytes(int64_t batch, int64_t n, size_t* bytes) {

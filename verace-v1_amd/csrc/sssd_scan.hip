@@ -21,8 +21,8 @@ hipError_t dispatch_scan(const void* q, const void* k, const void* v, const void
     return launch_sssd_chunked(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, B, T,
                                H, workspace, stream);
   if (use_step128(T, D))
-    return launch_sssd_step128(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, B * H,
-                               stream);
+    return launch_sssd_step128(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out,
+                               B, H, stream);
   return launch_sssd_seq(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, B, T, H, D,
                          stream);
 }

@@ -17,6 +17,7 @@
 // One workgroup barrier per token.  The next token's q/k/v are staged into a
 // second LDS buffer while the current one is processed.
 #include "vmi_common.h"
+#include "vmi_dispatch.h"
 
 namespace vmi {
 
@@ -29,11 +30,11 @@ struct seq_cfg {
   static_assert(RPT * 2 == CG, "reduce-scatter layout needs RPT == CG/2");
 };
 
-template <typename IO, int DMAX>
+template <typename IO, int DMAX, typename Map>
 __global__ __launch_bounds__(seq_cfg<DMAX>::NT) void sssd_seq_kernel(
     const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
     const void* __restrict__ delta, int delta_dtype, const float* psi_in,
-    IO* __restrict__ out, float* psi_out, int T, int H, int D) {
+    IO* __restrict__ out, float* psi_out, Map map, int T, int H, int D) {
   using C = seq_cfg<DMAX>;
   constexpr int CG = C::CG, RG = C::RG, RPT = C::RPT, NT = C::NT;
 
@@ -44,6 +45,8 @@ __global__ __launch_bounds__(seq_cfg<DMAX>::NT) void sssd_seq_kernel(
   const int b = bh / H;
   const int h = bh - b * H;
   const int64_t DD = static_cast<int64_t>(D) * D;
+  const int64_t si = psi_in != nullptr ? map.in_index(bh, H) : -1;  // < 0: identity
+  const int64_t di = map.out_index(bh, H);                         // < 0: no state write
 
   // staged token: q, k, v (fp32) and delta; double buffered
   __shared__ float s_tok[2][3][DMAX];
@@ -60,8 +63,8 @@ __global__ __launch_bounds__(seq_cfg<DMAX>::NT) void sssd_seq_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) psi[m][j] = 0.0f;
     if (r < D) {
-      if (psi_in != nullptr) {
-        const float* src = psi_in + bh * DD + static_cast<int64_t>(r) * D;
+      if (si >= 0) {
+        const float* src = psi_in + si * DD + static_cast<int64_t>(r) * D;
         if ((D & 3) == 0 && c0 < D) {
           const float4 x = *reinterpret_cast<const float4*>(src + c0);
           psi[m][0] = x.x; psi[m][1] = x.y; psi[m][2] = x.z; psi[m][3] = x.w;
@@ -219,8 +222,8 @@ __global__ __launch_bounds__(seq_cfg<DMAX>::NT) void sssd_seq_kernel(
 #pragma unroll
   for (int m = 0; m < RPT; ++m) {
     const int r = rg + RG * m;
-    if (r < D) {
-      float* dst = psi_out + bh * DD + static_cast<int64_t>(r) * D;
+    if (r < D && (!Map::kSlotted || di >= 0)) {
+      float* dst = psi_out + di * DD + static_cast<int64_t>(r) * D;
       if ((D & 3) == 0 && c0 < D) {
         *reinterpret_cast<float4*>(dst + c0) = make_float4(psi[m][0], psi[m][1], psi[m][2], psi[m][3]);
       } else {
@@ -233,45 +236,67 @@ __global__ __launch_bounds__(seq_cfg<DMAX>::NT) void sssd_seq_kernel(
 }
 
 // Host-side launcher: picks the smallest DMAX >= D.
-template <typename IO>
-hipError_t launch_sssd_seq_typed(const IO* q, const IO* k, const IO* v, const void* delta,
-                                 int delta_dtype, const float* psi_in, IO* out, float* psi_out,
-                                 int B, int T, int H, int D, hipStream_t stream) {
+template <typename IO, typename Map>
+hipError_t launch_sssd_seq_typed(const void* q, const void* k, const void* v, const void* delta,
+                                 int delta_dtype, const float* psi_in, void* out, float* psi_out,
+                                 int B, int T, int H, int D, hipStream_t stream, const Map& map) {
   const dim3 grid(B * H);
+  const IO* qq = static_cast<const IO*>(q);
+  const IO* kk = static_cast<const IO*>(k);
+  const IO* vv = static_cast<const IO*>(v);
+  IO* oo = static_cast<IO*>(out);
   if (D <= 32) {
-    hipLaunchKernelGGL((sssd_seq_kernel<IO, 32>), grid, dim3(seq_cfg<32>::NT), 0, stream, q, k, v,
-                       delta, delta_dtype, psi_in, out, psi_out, T, H, D);
+    hipLaunchKernelGGL((sssd_seq_kernel<IO, 32, Map>), grid, dim3(seq_cfg<32>::NT), 0, stream, qq,
+                       kk, vv, delta, delta_dtype, psi_in, oo, psi_out, map, T, H, D);
   } else if (D <= 64) {
-    hipLaunchKernelGGL((sssd_seq_kernel<IO, 64>), grid, dim3(seq_cfg<64>::NT), 0, stream, q, k, v,
-                       delta, delta_dtype, psi_in, out, psi_out, T, H, D);
+    hipLaunchKernelGGL((sssd_seq_kernel<IO, 64, Map>), grid, dim3(seq_cfg<64>::NT), 0, stream, qq,
+                       kk, vv, delta, delta_dtype, psi_in, oo, psi_out, map, T, H, D);
   } else if (D <= 128) {
-    hipLaunchKernelGGL((sssd_seq_kernel<IO, 128>), grid, dim3(seq_cfg<128>::NT), 0, stream, q, k,
-                       v, delta, delta_dtype, psi_in, out, psi_out, T, H, D);
+    hipLaunchKernelGGL((sssd_seq_kernel<IO, 128, Map>), grid, dim3(seq_cfg<128>::NT), 0, stream,
+                       qq, kk, vv, delta, delta_dtype, psi_in, oo, psi_out, map, T, H, D);
   } else {
-    hipLaunchKernelGGL((sssd_seq_kernel<IO, 256>), grid, dim3(seq_cfg<256>::NT), 0, stream, q, k,
-                       v, delta, delta_dtype, psi_in, out, psi_out, T, H, D);
+    hipLaunchKernelGGL((sssd_seq_kernel<IO, 256, Map>), grid, dim3(seq_cfg<256>::NT), 0, stream,
+                       qq, kk, vv, delta, delta_dtype, psi_in, oo, psi_out, map, T, H, D);
   }
   return hipGetLastError();
+}
+
+template <typename Map>
+hipError_t launch_seq_map(const void* q, const void* k, const void* v, const void* delta,
+                          int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                          float* psi_out, int B, int T, int H, int D, hipStream_t stream,
+                          const Map& map) {
+  if (io_dtype == VMI_F32)
+    return launch_sssd_seq_typed<float, Map>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, B,
+                                             T, H, D, stream, map);
+  if (io_dtype == VMI_BF16)
+    return launch_sssd_seq_typed<bf16_t, Map>(q, k, v, delta, delta_dtype, psi_in, out, psi_out,
+                                              B, T, H, D, stream, map);
+  return launch_sssd_seq_typed<f16_t, Map>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, B,
+                                           T, H, D, stream, map);
 }
 
 hipError_t launch_sssd_seq(const void* q, const void* k, const void* v, const void* delta,
                            int io_dtype, int delta_dtype, const float* psi_in, void* out,
                            float* psi_out, int B, int T, int H, int D, hipStream_t stream) {
-  switch (io_dtype) {
-    case VMI_F32:
-      return launch_sssd_seq_typed<float>(static_cast<const float*>(q), static_cast<const float*>(k),
-                                          static_cast<const float*>(v), delta, delta_dtype, psi_in,
-                                          static_cast<float*>(out), psi_out, B, T, H, D, stream);
-    case VMI_BF16:
-      return launch_sssd_seq_typed<bf16_t>(
-          static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
-          static_cast<const bf16_t*>(v), delta, delta_dtype, psi_in, static_cast<bf16_t*>(out),
-          psi_out, B, T, H, D, stream);
-    default:
-      return launch_sssd_seq_typed<f16_t>(
-          static_cast<const f16_t*>(q), static_cast<const f16_t*>(k), static_cast<const f16_t*>(v),
-          delta, delta_dtype, psi_in, static_cast<f16_t*>(out), psi_out, B, T, H, D, stream);
-  }
+  return launch_seq_map(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, B, T, H, D,
+                        stream, DenseStates{});
+}
+
+hipError_t launch_sssd_seq(const void* q, const void* k, const void* v, const void* delta,
+                           int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                           float* psi_out, int B, int T, int H, int D, hipStream_t stream,
+                           const StateMap& map) {
+  return launch_seq_map(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, B, T, H, D,
+                        stream, map);
+}
+
+hipError_t launch_sssd_seq(const void* q, const void* k, const void* v, const void* delta,
+                           int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                           float* psi_out, int B, int T, int H, int D, hipStream_t stream,
+                           const SlotArgs& map) {
+  return launch_seq_map(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, B, T, H, D,
+                        stream, map);
 }
 
 }  // namespace vmi

@@ -19,6 +19,9 @@
 //   Psi += k alpha + v beta      alpha, beta from vmi::cayley_coeffs
 //   o = Psi q                    row partials reduce-scattered over the 32 lanes
 //                                that share a row group
+// Where a head's state is read and written is the Map template parameter
+// (vmi_dispatch.h): the dense [B, H, D, D] layout, or slots of a decode state cache
+// (state_cache.hip), which may differ between read and write (copy-on-write).
 #include "vmi_common.h"
 #include "vmi_dispatch.h"
 
@@ -29,11 +32,11 @@ constexpr int D = 128;
 constexpr int NT = 256;
 constexpr int RPT = 16;  // rows per thread
 
-template <typename IO>
+template <typename IO, typename Map>
 __global__ __launch_bounds__(NT) void sssd_step128_kernel(
     const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
     const void* __restrict__ delta, int delta_dtype, const float* psi_in, IO* __restrict__ out,
-    float* psi_out, int BH) {
+    float* psi_out, Map map, int BH, int H) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -52,8 +55,9 @@ __global__ __launch_bounds__(NT) void sssd_step128_kernel(
   float tk0 = 0.f, tk1 = 0.f, tdl = 0.f;
 
   auto load_state = [&](float4* st, int bh) {
-    if (psi_in != nullptr) {
-      const float* src = psi_in + bh * DD + c0;
+    const int64_t si = psi_in != nullptr ? map.in_index(bh, H) : -1;  // uniform; < 0: identity
+    if (si >= 0) {
+      const float* src = psi_in + si * DD + c0;
 #pragma unroll
       for (int m = 0; m < RPT; ++m) st[m] = *reinterpret_cast<const float4*>(src + (rg + 8 * m) * D);
     } else {
@@ -134,7 +138,8 @@ __global__ __launch_bounds__(NT) void sssd_step128_kernel(
     const float4 be = make_float4(fmaf(M.m10, a4.x, M.m11 * b4.x), fmaf(M.m10, a4.y, M.m11 * b4.y),
                                   fmaf(M.m10, a4.z, M.m11 * b4.z), fmaf(M.m10, a4.w, M.m11 * b4.w));
     // update, store, and row partials of o = Psi' q
-    float* dst = psi_out + bh * DD + c0;
+    const int64_t di = map.out_index(bh, H);  // uniform; < 0 (slotted maps only): not written
+    float* dst = psi_out + (di < 0 ? 0 : di) * DD + c0;
     float po[RPT];
 #pragma unroll
     for (int m = 0; m < RPT; ++m) {
@@ -143,7 +148,7 @@ __global__ __launch_bounds__(NT) void sssd_step128_kernel(
       x.y = fmaf(kr[m], al.y, fmaf(vr[m], be.y, x.y));
       x.z = fmaf(kr[m], al.z, fmaf(vr[m], be.z, x.z));
       x.w = fmaf(kr[m], al.w, fmaf(vr[m], be.w, x.w));
-      *reinterpret_cast<float4*>(dst + (rg + 8 * m) * D) = x;
+      if (!Map::kSlotted || di >= 0) *reinterpret_cast<float4*>(dst + (rg + 8 * m) * D) = x;
       po[m] = fmaf(x.x, qc.x, fmaf(x.y, qc.y, fmaf(x.z, qc.z, x.w * qc.w)));
     }
     // reduce-scatter po[] over the 32 lanes (cg) of this half-wave: after the
@@ -197,18 +202,36 @@ __global__ __launch_bounds__(NT) void sssd_step128_kernel(
   }
 }
 
-template <typename IO>
-hipError_t launch_typed(const IO* q, const IO* k, const IO* v, const void* delta, int delta_dtype,
-                        const float* psi_in, IO* out, float* psi_out, int BH, hipStream_t stream) {
+template <typename IO, typename Map>
+hipError_t launch_typed(const void* q, const void* k, const void* v, const void* delta,
+                        int delta_dtype, const float* psi_in, void* out, float* psi_out,
+                        const Map& map, int BH, int H, hipStream_t stream) {
   int dev = 0, cus = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
   const int grid = BH < cus ? BH : cus;
-  hipLaunchKernelGGL(sssd_step128_kernel<IO>, dim3(grid), dim3(NT), 0, stream, q, k, v, delta,
-                     delta_dtype, psi_in, out, psi_out, BH);
+  hipLaunchKernelGGL((sssd_step128_kernel<IO, Map>), dim3(grid), dim3(NT), 0, stream,
+                     static_cast<const IO*>(q), static_cast<const IO*>(k),
+                     static_cast<const IO*>(v), delta, delta_dtype, psi_in, static_cast<IO*>(out),
+                     psi_out, map, BH, H);
   return hipGetLastError();
+}
+
+template <typename Map>
+hipError_t launch_map(const void* q, const void* k, const void* v, const void* delta, int io_dtype,
+                      int delta_dtype, const float* psi_in, void* out, float* psi_out,
+                      const Map& map, int B, int H, hipStream_t stream) {
+  const int BH = B * H;
+  if (io_dtype == VMI_F32)
+    return launch_typed<float, Map>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, map, BH, H,
+                                    stream);
+  if (io_dtype == VMI_BF16)
+    return launch_typed<bf16_t, Map>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, map, BH,
+                                     H, stream);
+  return launch_typed<f16_t, Map>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, map, BH, H,
+                                  stream);
 }
 
 }  // namespace step
@@ -217,21 +240,25 @@ bool use_step128(int64_t T, int64_t D) { return T == 1 && D == step::D; }
 
 hipError_t launch_sssd_step128(const void* q, const void* k, const void* v, const void* delta,
                                int io_dtype, int delta_dtype, const float* psi_in, void* out,
-                               float* psi_out, int BH, hipStream_t stream) {
-  switch (io_dtype) {
-    case VMI_F32:
-      return step::launch_typed<float>(static_cast<const float*>(q), static_cast<const float*>(k),
-                                       static_cast<const float*>(v), delta, delta_dtype, psi_in,
-                                       static_cast<float*>(out), psi_out, BH, stream);
-    case VMI_BF16:
-      return step::launch_typed<bf16_t>(static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
-                                        static_cast<const bf16_t*>(v), delta, delta_dtype, psi_in,
-                                        static_cast<bf16_t*>(out), psi_out, BH, stream);
-    default:
-      return step::launch_typed<f16_t>(static_cast<const f16_t*>(q), static_cast<const f16_t*>(k),
-                                       static_cast<const f16_t*>(v), delta, delta_dtype, psi_in,
-                                       static_cast<f16_t*>(out), psi_out, BH, stream);
-  }
+                               float* psi_out, int B, int H, hipStream_t stream) {
+  return step::launch_map(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out,
+                          DenseStates{}, B, H, stream);
+}
+
+hipError_t launch_sssd_step128(const void* q, const void* k, const void* v, const void* delta,
+                               int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                               float* psi_out, const StateMap& map, int B, int H,
+                               hipStream_t stream) {
+  return step::launch_map(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, map, B, H,
+                          stream);
+}
+
+hipError_t launch_sssd_step128(const void* q, const void* k, const void* v, const void* delta,
+                               int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                               float* psi_out, const SlotArgs& map, int B, int H,
+                               hipStream_t stream) {
+  return step::launch_map(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, map, B, H,
+                          stream);
 }
 
 }  // namespace vmi

@@ -7,17 +7,84 @@
 
 namespace vmi {
 
+// capi.hip: maps a HIP error to VMI_ERR_HIP and records it for vmi_last_hip_error().
+int hip_status(hipError_t e);
+
+// Where the [D, D] state of head bh = b*H + h (batch item b, head h) lives, as an index
+// into psi_in / psi_out in units of D*D floats:
+//   DenseStates  index bh (the reference layout [B, H, D, D]);
+//   StateMap     slots of a decode state cache: psi_in and psi_out are the same pool of
+//                nslots slots of H states each, item b reads slot in_slot[b] and writes
+//                slot out_slot[b] (device arrays);
+//   SlotArgs     the same with the slot indexes carried in the kernel arguments (no
+//                device array, no host-to-device copy; at most kMaxSlotArgs items).
+// In the slotted maps an input index outside [0, nslots) (-1 by convention) starts from
+// the identity and an output index outside it drops the state write.
+struct DenseStates {
+  static constexpr bool kSlotted = false;  // every index valid: no guard on the writes
+  __device__ __forceinline__ int64_t in_index(int bh, int) const { return bh; }
+  __device__ __forceinline__ int64_t out_index(int bh, int) const { return bh; }
+};
+
+__device__ __forceinline__ int64_t slot_index(int s, int nslots, int bh, int H) {
+  return (s >= 0 && s < nslots) ? static_cast<int64_t>(s) * H + bh % H : -1;
+}
+
+struct StateMap {
+  static constexpr bool kSlotted = true;
+  const int32_t* in_slot;
+  const int32_t* out_slot;
+  int nslots;
+  __device__ __forceinline__ int64_t in_index(int bh, int H) const {
+    return slot_index(in_slot[bh / H], nslots, bh, H);
+  }
+  __device__ __forceinline__ int64_t out_index(int bh, int H) const {
+    return slot_index(out_slot[bh / H], nslots, bh, H);
+  }
+};
+
+constexpr int kMaxSlotArgs = 256;
+struct SlotArgs {
+  static constexpr bool kSlotted = true;
+  int32_t in_slot[kMaxSlotArgs];
+  int32_t out_slot[kMaxSlotArgs];
+  int nslots;
+  __device__ __forceinline__ int64_t in_index(int bh, int H) const {
+    return slot_index(in_slot[bh / H], nslots, bh, H);
+  }
+  __device__ __forceinline__ int64_t out_index(int bh, int H) const {
+    return slot_index(out_slot[bh / H], nslots, bh, H);
+  }
+};
+
 // sssd_seq.hip: token-sequential fp32 scan, one workgroup per (b, h).
 hipError_t launch_sssd_seq(const void* q, const void* k, const void* v, const void* delta,
                            int io_dtype, int delta_dtype, const float* psi_in, void* out,
                            float* psi_out, int B, int T, int H, int D, hipStream_t stream);
+hipError_t launch_sssd_seq(const void* q, const void* k, const void* v, const void* delta,
+                           int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                           float* psi_out, int B, int T, int H, int D, hipStream_t stream,
+                           const StateMap& map);
+hipError_t launch_sssd_seq(const void* q, const void* k, const void* v, const void* delta,
+                           int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                           float* psi_out, int B, int T, int H, int D, hipStream_t stream,
+                           const SlotArgs& map);
 
 // sssd_step.hip: single-token step for head_dim 128 (persistent, loads of the next
-// head overlap the update and store of the current one).  psi_in may equal psi_out.
+// head overlap the update and store of the current one).  psi_in may equal psi_out;
+// `map` places the states (dense, or slots of a decode state cache).
 bool use_step128(int64_t T, int64_t D);
 hipError_t launch_sssd_step128(const void* q, const void* k, const void* v, const void* delta,
                                int io_dtype, int delta_dtype, const float* psi_in, void* out,
-                               float* psi_out, int BH, hipStream_t stream);
+                               float* psi_out, int B, int H, hipStream_t stream);
+hipError_t launch_sssd_step128(const void* q, const void* k, const void* v, const void* delta,
+                               int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                               float* psi_out, const StateMap& map, int B, int H,
+                               hipStream_t stream);
+hipError_t launch_sssd_step128(const void* q, const void* k, const void* v, const void* delta,
+                               int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                               float* psi_out, const SlotArgs& map, int B, int H,
+                               hipStream_t stream);
 
 // sssd_scan.hip: picks the kernel family for a prefill scan.
 size_t scan_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int io_dtype);

@@ -5,6 +5,9 @@ Drop-in replacements for the reference's SSSD hot path:
 * ``SSSDAttention``            <- ``verace_v1.modules.sssd_attention.SSSDAttention``
 * ``launch_sssd_hip_scan``     <- ``verace_v1.serving.triton_kernels.launch_sssd_triton_scan``
 * ``sssd_step_``               -- in-place single-token decode step (opt-in)
+* ``SSSDStateCache``           -- per-layer decode state pools with copy-on-write
+                                  branches (replaces the ``layer_states`` lists of
+                                  ``acd_engine.py`` / ``hyper_generate.py``)
 * ``newton_schulz_unitary_retraction`` / ``parallel_newton_schulz_retraction``
                                <- ``verace_v1.modules.cham_memory`` (same names)
 * ``HAS_HIP``                  <- ``verace_v1.serving.triton_kernels.HAS_TRITON``
@@ -14,10 +17,13 @@ All compute runs in ``libverace_sssd.so`` (C ABI: ``include/verace_sssd.h``).
 from .hip_kernels import (HAS_HIP, launch_sssd_hip_scan, newton_schulz_unitary_retraction,
                           parallel_newton_schulz_retraction, sssd_step_)
 from .sssd_attention import SSSDAttention
+from .state_cache import SlotTable, SSSDStateCache
 
 __all__ = [
     "HAS_HIP",
     "SSSDAttention",
+    "SSSDStateCache",
+    "SlotTable",
     "launch_sssd_hip_scan",
     "sssd_step_",
     "newton_schulz_unitary_retraction",

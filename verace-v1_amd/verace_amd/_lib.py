@@ -24,6 +24,16 @@ EXPORTED = (
     "vmi_sssd_scan_workspace_bytes",
     "vmi_sssd_scan_fwd",
     "vmi_sssd_step_inplace",
+    "vmi_sssd_step_slots",
+    "vmi_state_cache_create",
+    "vmi_state_cache_destroy",
+    "vmi_state_cache_new",
+    "vmi_state_cache_fork",
+    "vmi_state_cache_release",
+    "vmi_state_cache_plan",
+    "vmi_state_cache_slots",
+    "vmi_state_cache_refs",
+    "vmi_state_cache_step",
     "vmi_cham_ns_workspace_bytes",
     "vmi_cham_ns_retraction",
 )
@@ -54,6 +64,22 @@ def _declare(lib):
     lib.vmi_sssd_scan_fwd.restype = i32
     lib.vmi_sssd_step_inplace.argtypes = [vp, vp, vp, vp, i32, i32, vp, vp, i64, i64, i64, vp]
     lib.vmi_sssd_step_inplace.restype = i32
+    lib.vmi_sssd_step_slots.argtypes = [vp, vp, vp, vp, i32, i32, vp, i64, vp, vp, vp, i64, i64,
+                                        i64, vp]
+    lib.vmi_sssd_step_slots.restype = i32
+    pi64 = ctypes.POINTER(i64)
+    pi32 = ctypes.POINTER(i32)
+    lib.vmi_state_cache_create.argtypes = [i64, i64, i64, i64, vp, ctypes.POINTER(vp)]
+    lib.vmi_state_cache_destroy.argtypes = [vp]
+    lib.vmi_state_cache_new.argtypes = [vp, i64, pi64]
+    lib.vmi_state_cache_fork.argtypes = [vp, i64, i64, pi64]
+    lib.vmi_state_cache_release.argtypes = [vp, pi64, i64]
+    lib.vmi_state_cache_plan.argtypes = [vp, i64, pi64, i64, pi32, pi32]
+    lib.vmi_state_cache_slots.argtypes = [vp, i64, pi64, i64, pi32]
+    lib.vmi_state_cache_refs.argtypes = [vp, i64, pi32, pi64]
+    lib.vmi_state_cache_step.argtypes = [vp, i64, pi64, i64, vp, vp, vp, vp, i32, i32, vp, vp]
+    for name in ("create", "destroy", "new", "fork", "release", "plan", "slots", "refs", "step"):
+        getattr(lib, "vmi_state_cache_" + name).restype = i32
     lib.vmi_cham_ns_workspace_bytes.argtypes = [i64, i64, ctypes.POINTER(sz)]
     lib.vmi_cham_ns_workspace_bytes.restype = i32
     lib.vmi_cham_ns_retraction.argtypes = [vp, vp, vp, vp, i64, i64, i32, vp, sz, vp]

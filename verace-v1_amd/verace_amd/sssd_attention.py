@@ -77,3 +77,29 @@ class SSSDAttention(nn.Module):
         if return_state:
             return output, psi
         return output, None
+
+    def forward_cached(self, x: torch.Tensor, cache, layer: int, handles,
+                       active_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """``forward`` with the per-item states kept in an :class:`SSSDStateCache`.
+
+        Item b of ``x`` [B, T, hidden] continues sequence ``handles[b]`` at ``layer``: the
+        reference passes ``initial_state=layer_states[layer][b]`` and stores the returned
+        state back (``acd_engine.py:102-126``).  T = 1 is one batched step over the cache
+        slots (in place, or copy-on-write for handles that share a slot); T > 1 runs the
+        prefill scan from the handles' states and writes the final states back.
+        """
+        if not x.is_cuda:
+            raise RuntimeError("verace_amd.SSSDAttention runs on a HIP device only")
+        if x.requires_grad:
+            raise RuntimeError("verace_amd.SSSDAttention has no backward kernel")
+        b, s, _ = x.shape
+        if len(handles) != b:
+            raise ValueError(f"verace_amd: {len(handles)} handles for a batch of {b}")
+        q, k, v, delta = self.project(x, active_mask)
+        if s == 1:
+            o = cache.step(layer, q, k, v, delta, handles)
+        else:
+            o, psi = launch_sssd_hip_scan(q, k, v, delta, cache.read(layer, handles))
+            cache.write(layer, handles, psi)
+        o_norm = self.head_rmsnorm(o).view(b, s, self.num_heads * self.head_dim)
+        return self.w_out(o_norm)
