@@ -267,6 +267,44 @@ def bench_decode_cache(device, branches=4, tokens=64):
     }
 
 
+def bench_module_full(device, iters=20, warmup=5):
+    """FULL SSSD sub-layer (B=4 T=2048 hidden=1024 H=8 D=128, bf16 weights and inputs):
+    SSSDAttention.forward(x, return_state=True) end to end, with the projections fused into
+    the scan (one GEMM against the stacked weights; normalisation, delta, mask and head
+    RMSNorm inside the scan kernels) against the same module on the reference's unfused op
+    sequence (four projection GEMMs, F.normalize x3, sigmoid, the scan, nn.RMSNorm)."""
+    import torch
+    from verace_amd import SSSDAttention
+    B, T, hidden, H, D = 4, 2048, 1024, 8, 128
+    torch.manual_seed(0)
+    m = SSSDAttention(hidden, H, D).to(device).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(1)
+    xs = [torch.randn(B, T, hidden, generator=g).to(torch.bfloat16).to(device) for _ in range(2)]
+    stream = torch.cuda.current_stream(device)
+    res = {}
+    with torch.no_grad():
+        for name, fused in (("fused", True), ("unfused", False)):
+            m.fuse_projections = fused
+            for i in range(warmup):
+                m(xs[i % 2], return_state=True)
+            torch.cuda.synchronize()
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+            ev[0].record(stream)
+            for i in range(iters):
+                m(xs[i % 2], return_state=True)
+                ev[i + 1].record(stream)
+            torch.cuda.synchronize()
+            res[name] = statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(iters))
+        m.fuse_projections = True
+    return {
+        "config": "FULL SSSD sub-layer: B=4 T=2048 hidden=1024 H=8 D=128 bf16, forward with state",
+        "fused_us_median": round(res["fused"], 2),
+        "unfused_us_median": round(res["unfused"], 2),
+        "speedup": round(res["unfused"] / res["fused"], 3),
+        "tokens_per_s_fused": round(B * T / (res["fused"] * 1e-6), 1),
+    }
+
+
 def cpu_baseline(target_seconds=12.0):
     """The oracle's fp32 restatement of the reference's eager path (oracle/sssd_eager.py),
     timed on the host on a bounded prefix of the OP workload, T chunked by 256."""
@@ -352,6 +390,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-module", action="store_true",
+                    help="skip the FULL SSSD sub-layer (fused vs unfused projections) timing")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc counter CSVs into "
                          "profiles/pmc_traffic_op_scan.json and exit")
@@ -417,6 +457,8 @@ def main():
     if not args.no_decode:
         result["decode"] = bench_decode(device)
         result["decode_cache"] = bench_decode_cache(device)
+    if not args.no_module:
+        result["module_full"] = bench_module_full(device)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

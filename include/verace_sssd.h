@@ -86,6 +86,29 @@ int vmi_sssd_scan_fwd(const void* q, const void* k, const void* v,
                       int64_t B, int64_t T, int64_t H, int64_t D,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* Prefill scan on the raw projections, with the steps either side of the scan fused:
+ * replaces sssd_attention.py:114-126 (F.normalize of q, k, v; delta = 0.1 *
+ * sigmoid(w_delta x) * active_mask) and :177 (head_rmsnorm) around the scan.
+ *   proj   : [B, T, proj_stride] io_dtype, the output of one GEMM x [W_q; W_k; W_v;
+ *            W_delta]^T (q, k, v of head h at columns h*D, H*D + h*D, 2*H*D + h*D,
+ *            the delta logit at 3*H*D + h; proj_stride >= 3*H*D + H, a multiple of 8,
+ *            proj 16-byte aligned), read once;
+ *   mask   : [B, T] uint8 (nonzero = active) or NULL (all active);
+ *   rms_weight : [D] float32 or NULL; out = rms_weight * o * rsqrt(mean_d(o^2) +
+ *            rms_eps) (nn.RMSNorm; its default eps is torch.finfo(dtype).eps), or o when
+ *            NULL;
+ *   out    : [B, T, H, D] io_dtype; psi_in / psi_out as for vmi_sssd_scan_fwd.
+ * q, k, v are scaled by 1 / max(|.|, 1e-12) in fp32 inside the kernel.  Supported:
+ * io_dtype BF16 or F16, D = 128, T >= 32 (otherwise VMI_ERR_UNSUPPORTED: run the
+ * unfused ops and vmi_sssd_scan_fwd).  Workspace from
+ * vmi_sssd_scan_fused_workspace_bytes. */
+int vmi_sssd_scan_fused_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D,
+                                        int io_dtype, size_t* bytes);
+int vmi_sssd_scan_fused(const void* proj, int64_t proj_stride, int io_dtype, const uint8_t* mask,
+                        const float* rms_weight, float rms_eps, const float* psi_in,
+                        void* out, float* psi_out, int64_t B, int64_t T, int64_t H,
+                        int64_t D, void* workspace, size_t workspace_bytes, void* stream);
+
 /* One decode step (T = 1) with the state updated in place:
  *   psi <- R psi ;  out = psi q.
  * Replaces the reference's incremental forward at seq_len 1

@@ -80,6 +80,39 @@ int vmi_sssd_scan_fwd(const void* q, const void* k, const void* v, const void* d
                                        workspace_bytes, s));
 }
 
+int vmi_sssd_scan_fused_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int io_dtype,
+                                        size_t* bytes) {
+  if (bytes == nullptr || B < 0 || T < 0 || H < 0 || D < 1 || !valid_dtype(io_dtype))
+    return VMI_ERR_INVALID_ARG;
+  if (!vmi::use_chunk_path(T, D, io_dtype)) return VMI_ERR_UNSUPPORTED;
+  *bytes = vmi::chunk_workspace_bytes(B, T, H, D, io_dtype);
+  return VMI_OK;
+}
+
+int vmi_sssd_scan_fused(const void* proj, int64_t proj_stride, int io_dtype, const uint8_t* mask,
+                        const float* rms_weight, float rms_eps, const float* psi_in, void* out,
+                        float* psi_out, int64_t B, int64_t T, int64_t H, int64_t D,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  if (!valid_dtype(io_dtype)) return VMI_ERR_INVALID_ARG;
+  if (B < 0 || T < 0 || H < 0 || D < 1 || !(rms_eps >= 0.0f)) return VMI_ERR_INVALID_ARG;
+  if (B * H > INT32_MAX || B * T > INT32_MAX) return VMI_ERR_INVALID_ARG;
+  if (!vmi::use_chunk_path(T, D, io_dtype)) return VMI_ERR_UNSUPPORTED;
+  if (proj == nullptr || out == nullptr || psi_out == nullptr) return VMI_ERR_INVALID_ARG;
+  // 16-byte vector loads of every row: the row stride a multiple of 8 elements, the base aligned
+  if (proj_stride < 3 * H * D + H || proj_stride % 8 != 0 ||
+      reinterpret_cast<uintptr_t>(proj) % 16 != 0)
+    return VMI_ERR_INVALID_ARG;
+  const size_t state_bytes = static_cast<size_t>(B * H) * D * D * sizeof(float);
+  if (psi_in != nullptr && ranges_overlap(psi_in, state_bytes, psi_out, state_bytes))
+    return VMI_ERR_ALIAS;
+  const size_t need = vmi::chunk_workspace_bytes(B, T, H, D, io_dtype);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return VMI_ERR_WORKSPACE;
+  if (B == 0 || H == 0) return VMI_OK;
+  return hip_status(vmi::launch_sssd_chunked_fused(
+      proj, proj_stride, io_dtype, mask, rms_weight, rms_eps, psi_in, out, psi_out, static_cast<int>(B),
+      static_cast<int>(T), static_cast<int>(H), workspace, static_cast<hipStream_t>(stream)));
+}
+
 int vmi_sssd_step_inplace(const void* q, const void* k, const void* v, const void* delta,
                           int io_dtype, int delta_dtype, float* psi, void* out, int64_t B,
                           int64_t H, int64_t D, void* stream) {

@@ -45,6 +45,15 @@
 //   pass B (sssd_carry_kernel): start_s = (part 2 of s-1)(part 1 of s-1) start_{s-1},
 //          column blocks in parallel workgroups, bf16x3 MFMA (fp32-faithful),
 //   pass C (READOUT=true): every segment from its start state, with outputs.
+//
+// Fused mode (FUSED=true, vmi_sssd_scan_fused): the inputs are the raw projections
+// [B, T, stride] of one GEMM x [W_q; W_k; W_v; W_delta]^T.  The producers normalise the
+// k, v rows (norms from a Gram matrix of the raw rows, then one fp32 scaling and one f16
+// rounding) and the q rows (sum of squares over a DPP row), and form delta = 0.1
+// sigmoid(logit) * mask; the readout waves apply head RMSNorm, whose per-token mean
+// square spans both readout waves: each keeps its rows of chunk c in registers for one
+// iteration and stores them once both partial sums are in LDS.  With 8 producers the k/v
+// normalisation takes the otherwise empty phase.
 #include <type_traits>
 
 #include "vmi_common.h"
@@ -123,6 +132,7 @@ struct Smem {
   E zst[2][READOUT ? D * ZST_LD : 1];  // readout stash (chunk parity): Z, transposed
   PScratch pscr[Cfg<READOUT>::NSCR];   // producer scratch (chunk parity / producer wave)
   float smax[NCW];              // per consumer wave: max |start state| of its slab
+  float rsum[READOUT ? 2 * Cfg<READOUT>::NRW * C : 1];  // fused RMSNorm: [chunk parity][readout wave][token]
 };
 
 struct Args {
@@ -146,6 +156,17 @@ struct Args {
   // exactly one piece boundary inside every segment).  Factor f of sequence bh is at
   // ends[f * BH + bh].  With npieces = 0 the pieces are the segments, factor s = P_s.
   int npieces;
+  // input layout: q/k/v element (t, d) of head h at q/k/v + (b*T + t)*in_stride + h*D + d,
+  // delta of (t, h) at delta + (b*T + t)*dl_stride + h (the reference layout has
+  // in_stride = H*D, dl_stride = H; the fused layout is the raw projection [B, T, 3HD + H])
+  int64_t in_stride;
+  int64_t dl_stride;
+  // fused mode only (the FUSED kernels): q/k/v are normalised in the kernel, delta is the raw
+  // logit (0.1 sigmoid(delta) * mask[b*T + t]; mask may be null), and with rms_w the output
+  // is head_rmsnorm(o) = o * rsqrt(mean(o^2) + rms_eps) * rms_w
+  const uint8_t* mask;
+  const float* rms_w;
+  float rms_eps;
 };
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also waits for every
@@ -216,7 +237,54 @@ template <> __device__ __forceinline__ uint4 to_f16x8<__bf16>(uint4 x) {
   return make_uint4(cv(x.x), cv(x.y), cv(x.z), cv(x.w));
 }
 
-template <typename IO, typename DT, bool READOUT>
+// The same with every value multiplied by s in fp32 first (one rounding to f16).
+template <typename IO> __device__ __forceinline__ float lo16_f32(unsigned u);
+template <typename IO> __device__ __forceinline__ float hi16_f32(unsigned u);
+template <> __device__ __forceinline__ float lo16_f32<__bf16>(unsigned u) { return __uint_as_float(u << 16); }
+template <> __device__ __forceinline__ float hi16_f32<__bf16>(unsigned u) {
+  return __uint_as_float(u & 0xffff0000u);
+}
+template <> __device__ __forceinline__ float lo16_f32<_Float16>(unsigned u) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(u)));
+}
+template <> __device__ __forceinline__ float hi16_f32<_Float16>(unsigned u) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(u >> 16)));
+}
+template <typename IO> __device__ __forceinline__ uint4 to_f16x8_scaled(uint4 x, float s) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  auto cv = [s](unsigned u) {
+    h2 h;
+    h[0] = static_cast<_Float16>(lo16_f32<IO>(u) * s);
+    h[1] = static_cast<_Float16>(hi16_f32<IO>(u) * s);
+    return __builtin_bit_cast(unsigned, h);
+  };
+  return make_uint4(cv(x.x), cv(x.y), cv(x.z), cv(x.w));
+}
+// Sum over the 16 lanes of a DPP row (lanes 16i .. 16i+15): four DPP adds, no LDS.
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f32<0xB1>(x);   // quad_perm(1, 0, 3, 2)
+  x += dpp_f32<0x4E>(x);   // quad_perm(2, 3, 0, 1)
+  x += dpp_f32<0x141>(x);  // row_half_mirror: lane i <-> 7 - i within each half row
+  x += dpp_f32<0x140>(x);  // row_mirror: lane i <-> 15 - i
+  return x;
+}
+
+template <typename IO> __device__ __forceinline__ float sumsq8(uint4 x) {
+  float acc = 0.f;
+  const unsigned w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a0 = lo16_f32<IO>(w[i]), a1 = hi16_f32<IO>(w[i]);
+    acc = fmaf(a0, a0, acc);
+    acc = fmaf(a1, a1, acc);
+  }
+  return acc;
+}
+
+template <typename IO, typename DT, bool READOUT, bool FUSED>
 __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   constexpr int NPW = Cfg<READOUT>::NPW;
   constexpr int NRW = Cfg<READOUT>::NRW;
@@ -250,9 +318,11 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   if (nch <= 0) return;  // uniform across the workgroup
 
   const int64_t DD = static_cast<int64_t>(D) * D;
-  const int64_t tok_stride = static_cast<int64_t>(a.H) * D;
-  const int64_t tok_base = (static_cast<int64_t>(b) * a.T * a.H + h) * D;
-  const int64_t dl_base = static_cast<int64_t>(b) * a.T * a.H + h;
+  const int64_t tok_stride = a.in_stride;
+  const int64_t tok_base = static_cast<int64_t>(b) * a.T * a.in_stride + static_cast<int64_t>(h) * D;
+  const int64_t dl_base = static_cast<int64_t>(b) * a.T * a.dl_stride + h;
+  const int64_t out_stride = static_cast<int64_t>(a.H) * D;
+  const int64_t out_base = (static_cast<int64_t>(b) * a.T * a.H + h) * D;
   const IO* gq = static_cast<const IO*>(a.q);
   const IO* gk = static_cast<const IO*>(a.k);
   const IO* gv = static_cast<const IO*>(a.v);
@@ -318,6 +388,7 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
     uint4 kv[8];  // k/v in Gram-operand order: rho = l32, features 16ks + 8g + 0..7
     uint4 q[4];   // q: e = lane + 64m -> token e>>4, features 8*(e&15) + 0..7
     DT d;         // raw delta of token `lane` (lanes 0..15)
+    uint8_t mk;   // fused mode: active-mask entry of token `lane`
   };
 
   // Branch-free loads: token indices are clamped to T-1 for the address and tokens
@@ -337,7 +408,8 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
       }
     }
     const int td = min(t0 + (lane & (C - 1)), a.T - 1);
-    r.d = static_cast<const DT*>(a.delta)[dl_base + static_cast<int64_t>(td) * a.H];
+    r.d = static_cast<const DT*>(a.delta)[dl_base + static_cast<int64_t>(td) * a.dl_stride];
+    if constexpr (FUSED) r.mk = a.mask ? a.mask[static_cast<int64_t>(b) * a.T + td] : 1;
   };
 
   auto dot8 = [](const float* x, const float* y) {
@@ -351,8 +423,8 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
     return fmaf(x1.w, y1.w, sacc);
   };
 
-  // zero the tokens past the end, convert U to f16, Gram matrix, Cayley blocks
-  auto p_gram = [&](Regs& r, int n, PScratch& P) {
+  // zero the tokens past the end; fused mode: normalise the k, v rows (to f16)
+  auto p_prep = [&](Regs& r, int n, PScratch& P) {
     const int t0 = (chunk0 + n) * C;
     if (t0 + C > a.T) {  // last, partial chunk
       const uint4 z = make_uint4(0, 0, 0, 0);
@@ -367,10 +439,37 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
       }
       if (t0 + (lane & (C - 1)) >= a.T) r.d = DT{};
     }
-    // U as f16 (what the consumers use); G = U^T U from the same values, so every
-    // chunk factor I + U T~ U^T stays exactly consistent with its Gram matrix
+    if constexpr (FUSED) {
+      // raw k, v rows: their norms from the diagonal of the raw Gram matrix (MFMA on the
+      // input type, fp32 accumulation), then each row scaled by 1 / max(|row|, 1e-12) in
+      // fp32 and rounded once to f16 (F.normalize, sssd_attention.py:116-118)
+      typedef mfma_t<IO> MR;
+      f32x16 racc = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) r.kv[ks] = to_f16x8<IO>(r.kv[ks]);
+      for (int ks = 0; ks < 8; ++ks) {
+        const typename MR::v8 x = __builtin_bit_cast(typename MR::v8, r.kv[ks]);
+        racc = MR::mma32(x, x, racc);
+      }
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<float4*>(&P.gram[l32 * T_LD + 8 * q4 + 4 * g]) =
+            make_float4(racc[4 * q4], racc[4 * q4 + 1], racc[4 * q4 + 2], racc[4 * q4 + 3]);
+      wave_sync();
+      const float inv = rsqrtf(fmaxf(P.gram[l32 * T_LD + l32], 1e-24f));  // 1 / max(|row|, 1e-12)
+      wave_sync();  // every lane has read its diagonal entry before the Gram below lands
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) r.kv[ks] = to_f16x8_scaled<IO>(r.kv[ks], inv);
+    }
+  };
+
+  // U as f16 (what the consumers use); G = U^T U from the same values, so every chunk
+  // factor I + U T~ U^T stays exactly consistent with its Gram matrix; Cayley blocks
+  auto p_gram = [&](Regs& r, int n, PScratch& P) {
+    const int t0 = (chunk0 + n) * C;
+    if constexpr (!FUSED) {
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) r.kv[ks] = to_f16x8<IO>(r.kv[ks]);
+    }
     f32x16 gacc = {};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
@@ -388,7 +487,10 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
       const float kk = P.gram[(2 * t) * T_LD + 2 * t];
       const float vv = P.gram[(2 * t + 1) * T_LD + 2 * t + 1];
       const float kv = P.gram[(2 * t) * T_LD + 2 * t + 1];
-      const cayley2 M = cayley_coeffs(io<DT>::to_f32(r.d), kk, vv, kv);
+      float dl = io<DT>::to_f32(r.d);
+      if constexpr (FUSED)  // delta = 0.1 sigmoid(w_delta x) * active_mask (sssd_attention.py:120-126)
+        dl = (r.mk && t0 + t < a.T) ? 0.1f / (1.f + __expf(-dl)) : 0.f;
+      const cayley2 M = cayley_coeffs(dl, kk, vv, kv);
       P.mcoef[t] = make_float4(M.m00, M.m01, M.m10, M.m11);
     }
   };
@@ -480,8 +582,17 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   };
 
   // the write: U and q rows, T~ (f16 hi + lo) for the consumers
-  auto p_write = [&](const Regs& r, int n, const float* tv, const float* cv) {
+  auto p_write = [&](Regs& r, int n, const float* tv, const float* cv) {
     E* tb = sm.tok[n % 3];
+    if constexpr (FUSED && READOUT) {
+      // q rows normalised here (the lightest phase): token (lane + 64m) >> 4 spans 16
+      // consecutive lanes
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const float s2 = row16_sum(sumsq8<IO>(r.q[m]));
+        r.q[m] = to_f16x8_scaled<IO>(r.q[m], rsqrtf(fmaxf(s2, 1e-24f)));
+      }
+    }
     E* tdst = tb + rho_slot(l32) * U_LD;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) *reinterpret_cast<uint4*>(tdst + 16 * ks + 8 * g) = r.kv[ks];
@@ -489,7 +600,8 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const int e = lane + 64 * m;
-        *reinterpret_cast<uint4*>(tb + Q_OFF + (e >> 4) * Q_LD + 8 * (e & 15)) = to_f16x8<IO>(r.q[m]);
+        *reinterpret_cast<uint4*>(tb + Q_OFF + (e >> 4) * Q_LD + 8 * (e & 15)) =
+            FUSED ? r.q[m] : to_f16x8<IO>(r.q[m]);  // fused: already normalised f16
       }
     }
     // T~ as f16 hi + lo.  Lanes pair up (lane, lane ^ 1) on adjacent columns: the even
@@ -532,6 +644,7 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
           if (phase == 0) {
             p_load(r, n);
           } else if (phase == 1) {
+            p_prep(r, n, P);
             p_gram(r, n, P);
             wave_sync();
             p_diag(P);
@@ -544,14 +657,23 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
           } else {
             p_write(r, n, tv, cv);
           }
-        } else {
+        } else if constexpr (!FUSED) {
           if (phase == 0) p_load(r, n);
-          else if (phase == 1) p_gram(r, n, P);
+          else if (phase == 1) { p_prep(r, n, P); p_gram(r, n, P); }
           else if (phase == 2) p_diag(P);
           else if (phase == 3) od_1a(P, tv);
           else if (phase == 4) od_1b(P, tv);
           else if (phase == 5) od_c(P, cv);
           else if (phase == 7) p_write(r, n, tv, cv);
+        } else {  // the k, v normalisation takes the otherwise empty slot
+          if (phase == 0) p_load(r, n);
+          else if (phase == 1) p_prep(r, n, P);
+          else if (phase == 2) p_gram(r, n, P);
+          else if (phase == 3) p_diag(P);
+          else if (phase == 4) od_1a(P, tv);
+          else if (phase == 5) od_1b(P, tv);
+          else if (phase == 6) od_c(P, cv);
+          else p_write(r, n, tv, cv);
         }
       }
       lds_barrier();  // (A)
@@ -593,11 +715,15 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
     const int offQ = Q_OFF + l16 * Q_LD + 8 * pg;
     const E* const pst_rd = sm.pst[0] + j_slot(8 * pg + (l16 >> 2)) * PST_LD + RWR * rw + 4 * (l16 & 3);
     const E* const zst_rd = sm.zst[0] + j_slot(8 * pg + (l16 >> 2)) * ZST_LD + 4 * (l16 & 3);
-    auto readout = [&](int c) {
+    // O of chunk c (rows of this wave, scaled state domain): lane (g4, t = l16) gets
+    // O[RWR rw + 16 tl + 4 g4 + 0..3][t] in O[tl]
+    auto readout_compute = [&](int c, f32x4* O) {
       const E* tb = sm.tok[c % 3];
       const E* const pst_c = pst_rd + (c & 1) * PST_BUF;
       const E* const zst_c = zst_rd + (c & 1) * ZST_BUF;
-      f32x4 O[TL] = {}, Y[2] = {};
+      f32x4 Y[2] = {};
+#pragma unroll
+      for (int tl = 0; tl < TL; ++tl) O[tl] = f32x4{};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const V8 bq = lds8<E>(tb + offQ + 32 * ks);
@@ -622,31 +748,82 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
 #pragma unroll
       for (int tl = 0; tl < TL; ++tl)
         O[tl] = MM::mma16(lds_tr4x2<E>(tb + offO + 16 * tl, tb + offO + U_LD + 16 * tl), by, O[tl]);
-      // lane (g4, t = l16) holds O[RWR rw + 16 tl + 4 g4 + 0..3][t].  Stored through a
-      // buffer resource spanning this chunk's valid tokens: rows past the end of the
-      // sequence fall outside it and the hardware drops them, so no branch is needed.
+    };
+    // Stored through a buffer resource spanning chunk c's valid tokens: rows past the end
+    // of the sequence fall outside it and the hardware drops them, so no branch is needed.
+    // Element (row, t) is written as O * scale (* wr[tl][r] when given).
+    auto store_out = [&](int c, const f32x4* O, float scale, const float (*wr)[4]) {
       const int t0 = (chunk0 + c) * C;
       const int nvalid = a.out ? min(C, a.T - t0) : 0;
       const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
-          static_cast<IO*>(a.out) + tok_base + static_cast<int64_t>(t0) * tok_stride, (short)0,
-          nvalid * static_cast<int>(tok_stride) * static_cast<int>(sizeof(IO)), 0x00020000);
-      const int ooff = (l16 * static_cast<int>(tok_stride) + RWR * rw + 4 * g4) * static_cast<int>(sizeof(IO));
+          static_cast<IO*>(a.out) + out_base + static_cast<int64_t>(t0) * out_stride, (short)0,
+          nvalid * static_cast<int>(out_stride) * static_cast<int>(sizeof(IO)), 0x00020000);
+      const int ooff = (l16 * static_cast<int>(out_stride) + RWR * rw + 4 * g4) * static_cast<int>(sizeof(IO));
 #pragma unroll
       for (int tl = 0; tl < TL; ++tl) {
         typedef IO io4 __attribute__((ext_vector_type(4)));
         typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
         io4 o4;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o4[r] = static_cast<IO>(O[tl][r] * inv_s);
+        for (int r = 0; r < 4; ++r)
+          o4[r] = static_cast<IO>(O[tl][r] * (wr ? scale * wr[tl][r] : scale));
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o4), orsrc,
                                               ooff + 16 * tl * static_cast<int>(sizeof(IO)), 0, 0);
       }
     };
-    for (int it = -NPW; it <= last; ++it) {
-      if (it >= 1) readout(it - 1);  // it - 1 < nch since last = nch
-      lds_barrier();  // (A)
+    if constexpr (!FUSED) {
+      for (int it = -NPW; it <= last; ++it) {
+        if (it >= 1) {  // it - 1 < nch since last = nch
+          f32x4 O[TL];
+          readout_compute(it - 1, O);
+          store_out(it - 1, O, inv_s, nullptr);
+        }
+        lds_barrier();  // (A)
+      }
+      return;
+    } else {
+      // Fused head RMSNorm (sssd_attention.py:177-178, nn.RMSNorm over D): a token's
+      // mean(o^2) sums over both readout waves' rows.  Each wave writes its partial sum
+      // of chunk c to rsum[c & 1] in iteration c+1 and keeps O in registers; after the
+      // next barrier both partials are visible and the chunk is scaled and stored.
+      float wr[TL][4];
+#pragma unroll
+      for (int tl = 0; tl < TL; ++tl)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          wr[tl][r] = a.rms_w ? a.rms_w[RWR * rw + 16 * tl + 4 * g4 + r] : 1.f;
+      f32x4 Op[TL];
+      auto finalize = [&](int c, const f32x4* O) {
+        float scale = inv_s;
+        if (a.rms_w) {
+          float s2 = 0.f;
+#pragma unroll
+          for (int w = 0; w < NRW; ++w) s2 += sm.rsum[((c & 1) * NRW + w) * C + l16];
+          scale = inv_s * rsqrtf(s2 * inv_s * inv_s * (1.f / D) + a.rms_eps);
+        }
+        store_out(c, O, scale, wr);
+      };
+      for (int it = -NPW; it <= last; ++it) {
+        if (it >= 1) {
+          f32x4 O[TL];
+          readout_compute(it - 1, O);
+          float s2 = 0.f;
+#pragma unroll
+          for (int tl = 0; tl < TL; ++tl)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s2 = fmaf(O[tl][r], O[tl][r], s2);
+          s2 += __shfl_xor(s2, 16);
+          s2 += __shfl_xor(s2, 32);
+          if (g4 == 0) sm.rsum[(((it - 1) & 1) * NRW + rw) * C + l16] = s2;
+          if (it >= 2) finalize(it - 2, Op);
+#pragma unroll
+          for (int tl = 0; tl < TL; ++tl) Op[tl] = O[tl];
+        }
+        lds_barrier();  // (A)
+      }
+      if (last >= 1) finalize(last - 1, Op);
+      return;
     }
-    return;
   }
 
   // ================================================== consumers
@@ -947,15 +1124,14 @@ bool chunk_path(int64_t T, int64_t D, int io_dtype) {
   return D == chunk::D && (io_dtype == VMI_BF16 || io_dtype == VMI_F16) && T >= 2 * chunk::C;
 }
 
-template <typename IO, typename DT>
-hipError_t run_chunked(const void* q, const void* k, const void* v, const void* delta,
-                       int delta_dtype, const float* psi_in, void* out, float* psi_out, int B,
-                       int T, int H, void* workspace, hipStream_t stream) {
+// The three launches of one scan; `a` carries the inputs (pointers, strides, fused-mode
+// fields), the rest is filled in here.
+template <typename IO, typename DT, bool FUSED>
+hipError_t run_chunked_args(chunk::Args a, const float* psi_in, void* out, float* psi_out, int B,
+                            int T, int H, void* workspace, hipStream_t stream) {
   const int BH = B * H;
   const Plan p = make_plan(BH, T);
   const int64_t DD = static_cast<int64_t>(chunk::D) * chunk::D;
-  chunk::Args a;
-  a.q = q; a.k = k; a.v = v; a.delta = delta; a.delta_dtype = delta_dtype;
   a.T = T; a.H = H; a.BH = BH;
   a.seg_chunks = p.seg_chunks;
   a.nseg = p.nseg;
@@ -971,7 +1147,7 @@ hipError_t run_chunked(const void* q, const void* k, const void* v, const void* 
     pa.ends = P;
     pa.end_mode = 0;
     pa.npieces = p.npieces;
-    hipLaunchKernelGGL((chunk::sssd_chunk_kernel<IO, DT, false>),
+    hipLaunchKernelGGL((chunk::sssd_chunk_kernel<IO, DT, false, FUSED>),
                        dim3(BH, p.npieces > 0 ? p.npieces : p.nseg - 1),
                        dim3(chunk::Cfg<false>::NT), 0, stream, pa);
     hipError_t e = hipGetLastError();
@@ -987,9 +1163,41 @@ hipError_t run_chunked(const void* q, const void* k, const void* v, const void* 
   a.out = out;
   a.ends = psi_out;
   a.end_mode = 1;
-  hipLaunchKernelGGL((chunk::sssd_chunk_kernel<IO, DT, true>), dim3(BH, p.nseg), dim3(chunk::Cfg<true>::NT),
-                     0, stream, a);
+  hipLaunchKernelGGL((chunk::sssd_chunk_kernel<IO, DT, true, FUSED>), dim3(BH, p.nseg),
+                     dim3(chunk::Cfg<true>::NT), 0, stream, a);
   return hipGetLastError();
+}
+
+template <typename IO, typename DT>
+hipError_t run_chunked(const void* q, const void* k, const void* v, const void* delta,
+                       int delta_dtype, const float* psi_in, void* out, float* psi_out, int B,
+                       int T, int H, void* workspace, hipStream_t stream) {
+  chunk::Args a{};
+  a.q = q; a.k = k; a.v = v; a.delta = delta; a.delta_dtype = delta_dtype;
+  a.in_stride = static_cast<int64_t>(H) * chunk::D;
+  a.dl_stride = H;
+  return run_chunked_args<IO, DT, false>(a, psi_in, out, psi_out, B, T, H, workspace, stream);
+}
+
+// Raw projections proj [B, T, proj_stride] = x [W_q; W_k; W_v; W_delta]^T: q, k, v of head h
+// at columns h*D, HD + h*D, 2HD + h*D, the delta logit at column 3HD + h.
+template <typename IO>
+hipError_t run_chunked_fused(const void* proj, int64_t proj_stride, const uint8_t* mask,
+                             const float* rms_w,
+                             float rms_eps, const float* psi_in, void* out, float* psi_out, int B,
+                             int T, int H, void* workspace, hipStream_t stream) {
+  const int64_t HD = static_cast<int64_t>(H) * chunk::D;
+  const IO* base = static_cast<const IO*>(proj);
+  chunk::Args a{};
+  a.q = base; a.k = base + HD; a.v = base + 2 * HD; a.delta = base + 3 * HD;
+  a.delta_dtype = std::is_same<IO, __bf16>::value ? VMI_BF16 : VMI_F16;
+  a.in_stride = proj_stride;
+  a.dl_stride = proj_stride;
+  a.mask = mask;
+  a.rms_w = rms_w;
+  a.rms_eps = rms_eps;
+  typedef typename std::conditional<std::is_same<IO, __bf16>::value, bf16_t, f16_t>::type DT;
+  return run_chunked_args<IO, DT, true>(a, psi_in, out, psi_out, B, T, H, workspace, stream);
 }
 
 }  // namespace
@@ -1002,6 +1210,18 @@ size_t chunk_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int io_
 }
 
 bool use_chunk_path(int64_t T, int64_t D, int io_dtype) { return chunk_path(T, D, io_dtype); }
+
+hipError_t launch_sssd_chunked_fused(const void* proj, int64_t proj_stride, int io_dtype,
+                                     const uint8_t* mask,
+                                     const float* rms_w, float rms_eps, const float* psi_in,
+                                     void* out, float* psi_out, int B, int T, int H,
+                                     void* workspace, hipStream_t stream) {
+  if (io_dtype == VMI_BF16)
+    return run_chunked_fused<__bf16>(proj, proj_stride, mask, rms_w, rms_eps, psi_in, out, psi_out, B, T, H,
+                                     workspace, stream);
+  return run_chunked_fused<_Float16>(proj, proj_stride, mask, rms_w, rms_eps, psi_in, out, psi_out, B, T, H,
+                                     workspace, stream);
+}
 
 hipError_t launch_sssd_chunked(const void* q, const void* k, const void* v, const void* delta,
                                int io_dtype, int delta_dtype, const float* psi_in, void* out,

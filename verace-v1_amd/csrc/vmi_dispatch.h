@@ -101,6 +101,15 @@ hipError_t launch_sssd_chunked(const void* q, const void* k, const void* v, cons
                                float* psi_out, int B, int T, int H, void* workspace,
                                hipStream_t stream);
 
+// sssd_chunk.hip, fused projections: proj [B, T, 3HD + H] raw (x [W_q; W_k; W_v; W_delta]^T);
+// q, k, v normalised and delta = 0.1 sigmoid(.) * mask in the kernel; out = head_rmsnorm(o)
+// when rms_w is given (else o).  Needs use_chunk_path(T, 128, io_dtype).
+hipError_t launch_sssd_chunked_fused(const void* proj, int64_t proj_stride, int io_dtype,
+                                     const uint8_t* mask,
+                                     const float* rms_w, float rms_eps, const float* psi_in,
+                                     void* out, float* psi_out, int B, int T, int H,
+                                     void* workspace, hipStream_t stream);
+
 // cham_ns.hip: Newton-Schulz unitary retraction.
 size_t ns_workspace_bytes(int64_t batch, int64_t n);
 hipError_t launch_ns_retraction(const float* h_real, const float* h_imag, float* out_real,

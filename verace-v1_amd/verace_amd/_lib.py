@@ -23,6 +23,8 @@ EXPORTED = (
     "vmi_last_hip_error",
     "vmi_sssd_scan_workspace_bytes",
     "vmi_sssd_scan_fwd",
+    "vmi_sssd_scan_fused_workspace_bytes",
+    "vmi_sssd_scan_fused",
     "vmi_sssd_step_inplace",
     "vmi_sssd_step_slots",
     "vmi_state_cache_create",
@@ -62,6 +64,11 @@ def _declare(lib):
     lib.vmi_sssd_scan_fwd.argtypes = [vp, vp, vp, vp, i32, i32, vp, vp, vp, i64, i64, i64, i64,
                                       vp, sz, vp]
     lib.vmi_sssd_scan_fwd.restype = i32
+    lib.vmi_sssd_scan_fused_workspace_bytes.argtypes = [i64, i64, i64, i64, i32, ctypes.POINTER(sz)]
+    lib.vmi_sssd_scan_fused_workspace_bytes.restype = i32
+    lib.vmi_sssd_scan_fused.argtypes = [vp, i64, i32, vp, vp, ctypes.c_float, vp, vp, vp, i64, i64,
+                                        i64, i64, vp, sz, vp]
+    lib.vmi_sssd_scan_fused.restype = i32
     lib.vmi_sssd_step_inplace.argtypes = [vp, vp, vp, vp, i32, i32, vp, vp, i64, i64, i64, vp]
     lib.vmi_sssd_step_inplace.restype = i32
     lib.vmi_sssd_step_slots.argtypes = [vp, vp, vp, vp, i32, i32, vp, i64, vp, vp, vp, i64, i64,

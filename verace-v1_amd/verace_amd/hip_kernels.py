@@ -16,6 +16,7 @@ a missing library or a failing call raise.
 from __future__ import annotations
 
 import ctypes
+import math
 from typing import Optional, Tuple
 
 import torch
@@ -95,6 +96,91 @@ def launch_sssd_hip_scan(
                                      d_code, _ptr(psi_in), _ptr(out), _ptr(psi_out), b, s, h, d_k,
                                      _ptr(ws), ws_bytes.value, _lib.stream_handle(q.device)),
                "vmi_sssd_scan_fwd")
+    return out, psi_out
+
+
+_RMS_EPS = {}
+
+
+def rms_default_eps(dtype: torch.dtype) -> float:
+    """The eps that ``nn.RMSNorm(eps=None)`` actually adds for inputs of ``dtype`` in the
+    installed torch.  The documentation says ``finfo(dtype).eps``; torch 2.10 adds the eps of
+    its fp32 compute type for bf16/fp16 inputs (2^-7 would change a unit-norm head's output by
+    ~30 %), so it is measured once per dtype on the host: y = rms_norm(a) = a / sqrt(a^2 + eps)
+    for one element a, and the nearer of the two candidates is taken."""
+    if dtype not in _RMS_EPS:
+        a = 2.0 ** -10
+        y = float(torch.nn.functional.rms_norm(torch.tensor([a], dtype=dtype), [1]).double())
+        est = max((a / y) ** 2 - a * a, 1e-30)
+        cands = (torch.finfo(torch.float32).eps, torch.finfo(dtype).eps)
+        _RMS_EPS[dtype] = min(cands, key=lambda e: abs(math.log(est / e)))
+    return _RMS_EPS[dtype]
+
+
+def fused_scan_supported(x_dtype: torch.dtype, seq_len: int, head_dim: int) -> bool:
+    """Whether :func:`launch_sssd_hip_scan_fused` runs these shapes (bf16/fp16, D = 128,
+    T >= 32); other shapes take the unfused ops and :func:`launch_sssd_hip_scan`."""
+    return x_dtype in (torch.bfloat16, torch.float16) and head_dim == 128 and seq_len >= 32
+
+
+def launch_sssd_hip_scan_fused(
+    proj: torch.Tensor,
+    num_heads: int,
+    head_dim: int,
+    active_mask: Optional[torch.Tensor] = None,
+    rms_weight: Optional[torch.Tensor] = None,
+    rms_eps: Optional[float] = None,
+    initial_state: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The scan with the steps either side of it fused (``sssd_attention.py:114-126`` and
+    ``:177``): ``proj`` [B, T, >= 3HD + H] is ``x @ [W_q; W_k; W_v; W_delta].T`` (raw); q, k,
+    v are L2-normalised, ``delta = 0.1 * sigmoid(.) * active_mask`` is formed and, with
+    ``rms_weight``, the output is ``head_rmsnorm(o)`` (``rms_eps`` None = the eps torch's
+    ``nn.RMSNorm`` adds by default, :func:`rms_default_eps`), all inside the kernels.  Returns (out [B, T, H, D] in proj's
+    dtype, final state [B, H, D, D] float32).  Shapes outside :func:`fused_scan_supported`
+    raise."""
+    _require_device(proj, "proj")
+    if proj.dim() != 3:
+        raise RuntimeError(f"verace_amd: proj must be [B, T, N], got {tuple(proj.shape)}")
+    b, s, n = proj.shape
+    H, D = num_heads, head_dim
+    if not fused_scan_supported(proj.dtype, s, D):
+        raise RuntimeError("verace_amd: fused scan needs bf16/fp16, head_dim 128 and T >= 32")
+    if n < 3 * H * D + H:
+        raise RuntimeError(f"verace_amd: proj has {n} columns, needs >= {3 * H * D + H}")
+    if proj.stride(2) != 1 or proj.stride(1) % 8 != 0 or proj.stride(0) != s * proj.stride(1) \
+            or proj.data_ptr() % 16 != 0:
+        proj = _aligned(torch.nn.functional.pad(proj, (0, (-n) % 8)).contiguous())
+    row = proj.stride(1)
+    mask = None
+    if active_mask is not None:
+        _require_device(active_mask, "active_mask")
+        mask = active_mask.reshape(b, s).to(torch.uint8).contiguous()
+    w = None
+    eps = 0.0
+    if rms_weight is not None:
+        _require_device(rms_weight, "rms_weight")
+        w = rms_weight.to(torch.float32).contiguous()
+        eps = rms_default_eps(proj.dtype) if rms_eps is None else float(rms_eps)
+    psi_in = None
+    if initial_state is not None:
+        _require_device(initial_state, "initial_state")
+        if tuple(initial_state.shape) != (b, H, D, D):
+            raise RuntimeError(f"verace_amd: initial_state must be {(b, H, D, D)}, "
+                               f"got {tuple(initial_state.shape)}")
+        psi_in = initial_state.to(torch.float32).contiguous()
+    out = torch.empty(b, s, H, D, device=proj.device, dtype=proj.dtype)
+    psi_out = torch.empty(b, H, D, D, device=proj.device, dtype=torch.float32)
+    lib = _lib.load()
+    io_code = _lib.dtype_code(proj.dtype)
+    ws_bytes = ctypes.c_size_t(0)
+    _lib.check(lib.vmi_sssd_scan_fused_workspace_bytes(b, s, H, D, io_code, ctypes.byref(ws_bytes)),
+               "vmi_sssd_scan_fused_workspace_bytes")
+    ws = torch.empty(ws_bytes.value, device=proj.device, dtype=torch.uint8) if ws_bytes.value else None
+    _lib.check(lib.vmi_sssd_scan_fused(_ptr(proj), row, io_code, _ptr(mask), _ptr(w), eps,
+                                       _ptr(psi_in), _ptr(out), _ptr(psi_out), b, s, H, D, _ptr(ws),
+                                       ws_bytes.value, _lib.stream_handle(proj.device)),
+               "vmi_sssd_scan_fused")
     return out, psi_out
 
 

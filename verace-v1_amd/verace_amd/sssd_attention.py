@@ -8,10 +8,12 @@ parameters are created in the same order, so ``torch.manual_seed(s); SSSDAttenti
 yields the same initial weights as the reference.
 
 The forward is the reference's inference path (:114-136) with
-``launch_sssd_triton_scan`` replaced by :func:`launch_sssd_hip_scan`:
-projections, L2 normalisation, ``delta = 0.1 * sigmoid(w_delta x)`` and the
-halted-token mask run as torch ops around the HIP scan; ``head_rmsnorm`` and ``w_out``
-follow it.  Only device tensors that do not require grad are accepted -- the reference's
+``launch_sssd_triton_scan`` replaced by the HIP scan.  Where the fused scan runs (bf16 /
+fp16, head_dim 128, T >= 32) the four projections are one GEMM against the stacked
+weights and the L2 normalisation, ``delta = 0.1 * sigmoid(w_delta x)``, the halted-token
+mask and ``head_rmsnorm`` happen inside the scan kernels
+(:func:`launch_sssd_hip_scan_fused`); elsewhere they run as torch ops around
+:func:`launch_sssd_hip_scan`.  ``w_out`` follows.  Only device tensors that do not require grad are accepted -- the reference's
 eager autograd path (:138-176) is the training path, for which no backward kernel
 exists here, so such calls raise instead of silently running something else.
 """
@@ -23,7 +25,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .hip_kernels import launch_sssd_hip_scan
+from .hip_kernels import fused_scan_supported, launch_sssd_hip_scan, launch_sssd_hip_scan_fused
 
 
 class SSSDAttention(nn.Module):
@@ -40,6 +42,37 @@ class SSSDAttention(nn.Module):
         self.w_delta = nn.Linear(hidden_dim, num_heads, bias=False)
         self.head_rmsnorm = nn.RMSNorm(head_dim)
         self.w_out = nn.Linear(num_heads * head_dim, hidden_dim, bias=False)
+        self.fuse_projections = True  # False: always the unfused torch ops around the scan
+        self._proj_key = None
+        self._proj_cat = None
+
+    def _stacked_weight(self) -> torch.Tensor:
+        """[W_q; W_k; W_v; W_delta] as one [3HD + H, hidden] weight, rebuilt whenever one of
+        the four changes (storage or in-place update).  Zero rows pad it to a multiple of 256:
+        hipBLASLt picks a much slower kernel for N = 3HD + H (at FULL, N = 3080 ran 95.7 us
+        against 66.4 us for N = 3328 on MI355X), and the scan skips the padding columns."""
+        ws = (self.w_q.weight, self.w_k.weight, self.w_v.weight, self.w_delta.weight)
+        key = tuple((w.data_ptr(), w._version, w.dtype) for w in ws)
+        if self._proj_key != key:
+            cat = torch.cat([w.detach() for w in ws], 0)
+            pad = (-cat.shape[0]) % 256
+            if pad:
+                cat = torch.cat([cat, cat.new_zeros(pad, cat.shape[1])], 0)
+            self._proj_cat, self._proj_key = cat, key
+        return self._proj_cat
+
+    def _fused(self, x: torch.Tensor) -> bool:
+        return (self.fuse_projections and fused_scan_supported(x.dtype, x.shape[1], self.head_dim)
+                and all(w.dtype == x.dtype for w in (self.w_q.weight, self.w_k.weight,
+                                                      self.w_v.weight, self.w_delta.weight)))
+
+    def _scan_fused(self, x, initial_state, active_mask):
+        proj = F.linear(x, self._stacked_weight())
+        w = self.head_rmsnorm.weight
+        if w is None:
+            w = torch.ones(self.head_dim, device=x.device)
+        return launch_sssd_hip_scan_fused(proj, self.num_heads, self.head_dim, active_mask, w,
+                                          self.head_rmsnorm.eps, initial_state)
 
     def project(self, x: torch.Tensor, active_mask: Optional[torch.Tensor] = None):
         """q, k, v [B,T,H,D] (L2-normalised) and delta [B,T,H] as the reference builds them
@@ -70,9 +103,13 @@ class SSSDAttention(nn.Module):
             raise RuntimeError("verace_amd.SSSDAttention has no backward kernel; the reference "
                                "trains through its eager autograd path (sssd_attention.py:138-176)")
         b, s, _ = x.shape
-        q, k, v, delta = self.project(x, active_mask)
-        o, psi = launch_sssd_hip_scan(q, k, v, delta, initial_state)
-        o_norm = self.head_rmsnorm(o).view(b, s, self.num_heads * self.head_dim)
+        if self._fused(x):
+            o_norm, psi = self._scan_fused(x, initial_state, active_mask)
+            o_norm = o_norm.view(b, s, self.num_heads * self.head_dim)
+        else:
+            q, k, v, delta = self.project(x, active_mask)
+            o, psi = launch_sssd_hip_scan(q, k, v, delta, initial_state)
+            o_norm = self.head_rmsnorm(o).view(b, s, self.num_heads * self.head_dim)
         output = self.w_out(o_norm)
         if return_state:
             return output, psi
@@ -95,6 +132,10 @@ class SSSDAttention(nn.Module):
         b, s, _ = x.shape
         if len(handles) != b:
             raise ValueError(f"verace_amd: {len(handles)} handles for a batch of {b}")
+        if self._fused(x):
+            o_norm, psi = self._scan_fused(x, cache.read(layer, handles), active_mask)
+            cache.write(layer, handles, psi)
+            return self.w_out(o_norm.view(b, s, self.num_heads * self.head_dim))
         q, k, v, delta = self.project(x, active_mask)
         if s == 1:
             o = cache.step(layer, q, k, v, delta, handles)
