@@ -305,6 +305,42 @@ def bench_module_full(device, iters=20, warmup=5):
     }
 
 
+def bench_cham(device, iters=5, warmup=2):
+    """CHAM holographic scan (row f1) at B=4 T=2048 h=128 fp32 (h = 128 is the largest the
+    reference's single-program kernel handles): launch_cham_hip_update end to end.
+    Roofline: the readout's 27 complex matrix-vector products per token (8 h^2 flops
+    each) plus the rank-2 update run on fp32 VALU, so flops / (fp32 VALU peak, 78.6
+    TFLOP/s without packed math)."""
+    import torch
+    from verace_amd import launch_cham_hip_update
+    B, T, h = 4, 2048, 128
+    g = torch.Generator().manual_seed(0)
+    nrm = torch.nn.functional.normalize
+    q = nrm(torch.randn(B, T, h, generator=g), dim=-1).to(device)
+    k = nrm(torch.randn(B, T, h, generator=g), dim=-1).to(device)
+    v = nrm(torch.randn(B, T, h, generator=g), dim=-1).to(device)
+    gam = (0.1 * torch.sigmoid(torch.randn(B, T, generator=g))).to(device)
+    for _ in range(warmup):
+        launch_cham_hip_update(q, k, v, gam)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(device)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+    ev[0].record(stream)
+    for i in range(iters):
+        launch_cham_hip_update(q, k, v, gam)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    us = statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(iters))
+    flops = B * T * (27 * 8 + 16) * h * h   # readout mat-vecs + the rank-2 update (both passes)
+    return {
+        "config": "CHAM scan B=4 T=2048 h=128 fp32, identity start",
+        "us_median": round(us, 1),
+        "tokens_per_s": round(B * T / (us * 1e-6), 1),
+        "valu_tflops": round(flops / (us * 1e-6) / 1e12, 2),
+        "valu_frac": round(flops / (us * 1e-6) / 78.6e12, 4),
+    }
+
+
 def cpu_baseline(target_seconds=12.0):
     """The oracle's fp32 restatement of the reference's eager path (oracle/sssd_eager.py),
     timed on the host on a bounded prefix of the OP workload, T chunked by 256."""
@@ -459,6 +495,7 @@ def main():
         result["decode_cache"] = bench_decode_cache(device)
     if not args.no_module:
         result["module_full"] = bench_module_full(device)
+        result["cham"] = bench_cham(device)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

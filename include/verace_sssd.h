@@ -179,6 +179,25 @@ int vmi_state_cache_step(vmi_state_cache* cache, int64_t layer, const int64_t* h
                          const void* delta, int io_dtype, int delta_dtype, void* out,
                          void* stream);
 
+/* CHAM holographic scan, holographic_dim h <= 128 (the range of the reference's
+ * single-program kernel): replaces launch_cham_triton_update /
+ * cham_holographic_scan_kernel (triton_kernels.py:151-306, :639-685) and the eager
+ * path of ContinuousHolographicMemory.forward (cham_memory.py:167-238).
+ *   H_t = U_t H_{t-1},  U_t = (I - i G_t/2)^-1 (I + i G_t/2),
+ *   G_t = gamma_t (k_t v_t^T + v_t k_t^T)       (exact Cayley, closed rank-2 form)
+ *   out_t = Re(NS_3(H_t) q_t)                   (3 Newton-Schulz steps, readout only)
+ * H_0 = (h0_real, h0_imag) or the identity (both NULL); the raw, never retracted H_T
+ * is written to (h_real_out, h_imag_out).
+ *   q, k, v, out : [B, T, h] io_dtype;  gamma : [B, T] gamma_dtype;
+ *   h0_*, h_*_out : [B, h, h] float32 (outputs must not overlap the inputs).
+ * h > 128: VMI_ERR_UNSUPPORTED.  Workspace from vmi_cham_scan_workspace_bytes. */
+int vmi_cham_scan_workspace_bytes(int64_t B, int64_t T, int64_t h, size_t* bytes);
+int vmi_cham_scan_fwd(const void* q, const void* k, const void* v, const void* gamma,
+                      int io_dtype, int gamma_dtype, const float* h0_real,
+                      const float* h0_imag, void* out, float* h_real_out,
+                      float* h_imag_out, int64_t B, int64_t T, int64_t h,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
 /* Newton-Schulz unitary retraction of a batch of complex matrices
  * H = Hr + i Hi, `steps` iterations of H <- 0.5 H (3I - H^H H), both halves
  * of every iteration computed from the pre-update H.

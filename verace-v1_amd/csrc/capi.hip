@@ -156,6 +156,41 @@ int vmi_sssd_step_slots(const void* q, const void* k, const void* v, const void*
                                          static_cast<int>(D), s, map));
 }
 
+int vmi_cham_scan_workspace_bytes(int64_t B, int64_t T, int64_t h, size_t* bytes) {
+  if (bytes == nullptr || B < 0 || T < 0 || h < 1) return VMI_ERR_INVALID_ARG;
+  if (!vmi::cham_scan_supported(h)) return VMI_ERR_UNSUPPORTED;
+  *bytes = vmi::cham_scan_workspace_bytes(B, T, h);
+  return VMI_OK;
+}
+
+int vmi_cham_scan_fwd(const void* q, const void* k, const void* v, const void* gamma,
+                      int io_dtype, int gamma_dtype, const float* h0_real, const float* h0_imag,
+                      void* out, float* h_real_out, float* h_imag_out, int64_t B, int64_t T,
+                      int64_t h, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!valid_dtype(io_dtype) || !valid_dtype(gamma_dtype)) return VMI_ERR_INVALID_ARG;
+  if (B < 0 || T < 0 || h < 1 || B * T > INT32_MAX) return VMI_ERR_INVALID_ARG;
+  if (!vmi::cham_scan_supported(h)) return VMI_ERR_UNSUPPORTED;
+  if ((h0_real == nullptr) != (h0_imag == nullptr)) return VMI_ERR_INVALID_ARG;
+  if (h_real_out == nullptr || h_imag_out == nullptr) return VMI_ERR_INVALID_ARG;
+  if (T > 0 && (q == nullptr || k == nullptr || v == nullptr || gamma == nullptr || out == nullptr))
+    return VMI_ERR_INVALID_ARG;
+  const size_t state_bytes = static_cast<size_t>(B) * h * h * sizeof(float);
+  if (h0_real != nullptr &&
+      (ranges_overlap(h0_real, state_bytes, h_real_out, state_bytes) ||
+       ranges_overlap(h0_real, state_bytes, h_imag_out, state_bytes) ||
+       ranges_overlap(h0_imag, state_bytes, h_real_out, state_bytes) ||
+       ranges_overlap(h0_imag, state_bytes, h_imag_out, state_bytes)))
+    return VMI_ERR_ALIAS;
+  const size_t need = vmi::cham_scan_workspace_bytes(B, T, h);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return VMI_ERR_WORKSPACE;
+  if (B == 0) return VMI_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return hip_status(vmi::launch_cham_scan(q, k, v, gamma, io_dtype, gamma_dtype, h0_real,
+                                          h0_imag, out, h_real_out, h_imag_out,
+                                          static_cast<int>(B), static_cast<int>(T),
+                                          static_cast<int>(h), workspace, s));
+}
+
 int vmi_cham_ns_workspace_bytes(int64_t batch, int64_t n, size_t* bytes) {
   if (bytes == nullptr || batch < 0 || n < 1) return VMI_ERR_INVALID_ARG;
   *bytes = vmi::ns_workspace_bytes(batch, n);

@@ -1,0 +1,583 @@
+// CHAM holographic scan (reference: verace_v1/modules/cham_memory.py:117-238 and
+// launch_cham_triton_update / cham_holographic_scan_kernel, triton_kernels.py:151-306,
+// 639-685), for holographic_dim h <= 128.
+//
+// Per token t (q, k, v in R^h, gamma scalar), with the raw complex state H = Hr + i Hi:
+//   G_t = gamma (k v^T + v k^T),  U_t = (I - i G_t/2)^-1 (I + i G_t/2)   (exact Cayley)
+//   H_t = U_t H_{t-1}        (raw state, never retracted; H_0 the initial hologram, so
+//                             H_t = P_t H_0 with the reference's prefix product P_t)
+//   rec_t = Re(NS_3(H_t) q_t),  NS_3 = three Newton-Schulz steps H <- H (3I - H^H H) / 2
+// The exported state is the raw H_T.
+//
+// Closed form.  With W = [k v], Gm = W^T W and X = i G/2 = W (i gamma/2 S) W^T (S the 2x2
+// swap), Woodbury gives (I - X)^-1 = I + W M W^T, M = (I - (i gamma/2) S Gm)^-1 (i gamma/2) S,
+// and U = 2 (I - X)^-1 - I = I + W (2M) W^T.  With g = gamma/2 and
+// det = 1 + g^2 (kk vv - kv^2) - 2 i g kv:
+//   N = 2M = (2/det) [[-g^2 vv, i g + g^2 kv], [i g + g^2 kv, -g^2 kk]]
+// (no division by gamma; N = 0 exactly at gamma = 0).  U H = H + k (N11 a + N12 b) +
+// v (N21 a + N22 b) with a = k^T H, b = v^T H (complex row vectors): O(h^2) per token.
+//
+// Readout without forming NS_3(H): NS_j(H) = H f_j(H^H H) for the polynomials
+// f_0 = 1, f_{j+1}(A) = f_j(A) (3 - A f_j(A)^2) / 2 (f_3 has degree 13), so
+//   NS_3(H) q = H f_3(A) q,  A z = H^H (H z),
+// evaluated by unrolling F_j(z) = F_{j-1}(3z - A F_{j-1}(F_{j-1}(z))) / 2 into a chain of
+// 13 applications of A (26 complex matrix-vector products) plus one final H y per token:
+// 27 * 8 h^2 flops instead of the 28 dense h x h products the reference runs per token.
+//
+// Two launches:
+//   pass 1 (cham_state_kernel), grid (B, ceil(h/2)), one wave per workgroup: the state
+//     columns evolve independently (a, b are per-column sums), so each workgroup carries
+//     two columns (32 lanes x 4 rows each) through all T tokens, writes every chunk-start
+//     state (every CH tokens) to the workspace and the final state to the output;
+//   pass 2 (cham_readout_kernel), grid (B, ceil(T/CH)), 256 threads: each workgroup loads
+//     its chunk-start state (thread (tr, tc) holds rows tr + 16i, columns 8tc..8tc+7),
+//     re-applies its tokens' updates and evaluates the readout of each of them.
+#include "vmi_common.h"
+#include "vmi_dispatch.h"
+
+namespace vmi {
+namespace cham {
+
+constexpr int HP = 128;   // padded holographic dim
+constexpr int CH = 16;    // tokens per chunk (pass 2 workgroup)
+
+struct NCoef {
+  float n11r, n11i, n12r, n12i, n22r, n22i;
+};
+
+__device__ __forceinline__ NCoef cayley_n(float gamma, float kk, float vv, float kv) {
+  const float g = 0.5f * gamma;
+  const float g2 = g * g;
+  const float dr = 1.f + g2 * (kk * vv - kv * kv);
+  const float di = -2.f * g * kv;
+  // 2 / |det|^2 (|det| >= 1), so 2/det = p conj(det); v_rcp_f32 (1 ulp) is plenty
+  const float p = 2.f * __builtin_amdgcn_rcpf(dr * dr + di * di);
+  NCoef n;
+  // (x + i y) * p (dr - i di)
+  auto mul = [&](float x, float y, float& re, float& im) {
+    re = p * (x * dr + y * di);
+    im = p * (y * dr - x * di);
+  };
+  mul(-g2 * vv, 0.f, n.n11r, n.n11i);
+  mul(g2 * kv, g, n.n12r, n.n12i);
+  mul(-g2 * kk, 0.f, n.n22r, n.n22i);
+  return n;
+}
+
+// Sum over the 16 lanes of a DPP row, result in every lane of the row.
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f32<0xB1>(x);   // quad_perm(1, 0, 3, 2)
+  x += dpp_f32<0x4E>(x);   // quad_perm(2, 3, 0, 1)
+  x += dpp_f32<0x141>(x);  // row_half_mirror
+  x += dpp_f32<0x140>(x);  // row_mirror
+  return x;
+}
+// Sum of the two 16-lane rows of each 32-lane half: v_permlane16_swap exchanges rows 1
+// and 0 (3 and 2) between its two operands, so the two results add to row0 + row1.
+__device__ __forceinline__ float row_pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i) { return io<T>::load(p, i); }
+
+// Raw 16/32-bit loads converted to fp32 only where they are used: a conversion (or any
+// use) right after a load makes the wave wait for it, which would serialise a batch of
+// loads meant to be in flight together.
+template <typename T> struct raw;
+template <> struct raw<float> {
+  typedef float type;
+  static __device__ __forceinline__ float f32(float x) { return x; }
+};
+template <> struct raw<bf16_t> {
+  typedef uint16_t type;
+  static __device__ __forceinline__ float f32(uint16_t x) { return bf16_to_f32(x); }
+};
+template <> struct raw<f16_t> {
+  typedef uint16_t type;
+  static __device__ __forceinline__ float f32(uint16_t x) {
+    return static_cast<float>(__builtin_bit_cast(f16_t, x));
+  }
+};
+template <typename T>
+__device__ __forceinline__ typename raw<T>::type ldraw(const T* p, int64_t i) {
+  return reinterpret_cast<const typename raw<T>::type*>(p)[i];
+}
+
+// ---------------------------------------------------------------- pass 1: states
+// Workgroup (b, cb): columns c = 2 cb + (lane >> 5); lane l32 = lane & 31 holds rows
+// l32 + 32 i (i < 4) of that column.  Each chunk's k, v, gamma go through LDS (one wave:
+// no barrier, LDS order within the wave; double-buffered by chunk parity); the next
+// chunk's are loaded into registers while the current one is processed.
+template <typename IO, typename GT>
+__global__ __launch_bounds__(64) void cham_state_kernel(
+    const IO* __restrict__ k, const IO* __restrict__ v, const GT* __restrict__ gamma,
+    const float* __restrict__ h0r, const float* __restrict__ h0i, float* __restrict__ wsr,
+    float* __restrict__ wsi, float* __restrict__ hr_out, float* __restrict__ hi_out, int T,
+    int h) {
+  const int lane = threadIdx.x;
+  const int l32 = lane & 31;
+  const int b = blockIdx.x;
+  const int c = 2 * blockIdx.y + (lane >> 5);
+  const bool colok = c < h;
+  const int64_t hh = static_cast<int64_t>(h) * h;
+  const int nch = (T + CH - 1) / CH;
+
+  __shared__ float sk[2][CH][HP], sv[2][CH][HP], sg[2][CH];
+  __shared__ NCoef sN[2][CH];  // the chunk's Cayley coefficients (independent of the state)
+
+  float Hr[4], Hi[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = l32 + 32 * i;
+    const bool ok = colok && r < h;
+    Hr[i] = ok ? (h0r ? h0r[b * hh + static_cast<int64_t>(r) * h + c] : (r == c ? 1.f : 0.f)) : 0.f;
+    Hi[i] = ok ? (h0i ? h0i[b * hh + static_cast<int64_t>(r) * h + c] : 0.f) : 0.f;
+  }
+  // chunk n's k, v (rows < h, zero elsewhere) and gamma: element e = lane + 64 i of the
+  // [CH][HP] block into registers (all loads issued together), then into buffer n & 1
+  constexpr int EPL = CH * HP / 64;
+  typename raw<IO>::type rk[EPL], rv[EPL];
+  typename raw<GT>::type rg = 0;
+  // element (tt, r) of the chunk's [CH][HP] block is valid when the token exists and r < h
+  auto valid = [&](int n, int i) {
+    const int e = lane + 64 * i;
+    return n * CH + e / HP < T && e % HP < h;
+  };
+  auto fetch = [&](int n) {
+    const int t0 = n * CH;
+    const int64_t cbase = (static_cast<int64_t>(b) * T + t0) * h;  // the chunk's rows
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      const int o = valid(n, i) ? (e / HP) * h + e % HP : 0;  // clamped: no branch
+      rk[i] = ldraw(k, cbase + o);
+      rv[i] = ldraw(v, cbase + o);
+    }
+    rg = ldraw(gamma, static_cast<int64_t>(b) * T + ((lane < CH && t0 + lane < T) ? t0 + lane : 0));
+  };
+  auto commit = [&](int n) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      const bool ok = valid(n, i);
+      sk[n & 1][e / HP][e % HP] = ok ? raw<IO>::f32(rk[i]) : 0.f;
+      sv[n & 1][e / HP][e % HP] = ok ? raw<IO>::f32(rv[i]) : 0.f;
+    }
+    if (lane < CH) sg[n & 1][lane] = n * CH + lane < T ? raw<GT>::f32(rg) : 0.f;
+    __builtin_amdgcn_wave_barrier();
+    // N of every token of the chunk: lane (tt, part) sums k.k, v.v, k.v over 32 rows (in a
+    // rotated order, so the 16 tokens read distinct banks), then a quad of lanes combines
+    const int tt = lane >> 2, part = lane & 3;
+    float kk = 0.f, vv = 0.f, kv = 0.f;
+#pragma unroll 8
+    for (int j = 0; j < 32; ++j) {
+      const int r = 32 * part + ((j + tt) & 31);
+      const float x = sk[n & 1][tt][r], y = sv[n & 1][tt][r];
+      kk = fmaf(x, x, kk);
+      vv = fmaf(y, y, vv);
+      kv = fmaf(x, y, kv);
+    }
+    kk += dpp_f32<0xB1>(kk); vv += dpp_f32<0xB1>(vv); kv += dpp_f32<0xB1>(kv);
+    kk += dpp_f32<0x4E>(kk); vv += dpp_f32<0x4E>(vv); kv += dpp_f32<0x4E>(kv);
+    if (part == 0) sN[n & 1][tt] = cayley_n(sg[n & 1][tt], kk, vv, kv);
+  };
+  if (nch > 0) {
+    fetch(0);
+    commit(0);
+  }
+  for (int n = 0; n < nch; ++n) {
+    if (n + 1 < nch) fetch(n + 1);  // lands while chunk n is processed
+    __builtin_amdgcn_wave_barrier();
+    const int nt = min(CH, T - n * CH);
+    // the next token's k, v rows are read while the current one is processed
+    float kn[4], vn[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kn[i] = sk[n & 1][0][l32 + 32 * i];
+      vn[i] = sv[n & 1][0][l32 + 32 * i];
+    }
+    for (int tt = 0; tt < nt; ++tt) {
+      float kr[4], vr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kr[i] = kn[i];
+        vr[i] = vn[i];
+      }
+      const int tn = tt + 1 < CH ? tt + 1 : tt;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kn[i] = sk[n & 1][tn][l32 + 32 * i];
+        vn[i] = sv[n & 1][tn][l32 + 32 * i];
+      }
+      const NCoef N = sN[n & 1][tt];
+      float s[4] = {0.f, 0.f, 0.f, 0.f};  // a = k^T H, b = v^T H (re, im)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[0] = fmaf(kr[i], Hr[i], s[0]);
+        s[1] = fmaf(kr[i], Hi[i], s[1]);
+        s[2] = fmaf(vr[i], Hr[i], s[2]);
+        s[3] = fmaf(vr[i], Hi[i], s[3]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s[j] = row_pair_sum(row16_sum(s[j]));  // this column's 32 lanes
+      // C = N11 a + N12 b,  D = N12 a + N22 b
+      const float cr = N.n11r * s[0] - N.n11i * s[1] + N.n12r * s[2] - N.n12i * s[3];
+      const float ci = N.n11r * s[1] + N.n11i * s[0] + N.n12r * s[3] + N.n12i * s[2];
+      const float dr = N.n12r * s[0] - N.n12i * s[1] + N.n22r * s[2] - N.n22i * s[3];
+      const float di = N.n12r * s[1] + N.n12i * s[0] + N.n22r * s[3] + N.n22i * s[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        Hr[i] = fmaf(kr[i], cr, fmaf(vr[i], dr, Hr[i]));
+        Hi[i] = fmaf(kr[i], ci, fmaf(vr[i], di, Hi[i]));
+      }
+    }
+    // chunk-start state of chunk n + 1 (the final state after the last chunk)
+    float* dr_ = (n + 1 < nch) ? wsr + (static_cast<int64_t>(b) * (nch - 1) + n) * hh : hr_out + b * hh;
+    float* di_ = (n + 1 < nch) ? wsi + (static_cast<int64_t>(b) * (nch - 1) + n) * hh : hi_out + b * hh;
+    if (colok) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = l32 + 32 * i;
+        if (r < h) {
+          dr_[static_cast<int64_t>(r) * h + c] = Hr[i];
+          di_[static_cast<int64_t>(r) * h + c] = Hi[i];
+        }
+      }
+    }
+    if (n + 1 < nch) commit(n + 1);  // buffer (n + 1) & 1 was last read by chunk n - 1
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (nch == 0 && colok) {  // T = 0: the state passes through
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = l32 + 32 * i;
+      if (r < h) {
+        hr_out[b * hh + static_cast<int64_t>(r) * h + c] = Hr[i];
+        hi_out[b * hh + static_cast<int64_t>(r) * h + c] = Hi[i];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- pass 2: readout
+// 256 threads, thread (tr, tc) = (tid >> 4, tid & 15) holds H[tr + 16 i][8 tc + j].
+// Vectors indexed by column (z, the results of H^H w) are held as the thread's 8
+// columns; vectors indexed by row (w = H z) as its 8 rows.  H z: row partials summed
+// over the 16 lanes of a DPP row (the 16 column groups); H^H w: column partials summed
+// over the 4 row groups of a wave (lane shuffles) and the 4 waves (LDS).
+constexpr int RNT = 256;
+
+template <typename IO, typename GT>
+__global__ __launch_bounds__(RNT) void cham_readout_kernel(
+    const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
+    const GT* __restrict__ gamma, const float* __restrict__ h0r, const float* __restrict__ h0i,
+    const float* __restrict__ wsr, const float* __restrict__ wsi, IO* __restrict__ out, int T,
+    int h) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int tr = tid >> 4, tc = tid & 15;
+  const int b = blockIdx.x, n = blockIdx.y;
+  const int nch = (T + CH - 1) / CH;
+  const int t0 = n * CH;
+  const int nt = min(CH, T - t0);
+  const int64_t hh = static_cast<int64_t>(h) * h;
+
+  __shared__ float sq[CH][HP], sk[CH][HP], sv[CH][HP];
+  __shared__ float sg[CH], sdots[CH][3];
+  __shared__ float4 scol[2][4][HP];   // per wave: column partials (double-buffered)
+
+  // stage the chunk's q, k, v, gamma
+  {
+    // all loads issued (clamped addresses, raw bits) before any store
+    constexpr int EPT = CH * HP / RNT;
+    typename raw<IO>::type xq[EPT], xk[EPT], xv[EPT];
+    const int64_t cbase = (static_cast<int64_t>(b) * T + t0) * h;
+#pragma unroll
+    for (int it = 0; it < EPT; ++it) {
+      const int e = tid + RNT * it;
+      const bool ok = e / HP < nt && e % HP < h;
+      const int o = ok ? (e / HP) * h + e % HP : 0;
+      xq[it] = ldraw(q, cbase + o);
+      xk[it] = ldraw(k, cbase + o);
+      xv[it] = ldraw(v, cbase + o);
+    }
+#pragma unroll
+    for (int it = 0; it < EPT; ++it) {
+      const int e = tid + RNT * it;
+      const int tt = e / HP, r = e % HP;
+      const bool ok = tt < nt && r < h;
+      sq[tt][r] = ok ? raw<IO>::f32(xq[it]) : 0.f;
+      sk[tt][r] = ok ? raw<IO>::f32(xk[it]) : 0.f;
+      sv[tt][r] = ok ? raw<IO>::f32(xv[it]) : 0.f;
+    }
+  }
+  if (tid < CH) sg[tid] = tid < nt ? ld(gamma, static_cast<int64_t>(b) * T + t0 + tid) : 0.f;
+
+  // chunk-start state
+  float Hr[8][8], Hi[8][8];
+  {
+    const float* sr = n == 0 ? h0r : wsr + (static_cast<int64_t>(b) * (nch - 1) + n - 1) * hh;
+    const float* si = n == 0 ? h0i : wsi + (static_cast<int64_t>(b) * (nch - 1) + n - 1) * hh;
+    const int64_t base = n == 0 ? b * hh : 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int r = tr + 16 * i, c = 8 * tc + j;
+        const bool ok = r < h && c < h;
+        const int64_t off = base + static_cast<int64_t>(r) * h + c;
+        Hr[i][j] = ok ? (sr ? sr[off] : (r == c ? 1.f : 0.f)) : 0.f;
+        Hi[i][j] = ok ? (si ? si[off] : 0.f) : 0.f;
+      }
+  }
+  __syncthreads();
+  if (tid < 3 * CH) {  // kk, vv, kv of every token of the chunk
+    const int tt = tid / 3, w = tid % 3;
+    const float* x = w == 1 ? sv[tt] : sk[tt];
+    const float* y = w == 0 ? sk[tt] : sv[tt];
+    float acc = 0.f;
+    for (int r = 0; r < HP; ++r) acc = fmaf(x[r], y[r], acc);
+    sdots[tt][w] = acc;
+  }
+
+  // column sums over the whole workgroup: partials p[j] (this thread's rows) ->
+  // per-column totals for the thread's 8 columns; parity selects the LDS buffer
+  int par = 0;
+  auto col_reduce2 = [&](float2* p, float2* tot) {  // the same for two quantities
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p[j].x += __shfl_xor(p[j].x, 16); p[j].y += __shfl_xor(p[j].y, 16);
+      p[j].x += __shfl_xor(p[j].x, 32); p[j].y += __shfl_xor(p[j].y, 32);
+    }
+    float2* sc = reinterpret_cast<float2*>(&scol[par][0][0]);  // [4 waves][HP] float2
+    if (lane < 16) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sc[wave * HP + 8 * tc + j] = p[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float2 s = sc[8 * tc + j];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        const float2 x = sc[w * HP + 8 * tc + j];
+        s.x += x.x; s.y += x.y;
+      }
+      tot[j] = s;
+    }
+    par ^= 1;
+  };
+  auto col_reduce = [&](float4* p, float4* tot) {
+    // p[j] for j < 8: 4 quantities of column 8tc + j; sum over the 4 row groups of
+    // the wave (lanes tc, tc + 16, tc + 32, tc + 48) and the 4 waves
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p[j].x += __shfl_xor(p[j].x, 16); p[j].y += __shfl_xor(p[j].y, 16);
+      p[j].z += __shfl_xor(p[j].z, 16); p[j].w += __shfl_xor(p[j].w, 16);
+      p[j].x += __shfl_xor(p[j].x, 32); p[j].y += __shfl_xor(p[j].y, 32);
+      p[j].z += __shfl_xor(p[j].z, 32); p[j].w += __shfl_xor(p[j].w, 32);
+    }
+    if (lane < 16) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) scol[par][wave][8 * tc + j] = p[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float4 s = scol[par][0][8 * tc + j];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        const float4 x = scol[par][w][8 * tc + j];
+        s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
+      }
+      tot[j] = s;
+    }
+    par ^= 1;
+  };
+
+  // complex vectors: column-indexed zc[j] = (re, im) at column 8tc + j
+  typedef float2 cvec[8];
+  // A z = H^H (H z) for a column-indexed z
+  auto applyA = [&](const cvec z, cvec out) {
+    float wr[8], wi[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float ar = 0.f, ai = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        ar = fmaf(Hr[i][j], z[j].x, fmaf(-Hi[i][j], z[j].y, ar));
+        ai = fmaf(Hr[i][j], z[j].y, fmaf(Hi[i][j], z[j].x, ai));
+      }
+      wr[i] = row16_sum(ar);
+      wi[i] = row16_sum(ai);
+    }
+    float2 p[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float ur = 0.f, ui = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        ur = fmaf(Hr[i][j], wr[i], fmaf(Hi[i][j], wi[i], ur));
+        ui = fmaf(Hr[i][j], wi[i], fmaf(-Hi[i][j], wr[i], ui));
+      }
+      p[j] = make_float2(ur, ui);
+    }
+    col_reduce2(p, out);
+  };
+  // y = f_3(A) x as a chain of 13 applications of A.  Unrolling the recursion
+  // F_J(x) = F_{J-1}(3x - A F_{J-1}(F_{J-1}(x))) / 2 (F_0 = id), every A's input is a
+  // linear combination of the previous A's output a, the current input, the input X2 of
+  // the innermost F_2 and the outer input X3 = x:
+  //   F_2(X2):  z1 = (3 X2 - A X2)/2, z2 = (3 z1 - A z1)/2, t = 3 X2 - A z2, F_2 = (3t - A t)/4
+  //   F_3(x):   R1 = F_2(x), R2 = F_2(R1), T = 3x - A R2, y = F_2(T)/2
+  // next = c_in * in + c_x2 * X2 + c_x3 * X3 + c_a * a, and X2 := next where a new F_2
+  // starts (after steps 3 and 8).  One copy of the A code runs in a loop.
+  auto apply_f3 = [&](cvec cur) {
+    cvec X2, X3;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) X2[j] = X3[j] = cur[j];
+    for (int st = 0; st < 13; ++st) {
+      const int s4 = st < 8 ? (st & 3) : (st == 8 ? 4 : (st - 9) & 3);
+      float c_in, c_x2, c_x3, c_a;
+      if (s4 == 0 || s4 == 1) { c_in = 1.5f; c_x2 = 0.f; c_x3 = 0.f; c_a = -0.5f; }
+      else if (s4 == 2) { c_in = 0.f; c_x2 = 3.f; c_x3 = 0.f; c_a = -1.f; }
+      else if (s4 == 3) { c_in = st == 12 ? 0.375f : 0.75f; c_x2 = 0.f; c_x3 = 0.f; c_a = st == 12 ? -0.125f : -0.25f; }
+      else { c_in = 0.f; c_x2 = 0.f; c_x3 = 3.f; c_a = -1.f; }
+      cvec a;
+      applyA(cur, a);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        cur[j].x = c_in * cur[j].x + c_x2 * X2[j].x + c_x3 * X3[j].x + c_a * a[j].x;
+        cur[j].y = c_in * cur[j].y + c_x2 * X2[j].y + c_x3 * X3[j].y + c_a * a[j].y;
+      }
+      if (st == 3 || st == 8) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) X2[j] = cur[j];
+      }
+    }
+  };
+
+  __syncthreads();  // sdots
+  for (int tt = 0; tt < nt; ++tt) {
+    // ---- update H <- U_t H
+    float kr[8], vr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      kr[i] = sk[tt][tr + 16 * i];
+      vr[i] = sv[tt][tr + 16 * i];
+    }
+    {
+      float4 p[8], tot[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float ar = 0.f, ai = 0.f, br = 0.f, bi = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          ar = fmaf(kr[i], Hr[i][j], ar);
+          ai = fmaf(kr[i], Hi[i][j], ai);
+          br = fmaf(vr[i], Hr[i][j], br);
+          bi = fmaf(vr[i], Hi[i][j], bi);
+        }
+        p[j] = make_float4(ar, ai, br, bi);
+      }
+      col_reduce(p, tot);
+      const NCoef N = cayley_n(sg[tt], sdots[tt][0], sdots[tt][1], sdots[tt][2]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float4 s = tot[j];
+        const float cr = N.n11r * s.x - N.n11i * s.y + N.n12r * s.z - N.n12i * s.w;
+        const float ci = N.n11r * s.y + N.n11i * s.x + N.n12r * s.w + N.n12i * s.z;
+        const float dr = N.n12r * s.x - N.n12i * s.y + N.n22r * s.z - N.n22i * s.w;
+        const float di = N.n12r * s.y + N.n12i * s.x + N.n22r * s.w + N.n22i * s.z;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          Hr[i][j] = fmaf(kr[i], cr, fmaf(vr[i], dr, Hr[i][j]));
+          Hi[i][j] = fmaf(kr[i], ci, fmaf(vr[i], di, Hi[i][j]));
+        }
+      }
+    }
+    // ---- readout rec = Re(H F_3(q))
+    cvec y;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = make_float2(sq[tt][8 * tc + j], 0.f);
+    apply_f3(y);
+    float rec[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s = fmaf(Hr[i][j], y[j].x, fmaf(-Hi[i][j], y[j].y, s));
+      rec[i] = row16_sum(s);
+    }
+    if (tc == 0) {
+      const int64_t off = (static_cast<int64_t>(b) * T + t0 + tt) * h;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = tr + 16 * i;
+        if (r < h) io<IO>::store(out, off + r, rec[i]);
+      }
+    }
+  }
+}
+
+template <typename IO, typename GT>
+hipError_t launch_typed(const void* q, const void* k, const void* v, const void* gamma,
+                        const float* h0r, const float* h0i, void* out, float* hr_out,
+                        float* hi_out, int B, int T, int h, float* ws, hipStream_t stream) {
+  const int nch = (T + CH - 1) / CH;
+  const int64_t wsplane = nch > 1 ? static_cast<int64_t>(B) * (nch - 1) * h * h : 0;
+  float* wsr = ws;
+  float* wsi = ws + wsplane;
+  hipLaunchKernelGGL((cham_state_kernel<IO, GT>), dim3(B, (h + 1) / 2), dim3(64), 0, stream,
+                     static_cast<const IO*>(k), static_cast<const IO*>(v),
+                     static_cast<const GT*>(gamma), h0r, h0i, wsr, wsi, hr_out, hi_out, T, h);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || nch == 0) return e;
+  hipLaunchKernelGGL((cham_readout_kernel<IO, GT>), dim3(B, nch), dim3(RNT), 0, stream,
+                     static_cast<const IO*>(q), static_cast<const IO*>(k),
+                     static_cast<const IO*>(v), static_cast<const GT*>(gamma), h0r, h0i, wsr,
+                     wsi, static_cast<IO*>(out), T, h);
+  return hipGetLastError();
+}
+
+template <typename IO>
+hipError_t launch_io(const void* q, const void* k, const void* v, const void* gamma,
+                     int gamma_dtype, const float* h0r, const float* h0i, void* out,
+                     float* hr_out, float* hi_out, int B, int T, int h, float* ws,
+                     hipStream_t stream) {
+  if (gamma_dtype == VMI_F32)
+    return launch_typed<IO, float>(q, k, v, gamma, h0r, h0i, out, hr_out, hi_out, B, T, h, ws, stream);
+  if (gamma_dtype == VMI_BF16)
+    return launch_typed<IO, bf16_t>(q, k, v, gamma, h0r, h0i, out, hr_out, hi_out, B, T, h, ws, stream);
+  return launch_typed<IO, f16_t>(q, k, v, gamma, h0r, h0i, out, hr_out, hi_out, B, T, h, ws, stream);
+}
+
+}  // namespace cham
+
+size_t cham_scan_workspace_bytes(int64_t B, int64_t T, int64_t h) {
+  const int64_t nch = (T + cham::CH - 1) / cham::CH;
+  return nch > 1 ? static_cast<size_t>(2 * B * (nch - 1) * h * h) * sizeof(float) : 0;
+}
+
+bool cham_scan_supported(int64_t h) { return h >= 1 && h <= cham::HP; }
+
+hipError_t launch_cham_scan(const void* q, const void* k, const void* v, const void* gamma,
+                            int io_dtype, int gamma_dtype, const float* h0r, const float* h0i,
+                            void* out, float* hr_out, float* hi_out, int B, int T, int h,
+                            void* workspace, hipStream_t stream) {
+  float* ws = static_cast<float*>(workspace);
+  if (io_dtype == VMI_F32)
+    return cham::launch_io<float>(q, k, v, gamma, gamma_dtype, h0r, h0i, out, hr_out, hi_out, B, T,
+                                  h, ws, stream);
+  if (io_dtype == VMI_BF16)
+    return cham::launch_io<bf16_t>(q, k, v, gamma, gamma_dtype, h0r, h0i, out, hr_out, hi_out, B,
+                                   T, h, ws, stream);
+  return cham::launch_io<f16_t>(q, k, v, gamma, gamma_dtype, h0r, h0i, out, hr_out, hi_out, B, T,
+                                h, ws, stream);
+}
+
+}  // namespace vmi

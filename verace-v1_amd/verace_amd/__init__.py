@@ -10,12 +10,15 @@ Drop-in replacements for the reference's SSSD hot path:
                                   ``acd_engine.py`` / ``hyper_generate.py``)
 * ``newton_schulz_unitary_retraction`` / ``parallel_newton_schulz_retraction``
                                <- ``verace_v1.modules.cham_memory`` (same names)
+* ``launch_cham_hip_update``   <- ``verace_v1.serving.triton_kernels.launch_cham_triton_update``
+                               (CHAM holographic scan, holographic_dim <= 128)
 * ``HAS_HIP``                  <- ``verace_v1.serving.triton_kernels.HAS_TRITON``
 
 All compute runs in ``libverace_sssd.so`` (C ABI: ``include/verace_sssd.h``).
 """
-from .hip_kernels import (HAS_HIP, launch_sssd_hip_scan, newton_schulz_unitary_retraction,
-                          parallel_newton_schulz_retraction, sssd_step_)
+from .hip_kernels import (HAS_HIP, launch_cham_hip_update, launch_sssd_hip_scan,
+                          newton_schulz_unitary_retraction, parallel_newton_schulz_retraction,
+                          sssd_step_)
 from .sssd_attention import SSSDAttention
 from .state_cache import SlotTable, SSSDStateCache
 
@@ -25,6 +28,7 @@ __all__ = [
     "SSSDStateCache",
     "SlotTable",
     "launch_sssd_hip_scan",
+    "launch_cham_hip_update",
     "sssd_step_",
     "newton_schulz_unitary_retraction",
     "parallel_newton_schulz_retraction",

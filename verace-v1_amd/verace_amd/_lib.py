@@ -36,6 +36,8 @@ EXPORTED = (
     "vmi_state_cache_slots",
     "vmi_state_cache_refs",
     "vmi_state_cache_step",
+    "vmi_cham_scan_workspace_bytes",
+    "vmi_cham_scan_fwd",
     "vmi_cham_ns_workspace_bytes",
     "vmi_cham_ns_retraction",
 )
@@ -87,6 +89,11 @@ def _declare(lib):
     lib.vmi_state_cache_step.argtypes = [vp, i64, pi64, i64, vp, vp, vp, vp, i32, i32, vp, vp]
     for name in ("create", "destroy", "new", "fork", "release", "plan", "slots", "refs", "step"):
         getattr(lib, "vmi_state_cache_" + name).restype = i32
+    lib.vmi_cham_scan_workspace_bytes.argtypes = [i64, i64, i64, ctypes.POINTER(sz)]
+    lib.vmi_cham_scan_workspace_bytes.restype = i32
+    lib.vmi_cham_scan_fwd.argtypes = [vp, vp, vp, vp, i32, i32, vp, vp, vp, vp, vp, i64, i64, i64,
+                                      vp, sz, vp]
+    lib.vmi_cham_scan_fwd.restype = i32
     lib.vmi_cham_ns_workspace_bytes.argtypes = [i64, i64, ctypes.POINTER(sz)]
     lib.vmi_cham_ns_workspace_bytes.restype = i32
     lib.vmi_cham_ns_retraction.argtypes = [vp, vp, vp, vp, i64, i64, i32, vp, sz, vp]

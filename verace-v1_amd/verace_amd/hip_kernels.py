@@ -221,6 +221,64 @@ def sssd_step_(
     return out
 
 
+def launch_cham_hip_update(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    gamma: torch.Tensor,
+    initial_hologram: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+):
+    """CHAM holographic scan on the GPU (replaces ``launch_cham_triton_update``,
+    ``triton_kernels.py:639-685``; parity target ``cham_memory.py:167-238``).
+
+    q, k, v: [batch, seq_len, holographic_dim] (h <= 128); gamma: [batch, seq_len];
+    initial_hologram: optional (H_real, H_imag) [batch, h, h], identity when None (never
+    modified).  Returns (out [batch, seq_len, h] in q's dtype = Re(NS_3(H_t) q_t),
+    (H_real, H_imag) the raw final state, float32).
+    """
+    _require_device(q, "q")
+    if q.dim() != 3:
+        raise RuntimeError(f"verace_amd: q must be [B, T, h], got {tuple(q.shape)}")
+    b, s, h = q.shape
+    for name, t in (("k", k), ("v", v)):
+        _require_device(t, name)
+        if t.shape != q.shape:
+            raise RuntimeError(f"verace_amd: {name} shape {tuple(t.shape)} != q shape {tuple(q.shape)}")
+    _require_device(gamma, "gamma")
+    if gamma.dim() == 3 and gamma.shape[-1] == 1:
+        gamma = gamma.squeeze(-1)
+    if tuple(gamma.shape) != (b, s):
+        raise RuntimeError(f"verace_amd: gamma must be [B, T] = {(b, s)}, got {tuple(gamma.shape)}")
+    io_code = _lib.dtype_code(q.dtype)
+    q_c = q.contiguous()
+    k_c = k.to(q.dtype).contiguous()
+    v_c = v.to(q.dtype).contiguous()
+    g_c = gamma.contiguous()
+    h0r = h0i = None
+    if initial_hologram is not None:
+        h0r, h0i = initial_hologram
+        for name, t in (("H_real", h0r), ("H_imag", h0i)):
+            _require_device(t, name)
+            if tuple(t.shape) != (b, h, h):
+                raise RuntimeError(f"verace_amd: {name} must be {(b, h, h)}, got {tuple(t.shape)}")
+        h0r = h0r.to(torch.float32).contiguous()
+        h0i = h0i.to(torch.float32).contiguous()
+    out = torch.empty_like(q_c)
+    hr = torch.empty(b, h, h, device=q.device, dtype=torch.float32)
+    hi = torch.empty(b, h, h, device=q.device, dtype=torch.float32)
+    lib = _lib.load()
+    ws_bytes = ctypes.c_size_t(0)
+    _lib.check(lib.vmi_cham_scan_workspace_bytes(b, s, h, ctypes.byref(ws_bytes)),
+               "vmi_cham_scan_workspace_bytes")
+    ws = torch.empty(ws_bytes.value, device=q.device, dtype=torch.uint8) if ws_bytes.value else None
+    _lib.check(lib.vmi_cham_scan_fwd(_ptr(q_c), _ptr(k_c), _ptr(v_c), _ptr(g_c), io_code,
+                                     _lib.dtype_code(g_c.dtype), _ptr(h0r), _ptr(h0i), _ptr(out),
+                                     _ptr(hr), _ptr(hi), b, s, h, _ptr(ws), ws_bytes.value,
+                                     _lib.stream_handle(q.device)),
+               "vmi_cham_scan_fwd")
+    return out, (hr, hi)
+
+
 def _ns(H_real: torch.Tensor, H_imag: torch.Tensor, steps: int) -> Tuple[torch.Tensor, torch.Tensor]:
     _require_device(H_real, "H_real")
     _require_device(H_imag, "H_imag")
