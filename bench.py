@@ -307,10 +307,12 @@ def bench_module_full(device, iters=20, warmup=5):
 
 def bench_cham(device, iters=5, warmup=2):
     """CHAM holographic scan (row f1) at B=4 T=2048 h=128 fp32 (h = 128 is the largest the
-    reference's single-program kernel handles): launch_cham_hip_update end to end.
-    Roofline: the readout's 27 complex matrix-vector products per token (8 h^2 flops
-    each) plus the rank-2 update run on fp32 VALU, so flops / (fp32 VALU peak, 78.6
-    TFLOP/s without packed math)."""
+    reference's single-program kernel handles): launch_cham_hip_update end to end, from the
+    identity start (readout Re(H_t q_t)) and from a unitary initial hologram (readout
+    through the 13-step Newton-Schulz polynomial per token).
+    Flops executed per token: the rank-2 update in both passes (2 x 16 h^2) plus the readout
+    (2 h^2, or 27 complex mat-vecs = 216 h^2 with an initial hologram), all fp32 VALU, so
+    the fraction is of the 78.6 TFLOP/s non-packed fp32 VALU peak."""
     import torch
     from verace_amd import launch_cham_hip_update
     B, T, h = 4, 2048, 128
@@ -320,25 +322,29 @@ def bench_cham(device, iters=5, warmup=2):
     k = nrm(torch.randn(B, T, h, generator=g), dim=-1).to(device)
     v = nrm(torch.randn(B, T, h, generator=g), dim=-1).to(device)
     gam = (0.1 * torch.sigmoid(torch.randn(B, T, generator=g))).to(device)
-    for _ in range(warmup):
-        launch_cham_hip_update(q, k, v, gam)
-    torch.cuda.synchronize()
+    Q = torch.linalg.qr(torch.complex(torch.randn(B, h, h, generator=g), torch.randn(B, h, h, generator=g)))[0]
+    h0 = (Q.real.contiguous().to(device), Q.imag.contiguous().to(device))
+    res = {"config": "CHAM scan B=4 T=2048 h=128 fp32"}
     stream = torch.cuda.current_stream(device)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
-    ev[0].record(stream)
-    for i in range(iters):
-        launch_cham_hip_update(q, k, v, gam)
-        ev[i + 1].record(stream)
-    torch.cuda.synchronize()
-    us = statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(iters))
-    flops = B * T * (27 * 8 + 16) * h * h   # readout mat-vecs + the rank-2 update (both passes)
-    return {
-        "config": "CHAM scan B=4 T=2048 h=128 fp32, identity start",
-        "us_median": round(us, 1),
-        "tokens_per_s": round(B * T / (us * 1e-6), 1),
-        "valu_tflops": round(flops / (us * 1e-6) / 1e12, 2),
-        "valu_frac": round(flops / (us * 1e-6) / 78.6e12, 4),
-    }
+    for name, init, per_tok in (("identity_start", None, 34), ("initial_hologram", h0, 248)):
+        for _ in range(warmup):
+            launch_cham_hip_update(q, k, v, gam, init)
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+        ev[0].record(stream)
+        for i in range(iters):
+            launch_cham_hip_update(q, k, v, gam, init)
+            ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        us = statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(iters))
+        flops = B * T * per_tok * h * h
+        res[name] = {
+            "us_median": round(us, 1),
+            "tokens_per_s": round(B * T / (us * 1e-6), 1),
+            "valu_tflops": round(flops / (us * 1e-6) / 1e12, 2),
+            "valu_frac": round(flops / (us * 1e-6) / 78.6e12, 4),
+        }
+    return res
 
 
 def cpu_baseline(target_seconds=12.0):

@@ -179,10 +179,11 @@ int vmi_state_cache_step(vmi_state_cache* cache, int64_t layer, const int64_t* h
                          const void* delta, int io_dtype, int delta_dtype, void* out,
                          void* stream);
 
-/* CHAM holographic scan, holographic_dim h <= 128 (the range of the reference's
- * single-program kernel): replaces launch_cham_triton_update /
- * cham_holographic_scan_kernel (triton_kernels.py:151-306, :639-685) and the eager
- * path of ContinuousHolographicMemory.forward (cham_memory.py:167-238).
+/* CHAM holographic scan, holographic_dim h <= 1024: replaces launch_cham_triton_update
+ * with its single-program kernel for h <= 128 (cham_holographic_scan_kernel,
+ * triton_kernels.py:151-306, :639-685) and its tiled route for larger h
+ * (launch_cham_triton_tiled, :477-597), and the eager path of
+ * ContinuousHolographicMemory.forward (cham_memory.py:167-238).
  *   H_t = U_t H_{t-1},  U_t = (I - i G_t/2)^-1 (I + i G_t/2),
  *   G_t = gamma_t (k_t v_t^T + v_t k_t^T)       (exact Cayley, closed rank-2 form)
  *   out_t = Re(NS_3(H_t) q_t)                   (3 Newton-Schulz steps, readout only)
@@ -190,7 +191,8 @@ int vmi_state_cache_step(vmi_state_cache* cache, int64_t layer, const int64_t* h
  * is written to (h_real_out, h_imag_out).
  *   q, k, v, out : [B, T, h] io_dtype;  gamma : [B, T] gamma_dtype;
  *   h0_*, h_*_out : [B, h, h] float32 (outputs must not overlap the inputs).
- * h > 128: VMI_ERR_UNSUPPORTED.  Workspace from vmi_cham_scan_workspace_bytes. */
+ * h > 1024: VMI_ERR_UNSUPPORTED.  Workspace from vmi_cham_scan_workspace_bytes (for
+ * h > 128 it holds a state snapshot per 64 tokens: about 2 B T h^2 / 64 floats). */
 int vmi_cham_scan_workspace_bytes(int64_t B, int64_t T, int64_t h, size_t* bytes);
 int vmi_cham_scan_fwd(const void* q, const void* k, const void* v, const void* gamma,
                       int io_dtype, int gamma_dtype, const float* h0_real,

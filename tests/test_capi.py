@@ -53,6 +53,14 @@ def test_workspace_query(lib):
     assert lib.vmi_sssd_scan_workspace_bytes(1, 1, 1, 16, 7, ctypes.byref(n)) == 1
     assert lib.vmi_cham_ns_workspace_bytes(2, 16, ctypes.byref(n)) == 0
     assert n.value == 6 * 2 * 16 * 16 * 4
+    # CHAM scan: h <= 128 keeps a state per 16 tokens after the first chunk; larger h a
+    # readout snapshot per 64 tokens (rows padded to 256/512/1024) plus the coefficient,
+    # Z and initial-retraction pieces; h > 1024 is not built
+    assert lib.vmi_cham_scan_workspace_bytes(2, 48, 128, ctypes.byref(n)) == 0
+    assert n.value == 2 * 2 * 2 * 128 * 128 * 4
+    assert lib.vmi_cham_scan_workspace_bytes(1, 64, 1024, ctypes.byref(n)) == 0
+    assert n.value >= (2 * 1024 * 1024 + 2 * 64 * 1024 + 8 * 1024 * 1024) * 4
+    assert lib.vmi_cham_scan_workspace_bytes(1, 64, 1025, ctypes.byref(n)) == 2
 
 
 def test_argument_errors_before_any_device_call(lib):

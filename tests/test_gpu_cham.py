@@ -4,7 +4,9 @@ the op-for-op eager restatement and to linalg.solve in tests/test_cham_oracle.py
 
 Shapes follow the reference's own CHAM tests (test_triton_kernels.py:153-279: (b, s, h) =
 (2, 8, 16), (1, 1, 16), (2, 5, 16), (2, 8, 20), halted tokens, gamma = 0 everywhere, s =
-100) plus h = 64 and 128 and chained calls.  Bars: fp32 I/O, out and final state within
+100) plus h = 64 and 128 and chained calls; h > 128 (the reference's tiled route, up to
+its default 1024) at ragged h and T crossing the 64-token readout chunks, from the
+identity, a unitary and a non-unitary initial hologram.  Bars: fp32 I/O, out and final state within
 1e-5 relative Frobenius error per batch item (the survey's fp32 bar); bf16 I/O within
 2e-2; an all-halted sequence leaves the state bit-exact (N = 0 exactly at gamma = 0).
 """
@@ -115,3 +117,51 @@ def test_cham_raw_state_stays_unitary_over_a_long_sequence(device):
     err = (H.conj().transpose(-1, -2) @ H - torch.eye(h, dtype=torch.complex128)).abs().max()
     print(f"[cham long] |H^H H - I| = {float(err):.2e}", flush=True)
     assert float(err) < 1e-3
+
+
+@pytest.mark.parametrize("B,T,h", [(2, 70, 130), (1, 129, 256), (2, 64, 300), (1, 40, 600),
+                                   (1, 20, 1024)])
+def test_cham_wide_matches_oracle(device, B, T, h):
+    print(f"[case] cham wide B={B} T={T} h={h}", flush=True)
+    _check(device, B, T, h, seed=B * 1000 + T + h, label="wide")
+
+
+@pytest.mark.parametrize("h,unitary", [(160, True), (160, False), (520, True)])
+def test_cham_wide_initial_hologram(device, h, unitary):
+    """Readout through R_0 = NS_3(H_0) carried beside the raw state."""
+    print(f"[case] cham wide H0 h={h} unitary={unitary}", flush=True)
+    B, T = 2, 70
+    g = torch.Generator().manual_seed(h + unitary)
+    Q = torch.linalg.qr(torch.complex(torch.randn(B, h, h, generator=g), torch.randn(B, h, h, generator=g)))[0]
+    if not unitary:
+        Q = Q * (1.0 + 0.05 * torch.randn(B, h, h, generator=g))
+    _check(device, B, T, h, seed=3, h0=(Q.real.contiguous(), Q.imag.contiguous()), label="wide-h0")
+
+
+def test_cham_wide_bf16_and_halted(device):
+    print("[case] cham wide bf16 halted", flush=True)
+    B, T, h = 2, 66, 256
+    halted = torch.ones(B, T)
+    halted[0, 10:30] = 0.0
+    halted[1, 60:] = 0.0
+    _check(device, B, T, h, seed=21, dtype=torch.bfloat16, halted=halted, label="wide-bf16")
+
+
+def test_cham_wide_all_halted_keeps_state_exactly(device):
+    print("[case] cham wide all halted", flush=True)
+    B, T, h = 1, 70, 384
+    q, k, v, gam = _inputs(B, T, h, 6, halted=torch.zeros(B, T))
+    out, hr, hi = _run(device, q, k, v, gam)
+    assert torch.equal(hr, torch.eye(h).expand(B, h, h)) and torch.count_nonzero(hi) == 0
+    assert torch.allclose(out, q, atol=1e-6)
+
+
+def test_cham_wide_chaining(device):
+    print("[case] cham wide chaining", flush=True)
+    B, T, h = 1, 150, 256
+    q, k, v, gam = _inputs(B, T, h, 23)
+    out, hr, hi = _run(device, q, k, v, gam)
+    o1, r1, i1 = _run(device, q[:, :77], k[:, :77], v[:, :77], gam[:, :77])
+    o2, r2, i2 = _run(device, q[:, 77:], k[:, 77:], v[:, 77:], gam[:, 77:], (r1, i1))
+    assert _rel(torch.cat([o1, o2], 1), out) <= 1e-5
+    assert _rel(r2, hr) <= 1e-5 and _rel(i2, hi) <= 1e-5

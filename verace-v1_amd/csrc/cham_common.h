@@ -1,0 +1,83 @@
+// Shared pieces of the CHAM scan kernels (cham_scan.hip for h <= 128, cham_wide.hip for
+// larger h): the closed-form Cayley coefficients of one token, cross-lane sums and raw
+// loads.
+#pragma once
+#include "vmi_common.h"
+
+namespace vmi {
+namespace cham {
+
+struct NCoef {
+  float n11r, n11i, n12r, n12i, n22r, n22i;
+};
+
+__device__ __forceinline__ NCoef cayley_n(float gamma, float kk, float vv, float kv) {
+  const float g = 0.5f * gamma;
+  const float g2 = g * g;
+  const float dr = 1.f + g2 * (kk * vv - kv * kv);
+  const float di = -2.f * g * kv;
+  // 2 / |det|^2 (|det| >= 1), so 2/det = p conj(det); v_rcp_f32 (1 ulp) is plenty
+  const float p = 2.f * __builtin_amdgcn_rcpf(dr * dr + di * di);
+  NCoef n;
+  // (x + i y) * p (dr - i di)
+  auto mul = [&](float x, float y, float& re, float& im) {
+    re = p * (x * dr + y * di);
+    im = p * (y * dr - x * di);
+  };
+  mul(-g2 * vv, 0.f, n.n11r, n.n11i);
+  mul(g2 * kv, g, n.n12r, n.n12i);
+  mul(-g2 * kk, 0.f, n.n22r, n.n22i);
+  return n;
+}
+
+// Sum over the 16 lanes of a DPP row, result in every lane of the row.
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f32<0xB1>(x);   // quad_perm(1, 0, 3, 2)
+  x += dpp_f32<0x4E>(x);   // quad_perm(2, 3, 0, 1)
+  x += dpp_f32<0x141>(x);  // row_half_mirror
+  x += dpp_f32<0x140>(x);  // row_mirror
+  return x;
+}
+// Sum of the two 16-lane rows of each 32-lane half: v_permlane16_swap exchanges rows 1
+// and 0 (3 and 2) between its two operands, so the two results add to row0 + row1.
+__device__ __forceinline__ float row_pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum of the two 32-lane halves of a wave (v_permlane32_swap, the same pattern).
+__device__ __forceinline__ float half_pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i) { return io<T>::load(p, i); }
+
+// Raw 16/32-bit loads converted to fp32 only where they are used: a conversion (or any
+// use) right after a load makes the wave wait for it, which would serialise a batch of
+// loads meant to be in flight together.
+template <typename T> struct raw;
+template <> struct raw<float> {
+  typedef float type;
+  static __device__ __forceinline__ float f32(float x) { return x; }
+};
+template <> struct raw<bf16_t> {
+  typedef uint16_t type;
+  static __device__ __forceinline__ float f32(uint16_t x) { return bf16_to_f32(x); }
+};
+template <> struct raw<f16_t> {
+  typedef uint16_t type;
+  static __device__ __forceinline__ float f32(uint16_t x) {
+    return static_cast<float>(__builtin_bit_cast(f16_t, x));
+  }
+};
+template <typename T>
+__device__ __forceinline__ typename raw<T>::type ldraw(const T* p, int64_t i) {
+  return reinterpret_cast<const typename raw<T>::type*>(p)[i];
+}
+
+}  // namespace cham
+}  // namespace vmi

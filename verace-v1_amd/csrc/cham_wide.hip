@@ -1,0 +1,476 @@
+// CHAM holographic scan for 128 < h <= 1024 (reference: launch_cham_triton_tiled and
+// _cham_rank2_update_kernel, verace_v1/serving/triton_kernels.py:403-453, :477-597, the
+// h > 128 route of launch_cham_triton_update; parity target cham_memory.py:167-238).
+// Same math as cham_scan.hip (closed-form Cayley factor U_t = I + W N W^T, raw state
+// H_t = U_t H_{t-1}); the readout uses
+//   NS_3(H_t) = H_t f_3(H_t^H H_t) = P_t H_0 f_3(H_0^H H_0) = P_t R_0,   R_0 = NS_3(H_0),
+// (every U_t is unitary, so H_t^H H_t = H_0^H H_0), i.e. rec_t = Re(R_t q_t) with
+// R_t = U_t R_{t-1}: R_0 = I from the identity start, else the Newton-Schulz retraction
+// of the initial hologram (cham_ns.hip), computed once.
+//
+// Launches, chunks of C2 = 64 tokens:
+//   1. wide_coef_kernel: N of every token (k.k, v.v, k.v over h) into the workspace;
+//   2. wide_cols_kernel: state columns carried through all T tokens (a column of U H
+//      depends only on the same column of H); blockIdx.z = 0 carries H (exported final
+//      state), = 1 carries R when it differs from H.  Writes the readout state at the
+//      start of every chunk (column-major, rows padded to HP);
+//   3. wide_z_kernel: Z_n = Q_n S_n^T on the fp32 MFMA, i.e. z_t = R_c q_t for every token
+//      of chunk n (R_c its start state);
+//   4. wide_apply_kernel: per token, x = z_t, then x <- U_j x for the chunk's tokens
+//      j <= t (x = R_t q_t) and rec_t = Re(x).
+#include "cham_common.h"
+#include "vmi_dispatch.h"
+
+namespace vmi {
+namespace chamw {
+
+using cham::NCoef;
+using cham::cayley_n;
+using cham::ldraw;
+using cham::raw;
+using cham::row16_sum;
+using cham::row_pair_sum;
+using cham::half_pair_sum;
+
+constexpr int C2 = 64;   // tokens per readout chunk (one state snapshot per chunk)
+constexpr int CHS = 8;   // tokens per LDS stage in the column kernels
+constexpr int NW = 8;    // waves per workgroup in the column kernels (2 columns per wave)
+constexpr int CNT = 64 * NW;
+constexpr int NCF = 8;   // floats per token in the coefficient array (NCoef + 2 pad)
+
+// ---------------------------------------------------------------- 1: coefficients
+template <typename IO, typename GT>
+__global__ __launch_bounds__(256) void wide_coef_kernel(const IO* __restrict__ k,
+                                                        const IO* __restrict__ v,
+                                                        const GT* __restrict__ gamma,
+                                                        float* __restrict__ coef, int BT, int h) {
+  const int lane = threadIdx.x & 63;
+  const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= BT) return;  // whole wave
+  const int64_t base = static_cast<int64_t>(tok) * h;
+  float kk = 0.f, vv = 0.f, kv = 0.f;
+  for (int r = lane; r < h; r += 64) {
+    const float x = io<IO>::load(k, base + r), y = io<IO>::load(v, base + r);
+    kk = fmaf(x, x, kk);
+    vv = fmaf(y, y, vv);
+    kv = fmaf(x, y, kv);
+  }
+  kk = row_pair_sum(row16_sum(kk));
+  vv = row_pair_sum(row16_sum(vv));
+  kv = row_pair_sum(row16_sum(kv));
+  kk += __shfl_xor(kk, 32);
+  vv += __shfl_xor(vv, 32);
+  kv += __shfl_xor(kv, 32);
+  if (lane == 0) {
+    const NCoef N = cayley_n(io<GT>::load(gamma, tok), kk, vv, kv);
+    float4* o = reinterpret_cast<float4*>(coef + static_cast<int64_t>(tok) * NCF);
+    o[0] = make_float4(N.n11r, N.n11i, N.n12r, N.n12i);
+    o[1] = make_float4(N.n22r, N.n22i, 0.f, 0.f);
+  }
+}
+
+// ---------------------------------------------------------------- shared column machinery
+// A column (of the state, or one token's vector) is held by LPC lanes (a wave carries
+// 64 / LPC of them); lane ll = lane % LPC holds rows 4 LPC i + 4 ll + e (i < RPL / 4,
+// e < 4) in x[4 i + e], HP = LPC * RPL rows in all.  The k, v rows and coefficients of
+// CHS tokens are staged in LDS for the whole workgroup.
+template <int HP_>
+struct alignas(16) Stage {
+  static constexpr int HP = HP_;
+  float k[2][CHS][HP];
+  float v[2][CHS][HP];
+  float n[2][CHS][NCF];
+};
+
+template <typename IO, int HP>
+struct Stager {
+  static constexpr int EPT = CHS * HP / CNT;
+  typename raw<IO>::type rk[EPT], rv[EPT];
+  float rn;
+  // tokens [t0, t0 + CHS) of sequence b; tokens from `last` on (one past the end of the
+  // scanned range) read as zeros
+  __device__ __forceinline__ void fetch(const IO* k, const IO* v, const float* coef, int b, int T,
+                                        int h, int t0, int last, int tid) {
+    const int64_t base = (static_cast<int64_t>(b) * T + t0) * h;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int e = tid + CNT * i;
+      const bool ok = t0 + e / HP < last && e % HP < h;
+      const int o = ok ? (e / HP) * h + e % HP : 0;  // clamped: no branch
+      rk[i] = ldraw(k, base + o);
+      rv[i] = ldraw(v, base + o);
+    }
+    const int tt = tid / NCF;
+    const bool nok = tid < CHS * NCF && t0 + tt < last;
+    rn = coef[nok ? (static_cast<int64_t>(b) * T + t0 + tt) * NCF + tid % NCF : 0];
+  }
+  __device__ __forceinline__ void commit(Stage<HP>& s, int buf, int t0, int last, int h, int tid) {
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int e = tid + CNT * i;
+      const bool ok = t0 + e / HP < last && e % HP < h;
+      s.k[buf][e / HP][e % HP] = ok ? raw<IO>::f32(rk[i]) : 0.f;
+      s.v[buf][e / HP][e % HP] = ok ? raw<IO>::f32(rv[i]) : 0.f;
+    }
+    // tokens past the range get N = 0: their update adds exact zeros
+    if (tid < CHS * NCF) s.n[buf][tid / NCF][tid % NCF] = t0 + tid / NCF < last ? rn : 0.f;
+  }
+};
+
+// x <- U x for token tt of buffer buf; `on` = 0 leaves x unchanged (N scaled to zero)
+template <int LPC, int RPL>
+__device__ __forceinline__ float col_sum(float x) {
+  x = row_pair_sum(row16_sum(x));
+  return LPC == 64 ? half_pair_sum(x) : x;
+}
+
+template <int LPC, int RPL>
+__device__ __forceinline__ void apply_token(const Stage<LPC * RPL>& s, int buf, int tt, int ll,
+                                            float (&xr)[RPL], float (&xi)[RPL], bool on) {
+  float kr[RPL], vr[RPL];
+#pragma unroll
+  for (int i = 0; i < RPL / 4; ++i) {
+    const float4 a = *reinterpret_cast<const float4*>(&s.k[buf][tt][4 * LPC * i + 4 * ll]);
+    const float4 c = *reinterpret_cast<const float4*>(&s.v[buf][tt][4 * LPC * i + 4 * ll]);
+    kr[4 * i] = a.x; kr[4 * i + 1] = a.y; kr[4 * i + 2] = a.z; kr[4 * i + 3] = a.w;
+    vr[4 * i] = c.x; vr[4 * i + 1] = c.y; vr[4 * i + 2] = c.z; vr[4 * i + 3] = c.w;
+  }
+  const float4 n0 = *reinterpret_cast<const float4*>(&s.n[buf][tt][0]);
+  const float4 n1 = *reinterpret_cast<const float4*>(&s.n[buf][tt][4]);
+  const float m = on ? 1.f : 0.f;
+  const float n11r = m * n0.x, n11i = m * n0.y, n12r = m * n0.z, n12i = m * n0.w;
+  const float n22r = m * n1.x, n22i = m * n1.y;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;  // a = k^T x, b = v^T x (re, im)
+#pragma unroll
+  for (int i = 0; i < RPL; ++i) {
+    s0 = fmaf(kr[i], xr[i], s0);
+    s1 = fmaf(kr[i], xi[i], s1);
+    s2 = fmaf(vr[i], xr[i], s2);
+    s3 = fmaf(vr[i], xi[i], s3);
+  }
+  s0 = col_sum<LPC, RPL>(s0);
+  s1 = col_sum<LPC, RPL>(s1);
+  s2 = col_sum<LPC, RPL>(s2);
+  s3 = col_sum<LPC, RPL>(s3);
+  const float cr = n11r * s0 - n11i * s1 + n12r * s2 - n12i * s3;
+  const float ci = n11r * s1 + n11i * s0 + n12r * s3 + n12i * s2;
+  const float dr = n12r * s0 - n12i * s1 + n22r * s2 - n22i * s3;
+  const float di = n12r * s1 + n12i * s0 + n22r * s3 + n22i * s2;
+#pragma unroll
+  for (int i = 0; i < RPL; ++i) {
+    xr[i] = fmaf(kr[i], cr, fmaf(vr[i], dr, xr[i]));
+    xi[i] = fmaf(kr[i], ci, fmaf(vr[i], di, xi[i]));
+  }
+}
+
+// ---------------------------------------------------------------- 2: state columns
+// snap: [B][nch][2][h][HP] (chunk-start readout state, column c as HP rows, zero padded)
+template <typename IO, int LPC, int RPL>
+__global__ __launch_bounds__(CNT) void wide_cols_kernel(
+    const IO* __restrict__ k, const IO* __restrict__ v, const float* __restrict__ coef,
+    const float* __restrict__ i0r, const float* __restrict__ i0i, const float* __restrict__ i1r,
+    const float* __restrict__ i1i, float* __restrict__ snap, float* __restrict__ fr,
+    float* __restrict__ fi, int T, int h, int nstates) {
+  constexpr int HP = LPC * RPL, CPW = 64 / LPC;  // rows, columns per wave
+  __shared__ Stage<HP> st;
+  const int tid = threadIdx.x, lane = tid & 63, ll = lane % LPC;
+  const int b = blockIdx.x;
+  const int c = (blockIdx.y * NW + (tid >> 6)) * CPW + lane / LPC;
+  const int z = blockIdx.z;
+  const bool colok = c < h;
+  const bool snaps = z == nstates - 1;  // this state is the readout state
+  const bool final_ = z == 0;           // this state is the exported raw state
+  const int64_t hh = static_cast<int64_t>(h) * h;
+  const int nch = (T + C2 - 1) / C2;
+  const float* ir = z == 0 ? i0r : i1r;
+  const float* ii = z == 0 ? i0i : i1i;
+
+  float xr[RPL], xi[RPL];
+#pragma unroll
+  for (int i = 0; i < RPL; ++i) {
+    const int r = 4 * LPC * (i / 4) + 4 * ll + (i & 3);
+    const bool ok = colok && r < h;
+    const int64_t off = b * hh + static_cast<int64_t>(r) * h + c;
+    xr[i] = ok ? (ir ? ir[off] : (r == c ? 1.f : 0.f)) : 0.f;
+    xi[i] = ok ? (ii ? ii[off] : 0.f) : 0.f;
+  }
+  auto write_snap = [&](int n) {
+    if (!snaps || !colok) return;
+    float* d = snap + ((static_cast<int64_t>(b) * nch + n) * 2) * h * HP + static_cast<int64_t>(c) * HP;
+#pragma unroll
+    for (int i = 0; i < RPL / 4; ++i) {
+      const int r = 4 * LPC * i + 4 * ll;
+      *reinterpret_cast<float4*>(d + r) = make_float4(xr[4 * i], xr[4 * i + 1], xr[4 * i + 2], xr[4 * i + 3]);
+      *reinterpret_cast<float4*>(d + static_cast<int64_t>(h) * HP + r) =
+          make_float4(xi[4 * i], xi[4 * i + 1], xi[4 * i + 2], xi[4 * i + 3]);
+    }
+  };
+  if (nch > 0) write_snap(0);
+
+  Stager<IO, HP> sg;
+  const int nst = (T + CHS - 1) / CHS;
+  if (nst > 0) {
+    sg.fetch(k, v, coef, b, T, h, 0, T, tid);
+    sg.commit(st, 0, 0, T, h, tid);
+  }
+  __syncthreads();
+  for (int s = 0; s < nst; ++s) {
+    if (s + 1 < nst) sg.fetch(k, v, coef, b, T, h, (s + 1) * CHS, T, tid);
+#pragma unroll
+    for (int tt = 0; tt < CHS; ++tt) apply_token<LPC, RPL>(st, s & 1, tt, ll, xr, xi, true);
+    if (((s + 1) * CHS) % C2 == 0 && (s + 1) * CHS < T) write_snap((s + 1) * CHS / C2);
+    if (s + 1 < nst) sg.commit(st, (s + 1) & 1, (s + 1) * CHS, T, h, tid);
+    __syncthreads();
+  }
+  if (final_ && colok) {
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) {
+      const int r = 4 * LPC * (i / 4) + 4 * ll + (i & 3);
+      if (r < h) {
+        fr[b * hh + static_cast<int64_t>(r) * h + c] = xr[i];
+        fi[b * hh + static_cast<int64_t>(r) * h + c] = xi[i];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- 3: Z = Q S^T (fp32 MFMA)
+// Workgroup (rb, n, b): Z[b][n][p][t][rb*64 .. +64] for the chunk's 64 tokens t, both
+// parts p, = sum_c q[t][c] S[b][n][p][c][r].  4 waves, each a 32 x 32 sub-tile of both
+// parts (v_mfma_f32_32x32x2f32, exact fp32 products), K = c in steps of 32 staged in LDS
+// (k-major), the next step's operands loaded into registers during the current one.
+constexpr int ZT = 64, ZK = 32, ZLD = ZT + 4;
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <typename IO>
+__global__ __launch_bounds__(256) void wide_z_kernel(const IO* __restrict__ q,
+                                                     const float* __restrict__ snap,
+                                                     float* __restrict__ Z, int T, int h, int HP) {
+  __shared__ float As[2][ZK][ZLD];
+  __shared__ float Br[2][ZK][ZLD];
+  __shared__ float Bi[2][ZK][ZLD];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wr = wave >> 1, wc = wave & 1, lm = lane & 31, g = lane >> 5;
+  const int r0 = blockIdx.x * ZT, n = blockIdx.y, b = blockIdx.z;
+  const int nch = gridDim.y;
+  const int t0 = n * C2, nt = min(C2, T - t0);
+  const float* sr = snap + ((static_cast<int64_t>(b) * nch + n) * 2) * h * HP;
+  const float* si = sr + static_cast<int64_t>(h) * HP;
+  const int64_t qb = (static_cast<int64_t>(b) * T + t0) * h;
+  constexpr int EPT = ZT * ZK / 256;
+  typename raw<IO>::type ra[EPT];
+  float rbr[EPT], rbi[EPT];
+  auto fetch = [&](int c0) {
+#pragma unroll
+    for (int s = 0; s < EPT; ++s) {
+      const int e = tid + 256 * s;
+      const int m = e / ZK, kk = e % ZK;  // A: token m, column c0 + kk
+      const bool ok = m < nt && c0 + kk < h;
+      ra[s] = ldraw(q, qb + (ok ? static_cast<int64_t>(m) * h + c0 + kk : 0));
+      const int kb = e / ZT, jb = e % ZT;  // B: column c0 + kb, row r0 + jb (< HP always)
+      const bool okb = c0 + kb < h;
+      const int64_t ob = okb ? static_cast<int64_t>(c0 + kb) * HP + r0 + jb : 0;
+      rbr[s] = sr[ob];
+      rbi[s] = si[ob];
+    }
+  };
+  auto commit = [&](int buf, int c0) {
+#pragma unroll
+    for (int s = 0; s < EPT; ++s) {
+      const int e = tid + 256 * s;
+      const int m = e / ZK, kk = e % ZK;
+      As[buf][kk][m] = (m < nt && c0 + kk < h) ? raw<IO>::f32(ra[s]) : 0.f;
+      const int kb = e / ZT, jb = e % ZT;
+      const bool okb = c0 + kb < h;
+      Br[buf][kb][jb] = okb ? rbr[s] : 0.f;
+      Bi[buf][kb][jb] = okb ? rbi[s] : 0.f;
+    }
+  };
+  f32x16 accr = {}, acci = {};
+  const int nk = (h + ZK - 1) / ZK;
+  fetch(0);
+  commit(0, 0);
+  __syncthreads();
+  for (int kc = 0; kc < nk; ++kc) {
+    const int buf = kc & 1;
+    if (kc + 1 < nk) fetch((kc + 1) * ZK);
+    const float* as = &As[buf][16 * g][32 * wr + lm];
+    const float* br = &Br[buf][16 * g][32 * wc + lm];
+    const float* bi = &Bi[buf][16 * g][32 * wc + lm];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const float a = as[s * ZLD];
+      accr = __builtin_amdgcn_mfma_f32_32x32x2f32(a, br[s * ZLD], accr, 0, 0, 0);
+      acci = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bi[s * ZLD], acci, 0, 0, 0);
+    }
+    if (kc + 1 < nk) commit(buf ^ 1, (kc + 1) * ZK);
+    __syncthreads();
+  }
+  // lane holds tokens 8(r/4) + 4g + r%4 of row lm of the wave's sub-tile
+  float* zr = Z + ((static_cast<int64_t>(b) * nch + n) * 2) * C2 * HP;
+  float* zi = zr + C2 * HP;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int t = 32 * wr + 8 * (r >> 2) + 4 * g + (r & 3);
+    const int j = r0 + 32 * wc + lm;
+    zr[static_cast<int64_t>(t) * HP + j] = accr[r];
+    zi[static_cast<int64_t>(t) * HP + j] = acci[r];
+  }
+}
+
+// ---------------------------------------------------------------- 4: per-token updates
+// Workgroup (b, n, zb): tokens tt = (NW zb + w) CPW + lane / LPC of chunk n; x = z_t,
+// then U_j x for j = 0 .. tt (chunk-relative), rec = Re(x).
+template <typename IO, int LPC, int RPL>
+__global__ __launch_bounds__(CNT) void wide_apply_kernel(
+    const IO* __restrict__ k, const IO* __restrict__ v, const float* __restrict__ coef,
+    const float* __restrict__ Z, IO* __restrict__ out, int T, int h) {
+  constexpr int HP = LPC * RPL, CPW = 64 / LPC;
+  constexpr int TPG = NW * CPW;  // tokens per workgroup
+  __shared__ Stage<HP> st;
+  const int tid = threadIdx.x, lane = tid & 63, ll = lane % LPC;
+  const int b = blockIdx.x, n = blockIdx.y;
+  const int nch = gridDim.y;
+  const int tt = (blockIdx.z * NW + (tid >> 6)) * CPW + lane / LPC;
+  const int t0 = n * C2, nt = min(C2, T - t0);
+  const int jend = min(nt, (blockIdx.z + 1) * TPG);  // steps the workgroup needs
+  if (blockIdx.z * TPG >= nt) return;                  // whole workgroup past the end
+
+  float xr[RPL], xi[RPL];
+  {
+    const float* zr = Z + ((static_cast<int64_t>(b) * nch + n) * 2) * C2 * HP + static_cast<int64_t>(min(tt, C2 - 1)) * HP;
+    const float* zi = zr + C2 * HP;
+#pragma unroll
+    for (int i = 0; i < RPL / 4; ++i) {
+      const float4 a = *reinterpret_cast<const float4*>(zr + 4 * LPC * i + 4 * ll);
+      const float4 c = *reinterpret_cast<const float4*>(zi + 4 * LPC * i + 4 * ll);
+      xr[4 * i] = a.x; xr[4 * i + 1] = a.y; xr[4 * i + 2] = a.z; xr[4 * i + 3] = a.w;
+      xi[4 * i] = c.x; xi[4 * i + 1] = c.y; xi[4 * i + 2] = c.z; xi[4 * i + 3] = c.w;
+    }
+  }
+  Stager<IO, HP> sg;
+  const int last = t0 + jend;
+  const int nst = (jend + CHS - 1) / CHS;
+  sg.fetch(k, v, coef, b, T, h, t0, last, tid);
+  sg.commit(st, 0, t0, last, h, tid);
+  __syncthreads();
+  for (int s = 0; s < nst; ++s) {
+    if (s + 1 < nst) sg.fetch(k, v, coef, b, T, h, t0 + (s + 1) * CHS, last, tid);
+#pragma unroll
+    for (int j = 0; j < CHS; ++j) apply_token<LPC, RPL>(st, s & 1, j, ll, xr, xi, s * CHS + j <= tt);
+    if (s + 1 < nst) sg.commit(st, (s + 1) & 1, t0 + (s + 1) * CHS, last, h, tid);
+    __syncthreads();
+  }
+  if (tt < nt) {
+    const int64_t o = (static_cast<int64_t>(b) * T + t0 + tt) * h;
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) {
+      const int r = 4 * LPC * (i / 4) + 4 * ll + (i & 3);
+      if (r < h) io<IO>::store(out, o + r, xr[i]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- host side
+int padded(int h) { return h <= 256 ? 256 : (h <= 512 ? 512 : 1024); }
+
+struct WideWs {
+  float *coef, *snap, *Z, *r0r, *r0i, *ns;
+  size_t floats;
+};
+WideWs carve(void* base, int64_t B, int64_t T, int64_t h) {
+  const int64_t HP = padded(static_cast<int>(h));
+  const int64_t nch = (T + C2 - 1) / C2;
+  const int64_t sizes[6] = {B * T * NCF, B * nch * 2 * h * HP, B * nch * 2 * C2 * HP,
+                            B * h * h, B * h * h, 6 * B * h * h};
+  WideWs w;
+  float* p = static_cast<float*>(base);
+  float** dst[6] = {&w.coef, &w.snap, &w.Z, &w.r0r, &w.r0i, &w.ns};
+  size_t off = 0;
+  for (int i = 0; i < 6; ++i) {
+    *dst[i] = p ? p + off : nullptr;
+    off += (sizes[i] + 63) / 64 * 64;  // 256-byte aligned pieces
+  }
+  w.floats = off;
+  return w;
+}
+
+template <typename IO, int LPC, int RPL>
+hipError_t launch_rpl(const void* q, const void* k, const void* v, const float* h0r,
+                      const float* h0i, void* out, float* hr_out, float* hi_out, int B, int T,
+                      int h, const WideWs& w, hipStream_t stream) {
+  constexpr int HP = LPC * RPL, CPG = NW * 64 / LPC;  // rows, columns per workgroup
+  const int nch = (T + C2 - 1) / C2;
+  const int nstates = h0r && nch > 0 ? 2 : 1;
+  hipLaunchKernelGGL((wide_cols_kernel<IO, LPC, RPL>), dim3(B, (h + CPG - 1) / CPG, nstates),
+                     dim3(CNT), 0, stream, static_cast<const IO*>(k), static_cast<const IO*>(v),
+                     w.coef, h0r, h0i, w.r0r, w.r0i, w.snap, hr_out, hi_out, T, h, nstates);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || nch == 0) return e;
+  hipLaunchKernelGGL((wide_z_kernel<IO>), dim3(HP / ZT, nch, B), dim3(256), 0, stream,
+                     static_cast<const IO*>(q), w.snap, w.Z, T, h, HP);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((wide_apply_kernel<IO, LPC, RPL>), dim3(B, nch, C2 / CPG), dim3(CNT), 0,
+                     stream, static_cast<const IO*>(k), static_cast<const IO*>(v), w.coef, w.Z,
+                     static_cast<IO*>(out), T, h);
+  return hipGetLastError();
+}
+
+template <typename IO, typename GT>
+hipError_t launch_typed(const void* q, const void* k, const void* v, const void* gamma,
+                        const float* h0r, const float* h0i, void* out, float* hr_out,
+                        float* hi_out, int B, int T, int h, void* workspace, hipStream_t stream) {
+  const WideWs w = carve(workspace, B, T, h);
+  const int BT = B * T;
+  if (BT > 0) {
+    hipLaunchKernelGGL((wide_coef_kernel<IO, GT>), dim3((BT + 3) / 4), dim3(256), 0, stream,
+                       static_cast<const IO*>(k), static_cast<const IO*>(v),
+                       static_cast<const GT*>(gamma), w.coef, BT, h);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (h0r && T > 0) {  // readout state R_0 = NS_3(H_0)
+    const hipError_t e = launch_ns_retraction(h0r, h0i, w.r0r, w.r0i, B, h, 3, w.ns, stream);
+    if (e != hipSuccess) return e;
+  }
+  const int hp = padded(h);
+  if (hp == 256) return launch_rpl<IO, 32, 8>(q, k, v, h0r, h0i, out, hr_out, hi_out, B, T, h, w, stream);
+  if (hp == 512) return launch_rpl<IO, 32, 16>(q, k, v, h0r, h0i, out, hr_out, hi_out, B, T, h, w, stream);
+  // h > 512: one column per 64-lane wave keeps the rows per lane at 16 (no spills)
+  return launch_rpl<IO, 64, 16>(q, k, v, h0r, h0i, out, hr_out, hi_out, B, T, h, w, stream);
+}
+
+template <typename IO>
+hipError_t launch_io(const void* q, const void* k, const void* v, const void* gamma,
+                     int gamma_dtype, const float* h0r, const float* h0i, void* out,
+                     float* hr_out, float* hi_out, int B, int T, int h, void* ws,
+                     hipStream_t stream) {
+  if (gamma_dtype == VMI_F32)
+    return launch_typed<IO, float>(q, k, v, gamma, h0r, h0i, out, hr_out, hi_out, B, T, h, ws, stream);
+  if (gamma_dtype == VMI_BF16)
+    return launch_typed<IO, bf16_t>(q, k, v, gamma, h0r, h0i, out, hr_out, hi_out, B, T, h, ws, stream);
+  return launch_typed<IO, f16_t>(q, k, v, gamma, h0r, h0i, out, hr_out, hi_out, B, T, h, ws, stream);
+}
+
+}  // namespace chamw
+
+size_t cham_wide_workspace_bytes(int64_t B, int64_t T, int64_t h) {
+  return chamw::carve(nullptr, B, T, h).floats * sizeof(float);
+}
+
+hipError_t launch_cham_wide(const void* q, const void* k, const void* v, const void* gamma,
+                            int io_dtype, int gamma_dtype, const float* h0r, const float* h0i,
+                            void* out, float* hr_out, float* hi_out, int B, int T, int h,
+                            void* workspace, hipStream_t stream) {
+  if (io_dtype == VMI_F32)
+    return chamw::launch_io<float>(q, k, v, gamma, gamma_dtype, h0r, h0i, out, hr_out, hi_out, B,
+                                   T, h, workspace, stream);
+  if (io_dtype == VMI_BF16)
+    return chamw::launch_io<bf16_t>(q, k, v, gamma, gamma_dtype, h0r, h0i, out, hr_out, hi_out,
+                                    B, T, h, workspace, stream);
+  return chamw::launch_io<f16_t>(q, k, v, gamma, gamma_dtype, h0r, h0i, out, hr_out, hi_out, B, T,
+                                 h, workspace, stream);
+}
+
+}  // namespace vmi

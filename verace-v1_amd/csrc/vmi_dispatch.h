@@ -110,11 +110,19 @@ hipError_t launch_sssd_chunked_fused(const void* proj, int64_t proj_stride, int 
                                      void* out, float* psi_out, int B, int T, int H,
                                      void* workspace, hipStream_t stream);
 
-// cham_scan.hip: CHAM holographic scan (h <= 128): raw complex state with exact Cayley
-// rank-2 updates, readout Re(NS_3(H_t) q_t) by matrix-vector products.
+// cham_scan.hip: CHAM holographic scan (h <= 128 there, larger h routed to cham_wide.hip):
+// raw complex state with exact Cayley rank-2 updates, readout Re(NS_3(H_t) q_t).
+constexpr int64_t kChamMaxDim = 1024;
 bool cham_scan_supported(int64_t h);
 size_t cham_scan_workspace_bytes(int64_t B, int64_t T, int64_t h);
 hipError_t launch_cham_scan(const void* q, const void* k, const void* v, const void* gamma,
+                            int io_dtype, int gamma_dtype, const float* h0r, const float* h0i,
+                            void* out, float* hr_out, float* hi_out, int B, int T, int h,
+                            void* workspace, hipStream_t stream);
+
+// cham_wide.hip: the same scan for 128 < h <= kChamMaxDim.
+size_t cham_wide_workspace_bytes(int64_t B, int64_t T, int64_t h);
+hipError_t launch_cham_wide(const void* q, const void* k, const void* v, const void* gamma,
                             int io_dtype, int gamma_dtype, const float* h0r, const float* h0i,
                             void* out, float* hr_out, float* hi_out, int B, int T, int h,
                             void* workspace, hipStream_t stream);

@@ -231,7 +231,7 @@ def launch_cham_hip_update(
     """CHAM holographic scan on the GPU (replaces ``launch_cham_triton_update``,
     ``triton_kernels.py:639-685``; parity target ``cham_memory.py:167-238``).
 
-    q, k, v: [batch, seq_len, holographic_dim] (h <= 128); gamma: [batch, seq_len];
+    q, k, v: [batch, seq_len, holographic_dim] (h <= 1024); gamma: [batch, seq_len];
     initial_hologram: optional (H_real, H_imag) [batch, h, h], identity when None (never
     modified).  Returns (out [batch, seq_len, h] in q's dtype = Re(NS_3(H_t) q_t),
     (H_real, H_imag) the raw final state, float32).
