@@ -149,3 +149,28 @@ def test_planted_mistakes_are_caught():
     assert np.abs(good - (hr[0] + 1j * hi[0])).max() < 1e-12
     assert np.abs(H0[0] @ P - good).max() > 1e-3
     assert np.abs(P_rev @ H0[0] - good).max() > 1e-3
+
+
+@pytest.mark.parametrize("eps", [0.0, 0.05])
+def test_readout_identity_ns_of_carried_state(eps):
+    """The kernels read out NS_3(H_t) q as P_t NS_3(H_0) q (every Cayley factor is unitary,
+    so H_t^H H_t = H_0^H H_0): check against NS_3 evaluated on every H_t, for a unitary and
+    a non-unitary H_0, and that the identity start reduces it to Re(H_t q)."""
+    B, T, h = 1, 9, 6
+    q, k, v, g = _inputs(B, T, h, 11)
+    g = g * 5.0
+    rng = np.random.default_rng(12)
+    H0 = _rand_h(rng, h, eps)
+    Rr, Ri = newton_schulz_retraction(torch.from_numpy(H0.real.copy()), torch.from_numpy(H0.imag.copy()), 3)
+    R = Rr.numpy() + 1j * Ri.numpy()
+    H = H0.copy()
+    for t in range(T):
+        U = cham_scan.cham_cayley_solve(k[0, t], v[0, t], g[0, t])
+        H = U @ H
+        R = U @ R
+        assert np.abs(cham_scan.ns_apply(H, q[0, t], 3) - R @ q[0, t]).max() < 1e-10
+    # identity start: NS_3(P_t) q = P_t q
+    P = np.eye(h, dtype=np.complex128)
+    for t in range(T):
+        P = cham_scan.cham_cayley_solve(k[0, t], v[0, t], g[0, t]) @ P
+        assert np.abs(cham_scan.ns_apply(P, q[0, t], 3) - P @ q[0, t]).max() < 1e-10
