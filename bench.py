@@ -347,6 +347,37 @@ def bench_cham(device, iters=5, warmup=2):
     return res
 
 
+def bench_backward(device, iters=5, warmup=2):
+    """Backward of the scan (row f4) at the FULL training shape B=4 T=2048 H=8 D=128, bf16:
+    launch_sssd_hip_scan_bwd (dq, dk, dv, ddelta from dOut, states rebuilt from the final
+    state) after one forward.  The reference differentiates its eager path instead."""
+    import torch
+    from verace_amd import launch_sssd_hip_scan, launch_sssd_hip_scan_bwd
+    B, T, H, D = 4, 2048, 8, 128
+    _, (q, k, v, delta) = make_inputs(B, T, H, D, seed=0, dtype=torch.bfloat16, device=device)
+    g = torch.Generator().manual_seed(1)
+    d_out = torch.randn(B, T, H, D, generator=g).to(torch.bfloat16).to(device)
+    _, psi = launch_sssd_hip_scan(q, k, v, delta)
+    for _ in range(warmup):
+        launch_sssd_hip_scan_bwd(q, k, v, delta, psi, d_out, None, False)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(device)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+    ev[0].record(stream)
+    for i in range(iters):
+        launch_sssd_hip_scan_bwd(q, k, v, delta, psi, d_out, None, False)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    us = statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(iters))
+    flops = B * T * H * 26 * D * D  # 13 D^2 FMA per token-head
+    return {
+        "config": "SSSD scan backward B=4 T=2048 H=8 D=128 bf16 (FULL training shape)",
+        "us_median": round(us, 1),
+        "tokens_per_s": round(B * T / (us * 1e-6), 1),
+        "valu_tflops": round(flops / (us * 1e-6) / 1e12, 2),
+    }
+
+
 def cpu_baseline(target_seconds=12.0):
     """The oracle's fp32 restatement of the reference's eager path (oracle/sssd_eager.py),
     timed on the host on a bounded prefix of the OP workload, T chunked by 256."""
@@ -502,6 +533,7 @@ def main():
     if not args.no_module:
         result["module_full"] = bench_module_full(device)
         result["cham"] = bench_cham(device)
+        result["scan_backward"] = bench_backward(device)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

@@ -179,6 +179,24 @@ int vmi_state_cache_step(vmi_state_cache* cache, int64_t layer, const int64_t* h
                          const void* delta, int io_dtype, int delta_dtype, void* out,
                          void* stream);
 
+/* Backward of the scan (training).  Replaces the eager autograd through
+ * sssd_attention.py:144-175 that the reference's training loop differentiates
+ * (pretrain.py:164-195): given the forward's inputs, its final state psi_T
+ * (vmi_sssd_scan_fwd's psi_out) and the gradients d_out = dL/dout [B,T,H,D]
+ * (d_out_dtype) and d_psi_T = dL/dpsi_T [B,H,D,D] fp32 (NULL: zero), writes
+ *   dq, dk, dv : [B,T,H,D] io_dtype;  d_delta : [B,T,H] delta_dtype;
+ *   d_psi0     : [B,H,D,D] fp32 = dL/d initial_state (NULL: not needed).
+ * The states are rebuilt in reverse from psi_T (every factor is exactly
+ * orthogonal), so nothing but psi_T is kept from the forward.  D = 64 or 128
+ * (otherwise VMI_ERR_UNSUPPORTED); workspace from vmi_sssd_scan_bwd_workspace_bytes
+ * (per-token partial sums: B T H (D/16)(2D + 8) floats). */
+int vmi_sssd_scan_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, size_t* bytes);
+int vmi_sssd_scan_bwd(const void* q, const void* k, const void* v, const void* delta,
+                      int io_dtype, int delta_dtype, const float* psi_T, const void* d_out,
+                      int d_out_dtype, const float* d_psi_T, void* dq, void* dk, void* dv,
+                      void* d_delta, float* d_psi0, int64_t B, int64_t T, int64_t H, int64_t D,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
 /* CHAM holographic scan, holographic_dim h <= 1024: replaces launch_cham_triton_update
  * with its single-program kernel for h <= 128 (cham_holographic_scan_kernel,
  * triton_kernels.py:151-306, :639-685) and its tiled route for larger h

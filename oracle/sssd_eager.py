@@ -75,6 +75,7 @@ def sssd_scan_eager(
     v: torch.Tensor,
     delta: torch.Tensor,
     initial_state: Optional[torch.Tensor] = None,
+    compute_dtype: torch.dtype = torch.float32,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """The eager scan of ``sssd_attention.py:144-175`` on CPU.
 
@@ -82,16 +83,19 @@ def sssd_scan_eager(
     delta: [B, T, H] or [B, T, H, 1]; initial_state: [B, H, D, D] or None (identity).
     Returns (o [B, T, H, D] fp32, Psi_T [B, H, D, D] fp32) -- the values the
     reference feeds to head_rmsnorm (:177) and returns as state (:181).
+    ``compute_dtype=torch.float64`` runs the same ops in fp64 (differentiable: the
+    gradients the reference's training takes through this path, without fp32 rounding).
     """
     b, s, H, D = q.shape
     if delta.dim() == 3:
         delta = delta.unsqueeze(-1)
-    q32, k32, v32, delta32 = q.float(), k.float(), v.float(), delta.float()
+    cd = compute_dtype
+    q32, k32, v32, delta32 = q.to(cd), k.to(cd), v.to(cd), delta.to(cd)
     if initial_state is not None:
-        Psi_0 = initial_state.float()
+        Psi_0 = initial_state.to(cd)
     else:
-        Psi_0 = torch.eye(D, dtype=torch.float32).unsqueeze(0).unsqueeze(0).repeat(b, H, 1, 1)
-    eye = torch.eye(D, dtype=torch.float32)
+        Psi_0 = torch.eye(D, dtype=cd).unsqueeze(0).unsqueeze(0).repeat(b, H, 1, 1)
+    eye = torch.eye(D, dtype=cd)
     kt_col = k32.transpose(1, 2).unsqueeze(-1)
     vt_row = v32.transpose(1, 2).unsqueeze(-2)
     vt_col = v32.transpose(1, 2).unsqueeze(-1)
@@ -128,7 +132,8 @@ def sssd_scan_eager_chunked(q, k, v, delta, initial_state=None, chunk: int = 256
 
 
 def sssd_module_forward(params: dict, x: torch.Tensor, num_heads: int, head_dim: int,
-                        initial_state=None, return_state: bool = False, active_mask=None):
+                        initial_state=None, return_state: bool = False, active_mask=None,
+                        compute_dtype: torch.dtype = torch.float32):
     """Eager ``SSSDAttention.forward`` (``sssd_attention.py:103-182``) with explicit weights.
 
     ``params`` holds the module's state_dict entries: ``w_q.weight``, ``w_k.weight``,
@@ -146,7 +151,7 @@ def sssd_module_forward(params: dict, x: torch.Tensor, num_heads: int, head_dim:
         while am.ndim < delta.ndim:
             am = am.unsqueeze(-1)
         delta = delta * am.to(delta.dtype)
-    o_seq, psi_T = sssd_scan_eager(q, k, v, delta, initial_state)
+    o_seq, psi_T = sssd_scan_eager(q, k, v, delta, initial_state, compute_dtype=compute_dtype)
     o_norm = F.rms_norm(o_seq, (D,), params["head_rmsnorm.weight"]).reshape(b, s, H * D)
     out = F.linear(o_norm, params["w_out.weight"])
     return out, (psi_T if return_state else None)

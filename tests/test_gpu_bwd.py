@@ -1,0 +1,134 @@
+"""GPU parity of the scan's backward (vmi_sssd_scan_bwd / SSSDScanFunction) against the
+gradients of the reference's training path: fp64 autograd through the eager restatement
+of ``sssd_attention.py:144-175`` (oracle/sssd_eager.py, pinned against finite
+differences and an independent closed form in tests/test_bwd_algebra.py).
+
+Bars: relative Frobenius error per gradient tensor <= 1e-5 for fp32 inputs (the fp32
+bar of the forward; the kernel rebuilds the states from the fp32 final state by R_t^T),
+<= 2e-2 for bf16 / fp16 inputs (gradients stored in the input type, the forward's f16
+operands); the module's gradients (every weight, x and the initial state) <= 1e-4 in
+fp32 (torch's fp32 GEMMs and RMSNorm around the scan).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sssd_eager
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(got, ref):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.sqrt(((got - ref) ** 2).sum()) / max(np.sqrt((ref ** 2).sum()), 1e-30))
+
+
+def _inputs(B, T, H, D, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    nrm = torch.nn.functional.normalize
+    q = nrm(torch.randn(B, T, H, D, generator=g), dim=-1).to(dtype)
+    k = nrm(torch.randn(B, T, H, D, generator=g), dim=-1).to(dtype)
+    v = nrm(torch.randn(B, T, H, D, generator=g), dim=-1).to(dtype)
+    d = (0.1 * torch.sigmoid(torch.randn(B, T, H, generator=g))).to(dtype)
+    psi0 = torch.linalg.qr(torch.randn(B, H, D, D, generator=g))[0]
+    w_o = torch.randn(B, T, H, D, generator=g)
+    w_s = torch.randn(B, H, D, D, generator=g)
+    return q, k, v, d, psi0, w_o, w_s
+
+
+def _oracle(q, k, v, d, psi0, w_o, w_s, with_state_grad):
+    a = [x.double().clone().requires_grad_(True) for x in (q, k, v, d)]
+    p0 = None if psi0 is None else psi0.double().clone().requires_grad_(True)
+    o, s = sssd_eager.sssd_scan_eager(*a, p0, compute_dtype=torch.float64)
+    loss = (o * w_o.double()).sum()
+    if with_state_grad:
+        loss = loss + (s * w_s.double()).sum()
+    loss.backward()
+    return [x.grad for x in a] + [None if p0 is None else p0.grad]
+
+
+@pytest.mark.parametrize("B,T,H,D,dtype,init,sgrad", [
+    (2, 40, 2, 64, torch.float32, True, True),
+    (1, 100, 2, 128, torch.float32, False, True),
+    (2, 64, 4, 128, torch.bfloat16, True, True),
+    (1, 1, 1, 128, torch.float32, True, False),
+    (2, 33, 3, 128, torch.float16, False, False),
+])
+def test_scan_backward_matches_oracle(device, B, T, H, D, dtype, init, sgrad):
+    from verace_amd import SSSDScanFunction
+    print(f"[case] bwd B={B} T={T} H={H} D={D} {dtype} init={init} state_grad={sgrad}", flush=True)
+    q, k, v, d, psi0, w_o, w_s = _inputs(B, T, H, D, seed=B * 100 + T + D, dtype=dtype)
+    if not init:
+        psi0 = None
+    ref = _oracle(q, k, v, d, psi0, w_o, w_s, sgrad)
+    a = [x.to(device).clone().requires_grad_(True) for x in (q, k, v, d)]
+    p0 = None if psi0 is None else psi0.to(device).clone().requires_grad_(True)
+    o, s = SSSDScanFunction.apply(*a, p0)
+    loss = (o.float() * w_o.to(device)).sum()
+    if sgrad:
+        loss = loss + (s * w_s.to(device)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    got = [x.grad for x in a] + [None if p0 is None else p0.grad]
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    for name, g_, r_ in zip(("dq", "dk", "dv", "ddelta", "dpsi0"), got, ref):
+        if r_ is None:
+            assert g_ is None
+            continue
+        e = _rel(g_.float().cpu(), r_)
+        print(f"[bwd {dtype} B{B} T{T} H{H} D{D}] {name} rel {e:.2e}", flush=True)
+        assert e <= tol, name
+
+
+def test_scan_backward_long_sequence(device):
+    """T = 1024: the reverse rebuild of the states stays accurate over a long sequence."""
+    from verace_amd import SSSDScanFunction
+    print("[case] bwd long T=1024", flush=True)
+    B, T, H, D = 1, 1024, 1, 128
+    q, k, v, d, psi0, w_o, w_s = _inputs(B, T, H, D, seed=77, dtype=torch.float32)
+    ref = _oracle(q, k, v, d, None, w_o, w_s, True)
+    a = [x.to(device).clone().requires_grad_(True) for x in (q, k, v, d)]
+    o, s = SSSDScanFunction.apply(*a, None)
+    ((o * w_o.to(device)).sum() + (s * w_s.to(device)).sum()).backward()
+    torch.cuda.synchronize()
+    for name, x, r_ in zip(("dq", "dk", "dv", "ddelta"), a, ref):
+        e = _rel(x.grad.cpu(), r_)
+        print(f"[bwd long] {name} rel {e:.2e}", flush=True)
+        assert e <= 1e-5, name
+
+
+def test_module_training_gradients(device):
+    """SSSDAttention with inputs that require grad (the reference's training path):
+    every parameter gradient, dx and d initial_state against the fp64 eager module."""
+    from verace_amd import SSSDAttention
+    print("[case] bwd module", flush=True)
+    torch.manual_seed(0)
+    hidden, H, D = 256, 2, 128
+    m = SSSDAttention(hidden, H, D).to(device)
+    g = torch.Generator().manual_seed(1)
+    B, T = 2, 48
+    x = torch.randn(B, T, hidden, generator=g)
+    st0 = torch.linalg.qr(torch.randn(B, H, D, D, generator=g))[0]
+    mask = torch.rand(B, T, generator=g) > 0.2
+    wy = torch.randn(B, T, hidden, generator=g)
+    ws = torch.randn(B, H, D, D, generator=g)
+    xd = x.to(device).requires_grad_(True)
+    sd = st0.to(device).requires_grad_(True)
+    y, s = m(xd, initial_state=sd, return_state=True, active_mask=mask.to(device))
+    ((y * wy.to(device)).sum() + (s * ws.to(device)).sum()).backward()
+    torch.cuda.synchronize()
+    params = {n: p.detach().cpu().double().clone().requires_grad_(True) for n, p in m.named_parameters()}
+    xr = x.double().requires_grad_(True)
+    sr = st0.double().requires_grad_(True)
+    yr, s_r = sssd_eager.sssd_module_forward(params, xr, H, D, sr, True, mask,
+                                            compute_dtype=torch.float64)
+    ((yr * wy.double()).sum() + (s_r * ws.double()).sum()).backward()
+    for n, p in m.named_parameters():
+        e = _rel(p.grad.cpu(), params[n].grad)
+        print(f"[bwd module] {n} rel {e:.2e}", flush=True)
+        assert e <= 1e-4, n
+    for name, got, r_ in (("x", xd.grad, xr.grad), ("initial_state", sd.grad, sr.grad)):
+        e = _rel(got.cpu(), r_)
+        print(f"[bwd module] d{name} rel {e:.2e}", flush=True)
+        assert e <= 1e-4, name

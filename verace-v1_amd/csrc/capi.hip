@@ -80,6 +80,42 @@ int vmi_sssd_scan_fwd(const void* q, const void* k, const void* v, const void* d
                                        workspace_bytes, s));
 }
 
+int vmi_sssd_scan_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, size_t* bytes) {
+  if (bytes == nullptr || B < 0 || T < 0 || H < 0 || D < 1) return VMI_ERR_INVALID_ARG;
+  if (!vmi::sssd_bwd_supported(D)) return VMI_ERR_UNSUPPORTED;
+  *bytes = vmi::sssd_bwd_workspace_bytes(B, T, H, D);
+  return VMI_OK;
+}
+
+int vmi_sssd_scan_bwd(const void* q, const void* k, const void* v, const void* delta,
+                      int io_dtype, int delta_dtype, const float* psi_T, const void* d_out,
+                      int d_out_dtype, const float* d_psi_T, void* dq, void* dk, void* dv,
+                      void* d_delta, float* d_psi0, int64_t B, int64_t T, int64_t H, int64_t D,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  if (!valid_dtype(io_dtype) || !valid_dtype(delta_dtype) || !valid_dtype(d_out_dtype))
+    return VMI_ERR_INVALID_ARG;
+  if (B < 0 || T < 0 || H < 0 || D < 1) return VMI_ERR_INVALID_ARG;
+  if (!vmi::sssd_bwd_supported(D)) return VMI_ERR_UNSUPPORTED;
+  if (B * H > INT32_MAX || B * T * H > INT32_MAX) return VMI_ERR_INVALID_ARG;
+  if (psi_T == nullptr) return VMI_ERR_INVALID_ARG;
+  if (T > 0 && (q == nullptr || k == nullptr || v == nullptr || delta == nullptr ||
+                d_out == nullptr || dq == nullptr || dk == nullptr || dv == nullptr ||
+                d_delta == nullptr))
+    return VMI_ERR_INVALID_ARG;
+  const size_t state_bytes = static_cast<size_t>(B * H) * D * D * sizeof(float);
+  if (d_psi0 != nullptr && (ranges_overlap(d_psi0, state_bytes, psi_T, state_bytes) ||
+                            (d_psi_T != nullptr && ranges_overlap(d_psi0, state_bytes, d_psi_T, state_bytes))))
+    return VMI_ERR_ALIAS;
+  const size_t need = vmi::sssd_bwd_workspace_bytes(B, T, H, D);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return VMI_ERR_WORKSPACE;
+  if (B == 0 || H == 0) return VMI_OK;
+  return hip_status(vmi::launch_sssd_bwd(q, k, v, delta, io_dtype, delta_dtype, psi_T, d_out,
+                                         d_out_dtype, d_psi_T, dq, dk, dv, d_delta, d_psi0,
+                                         static_cast<int>(B), static_cast<int>(T),
+                                         static_cast<int>(H), static_cast<int>(D), workspace,
+                                         static_cast<hipStream_t>(stream)));
+}
+
 int vmi_sssd_scan_fused_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int io_dtype,
                                         size_t* bytes) {
   if (bytes == nullptr || B < 0 || T < 0 || H < 0 || D < 1 || !valid_dtype(io_dtype))

@@ -3,9 +3,15 @@
 // loads.
 #pragma once
 #include "vmi_common.h"
+#include "vmi_lanes.h"
 
 namespace vmi {
 namespace cham {
+
+using vmi::dpp_f32;
+using vmi::half_pair_sum;
+using vmi::row16_sum;
+using vmi::row_pair_sum;
 
 struct NCoef {
   float n11r, n11i, n12r, n12i, n22r, n22i;
@@ -28,30 +34,6 @@ __device__ __forceinline__ NCoef cayley_n(float gamma, float kk, float vv, float
   mul(g2 * kv, g, n.n12r, n.n12i);
   mul(-g2 * kk, 0.f, n.n22r, n.n22i);
   return n;
-}
-
-// Sum over the 16 lanes of a DPP row, result in every lane of the row.
-template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float row16_sum(float x) {
-  x += dpp_f32<0xB1>(x);   // quad_perm(1, 0, 3, 2)
-  x += dpp_f32<0x4E>(x);   // quad_perm(2, 3, 0, 1)
-  x += dpp_f32<0x141>(x);  // row_half_mirror
-  x += dpp_f32<0x140>(x);  // row_mirror
-  return x;
-}
-// Sum of the two 16-lane rows of each 32-lane half: v_permlane16_swap exchanges rows 1
-// and 0 (3 and 2) between its two operands, so the two results add to row0 + row1.
-__device__ __forceinline__ float row_pair_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// Sum of the two 32-lane halves of a wave (v_permlane32_swap, the same pattern).
-__device__ __forceinline__ float half_pair_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i) { return io<T>::load(p, i); }

@@ -127,6 +127,15 @@ hipError_t launch_cham_wide(const void* q, const void* k, const void* v, const v
                             void* out, float* hr_out, float* hi_out, int B, int T, int h,
                             void* workspace, hipStream_t stream);
 
+// sssd_bwd.hip: backward of the scan (dq, dk, dv, ddelta, dPsi_0 from dOut, dPsi_T).
+bool sssd_bwd_supported(int64_t D);
+size_t sssd_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D);
+hipError_t launch_sssd_bwd(const void* q, const void* k, const void* v, const void* delta,
+                           int io_dtype, int delta_dtype, const float* psi_T, const void* dout,
+                           int dout_dtype, const float* dpsi_T, void* dq, void* dk, void* dv,
+                           void* ddelta, float* dpsi0, int B, int T, int H, int D, void* ws,
+                           hipStream_t stream);
+
 // cham_ns.hip: Newton-Schulz unitary retraction.
 size_t ns_workspace_bytes(int64_t batch, int64_t n);
 hipError_t launch_ns_retraction(const float* h_real, const float* h_imag, float* out_real,

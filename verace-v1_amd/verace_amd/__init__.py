@@ -4,6 +4,9 @@ Drop-in replacements for the reference's SSSD hot path:
 
 * ``SSSDAttention``            <- ``verace_v1.modules.sssd_attention.SSSDAttention``
 * ``launch_sssd_hip_scan``     <- ``verace_v1.serving.triton_kernels.launch_sssd_triton_scan``
+* ``SSSDScanFunction`` / ``sssd_scan`` / ``launch_sssd_hip_scan_bwd``
+                               -- the scan with its backward (training; the reference
+                                  differentiates its eager path instead)
 * ``sssd_step_``               -- in-place single-token decode step (opt-in)
 * ``SSSDStateCache``           -- per-layer decode state pools with copy-on-write
                                   branches (replaces the ``layer_states`` lists of
@@ -11,20 +14,24 @@ Drop-in replacements for the reference's SSSD hot path:
 * ``newton_schulz_unitary_retraction`` / ``parallel_newton_schulz_retraction``
                                <- ``verace_v1.modules.cham_memory`` (same names)
 * ``launch_cham_hip_update``   <- ``verace_v1.serving.triton_kernels.launch_cham_triton_update``
-                               (CHAM holographic scan, holographic_dim <= 128)
+                               (CHAM holographic scan, holographic_dim <= 1024)
 * ``HAS_HIP``                  <- ``verace_v1.serving.triton_kernels.HAS_TRITON``
 
 All compute runs in ``libverace_sssd.so`` (C ABI: ``include/verace_sssd.h``).
 """
-from .hip_kernels import (HAS_HIP, launch_cham_hip_update, launch_sssd_hip_scan,
+from .hip_kernels import (HAS_HIP, SSSDScanFunction, launch_cham_hip_update,
+                          launch_sssd_hip_scan, launch_sssd_hip_scan_bwd,
                           newton_schulz_unitary_retraction, parallel_newton_schulz_retraction,
-                          sssd_step_)
+                          sssd_scan, sssd_step_)
 from .sssd_attention import SSSDAttention
 from .state_cache import SlotTable, SSSDStateCache
 
 __all__ = [
     "HAS_HIP",
     "SSSDAttention",
+    "SSSDScanFunction",
+    "sssd_scan",
+    "launch_sssd_hip_scan_bwd",
     "SSSDStateCache",
     "SlotTable",
     "launch_sssd_hip_scan",

@@ -38,6 +38,8 @@ EXPORTED = (
     "vmi_state_cache_step",
     "vmi_cham_scan_workspace_bytes",
     "vmi_cham_scan_fwd",
+    "vmi_sssd_scan_bwd_workspace_bytes",
+    "vmi_sssd_scan_bwd",
     "vmi_cham_ns_workspace_bytes",
     "vmi_cham_ns_retraction",
 )
@@ -94,6 +96,11 @@ def _declare(lib):
     lib.vmi_cham_scan_fwd.argtypes = [vp, vp, vp, vp, i32, i32, vp, vp, vp, vp, vp, i64, i64, i64,
                                       vp, sz, vp]
     lib.vmi_cham_scan_fwd.restype = i32
+    lib.vmi_sssd_scan_bwd_workspace_bytes.argtypes = [i64, i64, i64, i64, ctypes.POINTER(sz)]
+    lib.vmi_sssd_scan_bwd_workspace_bytes.restype = i32
+    lib.vmi_sssd_scan_bwd.argtypes = [vp, vp, vp, vp, i32, i32, vp, vp, i32, vp, vp, vp, vp, vp,
+                                      vp, i64, i64, i64, i64, vp, sz, vp]
+    lib.vmi_sssd_scan_bwd.restype = i32
     lib.vmi_cham_ns_workspace_bytes.argtypes = [i64, i64, ctypes.POINTER(sz)]
     lib.vmi_cham_ns_workspace_bytes.restype = i32
     lib.vmi_cham_ns_retraction.argtypes = [vp, vp, vp, vp, i64, i64, i32, vp, sz, vp]

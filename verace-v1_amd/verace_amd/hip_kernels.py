@@ -99,6 +99,83 @@ def launch_sssd_hip_scan(
     return out, psi_out
 
 
+def launch_sssd_hip_scan_bwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    delta: torch.Tensor,
+    psi_T: torch.Tensor,
+    d_out: torch.Tensor,
+    d_psi_T: Optional[torch.Tensor] = None,
+    need_d_psi0: bool = True,
+):
+    """Gradients of :func:`launch_sssd_hip_scan` (the eager autograd of
+    ``sssd_attention.py:144-175`` that the reference trains through).
+
+    q, k, v: [B, T, H, D] as given to the forward; delta: [B, T, H]; psi_T: the forward's
+    final state [B, H, D, D] fp32; d_out: dL/dout [B, T, H, D]; d_psi_T: dL/dpsi_T or None.
+    Returns (dq, dk, dv in q's dtype, d_delta in delta's dtype, d_psi0 fp32 or None).
+    """
+    _require_device(q, "q")
+    b, s, h, d_k = q.shape
+    if delta.dim() == 4 and delta.shape[-1] == 1:
+        delta = delta.squeeze(-1)
+    io_code = _lib.dtype_code(q.dtype)
+    q_c = q.contiguous()
+    k_c = k.to(q.dtype).contiguous()
+    v_c = v.to(q.dtype).contiguous()
+    delta_c = delta.contiguous()
+    d_code = _lib.dtype_code(delta_c.dtype)
+    do_c = d_out.contiguous()
+    go_code = _lib.dtype_code(do_c.dtype)
+    psi_c = psi_T.to(torch.float32).contiguous()
+    dpsi_c = None if d_psi_T is None else d_psi_T.to(torch.float32).contiguous()
+    dq = torch.empty_like(q_c)
+    dk = torch.empty_like(q_c)
+    dv = torch.empty_like(q_c)
+    dd = torch.empty_like(delta_c)
+    dpsi0 = torch.empty(b, h, d_k, d_k, device=q.device, dtype=torch.float32) if need_d_psi0 else None
+    lib = _lib.load()
+    ws_bytes = ctypes.c_size_t(0)
+    _lib.check(lib.vmi_sssd_scan_bwd_workspace_bytes(b, s, h, d_k, ctypes.byref(ws_bytes)),
+               "vmi_sssd_scan_bwd_workspace_bytes")
+    ws = torch.empty(ws_bytes.value, device=q.device, dtype=torch.uint8) if ws_bytes.value else None
+    _lib.check(lib.vmi_sssd_scan_bwd(_ptr(q_c), _ptr(k_c), _ptr(v_c), _ptr(delta_c), io_code, d_code,
+                                     _ptr(psi_c), _ptr(do_c), go_code, _ptr(dpsi_c), _ptr(dq),
+                                     _ptr(dk), _ptr(dv), _ptr(dd), _ptr(dpsi0), b, s, h, d_k,
+                                     _ptr(ws), ws_bytes.value, _lib.stream_handle(q.device)),
+               "vmi_sssd_scan_bwd")
+    return dq, dk, dv, dd, dpsi0
+
+
+class SSSDScanFunction(torch.autograd.Function):
+    """The scan as an autograd node: forward :func:`launch_sssd_hip_scan`, backward
+    :func:`launch_sssd_hip_scan_bwd` (only the inputs and the final state are kept)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, delta, initial_state):
+        out, psi = launch_sssd_hip_scan(q, k, v, delta, initial_state)
+        ctx.save_for_backward(q, k, v, delta, psi)
+        ctx.init_dtype = None if initial_state is None else initial_state.dtype
+        return out, psi
+
+    @staticmethod
+    def backward(ctx, d_out, d_psi):
+        q, k, v, delta, psi = ctx.saved_tensors
+        need0 = ctx.init_dtype is not None and ctx.needs_input_grad[4]
+        dq, dk, dv, dd, dpsi0 = launch_sssd_hip_scan_bwd(q, k, v, delta, psi, d_out, d_psi, need0)
+        return (dq, dk.to(k.dtype), dv.to(v.dtype), dd.view(delta.shape),
+                None if dpsi0 is None else dpsi0.to(ctx.init_dtype))
+
+
+def sssd_scan(q, k, v, delta, initial_state=None):
+    """:func:`launch_sssd_hip_scan`, differentiable when autograd needs it."""
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad
+                                       for t in (q, k, v, delta, initial_state)):
+        return SSSDScanFunction.apply(q, k, v, delta, initial_state)
+    return launch_sssd_hip_scan(q, k, v, delta, initial_state)
+
+
 _RMS_EPS = {}
 
 

@@ -13,9 +13,10 @@ fp16, head_dim 128, T >= 32) the four projections are one GEMM against the stack
 weights and the L2 normalisation, ``delta = 0.1 * sigmoid(w_delta x)``, the halted-token
 mask and ``head_rmsnorm`` happen inside the scan kernels
 (:func:`launch_sssd_hip_scan_fused`); elsewhere they run as torch ops around
-:func:`launch_sssd_hip_scan`.  ``w_out`` follows.  Only device tensors that do not require grad are accepted -- the reference's
-eager autograd path (:138-176) is the training path, for which no backward kernel
-exists here, so such calls raise instead of silently running something else.
+:func:`launch_sssd_hip_scan`.  ``w_out`` follows.  When autograd needs gradients (the
+reference's training path, its eager autograd at :138-176) the projections and the
+RMSNorm stay torch ops and the scan is :class:`SSSDScanFunction`, whose backward runs
+on the HIP backward kernels.
 """
 from __future__ import annotations
 
@@ -25,7 +26,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .hip_kernels import fused_scan_supported, launch_sssd_hip_scan, launch_sssd_hip_scan_fused
+from .hip_kernels import (fused_scan_supported, launch_sssd_hip_scan, launch_sssd_hip_scan_fused,
+                          sssd_scan)
 
 
 class SSSDAttention(nn.Module):
@@ -99,11 +101,16 @@ class SSSDAttention(nn.Module):
         if not x.is_cuda:
             raise RuntimeError("verace_amd.SSSDAttention runs on a HIP device only; "
                                "move the module and inputs to the GPU")
-        if x.requires_grad:
-            raise RuntimeError("verace_amd.SSSDAttention has no backward kernel; the reference "
-                               "trains through its eager autograd path (sssd_attention.py:138-176)")
         b, s, _ = x.shape
-        if self._fused(x):
+        # the reference's gate (sssd_attention.py:129): inputs that require grad take the
+        # differentiable path
+        grad = torch.is_grad_enabled() and (
+            x.requires_grad or (initial_state is not None and initial_state.requires_grad))
+        if grad:
+            q, k, v, delta = self.project(x, active_mask)
+            o, psi = sssd_scan(q, k, v, delta, initial_state)
+            o_norm = self.head_rmsnorm(o).view(b, s, self.num_heads * self.head_dim)
+        elif self._fused(x):
             o_norm, psi = self._scan_fused(x, initial_state, active_mask)
             o_norm = o_norm.view(b, s, self.num_heads * self.head_dim)
         else:
