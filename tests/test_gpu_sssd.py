@@ -254,7 +254,9 @@ def test_module_matches_reference_golden(device):
                                    atol=1e-5)
 
 
-def test_module_rejects_cpu_and_grad(device):
+def test_module_rejects_cpu_and_grad_without_backward(device):
+    """CPU inputs raise; inputs that require grad raise in the forward when no backward
+    kernel exists for the head_dim (16 here), instead of failing later in backward()."""
     from verace_amd import SSSDAttention
     m = SSSDAttention(hidden_dim=32, num_heads=2, head_dim=16)
     with pytest.raises(RuntimeError):
