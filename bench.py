@@ -326,7 +326,8 @@ def bench_cham(device, iters=5, warmup=2):
     h0 = (Q.real.contiguous().to(device), Q.imag.contiguous().to(device))
     res = {"config": "CHAM scan B=4 T=2048 h=128 fp32"}
     stream = torch.cuda.current_stream(device)
-    for name, init, per_tok in (("identity_start", None, 34), ("initial_hologram", h0, 248)):
+    cases = [("identity_start", None, 34), ("initial_hologram", h0, 248)]
+    for name, init, per_tok in cases:
         for _ in range(warmup):
             launch_cham_hip_update(q, k, v, gam, init)
         torch.cuda.synchronize()
@@ -344,6 +345,31 @@ def bench_cham(device, iters=5, warmup=2):
             "valu_tflops": round(flops / (us * 1e-6) / 1e12, 2),
             "valu_frac": round(flops / (us * 1e-6) / 78.6e12, 4),
         }
+    # the reference's default holographic_dim (1024): prefill from the identity, and one
+    # decode token for 64 sequences with their held holograms (R_0 = NS_3(H_0) per call)
+    for name, (Bw, Tw, init_w) in (("h1024_identity_B4_T2048", (4, 2048, False)),
+                                   ("h1024_decode_B64_T1", (64, 1, True))):
+        hw = 1024
+        qw = nrm(torch.randn(Bw, Tw, hw, generator=g), dim=-1).to(device)
+        kw = nrm(torch.randn(Bw, Tw, hw, generator=g), dim=-1).to(device)
+        vw = nrm(torch.randn(Bw, Tw, hw, generator=g), dim=-1).to(device)
+        gw = (0.1 * torch.sigmoid(torch.randn(Bw, Tw, generator=g))).to(device)
+        iw = None
+        if init_w:
+            Qw = torch.linalg.qr(torch.complex(torch.randn(Bw, hw, hw), torch.randn(Bw, hw, hw)))[0]
+            iw = (Qw.real.contiguous().to(device), Qw.imag.contiguous().to(device))
+            del Qw
+        launch_cham_hip_update(qw, kw, vw, gw, iw)
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        ev[0].record(stream)
+        for i in range(3):
+            launch_cham_hip_update(qw, kw, vw, gw, iw)
+            ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        us = statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(3))
+        res[name] = {"us_median": round(us, 1), "tokens_per_s": round(Bw * Tw / (us * 1e-6), 1)}
+        del qw, kw, vw, gw, iw
     return res
 
 

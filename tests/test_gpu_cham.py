@@ -165,3 +165,29 @@ def test_cham_wide_chaining(device):
     o2, r2, i2 = _run(device, q[:, 77:], k[:, 77:], v[:, 77:], gam[:, 77:], (r1, i1))
     assert _rel(torch.cat([o1, o2], 1), out) <= 1e-5
     assert _rel(r2, hr) <= 1e-5 and _rel(i2, hi) <= 1e-5
+
+
+@pytest.mark.parametrize("B,T,h", [(2, 1, 256), (1, 16, 300), (3, 5, 1024)])
+def test_cham_wide_short_calls_with_initial_hologram(device, B, T, h):
+    """T <= 16 with an initial hologram: the readout goes through the matrix-vector chain
+    f_3(H_0^H H_0) q instead of NS_3(H_0); non-unitary H_0 included."""
+    print(f"[case] cham wide short B={B} T={T} h={h}", flush=True)
+    g = torch.Generator().manual_seed(B + T + h)
+    Q = torch.linalg.qr(torch.complex(torch.randn(B, h, h, generator=g), torch.randn(B, h, h, generator=g)))[0]
+    Q = Q * (1.0 + 0.03 * torch.randn(B, h, h, generator=g))
+    _check(device, B, T, h, seed=T + h, h0=(Q.real.contiguous(), Q.imag.contiguous()), label="wide-short")
+
+
+def test_cham_wide_decode_steps_chain_to_prefill(device):
+    """Prefill then single-token calls through the held hologram equal one long call."""
+    print("[case] cham wide decode chain", flush=True)
+    B, T, h = 2, 68, 512
+    q, k, v, gam = _inputs(B, T, h, 31)
+    out, hr, hi = _run(device, q, k, v, gam)
+    o, r, i = _run(device, q[:, :65], k[:, :65], v[:, :65], gam[:, :65])
+    outs = [o]
+    for t in range(65, T):
+        o, r, i = _run(device, q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1], gam[:, t:t + 1], (r, i))
+        outs.append(o)
+    assert _rel(torch.cat(outs, 1), out) <= 1e-5
+    assert _rel(r, hr) <= 1e-5 and _rel(i, hi) <= 1e-5

@@ -170,30 +170,48 @@ __global__ __launch_bounds__(CNT) void wide_cols_kernel(
     const IO* __restrict__ k, const IO* __restrict__ v, const float* __restrict__ coef,
     const float* __restrict__ i0r, const float* __restrict__ i0i, const float* __restrict__ i1r,
     const float* __restrict__ i1i, float* __restrict__ snap, float* __restrict__ fr,
-    float* __restrict__ fi, int T, int h, int nstates) {
+    float* __restrict__ fi, int T, int h, int nstates, int snap_on) {
   constexpr int HP = LPC * RPL, CPW = 64 / LPC;  // rows, columns per wave
+  constexpr int CPG = NW * CPW;                  // columns per workgroup
   __shared__ Stage<HP> st;
   const int tid = threadIdx.x, lane = tid & 63, ll = lane % LPC;
   const int b = blockIdx.x;
-  const int c = (blockIdx.y * NW + (tid >> 6)) * CPW + lane / LPC;
+  const int cl = (tid >> 6) * CPW + lane / LPC;  // column within the workgroup
+  const int c0 = blockIdx.y * CPG;
+  const int c = c0 + cl;
   const int z = blockIdx.z;
   const bool colok = c < h;
-  const bool snaps = z == nstates - 1;  // this state is the readout state
+  const bool snaps = snap_on && z == nstates - 1;  // this state is the readout state
   const bool final_ = z == 0;           // this state is the exported raw state
   const int64_t hh = static_cast<int64_t>(h) * h;
   const int nch = (T + C2 - 1) / C2;
   const float* ir = z == 0 ? i0r : i1r;
   const float* ii = z == 0 ? i0i : i1i;
 
+  // The row-major [h][h] states pass through LDS as the workgroup's [CPG][HP] column
+  // tiles (the stage buffers, free outside the token loop): global rows are read and
+  // written as CPG contiguous floats instead of one float per lane at a stride of h.
+  float* tr = &st.k[0][0][0];
+  float* ti = &st.v[0][0][0];
   float xr[RPL], xi[RPL];
+  if (ir) {
+    for (int e = tid; e < h * CPG; e += CNT) {
+      const int r = e / CPG, cc = e % CPG;
+      const bool ok = c0 + cc < h;
+      const int64_t off = b * hh + static_cast<int64_t>(r) * h + c0 + cc;
+      tr[cc * HP + r] = ok ? ir[off] : 0.f;
+      ti[cc * HP + r] = ok ? ii[off] : 0.f;
+    }
+    __syncthreads();
+  }
 #pragma unroll
   for (int i = 0; i < RPL; ++i) {
     const int r = 4 * LPC * (i / 4) + 4 * ll + (i & 3);
     const bool ok = colok && r < h;
-    const int64_t off = b * hh + static_cast<int64_t>(r) * h + c;
-    xr[i] = ok ? (ir ? ir[off] : (r == c ? 1.f : 0.f)) : 0.f;
-    xi[i] = ok ? (ii ? ii[off] : 0.f) : 0.f;
+    xr[i] = ok ? (ir ? tr[cl * HP + r] : (r == c ? 1.f : 0.f)) : 0.f;
+    xi[i] = ok ? (ii ? ti[cl * HP + r] : 0.f) : 0.f;
   }
+  __syncthreads();  // the tiles are reused by the token stages
   auto write_snap = [&](int n) {
     if (!snaps || !colok) return;
     float* d = snap + ((static_cast<int64_t>(b) * nch + n) * 2) * h * HP + static_cast<int64_t>(c) * HP;
@@ -222,13 +240,20 @@ __global__ __launch_bounds__(CNT) void wide_cols_kernel(
     if (s + 1 < nst) sg.commit(st, (s + 1) & 1, (s + 1) * CHS, T, h, tid);
     __syncthreads();
   }
-  if (final_ && colok) {
+  if (final_) {  // (uniform over the workgroup)
 #pragma unroll
     for (int i = 0; i < RPL; ++i) {
       const int r = 4 * LPC * (i / 4) + 4 * ll + (i & 3);
-      if (r < h) {
-        fr[b * hh + static_cast<int64_t>(r) * h + c] = xr[i];
-        fi[b * hh + static_cast<int64_t>(r) * h + c] = xi[i];
+      tr[cl * HP + r] = xr[i];
+      ti[cl * HP + r] = xi[i];
+    }
+    __syncthreads();
+    for (int e = tid; e < h * CPG; e += CNT) {
+      const int r = e / CPG, cc = e % CPG;
+      if (c0 + cc < h) {
+        const int64_t off = b * hh + static_cast<int64_t>(r) * h + c0 + cc;
+        fr[off] = tr[cc * HP + r];
+        fi[off] = ti[cc * HP + r];
       }
     }
   }
@@ -371,28 +396,203 @@ __global__ __launch_bounds__(CNT) void wide_apply_kernel(
   }
 }
 
+// ---------------------------------------------------------------- short calls: f_3(A_0) q
+// For a few tokens with an initial hologram, NS_3(H_0) (O(h^3)) costs far more than the
+// matrix-free readout: y_t = f_3(A_0) q_t by the 13 applications of A_0 = H_0^H H_0 of
+// cham_scan.hip's schedule, then z_t = H_0 y_t (= R_0 q_t).  Each application is two
+// complex matrix-vector products over all T tokens (batched over the sequences), one
+// launch each: bound by reading H_0.
+//
+// Vectors are complex [2][HP] planes at base + b sb + t st + p sp.  Workgroup (ob, b):
+// 64 outputs o of every token; the reduction index runs in tiles of 64 through LDS
+// (rows of H read coalesced), thread (o = tid / 4, quarter) sums every 4th index of a
+// tile, a quad of lanes combines at the end.
+constexpr int MVT = 16;  // the most tokens the short route takes
+
+struct VecRef {
+  float* p;
+  int64_t sb, st, sp;
+};
+
+template <bool CONJT>
+__global__ __launch_bounds__(256) void wide_cmv_kernel(
+    const float* __restrict__ Hr, const float* __restrict__ Hi, VecRef x, VecRef out, int T,
+    int h, VecRef cur, VecRef x2, VecRef x3, float c_in, float c_x2, float c_x3, float c_a,
+    int set_x2) {
+  __shared__ float sr[64][65], si[64][65];
+  __shared__ float sx[MVT][2][64];
+  const int tid = threadIdx.x, o_l = tid >> 2, qd = tid & 3;
+  const int o0 = blockIdx.x * 64, b = blockIdx.y;
+  const int64_t hh = static_cast<int64_t>(h) * h;
+  const float* hr = Hr + b * hh;
+  const float* hi = Hi + b * hh;
+  float ar[MVT], ai[MVT];
+#pragma unroll
+  for (int t = 0; t < MVT; ++t) ar[t] = ai[t] = 0.f;
+  // tile element e = tid + 256 s is (row, col) = (e / 64, e % 64) of H, coalesced over col;
+  // CONJT: rows = reduction index k, cols = outputs o; otherwise rows = outputs, cols = k.
+  // The next tile is loaded into registers (clamped addresses, masked at the LDS store)
+  // while the current one is used.
+  float rr_[16], ri_[16];
+  auto tile_ok = [&](int k0, int s_) {
+    const int e = tid + 256 * s_, rr = e >> 6, cc = e & 63;
+    return (CONJT ? k0 : o0) + rr < h && (CONJT ? o0 : k0) + cc < h;
+  };
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int s_ = 0; s_ < 16; ++s_) {
+      const int e = tid + 256 * s_, rr = e >> 6, cc = e & 63;
+      const int gr = (CONJT ? k0 : o0) + rr, gc = (CONJT ? o0 : k0) + cc;
+      const int64_t off = tile_ok(k0, s_) ? static_cast<int64_t>(gr) * h + gc : 0;
+      rr_[s_] = hr[off];
+      ri_[s_] = hi[off];
+    }
+  };
+  auto commit = [&](int k0) {
+#pragma unroll
+    for (int s_ = 0; s_ < 16; ++s_) {
+      const int e = tid + 256 * s_, rr = e >> 6, cc = e & 63;
+      const bool ok = tile_ok(k0, s_);
+      sr[rr][cc] = ok ? rr_[s_] : 0.f;
+      si[rr][cc] = ok ? ri_[s_] : 0.f;
+    }
+    for (int e = tid; e < T * 128; e += 256) {
+      const int t = e >> 7, p = (e >> 6) & 1, kk = e & 63;
+      sx[t][p][kk] = k0 + kk < h ? x.p[b * x.sb + t * x.st + p * x.sp + k0 + kk] : 0.f;
+    }
+  };
+  fetch(0);
+  for (int k0 = 0; k0 < h; k0 += 64) {
+    commit(k0);
+    __syncthreads();
+    if (k0 + 64 < h) fetch(k0 + 64);
+#pragma unroll 4
+    for (int j = 0; j < 16; ++j) {
+      const int kk = 4 * j + qd;
+      // CONJT: conj(H[k][o]);  else H[o][k]
+      const float mr = CONJT ? sr[kk][o_l] : sr[o_l][kk];
+      const float mi = CONJT ? -si[kk][o_l] : si[o_l][kk];
+#pragma unroll
+      for (int t = 0; t < MVT; ++t) {
+        if (t < T) {
+          const float xr_ = sx[t][0][kk], xi_ = sx[t][1][kk];
+          ar[t] = fmaf(mr, xr_, fmaf(-mi, xi_, ar[t]));
+          ai[t] = fmaf(mr, xi_, fmaf(mi, xr_, ai[t]));
+        }
+      }
+    }
+    __syncthreads();
+  }
+  const int o = o0 + o_l;
+#pragma unroll
+  for (int t = 0; t < MVT; ++t) {
+    if (t < T) {
+      float r_ = ar[t], i_ = ai[t];
+      r_ += dpp_f32<0xB1>(r_); i_ += dpp_f32<0xB1>(i_);
+      r_ += dpp_f32<0x4E>(r_); i_ += dpp_f32<0x4E>(i_);
+      if (qd == 0) {
+        const bool ok = o < h;
+        const int64_t oc = b * cur.sb + t * cur.st + o;
+        float nr = c_a * r_, ni = c_a * i_;
+        if (c_in != 0.f) { nr = fmaf(c_in, cur.p[oc], nr); ni = fmaf(c_in, cur.p[oc + cur.sp], ni); }
+        if (c_x2 != 0.f) {
+          const int64_t o2 = b * x2.sb + t * x2.st + o;
+          nr = fmaf(c_x2, x2.p[o2], nr); ni = fmaf(c_x2, x2.p[o2 + x2.sp], ni);
+        }
+        if (c_x3 != 0.f) {
+          const int64_t o3 = b * x3.sb + t * x3.st + o;
+          nr = fmaf(c_x3, x3.p[o3], nr); ni = fmaf(c_x3, x3.p[o3 + x3.sp], ni);
+        }
+        const int64_t oo = b * out.sb + t * out.st + o;
+        out.p[oo] = ok ? nr : 0.f;
+        out.p[oo + out.sp] = ok ? ni : 0.f;
+        if (set_x2) {
+          const int64_t o2 = b * x2.sb + t * x2.st + o;
+          x2.p[o2] = ok ? nr : 0.f;
+          x2.p[o2 + x2.sp] = ok ? ni : 0.f;
+        }
+      }
+    }
+  }
+}
+
+// cur = X2 = X3 = q (imaginary parts zero), rows past h zero
+template <typename IO>
+__global__ __launch_bounds__(256) void wide_vec_init_kernel(const IO* __restrict__ q, VecRef cur,
+                                                            VecRef x2, VecRef x3, int T, int h,
+                                                            int HP) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (e >= static_cast<int64_t>(T) * HP) return;
+  const int t = static_cast<int>(e / HP), r = static_cast<int>(e % HP);
+  const float x = r < h ? io<IO>::load(q, (static_cast<int64_t>(b) * T + t) * h + r) : 0.f;
+  cur.p[b * cur.sb + t * cur.st + r] = x;
+  cur.p[b * cur.sb + t * cur.st + cur.sp + r] = 0.f;
+  x2.p[b * x2.sb + t * x2.st + r] = x;
+  x2.p[b * x2.sb + t * x2.st + x2.sp + r] = 0.f;
+  x3.p[b * x3.sb + t * x3.st + r] = x;
+  x3.p[b * x3.sb + t * x3.st + x3.sp + r] = 0.f;
+}
+
 // ---------------------------------------------------------------- host side
 int padded(int h) { return h <= 256 ? 256 : (h <= 512 ? 512 : 1024); }
 
 struct WideWs {
-  float *coef, *snap, *Z, *r0r, *r0i, *ns;
+  float *coef, *snap, *Z, *r0r, *r0i, *ns, *vec;
   size_t floats;
 };
+// (the short route with an initial hologram uses coef, Z and vec; the long one all but vec)
 WideWs carve(void* base, int64_t B, int64_t T, int64_t h) {
   const int64_t HP = padded(static_cast<int>(h));
   const int64_t nch = (T + C2 - 1) / C2;
-  const int64_t sizes[6] = {B * T * NCF, B * nch * 2 * h * HP, B * nch * 2 * C2 * HP,
-                            B * h * h, B * h * h, 6 * B * h * h};
+  const int64_t sizes[7] = {B * T * NCF, B * nch * 2 * h * HP, B * nch * 2 * C2 * HP,
+                            B * h * h, B * h * h, 6 * B * h * h, 4 * B * MVT * 2 * HP};
   WideWs w;
   float* p = static_cast<float*>(base);
-  float** dst[6] = {&w.coef, &w.snap, &w.Z, &w.r0r, &w.r0i, &w.ns};
+  float** dst[7] = {&w.coef, &w.snap, &w.Z, &w.r0r, &w.r0i, &w.ns, &w.vec};
   size_t off = 0;
-  for (int i = 0; i < 6; ++i) {
+  for (int i = 0; i < 7; ++i) {
     *dst[i] = p ? p + off : nullptr;
     off += (sizes[i] + 63) / 64 * 64;  // 256-byte aligned pieces
   }
   w.floats = off;
   return w;
+}
+
+// Short route: Z = H_0 f_3(A_0) Q by the matrix-vector chain (one chunk, T <= MVT).
+template <typename IO>
+hipError_t short_readout(const void* q, const float* h0r, const float* h0i, int B, int T, int h,
+                         int HP, const WideWs& w, hipStream_t stream) {
+  const int64_t vs = static_cast<int64_t>(B) * MVT * 2 * HP;
+  auto vec = [&](int i) {
+    return VecRef{w.vec + i * vs, static_cast<int64_t>(T) * 2 * HP, 2 * HP, HP};
+  };
+  const VecRef cur = vec(0), wv = vec(1), x2 = vec(2), x3 = vec(3);
+  const VecRef zref{w.Z, 2 * static_cast<int64_t>(C2) * HP, HP, static_cast<int64_t>(C2) * HP};
+  hipLaunchKernelGGL((wide_vec_init_kernel<IO>), dim3((T * HP + 255) / 256, B), dim3(256), 0, stream,
+                     static_cast<const IO*>(q), cur, x2, x3, T, h, HP);
+  hipError_t e = hipGetLastError();
+  const dim3 grid(HP / 64, B);
+  for (int st = 0; st < 13 && e == hipSuccess; ++st) {
+    // the schedule of cham_scan.hip's apply_f3: next = c_in cur + c_x2 X2 + c_x3 X3 + c_a A cur
+    const int s4 = st < 8 ? (st & 3) : (st == 8 ? 4 : (st - 9) & 3);
+    float c_in, c_x2, c_x3, c_a;
+    if (s4 == 0 || s4 == 1) { c_in = 1.5f; c_x2 = 0.f; c_x3 = 0.f; c_a = -0.5f; }
+    else if (s4 == 2) { c_in = 0.f; c_x2 = 3.f; c_x3 = 0.f; c_a = -1.f; }
+    else if (s4 == 3) { c_in = st == 12 ? 0.375f : 0.75f; c_x2 = 0.f; c_x3 = 0.f; c_a = st == 12 ? -0.125f : -0.25f; }
+    else { c_in = 0.f; c_x2 = 0.f; c_x3 = 3.f; c_a = -1.f; }
+    hipLaunchKernelGGL((wide_cmv_kernel<false>), grid, dim3(256), 0, stream, h0r, h0i, cur, wv, T,
+                       h, cur, x2, x3, 0.f, 0.f, 0.f, 1.f, 0);
+    e = hipGetLastError();
+    if (e != hipSuccess) break;
+    hipLaunchKernelGGL((wide_cmv_kernel<true>), grid, dim3(256), 0, stream, h0r, h0i, wv, cur, T,
+                       h, cur, x2, x3, c_in, c_x2, c_x3, c_a, (st == 3 || st == 8) ? 1 : 0);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((wide_cmv_kernel<false>), grid, dim3(256), 0, stream, h0r, h0i, cur, zref, T,
+                     h, cur, x2, x3, 0.f, 0.f, 0.f, 1.f, 0);
+  return hipGetLastError();
 }
 
 template <typename IO, int LPC, int RPL>
@@ -401,15 +601,21 @@ hipError_t launch_rpl(const void* q, const void* k, const void* v, const float* 
                       int h, const WideWs& w, hipStream_t stream) {
   constexpr int HP = LPC * RPL, CPG = NW * 64 / LPC;  // rows, columns per workgroup
   const int nch = (T + C2 - 1) / C2;
-  const int nstates = h0r && nch > 0 ? 2 : 1;
+  const bool shortr = h0r && T <= MVT;
+  const int nstates = h0r && nch > 0 && !shortr ? 2 : 1;
   hipLaunchKernelGGL((wide_cols_kernel<IO, LPC, RPL>), dim3(B, (h + CPG - 1) / CPG, nstates),
                      dim3(CNT), 0, stream, static_cast<const IO*>(k), static_cast<const IO*>(v),
-                     w.coef, h0r, h0i, w.r0r, w.r0i, w.snap, hr_out, hi_out, T, h, nstates);
+                     w.coef, h0r, h0i, w.r0r, w.r0i, w.snap, hr_out, hi_out, T, h, nstates,
+                     shortr ? 0 : 1);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nch == 0) return e;
-  hipLaunchKernelGGL((wide_z_kernel<IO>), dim3(HP / ZT, nch, B), dim3(256), 0, stream,
-                     static_cast<const IO*>(q), w.snap, w.Z, T, h, HP);
-  e = hipGetLastError();
+  if (shortr) {
+    e = short_readout<IO>(q, h0r, h0i, B, T, h, HP, w, stream);
+  } else {
+    hipLaunchKernelGGL((wide_z_kernel<IO>), dim3(HP / ZT, nch, B), dim3(256), 0, stream,
+                       static_cast<const IO*>(q), w.snap, w.Z, T, h, HP);
+    e = hipGetLastError();
+  }
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((wide_apply_kernel<IO, LPC, RPL>), dim3(B, nch, C2 / CPG), dim3(CNT), 0,
                      stream, static_cast<const IO*>(k), static_cast<const IO*>(v), w.coef, w.Z,
@@ -430,7 +636,7 @@ hipError_t launch_typed(const void* q, const void* k, const void* v, const void*
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if (h0r && T > 0) {  // readout state R_0 = NS_3(H_0)
+  if (h0r && T > MVT) {  // readout state R_0 = NS_3(H_0) (short calls: chain in launch_rpl)
     const hipError_t e = launch_ns_retraction(h0r, h0i, w.r0r, w.r0i, B, h, 3, w.ns, stream);
     if (e != hipSuccess) return e;
   }
