@@ -191,3 +191,16 @@ def test_cham_wide_decode_steps_chain_to_prefill(device):
         outs.append(o)
     assert _rel(torch.cat(outs, 1), out) <= 1e-5
     assert _rel(r, hr) <= 1e-5 and _rel(i, hi) <= 1e-5
+
+
+@pytest.mark.parametrize("B,T,h,unitary", [(2, 100, 64, True), (2, 100, 64, False), (1, 130, 128, True),
+                                           (1, 64, 20, False)])
+def test_cham_long_calls_with_initial_hologram(device, B, T, h, unitary):
+    """h <= 128, T >= 64 with an initial hologram: the readout state R_t = P_t NS_3(H_0) is
+    carried beside the raw state."""
+    print(f"[case] cham R-route B={B} T={T} h={h} unitary={unitary}", flush=True)
+    g = torch.Generator().manual_seed(T + h)
+    Q = torch.linalg.qr(torch.complex(torch.randn(B, h, h, generator=g), torch.randn(B, h, h, generator=g)))[0]
+    if not unitary:
+        Q = Q * (1.0 + 0.05 * torch.randn(B, h, h, generator=g))
+    _check(device, B, T, h, seed=T, h0=(Q.real.contiguous(), Q.imag.contiguous()), label="r-route")

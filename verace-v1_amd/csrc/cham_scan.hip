@@ -53,12 +53,18 @@ constexpr int CH = 16;    // tokens per chunk (pass 2 workgroup)
 template <typename IO, typename GT>
 __global__ __launch_bounds__(64) void cham_state_kernel(
     const IO* __restrict__ k, const IO* __restrict__ v, const GT* __restrict__ gamma,
-    const float* __restrict__ h0r, const float* __restrict__ h0i, float* __restrict__ wsr,
-    float* __restrict__ wsi, float* __restrict__ hr_out, float* __restrict__ hi_out, int T,
-    int h) {
+    const float* __restrict__ i0r, const float* __restrict__ i0i, const float* __restrict__ i1r,
+    const float* __restrict__ i1i, float* __restrict__ wsr, float* __restrict__ wsi,
+    float* __restrict__ hr_out, float* __restrict__ hi_out, int T, int h, int nstates) {
   const int lane = threadIdx.x;
   const int l32 = lane & 31;
   const int b = blockIdx.x;
+  // blockIdx.z = 0 carries the raw state (exported), = nstates - 1 the readout state
+  // (its chunk-start states go to the workspace)
+  const int z = blockIdx.z;
+  const bool snaps = z == nstates - 1, final_ = z == 0;
+  const float* h0r = z == 0 ? i0r : i1r;
+  const float* h0i = z == 0 ? i0i : i1i;
   const int c = 2 * blockIdx.y + (lane >> 5);
   const bool colok = c < h;
   const int64_t hh = static_cast<int64_t>(h) * h;
@@ -182,7 +188,7 @@ __global__ __launch_bounds__(64) void cham_state_kernel(
     // chunk-start state of chunk n + 1 (the final state after the last chunk)
     float* dr_ = (n + 1 < nch) ? wsr + (static_cast<int64_t>(b) * (nch - 1) + n) * hh : hr_out + b * hh;
     float* di_ = (n + 1 < nch) ? wsi + (static_cast<int64_t>(b) * (nch - 1) + n) * hh : hi_out + b * hh;
-    if (colok) {
+    if (colok && ((n + 1 < nch) ? snaps : final_)) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = l32 + 32 * i;
@@ -195,7 +201,7 @@ __global__ __launch_bounds__(64) void cham_state_kernel(
     if (n + 1 < nch) commit(n + 1);  // buffer (n + 1) & 1 was last read by chunk n - 1
     __builtin_amdgcn_wave_barrier();
   }
-  if (nch == 0 && colok) {  // T = 0: the state passes through
+  if (nch == 0 && colok && final_) {  // T = 0: the state passes through
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = l32 + 32 * i;
@@ -469,6 +475,12 @@ __global__ __launch_bounds__(RNT) void cham_readout_kernel(
   }
 }
 
+// With an initial hologram and at least RTOK tokens the readout state R_t = P_t NS_3(H_0)
+// is carried beside the raw state (pass 1 with two states, NS_3(H_0) once per call) and
+// pass 2 reads out Re(R_t q_t) like the identity start; shorter calls evaluate the
+// polynomial per token on H_t instead.
+constexpr int RTOK = 64;
+
 template <typename IO, typename GT>
 hipError_t launch_typed(const void* q, const void* k, const void* v, const void* gamma,
                         const float* h0r, const float* h0i, void* out, float* hr_out,
@@ -477,16 +489,31 @@ hipError_t launch_typed(const void* q, const void* k, const void* v, const void*
   const int64_t wsplane = nch > 1 ? static_cast<int64_t>(B) * (nch - 1) * h * h : 0;
   float* wsr = ws;
   float* wsi = ws + wsplane;
-  hipLaunchKernelGGL((cham_state_kernel<IO, GT>), dim3(B, (h + 1) / 2), dim3(64), 0, stream,
-                     static_cast<const IO*>(k), static_cast<const IO*>(v),
-                     static_cast<const GT*>(gamma), h0r, h0i, wsr, wsi, hr_out, hi_out, T, h);
+  const bool rroute = h0r != nullptr && T >= RTOK;
+  const float* r0r = nullptr;
+  const float* r0i = nullptr;
+  if (rroute) {
+    float* rr = ws + 2 * wsplane;
+    float* ri = rr + static_cast<int64_t>(B) * h * h;
+    float* nsws = ri + static_cast<int64_t>(B) * h * h;
+    const hipError_t e = launch_ns_retraction(h0r, h0i, rr, ri, B, h, 3, nsws, stream);
+    if (e != hipSuccess) return e;
+    r0r = rr;
+    r0i = ri;
+  }
+  const int nstates = rroute ? 2 : 1;
+  hipLaunchKernelGGL((cham_state_kernel<IO, GT>), dim3(B, (h + 1) / 2, nstates), dim3(64), 0,
+                     stream, static_cast<const IO*>(k), static_cast<const IO*>(v),
+                     static_cast<const GT*>(gamma), h0r, h0i, r0r, r0i, wsr, wsi, hr_out, hi_out,
+                     T, h, nstates);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nch == 0) return e;
-  if (h0r == nullptr)
+  if (h0r == nullptr || rroute)
     hipLaunchKernelGGL((cham_readout_kernel<IO, GT, false>), dim3(B, nch), dim3(RNT), 0, stream,
                        static_cast<const IO*>(q), static_cast<const IO*>(k),
-                       static_cast<const IO*>(v), static_cast<const GT*>(gamma), h0r, h0i, wsr,
-                       wsi, static_cast<IO*>(out), T, h);
+                       static_cast<const IO*>(v), static_cast<const GT*>(gamma),
+                       rroute ? r0r : nullptr, rroute ? r0i : nullptr, wsr, wsi,
+                       static_cast<IO*>(out), T, h);
   else
     hipLaunchKernelGGL((cham_readout_kernel<IO, GT, true>), dim3(B, nch), dim3(RNT), 0, stream,
                        static_cast<const IO*>(q), static_cast<const IO*>(k),
@@ -512,7 +539,11 @@ hipError_t launch_io(const void* q, const void* k, const void* v, const void* ga
 size_t cham_scan_workspace_bytes(int64_t B, int64_t T, int64_t h) {
   if (h > cham::HP) return cham_wide_workspace_bytes(B, T, h);
   const int64_t nch = (T + cham::CH - 1) / cham::CH;
-  return nch > 1 ? static_cast<size_t>(2 * B * (nch - 1) * h * h) * sizeof(float) : 0;
+  // chunk-start states, plus R_0 and the retraction's scratch for calls of RTOK+ tokens
+  // (sized for them whether or not an initial hologram is given)
+  const int64_t states = nch > 1 ? 2 * B * (nch - 1) * h * h : 0;
+  const int64_t rpart = T >= cham::RTOK ? 8 * B * h * h : 0;
+  return static_cast<size_t>(states + rpart) * sizeof(float);
 }
 
 bool cham_scan_supported(int64_t h) { return h >= 1 && h <= kChamMaxDim; }
