@@ -15,12 +15,12 @@
 // (vmi::cayley_coeffs); the reduce kernel carries dL/dM through them into dk, dv,
 // ddelta.
 //
-// Kernel 1 (sssd_bwd_cols_kernel), grid (D / 16, B H), 256 threads: the columns of Psi
+// Kernel 1 (sssd_bwd_cols_kernel), grid (D / 16, B H), 512 threads: the columns of Psi
 // and Lambda evolve independently under left multiplication, so a workgroup carries 16
 // columns of both through all T tokens in reverse; thread (w, lane) holds rows
-// lane % 16 + 16 r of column 4 w + lane / 16 (column sums: one DPP row).  dq is complete
-// per column; the row sums over columns (dL/dU) and dL/dM are summed over the
-// workgroup's 16 columns and written as per-token partials.
+// lane % 32 + 32 r of column 2 w + lane / 32 (column sums: two DPP rows; two waves per
+// SIMD).  dq is complete per column; the row sums over columns (dL/dU) and dL/dM are
+// summed over the workgroup's 16 columns and written as per-token partials.
 // Kernel 2 (sssd_bwd_reduce_kernel), one wave per token-head: sums the D / 16 partials
 // and applies the chain rule through M.
 #include "vmi_common.h"
@@ -32,7 +32,9 @@ namespace bwd {
 
 constexpr int CB = 16;  // columns per workgroup
 constexpr int SB = 16;  // tokens per LDS stage
-constexpr int NT = 256;
+constexpr int NT = 512;
+constexpr int LPC = 32;           // lanes per column
+constexpr int NWV = NT / 64;      // waves (2 columns each)
 
 template <int D> struct Part { static constexpr int size = 2 * D + 8; };  // dU rows, dM, pad
 
@@ -42,12 +44,12 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
     const void* __restrict__ delta, int delta_dtype, const float* __restrict__ psi_T,
     const GO* __restrict__ dout, const float* __restrict__ dpsi_T, IO* __restrict__ dq,
     float* __restrict__ dpsi0, float* __restrict__ part, int T, int H) {
-  constexpr int RPT = D / 16;  // rows per thread
+  constexpr int RPT = D / LPC;  // rows per thread
   constexpr int PS = Part<D>::size;
   constexpr int NBLK = D / CB;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int rg = lane & 15;
-  const int cl = 4 * wave + (lane >> 4);  // column within the block
+  const int rg = lane & (LPC - 1);
+  const int cl = 2 * wave + (lane >> 5);  // column within the block
   const int blk = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, hd = bh % H;
   const int j = blk * CB + cl;            // state column
@@ -57,13 +59,13 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
   __shared__ float sq[2][SB][CB];
   __shared__ float sco[2][SB][8];  // m00 m01 m10 m11 kk kv vv -
   __shared__ float sdl[2][SB];
-  __shared__ float sred[2][4][2 * D + 4];
+  __shared__ float sred[2][NWV][2 * D + 4];  // per-wave partials, double-buffered
 
   // state columns: psi = Psi^(T)[:, j], lam = dL/dPsi_T[:, j]
   float psi[RPT], lam[RPT];
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
-    const int64_t o = bh * DD + static_cast<int64_t>(rg + 16 * r) * D + j;
+    const int64_t o = bh * DD + static_cast<int64_t>(rg + LPC * r) * D + j;
     psi[r] = psi_T[o];
     lam[r] = dpsi_T ? dpsi_T[o] : 0.f;
   }
@@ -85,7 +87,7 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
     }
     {
       const int t = T - 1 - (SB * s + tid / CB);
-      rq = t >= 0 ? io<IO>::load(q, tok_index(t) * D + blk * CB + tid % CB) : 0.f;
+      rq = (tid < SB * CB && t >= 0) ? io<IO>::load(q, tok_index(t) * D + blk * CB + tid % CB) : 0.f;
     }
     {
       const int t = T - 1 - (SB * s + tid);
@@ -102,23 +104,23 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
       sv[buf][x / D][x % D] = ok ? rv[e] : 0.f;
       sdo[buf][x / D][x % D] = ok ? rdo[e] : 0.f;
     }
-    sq[buf][tid / CB][tid % CB] = rq;  // SB * CB == NT
+    if (tid < SB * CB) sq[buf][tid / CB][tid % CB] = rq;
     if (tid < SB) sdl[buf][tid] = rd;
     __syncthreads();
-    // Gram entries and M of each token: the 16 lanes of DPP row tt sum over D / 16 rows
+    // Gram entries and M of each token: the 32 lanes of half-wave tt sum over D / 32 rows
     {
-      const int tt = tid >> 4;
+      const int tt = tid >> 5;  // SB * 32 == NT
       float kk = 0.f, vv = 0.f, kv = 0.f;
 #pragma unroll
       for (int r = 0; r < RPT; ++r) {
-        const float x = sk[buf][tt][rg + 16 * r], y = sv[buf][tt][rg + 16 * r];
+        const float x = sk[buf][tt][rg + LPC * r], y = sv[buf][tt][rg + LPC * r];
         kk = fmaf(x, x, kk);
         vv = fmaf(y, y, vv);
         kv = fmaf(x, y, kv);
       }
-      kk = row16_sum(kk);
-      vv = row16_sum(vv);
-      kv = row16_sum(kv);
+      kk = row_pair_sum(row16_sum(kk));
+      vv = row_pair_sum(row16_sum(vv));
+      kv = row_pair_sum(row16_sum(kv));
       if (rg == 0) {
         const cayley2 m = cayley_coeffs(sdl[buf][tt], kk, vv, kv);
         sco[buf][tt][0] = m.m00; sco[buf][tt][1] = m.m01;
@@ -144,9 +146,9 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
       float kr[RPT], vr[RPT], dr[RPT];
 #pragma unroll
       for (int r = 0; r < RPT; ++r) {
-        kr[r] = sk[buf][i][rg + 16 * r];
-        vr[r] = sv[buf][i][rg + 16 * r];
-        dr[r] = sdo[buf][i][rg + 16 * r];
+        kr[r] = sk[buf][i][rg + LPC * r];
+        vr[r] = sv[buf][i][rg + LPC * r];
+        dr[r] = sdo[buf][i][rg + LPC * r];
       }
       const float qj = sq[buf][i][cl];
       const float m00 = sco[buf][i][0], m01 = sco[buf][i][1], m10 = sco[buf][i][2], m11 = sco[buf][i][3];
@@ -162,11 +164,11 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
         B0 = fmaf(kr[r], lam[r], B0);
         B1 = fmaf(vr[r], lam[r], B1);
       }
-      a1 = row16_sum(a1);
-      b1 = row16_sum(b1);
-      dqs = row16_sum(dqs);
-      B0 = row16_sum(B0);
-      B1 = row16_sum(B1);
+      a1 = row_pair_sum(row16_sum(a1));
+      b1 = row_pair_sum(row16_sum(b1));
+      dqs = row_pair_sum(row16_sum(dqs));
+      B0 = row_pair_sum(row16_sum(B0));
+      B1 = row_pair_sum(row16_sum(B1));
       if (rg == 0) io<IO>::store(dq, tok_index(t) * D + j, dqs);
       // Psi^(t) = R^T Psi^(t+1): alpha = M^T (U^T psi);  A = U^T Psi^(t) = U^T psi + G alpha
       const float al0 = m00 * a1 + m10 * b1, al1 = m01 * a1 + m11 * b1;
@@ -182,27 +184,31 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
         u1[r] = fmaf(lam[r], p1, psi[r] * r1);
         lam[r] = fmaf(kr[r], r0, fmaf(vr[r], r1, lam[r]));
       }
-      // dU rows and dM summed over the wave's 4 columns, then over the 4 waves in LDS
+      // dU rows and dM summed over the wave's 2 columns, then over the waves in LDS
 #pragma unroll
       for (int r = 0; r < RPT; ++r) {
-        u0[r] = half_pair_sum(row_pair_sum(u0[r]));
-        u1[r] = half_pair_sum(row_pair_sum(u1[r]));
+        u0[r] = half_pair_sum(u0[r]);
+        u1[r] = half_pair_sum(u1[r]);
       }
       float dm[4] = {B0 * A0, B0 * A1, B1 * A0, B1 * A1};
 #pragma unroll
-      for (int x = 0; x < 4; ++x) dm[x] = half_pair_sum(row_pair_sum(dm[x]));
-      if (lane < 16) {
+      for (int x = 0; x < 4; ++x) dm[x] = half_pair_sum(dm[x]);
+      if (lane < LPC) {
 #pragma unroll
         for (int r = 0; r < RPT; ++r) {
-          sred[par][wave][2 * (rg + 16 * r)] = u0[r];
-          sred[par][wave][2 * (rg + 16 * r) + 1] = u1[r];
+          sred[par][wave][2 * (rg + LPC * r)] = u0[r];
+          sred[par][wave][2 * (rg + LPC * r) + 1] = u1[r];
         }
         if (lane < 4) sred[par][wave][2 * D + lane] = dm[lane];
       }
       __syncthreads();
       float* pp = part + ((static_cast<int64_t>(bh) * T + t) * NBLK + blk) * PS;
-      for (int x = tid; x < 2 * D + 4; x += NT)
-        pp[x] = sred[par][0][x] + sred[par][1][x] + sred[par][2][x] + sred[par][3][x];
+      for (int x = tid; x < 2 * D + 4; x += NT) {
+        float acc = sred[par][0][x];
+#pragma unroll
+        for (int w = 1; w < NWV; ++w) acc += sred[par][w][x];
+        pp[x] = acc;
+      }
       par ^= 1;
     }
     if (s + 1 < nst) commit(s + 1);  // buffer (s + 1) & 1 was last read in stage s - 1
@@ -210,7 +216,7 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
   }
   if (dpsi0) {
 #pragma unroll
-    for (int r = 0; r < RPT; ++r) dpsi0[bh * DD + static_cast<int64_t>(rg + 16 * r) * D + j] = lam[r];
+    for (int r = 0; r < RPT; ++r) dpsi0[bh * DD + static_cast<int64_t>(rg + LPC * r) * D + j] = lam[r];
   }
 }
 
