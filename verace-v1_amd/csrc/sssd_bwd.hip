@@ -18,9 +18,11 @@
 // Kernel 1 (sssd_bwd_cols_kernel), grid (D / 16, B H), 512 threads: the columns of Psi
 // and Lambda evolve independently under left multiplication, so a workgroup carries 16
 // columns of both through all T tokens in reverse; thread (w, lane) holds rows
-// lane % 32 + 32 r of column 2 w + lane / 32 (column sums: two DPP rows; two waves per
+// lane % 32 + 32 r of column 2 w + lane / 32 (column sums over 32 lanes; two waves per
 // SIMD).  dq is complete per column; the row sums over columns (dL/dU) and dL/dM are
-// summed over the workgroup's 16 columns and written as per-token partials.
+// summed over the workgroup's 16 columns (the wave's pair, then the 8 waves in LDS) and
+// written as per-token partials.  (One column per 64-lane wave, 16 waves: slower, the
+// 16-wave barrier and LDS sum cost more than the extra waves hide.)
 // Kernel 2 (sssd_bwd_reduce_kernel), one wave per token-head: sums the D / 16 partials
 // and applies the chain rule through M.
 #include "vmi_common.h"
@@ -34,9 +36,16 @@ constexpr int CB = 16;  // columns per workgroup
 constexpr int SB = 16;  // tokens per LDS stage
 constexpr int NT = 512;
 constexpr int LPC = 32;           // lanes per column
-constexpr int NWV = NT / 64;      // waves (2 columns each)
+constexpr int CPW = 64 / LPC;     // columns per wave
+constexpr int NWV = NT / 64;      // waves
 
 template <int D> struct Part { static constexpr int size = 2 * D + 8; };  // dU rows, dM, pad
+
+// sum over the LPC lanes of a column, result in all of them
+__device__ __forceinline__ float col_sum(float x) {
+  x = row_pair_sum(row16_sum(x));
+  return LPC == 64 ? half_pair_sum(x) : x;
+}
 
 template <typename IO, typename GO, int D>
 __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
@@ -49,7 +58,7 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
   constexpr int NBLK = D / CB;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int rg = lane & (LPC - 1);
-  const int cl = 2 * wave + (lane >> 5);  // column within the block
+  const int cl = CPW * wave + lane / LPC;  // column within the block
   const int blk = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, hd = bh % H;
   const int j = blk * CB + cl;            // state column
@@ -107,9 +116,9 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
     if (tid < SB * CB) sq[buf][tid / CB][tid % CB] = rq;
     if (tid < SB) sdl[buf][tid] = rd;
     __syncthreads();
-    // Gram entries and M of each token: the 32 lanes of half-wave tt sum over D / 32 rows
+    // Gram entries and M of each token: the LPC lanes tt sum over D / LPC rows
     {
-      const int tt = tid >> 5;  // SB * 32 == NT
+      const int tt = tid / LPC;  // SB * LPC == NT
       float kk = 0.f, vv = 0.f, kv = 0.f;
 #pragma unroll
       for (int r = 0; r < RPT; ++r) {
@@ -118,9 +127,9 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
         vv = fmaf(y, y, vv);
         kv = fmaf(x, y, kv);
       }
-      kk = row_pair_sum(row16_sum(kk));
-      vv = row_pair_sum(row16_sum(vv));
-      kv = row_pair_sum(row16_sum(kv));
+      kk = col_sum(kk);
+      vv = col_sum(vv);
+      kv = col_sum(kv);
       if (rg == 0) {
         const cayley2 m = cayley_coeffs(sdl[buf][tt], kk, vv, kv);
         sco[buf][tt][0] = m.m00; sco[buf][tt][1] = m.m01;
@@ -164,11 +173,11 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
         B0 = fmaf(kr[r], lam[r], B0);
         B1 = fmaf(vr[r], lam[r], B1);
       }
-      a1 = row_pair_sum(row16_sum(a1));
-      b1 = row_pair_sum(row16_sum(b1));
-      dqs = row_pair_sum(row16_sum(dqs));
-      B0 = row_pair_sum(row16_sum(B0));
-      B1 = row_pair_sum(row16_sum(B1));
+      a1 = col_sum(a1);
+      b1 = col_sum(b1);
+      dqs = col_sum(dqs);
+      B0 = col_sum(B0);
+      B1 = col_sum(B1);
       if (rg == 0) io<IO>::store(dq, tok_index(t) * D + j, dqs);
       // Psi^(t) = R^T Psi^(t+1): alpha = M^T (U^T psi);  A = U^T Psi^(t) = U^T psi + G alpha
       const float al0 = m00 * a1 + m10 * b1, al1 = m01 * a1 + m11 * b1;
@@ -184,15 +193,17 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
         u1[r] = fmaf(lam[r], p1, psi[r] * r1);
         lam[r] = fmaf(kr[r], r0, fmaf(vr[r], r1, lam[r]));
       }
-      // dU rows and dM summed over the wave's 2 columns, then over the waves in LDS
-#pragma unroll
-      for (int r = 0; r < RPT; ++r) {
-        u0[r] = half_pair_sum(u0[r]);
-        u1[r] = half_pair_sum(u1[r]);
-      }
+      // dU rows and dM summed over the wave's columns, then over the waves in LDS
       float dm[4] = {B0 * A0, B0 * A1, B1 * A0, B1 * A1};
+      if (CPW == 2) {
 #pragma unroll
-      for (int x = 0; x < 4; ++x) dm[x] = half_pair_sum(dm[x]);
+        for (int r = 0; r < RPT; ++r) {
+          u0[r] = half_pair_sum(u0[r]);
+          u1[r] = half_pair_sum(u1[r]);
+        }
+#pragma unroll
+        for (int x = 0; x < 4; ++x) dm[x] = half_pair_sum(dm[x]);
+      }
       if (lane < LPC) {
 #pragma unroll
         for (int r = 0; r < RPT; ++r) {
