@@ -1039,7 +1039,9 @@ __global__ __launch_bounds__(CARRY_NT) void sssd_carry_kernel(const float* psi0,
     fetch(pf, f + 2);
     // Y = F[32rb .. +31][:] X[:][32ch .. +31]; A row = l32, B column = l32, k-slots
     // 16ks + 8g + 0..7 in both operands
-    f32x16 Y = {};
+    // three independent accumulator chains (hi hi, hi lo, lo hi) interleave in the MFMA
+    // pipeline instead of one chain of 24 dependent products
+    f32x16 Y = {}, Y1 = {}, Y2 = {};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
       const int ka = 16 * ks + 8 * g;
@@ -1048,9 +1050,11 @@ __global__ __launch_bounds__(CARRY_NT) void sssd_carry_kernel(const float* psi0,
       const V8 bh8 = *reinterpret_cast<const V8*>(&xhi[(32 * ch + l32) * CP_LD + ka]);
       const V8 bl8 = *reinterpret_cast<const V8*>(&xlo[(32 * ch + l32) * CP_LD + ka]);
       Y = MM::mma32(ah, bh8, Y);
-      Y = MM::mma32(ah, bl8, Y);
-      Y = MM::mma32(al, bh8, Y);
+      Y1 = MM::mma32(ah, bl8, Y1);
+      Y2 = MM::mma32(al, bh8, Y2);
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Y[r] += Y1[r] + Y2[r];
     __syncthreads();  // every wave has read the factor and X before they are replaced
     // Y: lane (g, l32) holds rows 32rb + 8(r/4) + 4g + r%4 of column 32ch + l32
     const int colw = 32 * ch + l32;
