@@ -107,6 +107,39 @@ def check_scan(cpu_inputs, outs, B, H):
     return res
 
 
+def bench_long(device, iters=5):
+    """LONG config: B=1 T=65536 H=16 D=128 bf16 scan (delta = 0.05 sigmoid(z)) from the
+    identity, one call (the segment carry spans the whole sequence)."""
+    import torch
+    import torch.nn.functional as F
+    from verace_amd import launch_sssd_hip_scan
+    B, T, H, D = 1, 65536, 16, 128
+    g = torch.Generator().manual_seed(0)
+    q = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1).to(torch.bfloat16).to(device)
+    k = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1).to(torch.bfloat16).to(device)
+    v = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1).to(torch.bfloat16).to(device)
+    d = (0.05 * torch.sigmoid(torch.randn(B, T, H, generator=g))).to(torch.bfloat16).to(device)
+    launch_sssd_hip_scan(q, k, v, d)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(device)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+    ev[0].record(stream)
+    for i in range(iters):
+        _, psi = launch_sssd_hip_scan(q, k, v, d)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    us = statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(iters))
+    nbytes = algorithmic_bytes_scan(B, T, H, D)
+    nrm = psi.reshape(B * H, -1).norm(dim=-1) / D ** 0.5
+    return {
+        "config": "LONG: SSSD scan B=1 T=65536 H=16 D=128 bf16, identity start",
+        "us_median": round(us, 1),
+        "tokens_per_s": round(B * T / (us * 1e-6), 1),
+        "hbm_frac": round(nbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+        "state_norm_drift": float((nrm - 1).abs().max()),
+    }
+
+
 def bench_decode(device):
     """DEC op level: 12 layers x 256 single-token steps on B=64 H=8 D=128 states.
 
@@ -554,6 +587,7 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    result["long"] = bench_long(device)
     if not args.no_decode:
         result["decode"] = bench_decode(device)
         result["decode_cache"] = bench_decode_cache(device)

@@ -1111,8 +1111,13 @@ Plan make_plan(int64_t BH, int64_t T) {
   p.nseg = (p.nchunks + p.seg_chunks - 1) / p.seg_chunks;
   // Pass A covers segments 0 .. nseg-2.  Spread over nseg workgroups per sequence instead
   // of nseg-1 it fills as many CUs as pass C; every segment then holds exactly one piece
-  // boundary (given seg_chunks >= 2 nseg) and contributes two factors to the carry.
-  if (p.nseg > 1 && p.seg_chunks >= 2 * p.nseg) {
+  // boundary (given seg_chunks >= 2 nseg) and contributes two factors to the carry.  That
+  // saves seg_chunks / nseg chunk iterations of pass A (~1.4 us each) for nseg - 1 more
+  // carry products (~2.8 us each), so pieces only pay while
+  // seg_chunks > 2 nseg (nseg - 1) (OP: 64 > 24; the FULL shape, 16 chunks in 8
+  // segments, and LONG, 256 in 16, take one workgroup per segment).
+  if (p.nseg > 1 && p.seg_chunks >= 2 * p.nseg &&
+      p.seg_chunks > 2 * p.nseg * (p.nseg - 1)) {
     p.npieces = p.nseg;
     p.nfactors = 2 * (p.nseg - 1);
     p.fstride = 2;
