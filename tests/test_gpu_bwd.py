@@ -132,3 +132,18 @@ def test_module_training_gradients(device):
         e = _rel(got.cpu(), r_)
         print(f"[bwd module] d{name} rel {e:.2e}", flush=True)
         assert e <= 1e-4, name
+
+
+def test_scan_backward_empty_sequence(device):
+    """T = 0: the state gradient passes through unchanged; the other gradients are empty."""
+    from verace_amd import launch_sssd_hip_scan_bwd
+    print("[case] bwd T=0", flush=True)
+    B, H, D = 2, 3, 128
+    z = torch.zeros(B, 0, H, D, device=device)
+    d = torch.zeros(B, 0, H, device=device)
+    psi = torch.randn(B, H, D, D, device=device)
+    dpsi = torch.randn(B, H, D, D, device=device)
+    dq, dk, dv, dd, dpsi0 = launch_sssd_hip_scan_bwd(z, z, z, d, psi, z, dpsi, True)
+    torch.cuda.synchronize()
+    assert dq.shape == (B, 0, H, D) and dd.shape == (B, 0, H)
+    assert torch.equal(dpsi0, dpsi)

@@ -204,3 +204,18 @@ def test_cham_long_calls_with_initial_hologram(device, B, T, h, unitary):
     if not unitary:
         Q = Q * (1.0 + 0.05 * torch.randn(B, h, h, generator=g))
     _check(device, B, T, h, seed=T, h0=(Q.real.contiguous(), Q.imag.contiguous()), label="r-route")
+
+
+@pytest.mark.parametrize("h", [64, 300])
+def test_cham_empty_sequence_passes_the_state_through(device, h):
+    """T = 0: no output, and the final state is the initial hologram (or the identity)."""
+    print(f"[case] cham T=0 h={h}", flush=True)
+    B = 2
+    q, k, v, gam = _inputs(B, 0, h, 1)
+    g = torch.Generator().manual_seed(h)
+    H0 = (torch.randn(B, h, h, generator=g), torch.randn(B, h, h, generator=g))
+    out, hr, hi = _run(device, q, k, v, gam, H0)
+    assert out.shape == (B, 0, h)
+    assert torch.equal(hr, H0[0]) and torch.equal(hi, H0[1])
+    out, hr, hi = _run(device, q, k, v, gam)
+    assert torch.equal(hr, torch.eye(h).expand(B, h, h)) and torch.count_nonzero(hi) == 0
