@@ -83,7 +83,8 @@ int vmi_sssd_scan_fwd(const void* q, const void* k, const void* v, const void* d
 int vmi_sssd_scan_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, size_t* bytes) {
   if (bytes == nullptr || B < 0 || T < 0 || H < 0 || D < 1) return VMI_ERR_INVALID_ARG;
   if (!vmi::sssd_bwd_supported(D)) return VMI_ERR_UNSUPPORTED;
-  *bytes = vmi::sssd_bwd_workspace_bytes(B, T, H, D);
+  *bytes = T >= vmi::kBwdChunkMinT ? vmi::sssd_bwd_chunk_workspace_bytes(B, T, H, D)
+                                   : vmi::sssd_bwd_workspace_bytes(B, T, H, D);
   return VMI_OK;
 }
 
@@ -106,9 +107,17 @@ int vmi_sssd_scan_bwd(const void* q, const void* k, const void* v, const void* d
   if (d_psi0 != nullptr && (ranges_overlap(d_psi0, state_bytes, psi_T, state_bytes) ||
                             (d_psi_T != nullptr && ranges_overlap(d_psi0, state_bytes, d_psi_T, state_bytes))))
     return VMI_ERR_ALIAS;
-  const size_t need = vmi::sssd_bwd_workspace_bytes(B, T, H, D);
+  const bool chunked = T >= vmi::kBwdChunkMinT;
+  const size_t need = chunked ? vmi::sssd_bwd_chunk_workspace_bytes(B, T, H, D)
+                              : vmi::sssd_bwd_workspace_bytes(B, T, H, D);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return VMI_ERR_WORKSPACE;
   if (B == 0 || H == 0) return VMI_OK;
+  if (chunked)
+    return hip_status(vmi::launch_sssd_bwd_chunk(q, k, v, delta, io_dtype, delta_dtype, psi_T,
+                                                 d_out, d_out_dtype, d_psi_T, dq, dk, dv, d_delta,
+                                                 d_psi0, static_cast<int>(B), static_cast<int>(T),
+                                                 static_cast<int>(H), static_cast<int>(D),
+                                                 workspace, static_cast<hipStream_t>(stream)));
   return hip_status(vmi::launch_sssd_bwd(q, k, v, delta, io_dtype, delta_dtype, psi_T, d_out,
                                          d_out_dtype, d_psi_T, dq, dk, dv, d_delta, d_psi0,
                                          static_cast<int>(B), static_cast<int>(T),

@@ -1,0 +1,519 @@
+// Chunked (WY) backward of the SSSD scan: the per-token reverse recursion of sssd_bwd.hip
+// regrouped by chunks of C = 16 tokens, so every state-dependent product is a small GEMM
+// on the fp32 MFMA (v_mfma_f32_16x16x4f32: exact fp32 products, fp32 accumulation).
+//
+// Per chunk (U = [k_1 v_1 .. k_C v_C] D x 32, T~ = (I - L)^-1 blockdiag(M) 32 x 32, the
+// forward's chunk factor I + U T~ U^T, states Psi_s -> Psi_e, adjoints Lam_s <- Lam_e):
+//   Psi_s = Psi_e + U T~^T U^T Psi_e            (the factor is orthogonal)
+//   W = U^T Psi_s,  Z = T~ W,  X = mask o (Z Q),  dX = mask o (U^T dO)
+//   dZ = U^T Lam_e + dX Q^T,   dT~ = dZ W^T,     dW = T~^T dZ
+//   dQ = Z^T dX + Psi_s^T dO,  dU = Lam_e Z^T + dO X^T + Psi_s dW^T
+//   Lam_s = Lam_e + dO Q^T + U dW
+// (mask[rho][t] = token(rho) <= t).  Then, per chunk and without the state, dT~ through
+// T~ = A B (A = (I - L)^-1, B = blockdiag(M), L_ti = M_t G_ti for i < t):
+//   dA = dT~ B^T, dB = A^T dT~, dL = A^T dA A^T (strictly lower blocks),
+//   dM_t = dB_tt + sum_i dL_ti G_ti^T,  dG_ti = M_t^T dL_ti,
+// M_t(delta_t, kk, vv, kv) as in vmi::cayley_coeffs, dU += U (dG + dG^T).
+//
+// Launches:
+//   bwdc_prep_kernel  (grid (nch, B H)): T~, A, G, M of every chunk -> workspace;
+//   bwdc_cols_kernel  (grid (D/16, B H), 256 threads): 16 state columns of one sequence
+//     through the chunks in reverse, Psi and Lam in LDS; dQ of its columns directly, the
+//     column sums dT~ and dU as per-chunk partials;
+//   bwdc_reduce_kernel (grid (nch, B H)): sums the partials, dT~ -> dM, dG -> dk, dv, ddelta.
+#include "vmi_common.h"
+#include "vmi_dispatch.h"
+#include "vmi_lanes.h"
+
+namespace vmi {
+namespace bwdc {
+
+constexpr int C = 16;   // tokens per chunk
+constexpr int R = 32;   // rank rows of a chunk (k, v per token)
+constexpr int CB = 16;  // state columns per workgroup
+constexpr int NT = 256;
+// per-chunk record written by the prep kernel: T~, A = (I - L)^-1, G (R x R each), M blocks
+constexpr int REC = 3 * R * R + 4 * C;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+enum { kStore = 0, kAdd = 1, kMaskStore = 2 };
+
+// LDS row strides: 17 (mod 32) keeps the MFMA operand reads of both orientations at most
+// 2-way bank conflicted (lanes read 16 consecutive elements of 2 rows, or 2 consecutive
+// elements of 16 rows).
+constexpr int L16 = 17;  // 16-wide matrices
+constexpr int L32 = 33;  // 32-wide matrices
+
+// Cm (M x N, row stride ldc) (=|+=) opA(A) opB(B), K the inner size, all in LDS.
+// opA(m, k) = TA ? A[k lda + m] : A[m lda + k];  opB(k, n) = TB ? B[n ldb + k] : B[k ldb + n].
+// 16 x 16 output tiles round robin over NW waves starting at W0 (independent products of
+// one phase go to disjoint waves); v_mfma_f32_16x16x4f32 lane layout: A[m = lane % 16]
+// [k = lane / 16], B[k = lane / 16][n = lane % 16], D[4 (lane / 16) + r][lane % 16].  Two
+// accumulators over alternate k steps halve the dependent chain.  kMaskStore keeps the
+// (row = rank row rho, col = token t) entries with rho / 2 <= t.
+template <int M, int N, int K, bool TA, bool TB, int MODE, int W0 = 0, int NW = 4>
+__device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, int ldb, float* Cm,
+                                      int ldc, int wave, int lane) {
+  constexpr int TN = N / 16, NTILE = (M / 16) * TN;
+  if (wave < W0 || wave >= W0 + NW) return;
+  const int l16 = lane & 15, kq = lane >> 4;
+  for (int tile = wave - W0; tile < NTILE; tile += NW) {
+    const int tm = tile / TN, tn = tile % TN;
+    const int am = 16 * tm + l16, bn = 16 * tn + l16;
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int k0 = 0; k0 < K; k0 += 8) {
+      const int k = k0 + kq;
+      const float a0 = TA ? A[k * lda + am] : A[am * lda + k];
+      const float b0 = TB ? B[bn * ldb + k] : B[k * ldb + bn];
+      acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc0, 0, 0, 0);
+      if (k0 + 4 < K) {
+        const int k1 = k + 4;
+        const float a1 = TA ? A[k1 * lda + am] : A[am * lda + k1];
+        const float b1 = TB ? B[bn * ldb + k1] : B[k1 * ldb + bn];
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc1, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * tm + 4 * kq + r, col = bn;
+      const float x = acc0[r] + acc1[r];
+      float* p = Cm + row * ldc + col;
+      if (MODE == kStore) *p = x;
+      else if (MODE == kAdd) *p += x;
+      else *p = (row >> 1) <= col ? x : 0.f;
+    }
+  }
+}
+
+// dst (global, M x 32, row stride 32) = A1 B1^T + A2 B2^T + A3 B3^T with A_i [M][16] and
+// B_i [32][16] in LDS (row stride L16): the three products of one tile share one
+// accumulator, so the sum goes to memory once.
+template <int M>
+__device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B1, const float* A2,
+                                                 const float* B2, const float* A3, const float* B3,
+                                                 float* dst, int wave, int lane) {
+  constexpr int NTILE = (M / 16) * 2;
+  const int l16 = lane & 15, kq = lane >> 4;
+  for (int tile = wave; tile < NTILE; tile += NT / 64) {
+    const int tm = tile >> 1, tn = tile & 1;
+    const int am = 16 * tm + l16, bn = 16 * tn + l16;
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    const float* As[3] = {A1, A2, A3};
+    const float* Bs[3] = {B1, B2, B3};
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+#pragma unroll
+      for (int k0 = 0; k0 < 16; k0 += 8) {
+        const int k = k0 + kq;
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(As[u][am * L16 + k], Bs[u][bn * L16 + k], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(As[u][am * L16 + k + 4], Bs[u][bn * L16 + k + 4], acc1, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[(16 * tm + 4 * kq + r) * R + bn] = acc0[r] + acc1[r];
+  }
+}
+
+// G = U^T U, the Cayley blocks M_t, L and A = (I - L)^-1 of one chunk (LDS).
+// U: [D][R] (row i: k_t at 2t, v_t at 2t + 1; zero past the end); dl[t] the deltas.
+template <int D>
+__device__ void chunk_prep(const float* U, const float* dl, float* G, float* Mb, float* L,
+                           float* A, int tid, int wave, int lane) {
+  lgemm<R, R, D, true, false, kStore>(U, R, U, R, G, R, wave, lane);
+  __syncthreads();
+  if (tid < C) {
+    const int t = tid;
+    const cayley2 m = cayley_coeffs(dl[t], G[(2 * t) * R + 2 * t], G[(2 * t + 1) * R + 2 * t + 1],
+                                    G[(2 * t) * R + 2 * t + 1]);
+    Mb[4 * t + 0] = m.m00; Mb[4 * t + 1] = m.m01; Mb[4 * t + 2] = m.m10; Mb[4 * t + 3] = m.m11;
+  }
+  __syncthreads();
+  for (int e = tid; e < R * R; e += NT) {  // L[2t + a][2i + b] = (M_t G_ti)[a][b], i < t
+    const int r = e / R, c = e % R, t = r >> 1, i = c >> 1, a = r & 1, b = c & 1;
+    float x = 0.f;
+    if (i < t) x = Mb[4 * t + 2 * a] * G[(2 * t) * R + 2 * i + b] + Mb[4 * t + 2 * a + 1] * G[(2 * t + 1) * R + 2 * i + b];
+    L[e] = x;
+    A[e] = r == c ? 1.f : 0.f;
+  }
+  __syncthreads();
+  // A = I + L A, block row t from the rows of the earlier blocks
+  for (int t = 1; t < C; ++t) {
+    if (tid < 2 * R) {
+      const int r = 2 * t + (tid >> 5), c = tid & 31;
+      if ((c >> 1) < t) {
+        float x = 0.f;
+        for (int m = 2 * (c >> 1); m < 2 * t; ++m) x = fmaf(L[r * R + m], A[m * R + c], x);
+        A[r * R + c] = x;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- T~ of every chunk
+template <typename IO, int D>
+__global__ __launch_bounds__(NT) void bwdc_prep_kernel(const IO* __restrict__ k,
+                                                       const IO* __restrict__ v,
+                                                       const void* __restrict__ delta,
+                                                       int delta_dtype, float* __restrict__ tt,
+                                                       int T, int H) {
+  __shared__ float U[D * R], G[R * R], L[R * R], A[R * R], Mb[4 * C], dl[C];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, hd = bh % H;
+  const int nch = gridDim.x;
+  for (int e = tid; e < D * C; e += NT) {
+    const int t = e / D, i = e % D, tg = n * C + t;
+    const bool ok = tg < T;
+    const int64_t o = ((static_cast<int64_t>(b) * T + (ok ? tg : 0)) * H + hd) * D + i;
+    U[i * R + 2 * t] = ok ? io<IO>::load(k, o) : 0.f;
+    U[i * R + 2 * t + 1] = ok ? io<IO>::load(v, o) : 0.f;
+  }
+  if (tid < C) {
+    const int tg = n * C + tid;
+    dl[tid] = tg < T ? load_scalar(delta, delta_dtype, (static_cast<int64_t>(b) * T + tg) * H + hd) : 0.f;
+  }
+  __syncthreads();
+  chunk_prep<D>(U, dl, G, Mb, L, A, tid, wave, lane);
+  float* o = tt + (static_cast<int64_t>(bh) * nch + n) * REC;
+  for (int e = tid; e < R * R; e += NT) {  // T~ = A blockdiag(M), then A, G, M
+    const int r = e / R, c = e % R, s = c >> 1, cb = c & 1;
+    o[e] = A[r * R + 2 * s] * Mb[4 * s + cb] + A[r * R + 2 * s + 1] * Mb[4 * s + 2 + cb];
+    o[R * R + e] = A[e];
+    o[2 * R * R + e] = G[e];
+  }
+  if (tid < 4 * C) o[3 * R * R + tid] = Mb[tid];
+}
+
+// ---------------------------------------------------------------- state columns, in reverse
+// part layout per (bh, chunk, column block): dT~ partial [R][R], then dU partial [D][R].
+template <int D> struct PartC { static constexpr int size = R * R + D * R; };
+
+template <typename IO, typename GO, int D>
+__global__ __launch_bounds__(NT) void bwdc_cols_kernel(
+    const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
+    const float* __restrict__ tt, const float* __restrict__ psi_T, const GO* __restrict__ dout,
+    const float* __restrict__ dpsi_T, IO* __restrict__ dq, float* __restrict__ dpsi0,
+    float* __restrict__ part, int T, int H) {
+  constexpr int PS = PartC<D>::size;
+  constexpr int NBLK = D / CB;
+  // row strides: L32 for the 32-wide (rank index) matrices, L16 for the 16-wide ones
+  __shared__ float U[D * L32], Tt[R * L32], Qb[CB * L16], dO[D * L16];
+  __shared__ float Ps[D * L16], Lm[D * L16];
+  __shared__ float S1[R * L16], Wm[R * L16], Zm[R * L16], Xm[R * L16], dXm[R * L16],
+      dZm[R * L16], dWm[R * L16], QD[CB * L16];
+  __shared__ float dTp[R * L32], dQm[CB * L16];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int blk = blockIdx.x, bh = blockIdx.y, b = bh / H, hd = bh % H;
+  const int nch = (T + C - 1) / C;
+  const int64_t DD = static_cast<int64_t>(D) * D;
+
+  for (int e = tid; e < D * CB; e += NT) {
+    const int i = e / CB, jj = e % CB;
+    const int64_t o = bh * DD + static_cast<int64_t>(i) * D + blk * CB + jj;
+    Ps[i * L16 + jj] = psi_T[o];
+    Lm[i * L16 + jj] = dpsi_T ? dpsi_T[o] : 0.f;
+  }
+  // chunk n's inputs: registers first (the next chunk's arrive while this one runs)
+  constexpr int EU = D * C / NT;  // elements of k (and of v, dO) per thread
+  float rk[EU], rv[EU], rd[EU], rq, rt[R * R / NT];
+  auto tok = [&](int tg) { return (static_cast<int64_t>(b) * T + tg) * H + hd; };
+  auto fetch = [&](int n) {
+#pragma unroll
+    for (int m = 0; m < EU; ++m) {
+      const int e = tid + NT * m, t = e / D, i = e % D, tg = n * C + t;
+      const int64_t o = tok(tg < T ? tg : 0) * D + i;
+      rk[m] = io<IO>::load(k, o);
+      rv[m] = io<IO>::load(v, o);
+      rd[m] = io<GO>::load(dout, o);
+    }
+    {
+      const int t = tid / CB, jj = tid % CB, tg = n * C + t;  // CB * C == NT
+      rq = io<IO>::load(q, tok(tg < T ? tg : 0) * D + blk * CB + jj);
+    }
+#pragma unroll
+    for (int m = 0; m < R * R / NT; ++m)
+      rt[m] = tt[(static_cast<int64_t>(bh) * nch + n) * REC + tid + NT * m];
+  };
+  auto commit = [&](int n) {
+#pragma unroll
+    for (int m = 0; m < EU; ++m) {
+      const int e = tid + NT * m, t = e / D, i = e % D;
+      const bool ok = n * C + t < T;
+      U[i * L32 + 2 * t] = ok ? rk[m] : 0.f;
+      U[i * L32 + 2 * t + 1] = ok ? rv[m] : 0.f;
+      dO[i * L16 + t] = ok ? rd[m] : 0.f;
+    }
+    {
+      const int t = tid / CB, jj = tid % CB;
+      Qb[jj * L16 + t] = n * C + t < T ? rq : 0.f;
+    }
+#pragma unroll
+    for (int m = 0; m < R * R / NT; ++m) {
+      const int e = tid + NT * m;
+      Tt[(e / R) * L32 + e % R] = rt[m];
+    }
+  };
+
+  if (nch > 0) {
+    fetch(nch - 1);
+    commit(nch - 1);
+  }
+  __syncthreads();
+  for (int n = nch - 1; n >= 0; --n) {
+    if (n > 0) fetch(n - 1);
+    // Psi_s = Psi_e + U (T~^T (U^T Psi_e))
+    lgemm<R, CB, D, true, false, kStore>(U, L32, Ps, L16, S1, L16, wave, lane);
+    __syncthreads();
+    lgemm<R, CB, R, true, false, kStore>(Tt, L32, S1, L16, Wm, L16, wave, lane);
+    __syncthreads();
+    lgemm<D, CB, R, false, false, kAdd>(U, L32, Wm, L16, Ps, L16, wave, lane);
+    __syncthreads();
+    // W = U^T Psi_s (waves 0-1);  dX = mask o (U^T dO) (waves 2-3)
+    lgemm<R, CB, D, true, false, kStore, 0, 2>(U, L32, Ps, L16, Wm, L16, wave, lane);
+    lgemm<R, C, D, true, false, kMaskStore, 2, 2>(U, L32, dO, L16, dXm, L16, wave, lane);
+    __syncthreads();
+    // Z = T~ W (waves 0-1), Psi_s^T dO (wave 0, first term of dQ);
+    // dZ = U^T Lam_e + dX Q^T (waves 2-3)
+    lgemm<R, CB, R, false, false, kStore, 0, 2>(Tt, L32, Wm, L16, Zm, L16, wave, lane);
+    lgemm<CB, C, D, true, false, kStore, 1, 1>(Ps, L16, dO, L16, QD, L16, wave, lane);
+    lgemm<R, CB, D, true, false, kStore, 2, 2>(U, L32, Lm, L16, dZm, L16, wave, lane);
+    lgemm<R, CB, C, false, true, kAdd, 2, 2>(dXm, L16, Qb, L16, dZm, L16, wave, lane);
+    __syncthreads();
+    // X = mask o (Z Q) (wave 0);  dW = T~^T dZ (wave 1);  dT~ partial = dZ W^T (waves 2-3);
+    // dQ = Z^T dX + Psi_s^T dO (wave 0)
+    lgemm<R, C, CB, false, false, kMaskStore, 0, 1>(Zm, L16, Qb, L16, Xm, L16, wave, lane);
+    lgemm<R, CB, R, true, false, kStore, 1, 1>(Tt, L32, dZm, L16, dWm, L16, wave, lane);
+    lgemm<R, R, CB, false, true, kStore, 2, 2>(dZm, L16, Wm, L16, dTp, L32, wave, lane);
+    lgemm<CB, C, R, true, false, kStore, 0, 1>(Zm, L16, dXm, L16, dQm, L16, wave, lane);
+    __syncthreads();
+    // dU partial = Lam_e Z^T + dO X^T + Psi_s dW^T, straight to the workspace
+    float* pp = part + ((static_cast<int64_t>(bh) * nch + n) * NBLK + blk) * PS;
+    lgemm3_nt_global<D>(Lm, Zm, dO, Xm, Ps, dWm, pp + R * R, wave, lane);
+    __syncthreads();
+    // outputs of the chunk, then Lam_s = Lam_e + dO Q^T + U dW
+    {
+      for (int e = tid; e < R * R; e += NT) pp[e] = dTp[(e / R) * L32 + e % R];
+      const int jj = tid / C, t = tid % C, tg = n * C + t;  // CB * C == NT
+      if (tg < T) io<IO>::store(dq, tok(tg) * D + blk * CB + jj, dQm[jj * L16 + t] + QD[jj * L16 + t]);
+    }
+    lgemm<D, CB, C, false, true, kAdd>(dO, L16, Qb, L16, Lm, L16, wave, lane);
+    lgemm<D, CB, R, false, false, kAdd>(U, L32, dWm, L16, Lm, L16, wave, lane);
+    __syncthreads();
+    if (n > 0) commit(n - 1);
+    __syncthreads();
+  }
+  if (dpsi0) {
+    for (int e = tid; e < D * CB; e += NT) {
+      const int i = e / CB, jj = e % CB;
+      dpsi0[bh * DD + static_cast<int64_t>(i) * D + blk * CB + jj] = Lm[i * L16 + jj];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- per chunk: dT~ -> dk, dv, ddelta
+template <typename IO, int D>
+__global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
+    const IO* __restrict__ k, const IO* __restrict__ v, const void* __restrict__ delta,
+    int delta_dtype, const float* __restrict__ tt, const float* __restrict__ part,
+    IO* __restrict__ dk, IO* __restrict__ dv, void* __restrict__ ddelta, int T, int H) {
+  constexpr int PS = PartC<D>::size;
+  constexpr int NBLK = D / CB;
+  __shared__ float U[D * R], G[R * R], L[R * R], A[R * R], Mb[4 * C], dl[C];
+  __shared__ float dT[R * R], dA[R * R], tmp[R * R], dG[R * R], dU[D * R];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, hd = bh % H;
+  const int nch = gridDim.x;
+  auto tok = [&](int tg) { return (static_cast<int64_t>(b) * T + tg) * H + hd; };
+  for (int e = tid; e < D * C; e += NT) {
+    const int t = e / D, i = e % D, tg = n * C + t;
+    const bool ok = tg < T;
+    const int64_t o = tok(ok ? tg : 0) * D + i;
+    U[i * R + 2 * t] = ok ? io<IO>::load(k, o) : 0.f;
+    U[i * R + 2 * t + 1] = ok ? io<IO>::load(v, o) : 0.f;
+  }
+  if (tid < C) {
+    const int tg = n * C + tid;
+    dl[tid] = tg < T ? load_scalar(delta, delta_dtype, tok(tg)) : 0.f;
+  }
+  // the partials summed over the column blocks (16-byte loads, all blocks in flight)
+  {
+    const float4* pp = reinterpret_cast<const float4*>(part + (static_cast<int64_t>(bh) * nch + n) * NBLK * PS);
+    for (int e4 = tid; e4 < PS / 4; e4 += NT) {
+      float4 x[NBLK];
+#pragma unroll
+      for (int j = 0; j < NBLK; ++j) x[j] = pp[j * (PS / 4) + e4];
+      float4 s = x[0];
+#pragma unroll
+      for (int j = 1; j < NBLK; ++j) { s.x += x[j].x; s.y += x[j].y; s.z += x[j].z; s.w += x[j].w; }
+      const int e = 4 * e4;
+      float* dst = e < R * R ? dT + e : dU + (e - R * R);
+      dst[0] = s.x; dst[1] = s.y; dst[2] = s.z; dst[3] = s.w;
+    }
+  }
+  {  // A, G and M of the chunk from the prep kernel's record
+    const float* rec = tt + (static_cast<int64_t>(bh) * nch + n) * REC;
+    for (int e = tid; e < R * R; e += NT) {
+      A[e] = rec[R * R + e];
+      G[e] = rec[2 * R * R + e];
+    }
+    if (tid < 4 * C) Mb[tid] = rec[3 * R * R + tid];
+  }
+  __syncthreads();
+  // B = blockdiag(M) in tmp; dA = dT~ B^T (block structure: dA[r][2s + a] = sum_b dT[r][2s + b] M_s[a][b])
+  for (int e = tid; e < R * R; e += NT) {
+    const int r = e / R, c = e % R, s = c >> 1, a = c & 1;
+    dA[e] = dT[r * R + 2 * s] * Mb[4 * s + 2 * a] + dT[r * R + 2 * s + 1] * Mb[4 * s + 2 * a + 1];
+  }
+  __syncthreads();
+  // dB = A^T dT~ (diagonal blocks used) -> dG scratch later; tmp = A^T dA
+  lgemm<R, R, R, true, false, kStore>(A, R, dA, R, tmp, R, wave, lane);
+  lgemm<R, R, R, true, false, kStore>(A, R, dT, R, dG, R, wave, lane);  // dB (full)
+  __syncthreads();
+  // dL = tmp A^T  (into dA)
+  lgemm<R, R, R, false, true, kStore>(tmp, R, A, R, dA, R, wave, lane);
+  __syncthreads();
+  // dM_t = dB_tt + sum_{i<t} dL_ti G_ti^T; then the M chain; dG_ti = M_t^T dL_ti (i < t)
+  if (tid < 4 * C) {
+    const int t = tid >> 2, a = (tid >> 1) & 1, c = tid & 1;
+    float x = dG[(2 * t + a) * R + 2 * t + c];
+    for (int i = 0; i < t; ++i)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) x = fmaf(dA[(2 * t + a) * R + 2 * i + m], G[(2 * t + c) * R + 2 * i + m], x);
+    tmp[tid] = x;  // dM_t[a][c]
+  }
+  __syncthreads();
+  for (int e = tid; e < R * R; e += NT) {  // dG off-diagonal blocks (lower), zero elsewhere
+    const int r = e / R, c = e % R, t = r >> 1, i = c >> 1, a = r & 1;
+    float x = 0.f;
+    if (i < t)  // (M_t^T dL_ti)[a][cb] = sum_m M_t[m][a] dL_ti[m][cb]
+      x = Mb[4 * t + a] * dA[(2 * t) * R + c] + Mb[4 * t + 2 + a] * dA[(2 * t + 1) * R + c];
+    L[e] = x;  // L is free now: the new dG
+  }
+  __syncthreads();
+  if (tid < C) {  // M chain (vmi::cayley_coeffs) -> ddelta and the diagonal Gram entries
+    const int t = tid;
+    const float kk = G[(2 * t) * R + 2 * t], vv = G[(2 * t + 1) * R + 2 * t + 1], kv = G[(2 * t) * R + 2 * t + 1];
+    const float d00 = tmp[4 * t], d01 = tmp[4 * t + 1], d10 = tmp[4 * t + 2], d11 = tmp[4 * t + 3];
+    const float hh = 0.5f * dl[t], P = hh * hh;
+    const float graw = kk * vv - kv * kv, g = fmaxf(graw, 0.f);
+    const float c = 2.f / (1.f + P * g);
+    const float N00 = -P * vv, N01 = P * kv - hh, N10 = P * kv + hh, N11 = -P * kk;
+    const float S = d00 * N00 + d01 * N01 + d10 * N10 + d11 * N11;
+    float dh = c * (d01 * (2.f * hh * kv - 1.f) + d10 * (2.f * hh * kv + 1.f) - 2.f * hh * (d00 * vv + d11 * kk));
+    float dvv = -c * P * d00, dkk = -c * P * d11, dkv = c * P * (d01 + d10);
+    dh += S * (-c * c * hh * g);
+    const float dg = graw > 0.f ? S * (-0.5f * c * c * P) : 0.f;
+    dkk += dg * vv;
+    dvv += dg * kk;
+    dkv += -2.f * dg * kv;
+    L[(2 * t) * R + 2 * t] += dkk;
+    L[(2 * t + 1) * R + 2 * t + 1] += dvv;
+    L[(2 * t) * R + 2 * t + 1] += dkv;
+    const int tg = n * C + t;
+    if (tg < T) {
+      const float dd = 0.5f * dh;
+      const int64_t o = tok(tg);
+      if (delta_dtype == VMI_F32) static_cast<float*>(ddelta)[o] = dd;
+      else if (delta_dtype == VMI_BF16) static_cast<uint16_t*>(ddelta)[o] = f32_to_bf16(dd);
+      else static_cast<f16_t*>(ddelta)[o] = static_cast<f16_t>(dd);
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < R * R; e += NT) {  // symmetrise: dG + dG^T
+    const int r = e / R, c = e % R;
+    tmp[e] = L[r * R + c] + L[c * R + r];
+  }
+  __syncthreads();
+  lgemm<D, R, R, false, false, kAdd>(U, R, tmp, R, dU, R, wave, lane);
+  __syncthreads();
+  for (int e = tid; e < D * C; e += NT) {
+    const int t = e / D, i = e % D, tg = n * C + t;
+    if (tg < T) {
+      const int64_t o = tok(tg) * D + i;
+      io<IO>::store(dk, o, dU[i * R + 2 * t]);
+      io<IO>::store(dv, o, dU[i * R + 2 * t + 1]);
+    }
+  }
+}
+
+template <typename IO, typename GO, int D>
+hipError_t launch_d(const void* q, const void* k, const void* v, const void* delta,
+                    int delta_dtype, const float* psi_T, const void* dout, const float* dpsi_T,
+                    void* dq, void* dk, void* dv, void* ddelta, float* dpsi0, int B, int T,
+                    int H, void* ws, hipStream_t stream) {
+  const int nch = (T + C - 1) / C;
+  const int BH = B * H;
+  float* tt = static_cast<float*>(ws);
+  float* part = tt + static_cast<int64_t>(BH) * nch * REC;
+  if (nch > 0) {
+    hipLaunchKernelGGL((bwdc_prep_kernel<IO, D>), dim3(nch, BH), dim3(NT), 0, stream,
+                       static_cast<const IO*>(k), static_cast<const IO*>(v), delta, delta_dtype,
+                       tt, T, H);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((bwdc_cols_kernel<IO, GO, D>), dim3(D / CB, BH), dim3(NT), 0, stream,
+                     static_cast<const IO*>(q), static_cast<const IO*>(k),
+                     static_cast<const IO*>(v), tt, psi_T, static_cast<const GO*>(dout), dpsi_T,
+                     static_cast<IO*>(dq), dpsi0, part, T, H);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || nch == 0) return e;
+  hipLaunchKernelGGL((bwdc_reduce_kernel<IO, D>), dim3(nch, BH), dim3(NT), 0, stream,
+                     static_cast<const IO*>(k), static_cast<const IO*>(v), delta, delta_dtype,
+                     tt, part, static_cast<IO*>(dk), static_cast<IO*>(dv), ddelta, T, H);
+  return hipGetLastError();
+}
+
+template <typename IO, typename GO>
+hipError_t launch_go(const void* q, const void* k, const void* v, const void* delta,
+                     int delta_dtype, const float* psi_T, const void* dout, const float* dpsi_T,
+                     void* dq, void* dk, void* dv, void* ddelta, float* dpsi0, int B, int T,
+                     int H, int D, void* ws, hipStream_t stream) {
+  if (D == 64)
+    return launch_d<IO, GO, 64>(q, k, v, delta, delta_dtype, psi_T, dout, dpsi_T, dq, dk, dv,
+                                ddelta, dpsi0, B, T, H, ws, stream);
+  return launch_d<IO, GO, 128>(q, k, v, delta, delta_dtype, psi_T, dout, dpsi_T, dq, dk, dv,
+                               ddelta, dpsi0, B, T, H, ws, stream);
+}
+
+template <typename IO>
+hipError_t launch_io(const void* q, const void* k, const void* v, const void* delta,
+                     int delta_dtype, const float* psi_T, const void* dout, int dout_dtype,
+                     const float* dpsi_T, void* dq, void* dk, void* dv, void* ddelta,
+                     float* dpsi0, int B, int T, int H, int D, void* ws, hipStream_t stream) {
+  if (dout_dtype == VMI_F32)
+    return launch_go<IO, float>(q, k, v, delta, delta_dtype, psi_T, dout, dpsi_T, dq, dk, dv,
+                                ddelta, dpsi0, B, T, H, D, ws, stream);
+  if (dout_dtype == VMI_BF16)
+    return launch_go<IO, bf16_t>(q, k, v, delta, delta_dtype, psi_T, dout, dpsi_T, dq, dk, dv,
+                                 ddelta, dpsi0, B, T, H, D, ws, stream);
+  return launch_go<IO, f16_t>(q, k, v, delta, delta_dtype, psi_T, dout, dpsi_T, dq, dk, dv,
+                              ddelta, dpsi0, B, T, H, D, ws, stream);
+}
+
+}  // namespace bwdc
+
+size_t sssd_bwd_chunk_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D) {
+  const int64_t nch = (T + bwdc::C - 1) / bwdc::C;
+  const int64_t per = bwdc::REC + (D / bwdc::CB) * (bwdc::R * bwdc::R + D * bwdc::R);
+  return static_cast<size_t>(B * H * nch * per) * sizeof(float);
+}
+
+hipError_t launch_sssd_bwd_chunk(const void* q, const void* k, const void* v, const void* delta,
+                                 int io_dtype, int delta_dtype, const float* psi_T,
+                                 const void* dout, int dout_dtype, const float* dpsi_T, void* dq,
+                                 void* dk, void* dv, void* ddelta, float* dpsi0, int B, int T,
+                                 int H, int D, void* ws, hipStream_t stream) {
+  if (io_dtype == VMI_F32)
+    return bwdc::launch_io<float>(q, k, v, delta, delta_dtype, psi_T, dout, dout_dtype, dpsi_T, dq,
+                                  dk, dv, ddelta, dpsi0, B, T, H, D, ws, stream);
+  if (io_dtype == VMI_BF16)
+    return bwdc::launch_io<bf16_t>(q, k, v, delta, delta_dtype, psi_T, dout, dout_dtype, dpsi_T,
+                                   dq, dk, dv, ddelta, dpsi0, B, T, H, D, ws, stream);
+  return bwdc::launch_io<f16_t>(q, k, v, delta, delta_dtype, psi_T, dout, dout_dtype, dpsi_T, dq,
+                                dk, dv, ddelta, dpsi0, B, T, H, D, ws, stream);
+}
+
+}  // namespace vmi

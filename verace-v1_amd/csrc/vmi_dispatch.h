@@ -136,6 +136,16 @@ hipError_t launch_sssd_bwd(const void* q, const void* k, const void* v, const vo
                            void* ddelta, float* dpsi0, int B, int T, int H, int D, void* ws,
                            hipStream_t stream);
 
+// sssd_bwd_chunk.hip: the same backward in chunks of 16 tokens on the fp32 MFMA
+// (used for T >= kBwdChunkMinT).
+constexpr int64_t kBwdChunkMinT = 32;
+size_t sssd_bwd_chunk_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D);
+hipError_t launch_sssd_bwd_chunk(const void* q, const void* k, const void* v, const void* delta,
+                                 int io_dtype, int delta_dtype, const float* psi_T,
+                                 const void* dout, int dout_dtype, const float* dpsi_T, void* dq,
+                                 void* dk, void* dv, void* ddelta, float* dpsi0, int B, int T,
+                                 int H, int D, void* ws, hipStream_t stream);
+
 // cham_ns.hip: Newton-Schulz unitary retraction.
 size_t ns_workspace_bytes(int64_t batch, int64_t n);
 hipError_t launch_ns_retraction(const float* h_real, const float* h_imag, float* out_real,
