@@ -429,12 +429,12 @@ def bench_backward(device, iters=5, warmup=2):
         ev[i + 1].record(stream)
     torch.cuda.synchronize()
     us = statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(iters))
-    flops = B * T * H * 26 * D * D  # 13 D^2 FMA per token-head
+    flops = B * T * H * 26 * D * D  # 13 D^2 FMA per token-head (the per-token recursion)
     return {
         "config": "SSSD scan backward B=4 T=2048 H=8 D=128 bf16 (FULL training shape)",
         "us_median": round(us, 1),
         "tokens_per_s": round(B * T / (us * 1e-6), 1),
-        "valu_tflops": round(flops / (us * 1e-6) / 1e12, 2),
+        "algorithmic_tflops": round(flops / (us * 1e-6) / 1e12, 2),
     }
 
 
