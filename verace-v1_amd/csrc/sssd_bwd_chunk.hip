@@ -340,14 +340,19 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
   // the partials summed over the column blocks (16-byte loads, all blocks in flight)
   {
     const float4* pp = reinterpret_cast<const float4*>(part + (static_cast<int64_t>(bh) * nch + n) * NBLK * PS);
-    for (int e4 = tid; e4 < PS / 4; e4 += NT) {
-      float4 x[NBLK];
+    static_assert(PS % (4 * NT) == 0, "partials split evenly over the threads");
+    constexpr int NE = PS / (4 * NT);
+    float4 x[NE][NBLK];
 #pragma unroll
-      for (int j = 0; j < NBLK; ++j) x[j] = pp[j * (PS / 4) + e4];
-      float4 s = x[0];
+    for (int u = 0; u < NE; ++u)
 #pragma unroll
-      for (int j = 1; j < NBLK; ++j) { s.x += x[j].x; s.y += x[j].y; s.z += x[j].z; s.w += x[j].w; }
-      const int e = 4 * e4;
+      for (int j = 0; j < NBLK; ++j) x[u][j] = pp[j * (PS / 4) + tid + NT * u];
+#pragma unroll
+    for (int u = 0; u < NE; ++u) {
+      float4 s = x[u][0];
+#pragma unroll
+      for (int j = 1; j < NBLK; ++j) { s.x += x[u][j].x; s.y += x[u][j].y; s.z += x[u][j].z; s.w += x[u][j].w; }
+      const int e = 4 * (tid + NT * u);
       float* dst = e < R * R ? dT + e : dU + (e - R * R);
       dst[0] = s.x; dst[1] = s.y; dst[2] = s.z; dst[3] = s.w;
     }
