@@ -494,14 +494,24 @@ def pmc_summary(fetch_csv, write_csv, out_json):
         kern = {}
         for k, v in vals.items():
             if "sssd_chunk_kernel" in k or "sssd_carry_kernel" in k:
-                # the READOUT flag is the kernel template's last argument (mangled Lb0E / Lb1E)
+                # template <E, DT, READOUT, FUSED>: READOUT is the first of the two mangled
+                # bools (Lb0E / Lb1E); only the unfused kernels are the OP scan
                 flags = re.findall(r"Lb([01])E", k)
+                if "sssd_chunk_kernel" in k and (len(flags) < 2 or flags[1] == "1"):
+                    continue
                 tag = ("pass B (carry)" if "sssd_carry_kernel" in k else
-                       "pass C (readout)" if flags and flags[-1] == "1" else "pass A (segment transforms)")
+                       "pass C (readout)" if flags[0] == "1" else "pass A (segment transforms)")
                 kern[tag] = sum(v) / len(v) * scale
         res[counter] = {"scale": scale, "bytes_per_launch": kern, "bytes_per_scan": sum(kern.values())}
         total += sum(kern.values())
+        # the decode step (dense states), when the run included it
+        step = [x for k, v in vals.items() if "sssd_step128_kernel" in k and "DenseStates" in k for x in v]
+        if step:
+            res[counter]["decode_step_bytes_per_launch"] = sum(step) / len(step) * scale
     res["hbm_bytes_per_scan"] = total
+    if all("decode_step_bytes_per_launch" in res[c] for c in ("FETCH_SIZE", "WRITE_SIZE")):
+        res["hbm_bytes_per_decode_step"] = (res["FETCH_SIZE"]["decode_step_bytes_per_launch"] +
+                                            res["WRITE_SIZE"]["decode_step_bytes_per_launch"])
     with open(out_json, "w") as f:
         json.dump(res, f, indent=1)
     return res
@@ -523,6 +533,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-long", action="store_true", help="skip the LONG (T=65536) scan timing")
     ap.add_argument("--no-module", action="store_true",
                     help="skip the FULL SSSD sub-layer (fused vs unfused projections) timing")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -587,7 +598,8 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    result["long"] = bench_long(device)
+    if not args.no_long:
+        result["long"] = bench_long(device)
     if not args.no_decode:
         result["decode"] = bench_decode(device)
         result["decode_cache"] = bench_decode_cache(device)
