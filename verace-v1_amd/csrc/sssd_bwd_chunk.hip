@@ -21,6 +21,8 @@
 //     through the chunks in reverse, Psi and Lam in LDS; dQ of its columns directly, the
 //     column sums dT~ and dU as per-chunk partials;
 //   bwdc_reduce_kernel (grid (nch, B H)): sums the partials, dT~ -> dM, dG -> dk, dv, ddelta.
+#include <type_traits>
+
 #include "vmi_common.h"
 #include "vmi_dispatch.h"
 #include "vmi_lanes.h"
@@ -36,6 +38,11 @@ constexpr int NT = 256;
 constexpr int REC = 3 * R * R + 4 * C;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ short to_bf16(float x) {  // round to nearest even
+  return __builtin_bit_cast(short, static_cast<__bf16>(x));
+}
 
 enum { kStore = 0, kAdd = 1, kMaskStore = 2 };
 
@@ -52,7 +59,11 @@ constexpr int L32 = 33;  // 32-wide matrices
 // [k = lane / 16], B[k = lane / 16][n = lane % 16], D[4 (lane / 16) + r][lane % 16].  Two
 // accumulators over alternate k steps halve the dependent chain.  kMaskStore keeps the
 // (row = rank row rho, col = token t) entries with rho / 2 <= t.
-template <int M, int N, int K, bool TA, bool TB, int MODE, int W0 = 0, int NW = 4>
+// LP: operands rounded to bf16 (v_mfma_f32_16x16x16_bf16, lane (m, kq) supplies
+// A[m][4 kq .. 4 kq + 3] of a 16-wide k step), fp32 accumulation; for the bf16 / fp16
+// inputs' per-chunk gradient products only.
+template <int M, int N, int K, bool TA, bool TB, int MODE, int W0 = 0, int NW = 4,
+          bool LP = false>
 __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, int ldb, float* Cm,
                                       int ldc, int wave, int lane) {
   constexpr int TN = N / 16, NTILE = (M / 16) * TN;
@@ -62,6 +73,21 @@ __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, i
     const int tm = tile / TN, tn = tile % TN;
     const int am = 16 * tm + l16, bn = 16 * tn + l16;
     f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (LP) {
+      static_assert(K % 16 == 0, "bf16 steps of 16");
+#pragma unroll 4
+      for (int k0 = 0; k0 < K; k0 += 16) {
+        s16x4 a, b;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int k = k0 + 4 * kq + i;
+          a[i] = to_bf16(TA ? A[k * lda + am] : A[am * lda + k]);
+          b[i] = to_bf16(TB ? B[bn * ldb + k] : B[k * ldb + bn]);
+        }
+        if ((k0 >> 4) & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc1, 0, 0, 0);
+        else acc0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc0, 0, 0, 0);
+      }
+    } else {
 #pragma unroll 4
     for (int k0 = 0; k0 < K; k0 += 8) {
       const int k = k0 + kq;
@@ -74,6 +100,7 @@ __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, i
         const float b1 = TB ? B[bn * ldb + k1] : B[k1 * ldb + bn];
         acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc1, 0, 0, 0);
       }
+    }
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -90,7 +117,7 @@ __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, i
 // dst (global, M x 32, row stride 32) = A1 B1^T + A2 B2^T + A3 B3^T with A_i [M][16] and
 // B_i [32][16] in LDS (row stride L16): the three products of one tile share one
 // accumulator, so the sum goes to memory once.
-template <int M>
+template <int M, bool LP>
 __device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B1, const float* A2,
                                                  const float* B2, const float* A3, const float* B3,
                                                  float* dst, int wave, int lane) {
@@ -104,11 +131,22 @@ __device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B
     const float* Bs[3] = {B1, B2, B3};
 #pragma unroll
     for (int u = 0; u < 3; ++u) {
+      if constexpr (LP) {
+        s16x4 a, b;
 #pragma unroll
-      for (int k0 = 0; k0 < 16; k0 += 8) {
-        const int k = k0 + kq;
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(As[u][am * L16 + k], Bs[u][bn * L16 + k], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(As[u][am * L16 + k + 4], Bs[u][bn * L16 + k + 4], acc1, 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+          a[i] = to_bf16(As[u][am * L16 + 4 * kq + i]);
+          b[i] = to_bf16(Bs[u][bn * L16 + 4 * kq + i]);
+        }
+        if (u & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc1, 0, 0, 0);
+        else acc0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc0, 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int k0 = 0; k0 < 16; k0 += 8) {
+          const int k = k0 + kq;
+          acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(As[u][am * L16 + k], Bs[u][bn * L16 + k], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(As[u][am * L16 + k + 4], Bs[u][bn * L16 + k + 4], acc1, 0, 0, 0);
+        }
       }
     }
 #pragma unroll
@@ -198,6 +236,9 @@ __global__ __launch_bounds__(NT) void bwdc_cols_kernel(
     float* __restrict__ part, int T, int H) {
   constexpr int PS = PartC<D>::size;
   constexpr int NBLK = D / CB;
+  // bf16 / fp16 inputs: the per-chunk gradient products take bf16 operands (their 2e-2 bar);
+  // the state reconstruction and the adjoint update, carried across chunks, stay fp32
+  constexpr bool LP = !std::is_same<IO, float>::value;
   // row strides: L32 for the 32-wide (rank index) matrices, L16 for the 16-wide ones
   __shared__ float U[D * L32], Tt[R * L32], Qb[CB * L16], dO[D * L16];
   __shared__ float Ps[D * L16], Lm[D * L16];
@@ -271,26 +312,26 @@ __global__ __launch_bounds__(NT) void bwdc_cols_kernel(
     lgemm<D, CB, R, false, false, kAdd>(U, L32, Wm, L16, Ps, L16, wave, lane);
     __syncthreads();
     // W = U^T Psi_s (waves 0-1);  dX = mask o (U^T dO) (waves 2-3)
-    lgemm<R, CB, D, true, false, kStore, 0, 2>(U, L32, Ps, L16, Wm, L16, wave, lane);
-    lgemm<R, C, D, true, false, kMaskStore, 2, 2>(U, L32, dO, L16, dXm, L16, wave, lane);
+    lgemm<R, CB, D, true, false, kStore, 0, 2, LP>(U, L32, Ps, L16, Wm, L16, wave, lane);
+    lgemm<R, C, D, true, false, kMaskStore, 2, 2, LP>(U, L32, dO, L16, dXm, L16, wave, lane);
     __syncthreads();
     // Z = T~ W (waves 0-1), Psi_s^T dO (wave 0, first term of dQ);
     // dZ = U^T Lam_e + dX Q^T (waves 2-3)
-    lgemm<R, CB, R, false, false, kStore, 0, 2>(Tt, L32, Wm, L16, Zm, L16, wave, lane);
-    lgemm<CB, C, D, true, false, kStore, 1, 1>(Ps, L16, dO, L16, QD, L16, wave, lane);
-    lgemm<R, CB, D, true, false, kStore, 2, 2>(U, L32, Lm, L16, dZm, L16, wave, lane);
-    lgemm<R, CB, C, false, true, kAdd, 2, 2>(dXm, L16, Qb, L16, dZm, L16, wave, lane);
+    lgemm<R, CB, R, false, false, kStore, 0, 2, LP>(Tt, L32, Wm, L16, Zm, L16, wave, lane);
+    lgemm<CB, C, D, true, false, kStore, 1, 1, LP>(Ps, L16, dO, L16, QD, L16, wave, lane);
+    lgemm<R, CB, D, true, false, kStore, 2, 2, LP>(U, L32, Lm, L16, dZm, L16, wave, lane);
+    lgemm<R, CB, C, false, true, kAdd, 2, 2, LP>(dXm, L16, Qb, L16, dZm, L16, wave, lane);
     __syncthreads();
     // X = mask o (Z Q) (wave 0);  dW = T~^T dZ (wave 1);  dT~ partial = dZ W^T (waves 2-3);
     // dQ = Z^T dX + Psi_s^T dO (wave 0)
-    lgemm<R, C, CB, false, false, kMaskStore, 0, 1>(Zm, L16, Qb, L16, Xm, L16, wave, lane);
-    lgemm<R, CB, R, true, false, kStore, 1, 1>(Tt, L32, dZm, L16, dWm, L16, wave, lane);
-    lgemm<R, R, CB, false, true, kStore, 2, 2>(dZm, L16, Wm, L16, dTp, L32, wave, lane);
-    lgemm<CB, C, R, true, false, kStore, 0, 1>(Zm, L16, dXm, L16, dQm, L16, wave, lane);
+    lgemm<R, C, CB, false, false, kMaskStore, 0, 1, LP>(Zm, L16, Qb, L16, Xm, L16, wave, lane);
+    lgemm<R, CB, R, true, false, kStore, 1, 1, LP>(Tt, L32, dZm, L16, dWm, L16, wave, lane);
+    lgemm<R, R, CB, false, true, kStore, 2, 2, LP>(dZm, L16, Wm, L16, dTp, L32, wave, lane);
+    lgemm<CB, C, R, true, false, kStore, 0, 1, LP>(Zm, L16, dXm, L16, dQm, L16, wave, lane);
     __syncthreads();
     // dU partial = Lam_e Z^T + dO X^T + Psi_s dW^T, straight to the workspace
     float* pp = part + ((static_cast<int64_t>(bh) * nch + n) * NBLK + blk) * PS;
-    lgemm3_nt_global<D>(Lm, Zm, dO, Xm, Ps, dWm, pp + R * R, wave, lane);
+    lgemm3_nt_global<D, LP>(Lm, Zm, dO, Xm, Ps, dWm, pp + R * R, wave, lane);
     __syncthreads();
     // outputs of the chunk, then Lam_s = Lam_e + dO Q^T + U dW
     {
