@@ -361,81 +361,104 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
     IO* __restrict__ dk, IO* __restrict__ dv, void* __restrict__ ddelta, int T, int H) {
   constexpr int PS = PartC<D>::size;
   constexpr int NBLK = D / CB;
-  __shared__ float U[D * R], G[R * R], L[R * R], A[R * R], Mb[4 * C], dl[C];
-  __shared__ float dT[R * R], dA[R * R], tmp[R * R], dG[R * R], dU[D * R];
+  // U, A and tmp are read along rows by the MFMA operand loads: stride 33 (conflict-free)
+  __shared__ float U[D * L32], A[R * L32], tmp[R * L32];
+  __shared__ float G[R * R], L[R * R], Mb[4 * C], dl[C];
+  __shared__ float dT[R * R], dA[R * R], dG[R * R], dU[D * R];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, hd = bh % H;
   const int nch = gridDim.x;
   auto tok = [&](int tg) { return (static_cast<int64_t>(b) * T + tg) * H + hd; };
-  for (int e = tid; e < D * C; e += NT) {
-    const int t = e / D, i = e % D, tg = n * C + t;
-    const bool ok = tg < T;
-    const int64_t o = tok(ok ? tg : 0) * D + i;
-    U[i * R + 2 * t] = ok ? io<IO>::load(k, o) : 0.f;
-    U[i * R + 2 * t + 1] = ok ? io<IO>::load(v, o) : 0.f;
-  }
-  if (tid < C) {
-    const int tg = n * C + tid;
-    dl[tid] = tg < T ? load_scalar(delta, delta_dtype, tok(tg)) : 0.f;
-  }
-  // the partials summed over the column blocks (16-byte loads, all blocks in flight)
+  // every global load of the workgroup is issued before the first wait: the partials of all
+  // column blocks (16-byte loads), the chunk record (A, G, M) and the chunk's k, v, delta
+  static_assert(PS % (4 * NT) == 0, "partials split evenly over the threads");
+  constexpr int NE = PS / (4 * NT);
+  float4 x[NE][NBLK];
   {
     const float4* pp = reinterpret_cast<const float4*>(part + (static_cast<int64_t>(bh) * nch + n) * NBLK * PS);
-    static_assert(PS % (4 * NT) == 0, "partials split evenly over the threads");
-    constexpr int NE = PS / (4 * NT);
-    float4 x[NE][NBLK];
 #pragma unroll
     for (int u = 0; u < NE; ++u)
 #pragma unroll
       for (int j = 0; j < NBLK; ++j) x[u][j] = pp[j * (PS / 4) + tid + NT * u];
-#pragma unroll
-    for (int u = 0; u < NE; ++u) {
-      float4 s = x[u][0];
-#pragma unroll
-      for (int j = 1; j < NBLK; ++j) { s.x += x[u][j].x; s.y += x[u][j].y; s.z += x[u][j].z; s.w += x[u][j].w; }
-      const int e = 4 * (tid + NT * u);
-      float* dst = e < R * R ? dT + e : dU + (e - R * R);
-      dst[0] = s.x; dst[1] = s.y; dst[2] = s.z; dst[3] = s.w;
-    }
   }
-  {  // A, G and M of the chunk from the prep kernel's record
+  static_assert(R * R % NT == 0 && D * C % NT == 0 && 4 * C <= NT, "record and tokens split evenly");
+  constexpr int NR = R * R / NT, NK = D * C / NT;
+  float ra[NR], rg[NR], rm = 0.f, rd = 0.f;
+  {
     const float* rec = tt + (static_cast<int64_t>(bh) * nch + n) * REC;
-    for (int e = tid; e < R * R; e += NT) {
-      A[e] = rec[R * R + e];
-      G[e] = rec[2 * R * R + e];
+#pragma unroll
+    for (int u = 0; u < NR; ++u) {
+      ra[u] = rec[R * R + tid + NT * u];
+      rg[u] = rec[2 * R * R + tid + NT * u];
     }
-    if (tid < 4 * C) Mb[tid] = rec[3 * R * R + tid];
+    if (tid < 4 * C) rm = rec[3 * R * R + tid];
+  }
+  float rk[NK], rv[NK];
+#pragma unroll
+  for (int u = 0; u < NK; ++u) {
+    const int e = tid + NT * u, t = e / D, i = e % D, tg = n * C + t;
+    const int64_t o = tok(tg < T ? tg : 0) * D + i;
+    rk[u] = io<IO>::load(k, o);
+    rv[u] = io<IO>::load(v, o);
+  }
+  if (tid < C) {
+    const int tg = n * C + tid;
+    rd = tg < T ? load_scalar(delta, delta_dtype, tok(tg)) : 0.f;
+  }
+#pragma unroll
+  for (int u = 0; u < NR; ++u) {
+    const int e = tid + NT * u;
+    A[(e / R) * L32 + e % R] = ra[u];
+    G[e] = rg[u];
+  }
+  if (tid < 4 * C) Mb[tid] = rm;
+  if (tid < C) dl[tid] = rd;
+#pragma unroll
+  for (int u = 0; u < NK; ++u) {
+    const int e = tid + NT * u, t = e / D, i = e % D;
+    const bool ok = n * C + t < T;
+    U[i * L32 + 2 * t] = ok ? rk[u] : 0.f;
+    U[i * L32 + 2 * t + 1] = ok ? rv[u] : 0.f;
+  }
+#pragma unroll
+  for (int u = 0; u < NE; ++u) {
+    float4 s = x[u][0];
+#pragma unroll
+    for (int j = 1; j < NBLK; ++j) { s.x += x[u][j].x; s.y += x[u][j].y; s.z += x[u][j].z; s.w += x[u][j].w; }
+    const int e = 4 * (tid + NT * u);
+    float* dst = e < R * R ? dT + e : dU + (e - R * R);
+    *reinterpret_cast<float4*>(dst) = s;
   }
   __syncthreads();
-  // B = blockdiag(M) in tmp; dA = dT~ B^T (block structure: dA[r][2s + a] = sum_b dT[r][2s + b] M_s[a][b])
+  // B = blockdiag(M); dA = dT~ B^T (block structure: dA[r][2s + a] = sum_b dT[r][2s + b] M_s[a][b])
   for (int e = tid; e < R * R; e += NT) {
     const int r = e / R, c = e % R, s = c >> 1, a = c & 1;
     dA[e] = dT[r * R + 2 * s] * Mb[4 * s + 2 * a] + dT[r * R + 2 * s + 1] * Mb[4 * s + 2 * a + 1];
   }
   __syncthreads();
-  // dB = A^T dT~ (diagonal blocks used) -> dG scratch later; tmp = A^T dA
-  lgemm<R, R, R, true, false, kStore>(A, R, dA, R, tmp, R, wave, lane);
-  lgemm<R, R, R, true, false, kStore>(A, R, dT, R, dG, R, wave, lane);  // dB (full)
+  // tmp = A^T dA; dB = A^T dT~ (its diagonal blocks used) into dG
+  lgemm<R, R, R, true, false, kStore>(A, L32, dA, R, tmp, L32, wave, lane);
+  lgemm<R, R, R, true, false, kStore>(A, L32, dT, R, dG, R, wave, lane);
   __syncthreads();
   // dL = tmp A^T  (into dA)
-  lgemm<R, R, R, false, true, kStore>(tmp, R, A, R, dA, R, wave, lane);
+  lgemm<R, R, R, false, true, kStore>(tmp, L32, A, L32, dA, R, wave, lane);
   __syncthreads();
   // dM_t = dB_tt + sum_{i<t} dL_ti G_ti^T; then the M chain; dG_ti = M_t^T dL_ti (i < t)
   if (tid < 4 * C) {
     const int t = tid >> 2, a = (tid >> 1) & 1, c = tid & 1;
-    float x = dG[(2 * t + a) * R + 2 * t + c];
+    float y = dG[(2 * t + a) * R + 2 * t + c];
     for (int i = 0; i < t; ++i)
 #pragma unroll
-      for (int m = 0; m < 2; ++m) x = fmaf(dA[(2 * t + a) * R + 2 * i + m], G[(2 * t + c) * R + 2 * i + m], x);
-    tmp[tid] = x;  // dM_t[a][c]
+      for (int m = 0; m < 2; ++m) y = fmaf(dA[(2 * t + a) * R + 2 * i + m], G[(2 * t + c) * R + 2 * i + m], y);
+    tmp[tid] = y;  // dM_t[a][c]
   }
   __syncthreads();
   for (int e = tid; e < R * R; e += NT) {  // dG off-diagonal blocks (lower), zero elsewhere
     const int r = e / R, c = e % R, t = r >> 1, i = c >> 1, a = r & 1;
-    float x = 0.f;
+    float y = 0.f;
     if (i < t)  // (M_t^T dL_ti)[a][cb] = sum_m M_t[m][a] dL_ti[m][cb]
-      x = Mb[4 * t + a] * dA[(2 * t) * R + c] + Mb[4 * t + 2 + a] * dA[(2 * t + 1) * R + c];
-    L[e] = x;  // L is free now: the new dG
+      y = Mb[4 * t + a] * dA[(2 * t) * R + c] + Mb[4 * t + 2 + a] * dA[(2 * t + 1) * R + c];
+    L[e] = y;  // L is free now: the new dG
   }
   __syncthreads();
   if (tid < C) {  // M chain (vmi::cayley_coeffs) -> ddelta and the diagonal Gram entries
@@ -469,10 +492,10 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
   __syncthreads();
   for (int e = tid; e < R * R; e += NT) {  // symmetrise: dG + dG^T
     const int r = e / R, c = e % R;
-    tmp[e] = L[r * R + c] + L[c * R + r];
+    tmp[r * L32 + c] = L[r * R + c] + L[c * R + r];
   }
   __syncthreads();
-  lgemm<D, R, R, false, false, kAdd>(U, R, tmp, R, dU, R, wave, lane);
+  lgemm<D, R, R, false, false, kAdd>(U, L32, tmp, L32, dU, R, wave, lane);
   __syncthreads();
   for (int e = tid; e < D * C; e += NT) {
     const int t = e / D, i = e % D, tg = n * C + t;
