@@ -54,6 +54,7 @@ def _oracle(q, k, v, d, psi0, w_o, w_s, with_state_grad):
     (2, 64, 4, 128, torch.bfloat16, True, True),
     (1, 1, 1, 128, torch.float32, True, False),
     (2, 33, 3, 128, torch.float16, False, False),
+    (1, 50, 2, 64, torch.bfloat16, True, True),
 ])
 def test_scan_backward_matches_oracle(device, B, T, H, D, dtype, init, sgrad):
     from verace_amd import SSSDScanFunction

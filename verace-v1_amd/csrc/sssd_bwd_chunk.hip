@@ -46,11 +46,12 @@ __device__ __forceinline__ short to_bf16(float x) {  // round to nearest even
 
 enum { kStore = 0, kAdd = 1, kMaskStore = 2 };
 
-// LDS row strides: 17 (mod 32) keeps the MFMA operand reads of both orientations at most
-// 2-way bank conflicted (lanes read 16 consecutive elements of 2 rows, or 2 consecutive
-// elements of 16 rows).
-constexpr int L16 = 17;  // 16-wide matrices
-constexpr int L32 = 33;  // 32-wide matrices
+// LDS row strides (64 banks of 4 B): with 19 and 37 every MFMA operand read is at most 2-way
+// bank conflicted across the wave, in both orientations and for both lane layouts (fp32:
+// lane (m, kq) reads element k0 + kq of row m, or row k0 + kq of column m; bf16: elements
+// 4 kq + i).  17 and 33 are 4-way for the bf16 layout.
+constexpr int L16 = 19;  // 16-wide matrices
+constexpr int L32 = 37;  // 32-wide matrices
 
 // Cm (M x N, row stride ldc) (=|+=) opA(A) opB(B), K the inner size, all in LDS.
 // opA(m, k) = TA ? A[k lda + m] : A[m lda + k];  opB(k, n) = TB ? B[n ldb + k] : B[k ldb + n].
