@@ -29,6 +29,7 @@ for _p in (REPO_ROOT, PKG_DIR):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E spec-sheet peak, GB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 / f16 MFMA spec-sheet peak, TFLOP/s
 OP = dict(B=8, T=4096, H=8, D=128)
 DEC = dict(B=64, H=8, D=128, layers=12, steps=256, prefill=512)
 
@@ -352,12 +353,28 @@ def bench_module_full(device, iters=20, warmup=5):
             torch.cuda.synchronize()
             res[name] = statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(iters))
         m.fuse_projections = True
+        # the scan's share of the fused sub-layer: the fused scan op alone on the projections
+        from verace_amd import launch_sssd_hip_scan_fused
+        projs = [torch.nn.functional.linear(x, m._stacked_weight()) for x in xs]
+        w = m.head_rmsnorm.weight
+        for i in range(warmup):
+            launch_sssd_hip_scan_fused(projs[i % 2], H, D, None, w, m.head_rmsnorm.eps, None)
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+        ev[0].record(stream)
+        for i in range(iters):
+            launch_sssd_hip_scan_fused(projs[i % 2], H, D, None, w, m.head_rmsnorm.eps, None)
+            ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        res["scan"] = statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(iters))
     return {
         "config": "FULL SSSD sub-layer: B=4 T=2048 hidden=1024 H=8 D=128 bf16, forward with state",
         "fused_us_median": round(res["fused"], 2),
         "unfused_us_median": round(res["unfused"], 2),
         "speedup": round(res["unfused"] / res["fused"], 3),
         "tokens_per_s_fused": round(B * T / (res["fused"] * 1e-6), 1),
+        "scan_us_median": round(res["scan"], 2),
+        "scan_share_of_fused": round(res["scan"] / res["fused"], 3),
     }
 
 
@@ -610,6 +627,15 @@ def main():
             "traffic": load_traffic(),
             "algorithmic_bytes": nbytes,
             "kernel": "whole scan (all launches of one vmi_sssd_scan_fwd call)",
+            # the matrix-core side of the same time: 10 D^2 algorithmic flop per token-head
+            # (a, b = [k v]^T Psi, the rank-2 update, Psi q) against the dense f16 MFMA peak
+            # the scan's products run on
+            "mfma": {
+                "algorithmic_flops": 10 * D * D * B * T * H,
+                "tflops": round(10 * D * D * B * T * H / (ms * 1e-3) / 1e12, 2),
+                "peak_tflops": MFMA_F16_PEAK_TFLOPS,
+                "frac": round(10 * D * D * B * T * H / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+            },
         },
         "parity": parity,
         "wall_s_timed_region": round(wall, 3),

@@ -7,6 +7,8 @@ Drop-in replacements for the reference's SSSD hot path:
 * ``SSSDScanFunction`` / ``sssd_scan`` / ``launch_sssd_hip_scan_bwd``
                                -- the scan with its backward (training; the reference
                                   differentiates its eager path instead)
+* ``launch_sssd_hip_scan_fused`` -- the scan with the projections' normalisation, delta,
+                                  mask and head RMSNorm fused in (on x @ [W_q; W_k; W_v; W_delta].T)
 * ``sssd_step_``               -- in-place single-token decode step (opt-in)
 * ``SSSDStateCache``           -- per-layer decode state pools with copy-on-write
                                   branches (replaces the ``layer_states`` lists of
@@ -21,6 +23,7 @@ All compute runs in ``libverace_sssd.so`` (C ABI: ``include/verace_sssd.h``).
 """
 from .hip_kernels import (HAS_HIP, SSSDScanFunction, launch_cham_hip_update,
                           launch_sssd_hip_scan, launch_sssd_hip_scan_bwd,
+                          launch_sssd_hip_scan_fused,
                           newton_schulz_unitary_retraction, parallel_newton_schulz_retraction,
                           sssd_scan, sssd_step_)
 from .sssd_attention import SSSDAttention
@@ -35,6 +38,7 @@ __all__ = [
     "SSSDStateCache",
     "SlotTable",
     "launch_sssd_hip_scan",
+    "launch_sssd_hip_scan_fused",
     "launch_cham_hip_update",
     "sssd_step_",
     "newton_schulz_unitary_retraction",
