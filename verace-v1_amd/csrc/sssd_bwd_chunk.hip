@@ -156,11 +156,11 @@ __device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B
 }
 
 // G = U^T U, the Cayley blocks M_t, L and A = (I - L)^-1 of one chunk (LDS).
-// U: [D][R] (row i: k_t at 2t, v_t at 2t + 1; zero past the end); dl[t] the deltas.
+// U: [D][L32] (row i: k_t at 2t, v_t at 2t + 1; zero past the end); dl[t] the deltas.
 template <int D>
 __device__ void chunk_prep(const float* U, const float* dl, float* G, float* Mb, float* L,
                            float* A, int tid, int wave, int lane) {
-  lgemm<R, R, D, true, false, kStore>(U, R, U, R, G, R, wave, lane);
+  lgemm<R, R, D, true, false, kStore>(U, L32, U, L32, G, R, wave, lane);
   __syncthreads();
   if (tid < C) {
     const int t = tid;
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(NT) void bwdc_prep_kernel(const IO* __restrict__ k,
                                                        const void* __restrict__ delta,
                                                        int delta_dtype, float* __restrict__ tt,
                                                        int T, int H) {
-  __shared__ float U[D * R], G[R * R], L[R * R], A[R * R], Mb[4 * C], dl[C];
+  __shared__ float U[D * L32], G[R * R], L[R * R], A[R * R], Mb[4 * C], dl[C];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, hd = bh % H;
   const int nch = gridDim.x;
@@ -206,8 +206,8 @@ __global__ __launch_bounds__(NT) void bwdc_prep_kernel(const IO* __restrict__ k,
     const int t = e / D, i = e % D, tg = n * C + t;
     const bool ok = tg < T;
     const int64_t o = ((static_cast<int64_t>(b) * T + (ok ? tg : 0)) * H + hd) * D + i;
-    U[i * R + 2 * t] = ok ? io<IO>::load(k, o) : 0.f;
-    U[i * R + 2 * t + 1] = ok ? io<IO>::load(v, o) : 0.f;
+    U[i * L32 + 2 * t] = ok ? io<IO>::load(k, o) : 0.f;
+    U[i * L32 + 2 * t + 1] = ok ? io<IO>::load(v, o) : 0.f;
   }
   if (tid < C) {
     const int tg = n * C + tid;
