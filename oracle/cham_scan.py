@@ -2,8 +2,8 @@
 
 * ``cham_scan_eager`` follows ``verace_v1/modules/cham_memory.py:167-238`` in float64:
   G_t = gamma_t (k_t v_t^T + v_t k_t^T); U_t = solve(I - i G_t / 2, I + i G_t / 2)
-  (``_solve_cham_cayley``, :53-97, without its non-finite guard, which never triggers on
-  finite inputs); P_t = U_t ... U_1 (newest on the left, ``parallel_complex_prefix_scan``,
+  (``_solve_cham_cayley``, :53-97, with its non-finite guard: a non-finite solve becomes
+  U = I); P_t = U_t ... U_1 (newest on the left, ``parallel_complex_prefix_scan``,
   :241-293, evaluated sequentially); Hraw_t = P_t H_0 (:219-220, H_0 on the right);
   readout rec_t = Re(NS_3(Hraw_t)) q_t with the matrix Newton-Schulz retraction
   (``parallel_newton_schulz_retraction``, :296-315, via oracle.cham_ns); the exported state
@@ -26,11 +26,20 @@ from .cham_ns import newton_schulz_retraction
 
 
 def cham_cayley_solve(k, v, gamma):
-    """U = (I - iG/2)^-1 (I + iG/2), G = gamma (k v^T + v k^T); k, v [h], float64."""
+    """U = (I - iG/2)^-1 (I + iG/2), G = gamma (k v^T + v k^T); k, v [h], float64.
+
+    With the reference's non-finite guard (``_solve_cham_cayley``, cham_memory.py:68-95):
+    a solve whose result is not finite is redone on the substituted pair (I, I), i.e.
+    U = I."""
     h = k.shape[0]
-    G = gamma * (np.outer(k, v) + np.outer(v, k))
     eye = np.eye(h, dtype=np.complex128)
-    return np.linalg.solve(eye - 0.5j * G, eye + 0.5j * G)
+    with np.errstate(over="ignore", invalid="ignore"):
+        G = gamma * (np.outer(k, v) + np.outer(v, k))
+        right, left = eye - 0.5j * G, eye + 0.5j * G
+    if not (np.isfinite(right).all() and np.isfinite(left).all()):
+        return eye  # solve(I, I): numpy's LAPACK refuses non-finite matrices outright
+    U = np.linalg.solve(right, left)
+    return U if np.isfinite(U).all() else eye
 
 
 def cham_cayley_closed(k, v, gamma):

@@ -139,3 +139,25 @@ def scan_closed(q, k, v, delta, psi0=None) -> Tuple[np.ndarray, np.ndarray]:
         return sssd_scan_closed_c(q, k, v, delta, psi0)
     except (OSError, subprocess.CalledProcessError):
         return sssd_scan_closed_np(q, k, v, delta, psi0)
+
+
+def identity_substitute(k, v, delta):
+    """The reference's non-finite guard as an input substitution (``sssd_attention.py:45-71``):
+    a token-head whose Cayley factor is not finite (a NaN/Inf in its k, v or delta) gets
+    R = I, which is what the closed form yields for k = v = 0, delta = 0.  Returns cleaned
+    float64 copies of k [B,T,H,D], v and delta [B,T,H] and the bad mask [B,T,H].
+    Pinned against the eager restatement of the guard (``sssd_eager.solve_cayley``) in
+    tests/test_oracle_pins.py."""
+    k = np.array(k, dtype=np.float64)
+    v = np.array(v, dtype=np.float64)
+    delta = np.array(delta, dtype=np.float64)
+    if delta.ndim == 4:
+        delta = delta[..., 0]
+    with np.errstate(over="ignore", invalid="ignore"):
+        kk = (k * k).sum(-1)
+        vv = (v * v).sum(-1)
+    bad = ~(np.isfinite(kk) & np.isfinite(vv) & np.isfinite(delta))
+    k[bad] = 0.0
+    v[bad] = 0.0
+    delta[bad] = 0.0
+    return k, v, delta, bad

@@ -152,3 +152,52 @@ def test_scan_backward_empty_sequence(device):
     torch.cuda.synchronize()
     assert dq.shape == (B, 0, H, D) and dd.shape == (B, 0, H)
     assert torch.equal(dpsi0, dpsi)
+
+
+def test_module_rmsnorm_and_out_grads_with_detached_input(device):
+    """x that needs no grad while the parameters do (frozen features): the scan is not
+    differentiated (as the reference's GPU path), but head_rmsnorm and w_out still get their
+    gradients on every route -- the fused one (bf16, D = 128, T >= 32) included -- equal to
+    the unfused route's."""
+    from verace_amd import SSSDAttention
+    print("[case] rmsnorm grad with detached x", flush=True)
+    torch.manual_seed(0)
+    m = SSSDAttention(256, 2, 128).to(device).to(torch.bfloat16)
+    with torch.no_grad():
+        m.head_rmsnorm.weight.add_(0.1 * torch.randn_like(m.head_rmsnorm.weight))
+    x = torch.randn(2, 64, 256, device=device).bfloat16()
+    grads = {}
+    for fused in (True, False):
+        m.zero_grad(set_to_none=True)
+        m.fuse_projections = fused
+        y, _ = m(x)
+        y.float().square().sum().backward()
+        assert m.head_rmsnorm.weight.grad is not None and m.w_out.weight.grad is not None
+        assert m.w_q.weight.grad is None  # the scan cuts the graph, as the reference's GPU path
+        grads[fused] = (m.head_rmsnorm.weight.grad.float().cpu(), m.w_out.weight.grad.float().cpu())
+    torch.cuda.synchronize()
+    for a, b in zip(grads[True], grads[False]):
+        e = _rel(a.numpy(), b.numpy())
+        print(f"  fused vs unfused grad rel={e:.2e}", flush=True)
+        assert e <= 2e-2
+
+
+def test_backward_launcher_rejects_bad_shapes(device):
+    """launch_sssd_hip_scan_bwd validates every argument before any kernel is launched."""
+    from verace_amd import launch_sssd_hip_scan_bwd
+    B, T, H, D = 1, 8, 2, 64
+    q = torch.randn(B, T, H, D, device=device)
+    d = torch.zeros(B, T, H, device=device)
+    psi = torch.zeros(B, H, D, D, device=device)
+    with pytest.raises(RuntimeError):
+        launch_sssd_hip_scan_bwd(q, q[:, :4], q, d, psi, q)          # k shape
+    with pytest.raises(RuntimeError):
+        launch_sssd_hip_scan_bwd(q, q, q, d[:, :, :1], psi, q)       # delta shape
+    with pytest.raises(RuntimeError):
+        launch_sssd_hip_scan_bwd(q, q, q, d, psi[:, :1], q)          # psi_T shape
+    with pytest.raises(RuntimeError):
+        launch_sssd_hip_scan_bwd(q, q, q, d, psi, q[..., :32])       # d_out shape
+    with pytest.raises(RuntimeError):
+        launch_sssd_hip_scan_bwd(q, q, q, d, psi, q, psi[..., :8])   # d_psi_T shape
+    with pytest.raises(RuntimeError):
+        launch_sssd_hip_scan_bwd(q, q.cpu(), q, d, psi, q)           # device

@@ -281,3 +281,62 @@ def test_planted_ns_updated_real_part_reuse_is_caught():
         f = f * (3 - f * f) / 2
     expect = U @ np.diag(f) @ V.conj().T
     assert np.abs(Hi.numpy() - expect.imag).max() > 1e-3
+
+
+# ---------------------------------------------------------------- non-finite guard
+@pytest.mark.parametrize("what", ["k_nan", "k_inf", "v_nan", "v_ninf", "d_nan", "d_inf"])
+def test_identity_substitution_equals_eager_guard(what):
+    """The guard of sssd_attention.py:45-71 (restated op for op in sssd_eager.solve_cayley)
+    equals the substitution k = v = 0, delta = 0 for the bad token-heads fed to the fp64
+    closed form; a plain fp64 scan of the poisoned inputs is not finite (so the check
+    would fail if the guard were dropped from either side)."""
+    import warnings
+    B, T, H, D = 2, 9, 2, 8
+    q, k, v, d = _rand_inputs(B, T, H, D, seed=41)
+    k, v, d = k.clone(), v.clone(), d.clone()
+    for (b, t, h) in [(0, 0, 1), (1, 4, 0), (0, 8, 0)]:
+        if what == "k_nan":
+            k[b, t, h, 2] = float("nan")
+        elif what == "k_inf":
+            k[b, t, h, 0] = float("inf")
+        elif what == "v_nan":
+            v[b, t, h, 3] = float("nan")
+        elif what == "v_ninf":
+            v[b, t, h, 1] = -float("inf")
+        elif what == "d_nan":
+            d[b, t, h] = float("nan")
+        else:
+            d[b, t, h] = float("inf")
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        o_e, s_e = sssd_eager.sssd_scan_eager(q, k, v, d, compute_dtype=torch.float64)
+    kc, vc, dc, bad = sssd_closed.identity_substitute(k.numpy(), v.numpy(), d.numpy())
+    assert bad.sum() == 3
+    o_c, s_c = sssd_closed.sssd_scan_closed_np(q.numpy(), kc, vc, dc)
+    assert np.isfinite(o_e.numpy()).all()
+    assert _rel(o_e.numpy(), o_c) < 1e-12 and _rel(s_e.numpy(), s_c) < 1e-12
+    with np.errstate(invalid="ignore", over="ignore"):
+        o_raw, _ = sssd_closed.sssd_scan_closed_np(q.numpy(), k.numpy(), v.numpy(), d.numpy())
+    assert not np.isfinite(o_raw).all()
+
+
+def test_cham_eager_guard_equals_identity_substitution():
+    """The CHAM guard (cham_memory.py:68-95, in oracle.cham_scan.cham_cayley_solve): the
+    eager restatement on poisoned tokens equals the closed form with those tokens
+    substituted by gamma = 0 (U = I)."""
+    from oracle import cham_scan
+    rng = np.random.default_rng(3)
+    B, T, h = 1, 6, 5
+    q, k, v = (rng.standard_normal((B, T, h)) for _ in range(3))
+    gam = 0.1 / (1 + np.exp(-rng.standard_normal((B, T))))
+    k[0, 1, 2] = np.nan
+    v[0, 3, 0] = np.inf
+    gam[0, 5] = np.nan
+    rec_e, (hr_e, hi_e) = cham_scan.cham_scan_eager(q, k, v, gam)
+    kc, vc, gc = k.copy(), v.copy(), gam.copy()
+    for t in (1, 3, 5):
+        kc[0, t] = vc[0, t] = 0.0
+        gc[0, t] = 0.0
+    rec_c, (hr_c, hi_c) = cham_scan.cham_scan_closed(q, kc, vc, gc)
+    assert np.isfinite(rec_e).all() and np.isfinite(hr_e).all()
+    assert _rel(rec_e, rec_c) < 1e-10 and _rel(hr_e, hr_c) < 1e-10 and _rel(hi_e, hi_c) < 1e-10

@@ -36,6 +36,19 @@ __device__ __forceinline__ NCoef cayley_n(float gamma, float kk, float vv, float
   return n;
 }
 
+// The reference's non-finite guard (cham_memory.py:68-95): a token whose Cayley factor is
+// not finite (NaN or Inf in k, v or gamma, or an overflowing closed form) is replaced by
+// U = I.  Returns N = 0 and ok = false for such a token; the caller must also treat its k,
+// v as zero, since NaN * 0 is NaN.
+__device__ __forceinline__ NCoef cayley_n_guarded(float gamma, float kk, float vv, float kv,
+                                                  bool& ok) {
+  NCoef n = cayley_n(gamma, kk, vv, kv);
+  ok = finite4(gamma, kk, vv, kv) && finite4(n.n11r, n.n11i, n.n12r, n.n12i) &&
+       __builtin_isfinite(n.n22r) && __builtin_isfinite(n.n22i);
+  if (!ok) n = NCoef{0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  return n;
+}
+
 template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i) { return io<T>::load(p, i); }
 
 // Raw 16/32-bit loads converted to fp32 only where they are used: a conversion (or any

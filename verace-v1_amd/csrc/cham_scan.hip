@@ -127,7 +127,12 @@ __global__ __launch_bounds__(64) void cham_state_kernel(
     }
     kk += dpp_f32<0xB1>(kk); vv += dpp_f32<0xB1>(vv); kv += dpp_f32<0xB1>(kv);
     kk += dpp_f32<0x4E>(kk); vv += dpp_f32<0x4E>(vv); kv += dpp_f32<0x4E>(kv);
-    if (part == 0) sN[n & 1][tt] = cayley_n(sg[n & 1][tt], kk, vv, kv);
+    bool ok;
+    const NCoef N = cayley_n_guarded(sg[n & 1][tt], kk, vv, kv, ok);
+    if (part == 0) sN[n & 1][tt] = N;
+    if (!ok) {  // identity token: its k, v rows read as zero (each lane clears its 32 rows)
+      for (int j = 0; j < 32; ++j) sk[n & 1][tt][32 * part + j] = sv[n & 1][tt][32 * part + j] = 0.f;
+    }
   };
   if (nch > 0) {
     fetch(0);
@@ -415,10 +420,12 @@ __global__ __launch_bounds__(RNT) void cham_readout_kernel(
   for (int tt = 0; tt < nt; ++tt) {
     // ---- update H <- U_t H
     float kr[8], vr[8];
+    bool okn;
+    const NCoef N = cayley_n_guarded(sg[tt], sdots[tt][0], sdots[tt][1], sdots[tt][2], okn);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      kr[i] = sk[tt][tr + 16 * i];
-      vr[i] = sv[tt][tr + 16 * i];
+    for (int i = 0; i < 8; ++i) {  // an identity token's k, v read as zero
+      kr[i] = okn ? sk[tt][tr + 16 * i] : 0.f;
+      vr[i] = okn ? sv[tt][tr + 16 * i] : 0.f;
     }
     {
       float4 p[8], tot[8];
@@ -435,7 +442,6 @@ __global__ __launch_bounds__(RNT) void cham_readout_kernel(
         p[j] = make_float4(ar, ai, br, bi);
       }
       col_reduce(p, tot);
-      const NCoef N = cayley_n(sg[tt], sdots[tt][0], sdots[tt][1], sdots[tt][2]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float4 s = tot[j];

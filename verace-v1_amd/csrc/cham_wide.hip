@@ -62,7 +62,8 @@ __global__ __launch_bounds__(256) void wide_coef_kernel(const IO* __restrict__ k
   vv += __shfl_xor(vv, 32);
   kv += __shfl_xor(kv, 32);
   if (lane == 0) {
-    const NCoef N = cayley_n(io<GT>::load(gamma, tok), kk, vv, kv);
+    bool ok;  // identity token: N = 0 (its k, v are read as zero where staged)
+    const NCoef N = cham::cayley_n_guarded(io<GT>::load(gamma, tok), kk, vv, kv, ok);
     float4* o = reinterpret_cast<float4*>(coef + static_cast<int64_t>(tok) * NCF);
     o[0] = make_float4(N.n11r, N.n11i, N.n12r, N.n12i);
     o[1] = make_float4(N.n22r, N.n22i, 0.f, 0.f);
@@ -109,8 +110,10 @@ struct Stager {
     for (int i = 0; i < EPT; ++i) {
       const int e = tid + CNT * i;
       const bool ok = t0 + e / HP < last && e % HP < h;
-      s.k[buf][e / HP][e % HP] = ok ? raw<IO>::f32(rk[i]) : 0.f;
-      s.v[buf][e / HP][e % HP] = ok ? raw<IO>::f32(rv[i]) : 0.f;
+      // non-finite elements read as 0: their token has N = 0 (cayley_n_guarded), so its
+      // update adds exact zeros
+      s.k[buf][e / HP][e % HP] = ok ? finite_or_zero(raw<IO>::f32(rk[i])) : 0.f;
+      s.v[buf][e / HP][e % HP] = ok ? finite_or_zero(raw<IO>::f32(rv[i])) : 0.f;
     }
     // tokens past the range get N = 0: their update adds exact zeros
     if (tid < CHS * NCF) s.n[buf][tid / NCF][tid % NCF] = t0 + tid / NCF < last ? rn : 0.f;

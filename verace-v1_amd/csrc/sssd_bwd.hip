@@ -130,8 +130,16 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
       kk = col_sum(kk);
       vv = col_sum(vv);
       kv = col_sum(kv);
+      // a token with a non-finite Cayley factor is the identity: M = 0 and its k, v rows
+      // zeroed (each lane clears the elements it read; the stage is read after a barrier)
+      bool ok;
+      const cayley2 m = cayley_guarded(sdl[buf][tt], kk, vv, kv, ok);
+      if (!ok) {
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) sk[buf][tt][rg + LPC * r] = sv[buf][tt][rg + LPC * r] = 0.f;
+        kk = vv = kv = 0.f;
+      }
       if (rg == 0) {
-        const cayley2 m = cayley_coeffs(sdl[buf][tt], kk, vv, kv);
         sco[buf][tt][0] = m.m00; sco[buf][tt][1] = m.m01;
         sco[buf][tt][2] = m.m10; sco[buf][tt][3] = m.m11;
         sco[buf][tt][4] = kk; sco[buf][tt][5] = kv; sco[buf][tt][6] = vv;
@@ -284,7 +292,11 @@ __global__ __launch_bounds__(256) void sssd_bwd_reduce_kernel(
     d10 += pp[n * PS + 2 * D + 2];
     d11 += pp[n * PS + 2 * D + 3];
   }
-  const float hh = 0.5f * load_scalar(delta, delta_dtype, ti);
+  const float dl = load_scalar(delta, delta_dtype, ti);
+  // a token with a non-finite Cayley factor was the identity in the forward: no gradient
+  bool okm;
+  (void)cayley_guarded(dl, kk, vv, kv, okm);
+  const float hh = 0.5f * dl;
   const float P = hh * hh;
   const float graw = kk * vv - kv * kv;
   const float g = fmaxf(graw, 0.f);
@@ -304,12 +316,12 @@ __global__ __launch_bounds__(256) void sssd_bwd_reduce_kernel(
   for (int r = 0; r < RL; ++r) {
     const int i = lane + 64 * r;
     if (i < D) {
-      io<IO>::store(dk, ti * D + i, du0[r] + 2.f * dkk * kr[r] + dkv * vr[r]);
-      io<IO>::store(dv, ti * D + i, du1[r] + 2.f * dvv * vr[r] + dkv * kr[r]);
+      io<IO>::store(dk, ti * D + i, okm ? du0[r] + 2.f * dkk * kr[r] + dkv * vr[r] : 0.f);
+      io<IO>::store(dv, ti * D + i, okm ? du1[r] + 2.f * dvv * vr[r] + dkv * kr[r] : 0.f);
     }
   }
   if (lane == 0) {
-    const float dd = 0.5f * dh;
+    const float dd = okm ? 0.5f * dh : 0.f;
     if (delta_dtype == VMI_F32) static_cast<float*>(ddelta)[ti] = dd;
     else if (delta_dtype == VMI_BF16) static_cast<uint16_t*>(ddelta)[ti] = f32_to_bf16(dd);
     else static_cast<f16_t*>(ddelta)[ti] = static_cast<f16_t>(dd);

@@ -34,8 +34,12 @@ constexpr int C = 16;   // tokens per chunk
 constexpr int R = 32;   // rank rows of a chunk (k, v per token)
 constexpr int CB = 16;  // state columns per workgroup
 constexpr int NT = 256;
-// per-chunk record written by the prep kernel: T~, A = (I - L)^-1, G (R x R each), M blocks
-constexpr int REC = 3 * R * R + 4 * C;
+// per-chunk record written by the prep kernel: T~, A = (I - L)^-1, G (R x R each), M blocks,
+// then the bit mask of the chunk's tokens whose Cayley factor is not finite (the reference's
+// non-finite guard, sssd_attention.py:45-71: such a token is the identity, its U rows count
+// as zero and it gets no gradient) and 3 floats of padding (16-byte alignment)
+constexpr int REC_BAD = 3 * R * R + 4 * C;
+constexpr int REC = REC_BAD + 4;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -157,18 +161,33 @@ __device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B
 
 // G = U^T U, the Cayley blocks M_t, L and A = (I - L)^-1 of one chunk (LDS).
 // U: [D][L32] (row i: k_t at 2t, v_t at 2t + 1; zero past the end); dl[t] the deltas.
+// Tokens with a non-finite Cayley factor (vmi::cayley_guarded) get M = 0 and their U columns
+// zeroed, G is recomputed, and their bits are left in *badm.
 template <int D>
-__device__ void chunk_prep(const float* U, const float* dl, float* G, float* Mb, float* L,
-                           float* A, int tid, int wave, int lane) {
+__device__ void chunk_prep(float* U, const float* dl, float* G, float* Mb, float* L,
+                           float* A, int* badm, int tid, int wave, int lane) {
   lgemm<R, R, D, true, false, kStore>(U, L32, U, L32, G, R, wave, lane);
   __syncthreads();
+  bool ok = true;
   if (tid < C) {
     const int t = tid;
-    const cayley2 m = cayley_coeffs(dl[t], G[(2 * t) * R + 2 * t], G[(2 * t + 1) * R + 2 * t + 1],
-                                    G[(2 * t) * R + 2 * t + 1]);
+    const cayley2 m = cayley_guarded(dl[t], G[(2 * t) * R + 2 * t], G[(2 * t + 1) * R + 2 * t + 1],
+                                     G[(2 * t) * R + 2 * t + 1], ok);
     Mb[4 * t + 0] = m.m00; Mb[4 * t + 1] = m.m01; Mb[4 * t + 2] = m.m10; Mb[4 * t + 3] = m.m11;
   }
+  const uint64_t bal = __ballot(!ok);  // tokens are lanes 0..C-1 of wave 0
+  if (tid == 0) *badm = static_cast<int>(bal & ((1u << C) - 1));
   __syncthreads();
+  const int bad = *badm;
+  if (bad != 0) {  // uniform over the workgroup; only chunks holding such a token
+    for (int e = tid; e < D * R; e += NT) {
+      const int i = e / R, rho = e % R;
+      if ((bad >> (rho >> 1)) & 1) U[i * L32 + rho] = 0.f;
+    }
+    __syncthreads();
+    lgemm<R, R, D, true, false, kStore>(U, L32, U, L32, G, R, wave, lane);
+    __syncthreads();
+  }
   for (int e = tid; e < R * R; e += NT) {  // L[2t + a][2i + b] = (M_t G_ti)[a][b], i < t
     const int r = e / R, c = e % R, t = r >> 1, i = c >> 1, a = r & 1, b = c & 1;
     float x = 0.f;
@@ -199,6 +218,7 @@ __global__ __launch_bounds__(NT) void bwdc_prep_kernel(const IO* __restrict__ k,
                                                        int delta_dtype, float* __restrict__ tt,
                                                        int T, int H) {
   __shared__ float U[D * L32], G[R * R], L[R * R], A[R * R], Mb[4 * C], dl[C];
+  __shared__ int badm;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, hd = bh % H;
   const int nch = gridDim.x;
@@ -214,7 +234,7 @@ __global__ __launch_bounds__(NT) void bwdc_prep_kernel(const IO* __restrict__ k,
     dl[tid] = tg < T ? load_scalar(delta, delta_dtype, (static_cast<int64_t>(b) * T + tg) * H + hd) : 0.f;
   }
   __syncthreads();
-  chunk_prep<D>(U, dl, G, Mb, L, A, tid, wave, lane);
+  chunk_prep<D>(U, dl, G, Mb, L, A, &badm, tid, wave, lane);
   float* o = tt + (static_cast<int64_t>(bh) * nch + n) * REC;
   for (int e = tid; e < R * R; e += NT) {  // T~ = A blockdiag(M), then A, G, M
     const int r = e / R, c = e % R, s = c >> 1, cb = c & 1;
@@ -223,6 +243,7 @@ __global__ __launch_bounds__(NT) void bwdc_prep_kernel(const IO* __restrict__ k,
     o[2 * R * R + e] = G[e];
   }
   if (tid < 4 * C) o[3 * R * R + tid] = Mb[tid];
+  if (tid == 0) o[REC_BAD] = __int_as_float(badm);
 }
 
 // ---------------------------------------------------------------- state columns, in reverse
@@ -260,6 +281,7 @@ __global__ __launch_bounds__(NT) void bwdc_cols_kernel(
   // chunk n's inputs: registers first (the next chunk's arrive while this one runs)
   constexpr int EU = D * C / NT;  // elements of k (and of v, dO) per thread
   float rk[EU], rv[EU], rd[EU], rq, rt[R * R / NT];
+  int rbad = 0;  // tokens of the chunk that are the identity (non-finite Cayley factor)
   auto tok = [&](int tg) { return (static_cast<int64_t>(b) * T + tg) * H + hd; };
   auto fetch = [&](int n) {
 #pragma unroll
@@ -277,14 +299,16 @@ __global__ __launch_bounds__(NT) void bwdc_cols_kernel(
 #pragma unroll
     for (int m = 0; m < R * R / NT; ++m)
       rt[m] = tt[(static_cast<int64_t>(bh) * nch + n) * REC + tid + NT * m];
+    rbad = __float_as_int(tt[(static_cast<int64_t>(bh) * nch + n) * REC + REC_BAD]);
   };
   auto commit = [&](int n) {
 #pragma unroll
     for (int m = 0; m < EU; ++m) {
       const int e = tid + NT * m, t = e / D, i = e % D;
       const bool ok = n * C + t < T;
-      U[i * L32 + 2 * t] = ok ? rk[m] : 0.f;
-      U[i * L32 + 2 * t + 1] = ok ? rv[m] : 0.f;
+      const bool uk = ok && !((rbad >> t) & 1);
+      U[i * L32 + 2 * t] = uk ? rk[m] : 0.f;
+      U[i * L32 + 2 * t + 1] = uk ? rv[m] : 0.f;
       dO[i * L16 + t] = ok ? rd[m] : 0.f;
     }
     {
@@ -385,8 +409,10 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
   static_assert(R * R % NT == 0 && D * C % NT == 0 && 4 * C <= NT, "record and tokens split evenly");
   constexpr int NR = R * R / NT, NK = D * C / NT;
   float ra[NR], rg[NR], rm = 0.f, rd = 0.f;
+  int bad;  // tokens of the chunk that are the identity (non-finite Cayley factor): no gradient
   {
     const float* rec = tt + (static_cast<int64_t>(bh) * nch + n) * REC;
+    bad = __float_as_int(rec[REC_BAD]);
 #pragma unroll
     for (int u = 0; u < NR; ++u) {
       ra[u] = rec[R * R + tid + NT * u];
@@ -417,7 +443,7 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
 #pragma unroll
   for (int u = 0; u < NK; ++u) {
     const int e = tid + NT * u, t = e / D, i = e % D;
-    const bool ok = n * C + t < T;
+    const bool ok = n * C + t < T && !((bad >> t) & 1);
     U[i * L32 + 2 * t] = ok ? rk[u] : 0.f;
     U[i * L32 + 2 * t + 1] = ok ? rv[u] : 0.f;
   }
@@ -466,7 +492,7 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
     const int t = tid;
     const float kk = G[(2 * t) * R + 2 * t], vv = G[(2 * t + 1) * R + 2 * t + 1], kv = G[(2 * t) * R + 2 * t + 1];
     const float d00 = tmp[4 * t], d01 = tmp[4 * t + 1], d10 = tmp[4 * t + 2], d11 = tmp[4 * t + 3];
-    const float hh = 0.5f * dl[t], P = hh * hh;
+    const float hh = (bad >> t) & 1 ? 0.f : 0.5f * dl[t], P = hh * hh;  // identity token: no chain
     const float graw = kk * vv - kv * kv, g = fmaxf(graw, 0.f);
     const float c = 2.f / (1.f + P * g);
     const float N00 = -P * vv, N01 = P * kv - hh, N10 = P * kv + hh, N11 = -P * kk;
@@ -483,7 +509,7 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
     L[(2 * t) * R + 2 * t + 1] += dkv;
     const int tg = n * C + t;
     if (tg < T) {
-      const float dd = 0.5f * dh;
+      const float dd = (bad >> t) & 1 ? 0.f : 0.5f * dh;
       const int64_t o = tok(tg);
       if (delta_dtype == VMI_F32) static_cast<float*>(ddelta)[o] = dd;
       else if (delta_dtype == VMI_BF16) static_cast<uint16_t*>(ddelta)[o] = f32_to_bf16(dd);
@@ -502,8 +528,9 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
     const int t = e / D, i = e % D, tg = n * C + t;
     if (tg < T) {
       const int64_t o = tok(tg) * D + i;
-      io<IO>::store(dk, o, dU[i * R + 2 * t]);
-      io<IO>::store(dv, o, dU[i * R + 2 * t + 1]);
+      const bool z = (bad >> t) & 1;
+      io<IO>::store(dk, o, z ? 0.f : dU[i * R + 2 * t]);
+      io<IO>::store(dv, o, z ? 0.f : dU[i * R + 2 * t + 1]);
     }
   }
 }

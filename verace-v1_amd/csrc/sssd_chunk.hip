@@ -482,6 +482,7 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
       *reinterpret_cast<float4*>(&P.gram[l32 * T_LD + 8 * q4 + 4 * g]) =
           make_float4(gacc[4 * q4], gacc[4 * q4 + 1], gacc[4 * q4 + 2], gacc[4 * q4 + 3]);
     wave_sync();
+    bool ok = true;
     if (lane < C) {
       const int t = lane;
       const float kk = P.gram[(2 * t) * T_LD + 2 * t];
@@ -490,8 +491,30 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
       float dl = io<DT>::to_f32(r.d);
       if constexpr (FUSED)  // delta = 0.1 sigmoid(w_delta x) * active_mask (sssd_attention.py:120-126)
         dl = (r.mk && t0 + t < a.T) ? 0.1f / (1.f + __expf(-dl)) : 0.f;
-      const cayley2 M = cayley_coeffs(dl, kk, vv, kv);
+      const cayley2 M = cayley_guarded(dl, kk, vv, kv, ok);
       P.mcoef[t] = make_float4(M.m00, M.m01, M.m10, M.m11);
+    }
+    // Tokens with a non-finite Cayley factor act as R = I (cayley_guarded): their U rows
+    // are zeroed and the Gram matrix is recomputed, so no NaN/Inf reaches T~ or the
+    // consumers.  The branch is uniform over the wave and taken only for such chunks.
+    const uint64_t bad = __ballot(!ok);
+    if (bad != 0) {
+      if ((bad >> (l32 >> 1)) & 1) {
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) r.kv[ks] = make_uint4(0, 0, 0, 0);
+      }
+      f32x16 zacc = {};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const V8 x = *reinterpret_cast<const V8*>(&r.kv[ks]);
+        zacc = MM::mma32(x, x, zacc);
+      }
+      wave_sync();  // every lane has read its diagonal entries
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<float4*>(&P.gram[l32 * T_LD + 8 * q4 + 4 * g]) =
+            make_float4(zacc[4 * q4], zacc[4 * q4 + 1], zacc[4 * q4 + 2], zacc[4 * q4 + 3]);
+      wave_sync();
     }
   };
 

@@ -150,7 +150,13 @@ __global__ __launch_bounds__(seq_cfg<DMAX>::NT) void sssd_seq_kernel(
       vv += __shfl_xor(vv, off);
       kv += __shfl_xor(kv, off);
     }
-    const float dt = s_delta[cur];
+    // a token with a non-finite Cayley factor is the identity (uniform over the workgroup)
+    bool ok;
+    const cayley2 M = cayley_guarded(s_delta[cur], kk, vv, kv, ok);
+    if (!ok) {
+#pragma unroll
+      for (int m = 0; m < RPT; ++m) kr[m] = vr[m] = 0.f;
+    }
 
     // column-sum partials a_j = sum_i k_i Psi_ij, b_j = sum_i v_i Psi_ij
     float pa[4] = {0.f, 0.f, 0.f, 0.f}, pb[4] = {0.f, 0.f, 0.f, 0.f};
@@ -175,7 +181,6 @@ __global__ __launch_bounds__(seq_cfg<DMAX>::NT) void sssd_seq_kernel(
       a[0] += xa.x; a[1] += xa.y; a[2] += xa.z; a[3] += xa.w;
       bb[0] += xb.x; bb[1] += xb.y; bb[2] += xb.z; bb[3] += xb.w;
     }
-    const cayley2 M = cayley_coeffs(dt, kk, vv, kv);
     float al[4], be[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {

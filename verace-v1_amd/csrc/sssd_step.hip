@@ -106,6 +106,13 @@ __global__ __launch_bounds__(NT) void sssd_step128_kernel(
         kv += __shfl_xor(kv, off);
       }
     }
+    // a token with a non-finite Cayley factor is the identity (uniform over the workgroup)
+    bool ok;
+    const cayley2 M = cayley_guarded(s_delta[buf], kk, vv, kv, ok);
+    if (!ok) {
+#pragma unroll
+      for (int m = 0; m < RPT; ++m) kr[m] = vr[m] = 0.f;
+    }
     // column partials over this thread's 16 rows
     float4 pa = make_float4(0.f, 0.f, 0.f, 0.f), pb = pa;
 #pragma unroll
@@ -132,7 +139,6 @@ __global__ __launch_bounds__(NT) void sssd_step128_kernel(
       a4.x += xa.x; a4.y += xa.y; a4.z += xa.z; a4.w += xa.w;
       b4.x += xb.x; b4.y += xb.y; b4.z += xb.z; b4.w += xb.w;
     }
-    const cayley2 M = cayley_coeffs(s_delta[buf], kk, vv, kv);
     const float4 al = make_float4(fmaf(M.m00, a4.x, M.m01 * b4.x), fmaf(M.m00, a4.y, M.m01 * b4.y),
                                   fmaf(M.m00, a4.z, M.m01 * b4.z), fmaf(M.m00, a4.w, M.m01 * b4.w));
     const float4 be = make_float4(fmaf(M.m10, a4.x, M.m11 * b4.x), fmaf(M.m10, a4.y, M.m11 * b4.y),

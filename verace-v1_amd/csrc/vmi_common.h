@@ -86,4 +86,26 @@ __device__ __forceinline__ cayley2 cayley_coeffs(float delta, float kk, float vv
   return m;
 }
 
+__device__ __forceinline__ bool finite4(float a, float b, float c, float d) {
+  return __builtin_isfinite(a) && __builtin_isfinite(b) && __builtin_isfinite(c) &&
+         __builtin_isfinite(d);
+}
+
+// The reference's non-finite guard (sssd_attention.py:45-71): a token whose Cayley factor
+// is not finite -- a NaN or Inf in k, v or delta (the Gram entries are then not finite
+// either), or a closed form that overflows -- is replaced by R = I.  For such a token this
+// returns M = 0 and ok = false; the caller must also treat the token's k and v (its U rows)
+// as zero, because NaN * 0 is NaN: a zero M alone would not keep the state finite.
+__device__ __forceinline__ cayley2 cayley_guarded(float delta, float kk, float vv, float kv,
+                                                  bool& ok) {
+  cayley2 m = cayley_coeffs(delta, kk, vv, kv);
+  ok = finite4(delta, kk, vv, kv) && finite4(m.m00, m.m01, m.m10, m.m11);
+  if (!ok) m = cayley2{0.f, 0.f, 0.f, 0.f};
+  return m;
+}
+
+// Element of k or v as it enters a product: non-finite values read as 0 (used where a
+// kernel stages a token whose M is already 0 from cayley_guarded; see above).
+__device__ __forceinline__ float finite_or_zero(float x) { return __builtin_isfinite(x) ? x : 0.f; }
+
 }  // namespace vmi

@@ -117,9 +117,24 @@ def launch_sssd_hip_scan_bwd(
     Returns (dq, dk, dv in q's dtype, d_delta in delta's dtype, d_psi0 fp32 or None).
     """
     _require_device(q, "q")
+    if q.dim() != 4:
+        raise RuntimeError(f"verace_amd: q must be [B, T, H, D], got {tuple(q.shape)}")
     b, s, h, d_k = q.shape
+    for name, t in (("k", k), ("v", v), ("d_out", d_out)):
+        _require_device(t, name)
+        if t.shape != q.shape:
+            raise RuntimeError(f"verace_amd: {name} shape {tuple(t.shape)} != q shape {tuple(q.shape)}")
+    _require_device(delta, "delta")
     if delta.dim() == 4 and delta.shape[-1] == 1:
         delta = delta.squeeze(-1)
+    if tuple(delta.shape) != (b, s, h):
+        raise RuntimeError(f"verace_amd: delta must be [B, T, H] = {(b, s, h)}, got {tuple(delta.shape)}")
+    for name, t in (("psi_T", psi_T), ("d_psi_T", d_psi_T)):
+        if t is None:
+            continue
+        _require_device(t, name)
+        if tuple(t.shape) != (b, h, d_k, d_k):
+            raise RuntimeError(f"verace_amd: {name} must be {(b, h, d_k, d_k)}, got {tuple(t.shape)}")
     io_code = _lib.dtype_code(q.dtype)
     q_c = q.contiguous()
     k_c = k.to(q.dtype).contiguous()

@@ -68,13 +68,20 @@ class SSSDAttention(nn.Module):
                 and all(w.dtype == x.dtype for w in (self.w_q.weight, self.w_k.weight,
                                                       self.w_v.weight, self.w_delta.weight)))
 
-    def _scan_fused(self, x, initial_state, active_mask):
+    def _scan_fused(self, x, initial_state, active_mask, rmsnorm_in_kernel: bool = True):
+        """Fused projections + scan.  With ``rmsnorm_in_kernel`` the kernel applies
+        head_rmsnorm too and returns its output; otherwise it returns the raw scan output o
+        and the caller applies ``self.head_rmsnorm`` as a torch op (so its weight gets a
+        gradient)."""
         proj = F.linear(x, self._stacked_weight())
+        if not rmsnorm_in_kernel:
+            return launch_sssd_hip_scan_fused(proj, self.num_heads, self.head_dim, active_mask,
+                                              None, None, initial_state)
         w = self.head_rmsnorm.weight
         if w is None:
             w = torch.ones(self.head_dim, device=x.device)
-        return launch_sssd_hip_scan_fused(proj, self.num_heads, self.head_dim, active_mask, w,
-                                          self.head_rmsnorm.eps, initial_state)
+        return launch_sssd_hip_scan_fused(proj, self.num_heads, self.head_dim, active_mask,
+                                          w.detach(), self.head_rmsnorm.eps, initial_state)
 
     def project(self, x: torch.Tensor, active_mask: Optional[torch.Tensor] = None):
         """q, k, v [B,T,H,D] (L2-normalised) and delta [B,T,H] as the reference builds them
@@ -106,12 +113,20 @@ class SSSDAttention(nn.Module):
         # differentiable path
         grad = torch.is_grad_enabled() and (
             x.requires_grad or (initial_state is not None and initial_state.requires_grad))
+        # Otherwise the scan is not differentiated (as the reference's GPU path, whose
+        # Triton scan cuts the graph), but head_rmsnorm and w_out still are: the RMSNorm
+        # runs inside the fused kernel only when its weight needs no gradient.
+        rms_grad = (torch.is_grad_enabled() and self.head_rmsnorm.weight is not None
+                    and self.head_rmsnorm.weight.requires_grad)
         if grad:
             q, k, v, delta = self.project(x, active_mask)
             o, psi = sssd_scan(q, k, v, delta, initial_state)
             o_norm = self.head_rmsnorm(o).view(b, s, self.num_heads * self.head_dim)
         elif self._fused(x):
-            o_norm, psi = self._scan_fused(x, initial_state, active_mask)
+            o_norm, psi = self._scan_fused(x, initial_state, active_mask,
+                                           rmsnorm_in_kernel=not rms_grad)
+            if rms_grad:
+                o_norm = self.head_rmsnorm(o_norm)
             o_norm = o_norm.view(b, s, self.num_heads * self.head_dim)
         else:
             q, k, v, delta = self.project(x, active_mask)
@@ -140,9 +155,14 @@ class SSSDAttention(nn.Module):
         if len(handles) != b:
             raise ValueError(f"verace_amd: {len(handles)} handles for a batch of {b}")
         if self._fused(x):
-            o_norm, psi = self._scan_fused(x, cache.read(layer, handles), active_mask)
+            rms_grad = (torch.is_grad_enabled() and self.head_rmsnorm.weight is not None
+                        and self.head_rmsnorm.weight.requires_grad)
+            o_norm, psi = self._scan_fused(x, cache.read(layer, handles), active_mask,
+                                           rmsnorm_in_kernel=not rms_grad)
+            if rms_grad:
+                o_norm = self.head_rmsnorm(o_norm)
             cache.write(layer, handles, psi)
-            return self.w_out(o_norm.view(b, s, self.num_heads * self.head_dim))
+            return self.w_out(o_norm.reshape(b, s, self.num_heads * self.head_dim))
         q, k, v, delta = self.project(x, active_mask)
         if s == 1:
             o = cache.step(layer, q, k, v, delta, handles)
