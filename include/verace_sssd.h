@@ -218,6 +218,26 @@ int vmi_cham_scan_fwd(const void* q, const void* k, const void* v, const void* g
                       float* h_imag_out, int64_t B, int64_t T, int64_t h,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* One CHAM decode step (T = 1) with the holographic state updated in place:
+ *   H <- U H  (U the exact Cayley factor of the token, as in vmi_cham_scan_fwd),
+ *   R <- U R  when a readout state R is given,
+ *   out = Re(NS_3(H') q) = Re(R' q)   (R = NS_3(H) is carried by the caller; NULL means H
+ *                                      is unitary, e.g. it started from the identity, and
+ *                                      then NS_3(H') = H').
+ * Replaces the reference's incremental CHAM forward at seq_len 1 (cham_memory.py:117-238
+ * with initial_hologram, called per token from acd_engine.py:116-121 and
+ * hyper_generate.py:59-63), which returns a fresh raw state and retracts it for the readout;
+ * the in-place form is opt-in for callers that own the state (as vmi_sssd_step_inplace).
+ *   q, k, v, out : [B, 1, h] io_dtype;  gamma : [B] gamma_dtype;
+ *   h_real, h_imag (and r_real, r_imag) : [B, h, h] float32, read and written, distinct.
+ * h % 4 == 0 and h <= 1024 (otherwise VMI_ERR_UNSUPPORTED).  Workspace from
+ * vmi_cham_step_workspace_bytes (per-block readout partials: B (h/32) h floats). */
+int vmi_cham_step_workspace_bytes(int64_t B, int64_t h, size_t* bytes);
+int vmi_cham_step_inplace(const void* q, const void* k, const void* v, const void* gamma,
+                          int io_dtype, int gamma_dtype, float* h_real, float* h_imag,
+                          float* r_real, float* r_imag, void* out, int64_t B, int64_t h,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* Newton-Schulz unitary retraction of a batch of complex matrices
  * H = Hr + i Hi, `steps` iterations of H <- 0.5 H (3I - H^H H), both halves
  * of every iteration computed from the pre-update H.

@@ -1,0 +1,185 @@
+"""Writes tests/golden/model_golden.npz from the reference model (VeraceV1Model).
+
+Run in the development container only (the reference is not present on the GPU box):
+
+    python tests/golden/make_golden_model.py [/root/reference]
+
+Why an import is needed: the layer composition around the SSSD scan (backbone.py:53-101:
+RMSNorm, SSSD, CHAM, M-CMoE, residuals, the block-residual bookkeeping), the ACDE loop that
+drives it (acd_engine.py:36-167: per-item gathering, halting weights, per-item state
+threading) and the seed-0 random-init parameter values of the CPU config (which depend on
+the construction order, including the always-built vision encoder, backbone.py:119-125) are
+pinned by nothing but the reference itself.  Only data is written (token ids, outputs,
+states, parameter digests, one RNG state); no reference source is copied.
+
+Two models:
+  cpu  -- the CPU config of BASELINE.json (VeraceV1Model seed 0, hidden 256, 2 layers, H 4,
+          D 64, vocab 32000, chams_holographic_dim 1024, fp32, batch 2 x seq 128, ACDE on).
+          Its weights are not stored: the harness rebuilds them from seed 0 and the torch
+          RNG state right after the vision encoder's construction (stored here), and checks
+          every parameter against the digests stored here.  Recorded: logits digests and
+          slices, depth counts, every layer's SSSD state, CHAM hologram digests, and the
+          inputs and outputs of every SSSD and CHAM call (forward hooks).
+  tiny -- hidden 64, 4 layers, H 2, D 32, vocab 300, chams 32, M-CMoE 16 components of rank
+          4, halting threshold 0.0474 (some tokens halt after layer 2, so the per-item
+          gather of active tokens runs).  Its full non-vision state_dict is stored, with ACDE
+          logits, depth counts and layer states, static-depth logits, and a one-token
+          incremental step from the returned layer states (the generator's decode call,
+          hyper_generate.py:59-63).
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+OUT = os.path.join(HERE, "model_golden.npz")
+
+
+def _digest(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().double().reshape(-1)
+    head = t[:8]
+    if head.numel() < 8:
+        head = torch.cat([head, head.new_zeros(8 - head.numel())])
+    return np.concatenate([[float(t.sum()), float((t * t).sum())], head.numpy()])
+
+
+def main(ref_root: str) -> None:
+    sys.path.insert(0, ref_root)
+    import verace_v1.modules.backbone as bb  # noqa: E402
+    from verace_v1.config import VeraceV1Config  # noqa: E402
+
+    blobs = {}
+    torch.set_num_threads(8)
+
+    # ---- record the RNG state right after the vision encoder is built
+    orig_vis = bb.VeraceVisionEncoder
+    captured = {}
+
+    class _Vis(orig_vis):
+        def __init__(self, *a, **kw):
+            super().__init__(*a, **kw)
+            captured["rng"] = torch.get_rng_state().clone()
+
+    bb.VeraceVisionEncoder = _Vis
+    try:
+        # ================================================================ cpu config
+        cfg = VeraceV1Config(vocab_size=32000, hidden_dim=256, num_layers=2, num_heads=4,
+                             head_dim=64)
+        torch.manual_seed(0)
+        model = bb.VeraceV1Model(cfg).eval()
+        blobs["cpu/rng_after_vision"] = captured["rng"].numpy().copy()
+        names = []
+        for name, p in model.named_parameters():
+            if name.startswith("vision_encoder."):
+                continue
+            names.append(name)
+            blobs[f"cpu/digest/{name}"] = _digest(p)
+        blobs["cpu/param_names"] = np.array(names)
+        g = torch.Generator().manual_seed(0)
+        ids = torch.randint(0, cfg.vocab_size, (2, 128), generator=g)
+        blobs["cpu/input_ids"] = ids.numpy()
+        calls = {"sssd": [], "cham": []}
+
+        def hook(kind, layer):
+            def fn(mod, args, kwargs, out):
+                x = args[0]
+                rec = {"layer": layer, "x": x.detach().numpy().copy(),
+                       "y": out[0].detach().numpy().copy()}
+                if kind == "sssd":
+                    st = kwargs.get("initial_state")
+                    rec["init"] = None if st is None else st.detach().numpy().copy()
+                    rec["state"] = out[1].detach().numpy().copy()
+                else:
+                    hr, hi = out[1]
+                    rec["h_real"] = hr.detach().numpy().copy()
+                    rec["h_imag"] = hi.detach().numpy().copy()
+                calls[kind].append(rec)
+            return fn
+
+        hooks = []
+        for li, layer in enumerate(model.layers):
+            hooks.append(layer.sssd_attn.register_forward_hook(hook("sssd", li), with_kwargs=True))
+            hooks.append(layer.cham_memory.register_forward_hook(hook("cham", li), with_kwargs=True))
+        with torch.no_grad():
+            logits, depth, states = model(ids, return_layer_states=True)
+        for h in hooks:
+            h.remove()
+        blobs["cpu/logits_sum"] = logits.double().sum(-1).numpy()
+        blobs["cpu/logits_sq"] = (logits.double() ** 2).sum(-1).numpy()
+        blobs["cpu/logits_head"] = logits[..., :64].numpy().copy()
+        blobs["cpu/logits_argmax"] = logits.argmax(-1).numpy()
+        blobs["cpu/depth"] = depth.numpy()
+        blobs["cpu/sssd_states"] = np.stack([np.stack([s[0].numpy() for s in layer]) for layer in states])
+        for li, layer in enumerate(states):
+            for i, s in enumerate(layer):
+                hr, hi = s[1]
+                blobs[f"cpu/cham_state/{li}/{i}/norm"] = np.array([float(hr.double().norm()), float(hi.double().norm())])
+                blobs[f"cpu/cham_state/{li}/{i}/real16"] = hr[0, :16, :16].numpy().copy()
+                blobs[f"cpu/cham_state/{li}/{i}/imag16"] = hi[0, :16, :16].numpy().copy()
+        for kind in ("sssd", "cham"):
+            blobs[f"cpu/{kind}_calls"] = np.array(len(calls[kind]))
+            for j, rec in enumerate(calls[kind]):
+                for key, val in rec.items():
+                    if val is None:
+                        continue
+                    if kind == "cham" and key in ("h_real", "h_imag"):  # 8 MB each: digests
+                        blobs[f"cpu/{kind}/{j}/{key}/norm"] = np.array(float(np.linalg.norm(val.astype(np.float64))))
+                        blobs[f"cpu/{kind}/{j}/{key}/slice"] = val[0, :32, :32].copy()
+                        continue
+                    blobs[f"cpu/{kind}/{j}/{key}"] = np.asarray(val)
+        del model
+
+        # ================================================================ tiny model
+        @__import__("dataclasses").dataclass
+        class TinyVision:
+            embed_dim: int = 16
+            num_layers: int = 1
+            num_heads: int = 2
+            patch_size: int = 14
+
+        cfg = VeraceV1Config(vocab_size=300, hidden_dim=64, num_layers=4, num_heads=2, head_dim=32,
+                             chams_holographic_dim=32, mcmoe_rank=4, mcmoe_num_components=16,
+                             energy_halting_threshold=0.0474, vision_config=TinyVision())
+        torch.manual_seed(1)
+        model = bb.VeraceV1Model(cfg).eval()
+        for name, p in model.state_dict().items():
+            if not name.startswith("vision_encoder."):
+                blobs[f"tiny/param/{name}"] = p.numpy().copy()
+        g = torch.Generator().manual_seed(1)
+        ids = torch.randint(0, cfg.vocab_size, (2, 24), generator=g)
+        nxt = torch.randint(0, cfg.vocab_size, (2, 1), generator=g)
+        blobs["tiny/input_ids"] = ids.numpy()
+        blobs["tiny/next_ids"] = nxt.numpy()
+        with torch.no_grad():
+            logits, depth, states = model(ids, return_layer_states=True)
+            logits1, depth1, states1 = model(nxt, layer_states=states, return_layer_states=True)
+            logits_s, depth_s = model(ids, use_adaptive_depth=False)
+        blobs["tiny/logits"] = logits.numpy()
+        blobs["tiny/depth"] = depth.numpy()
+        blobs["tiny/logits_step"] = logits1.numpy()
+        blobs["tiny/depth_step"] = depth1.numpy()
+        blobs["tiny/logits_static"] = logits_s.numpy()
+        for tag, st in (("states", states), ("states_step", states1)):
+            for li, layer in enumerate(st):
+                for i, s in enumerate(layer):
+                    if s is None:
+                        continue
+                    blobs[f"tiny/{tag}/{li}/{i}/sssd"] = s[0].numpy().copy()
+                    blobs[f"tiny/{tag}/{li}/{i}/cham_real"] = s[1][0].numpy().copy()
+                    blobs[f"tiny/{tag}/{li}/{i}/cham_imag"] = s[1][1].numpy().copy()
+        blobs["tiny/config"] = np.array([cfg.vocab_size, cfg.hidden_dim, cfg.num_layers, cfg.num_heads,
+                                         cfg.head_dim, cfg.chams_holographic_dim, cfg.mcmoe_rank,
+                                         cfg.mcmoe_num_components], dtype=np.int64)
+        blobs["tiny/halting_threshold"] = np.array(cfg.energy_halting_threshold)
+    finally:
+        bb.VeraceVisionEncoder = orig_vis
+    np.savez_compressed(OUT, **blobs)
+    print(f"wrote {OUT} ({os.path.getsize(OUT) / 1e6:.2f} MB, torch {torch.__version__})")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")

@@ -120,6 +120,14 @@ hipError_t launch_cham_scan(const void* q, const void* k, const void* v, const v
                             void* out, float* hr_out, float* hi_out, int B, int T, int h,
                             void* workspace, hipStream_t stream);
 
+// cham_step.hip: single-token CHAM step, states updated in place (h % 4 == 0, h <= 1024);
+// rr/ri (the readout state) may be null (then the readout uses H).
+size_t cham_step_workspace_bytes(int64_t B, int64_t h);
+hipError_t launch_cham_step(const void* q, const void* k, const void* v, const void* gamma,
+                            int io_dtype, int gamma_dtype, float* hr, float* hi, float* rr,
+                            float* ri, void* out, int B, int h, void* workspace,
+                            hipStream_t stream);
+
 // cham_wide.hip: the same scan for 128 < h <= kChamMaxDim.
 size_t cham_wide_workspace_bytes(int64_t B, int64_t T, int64_t h);
 hipError_t launch_cham_wide(const void* q, const void* k, const void* v, const void* gamma,

@@ -17,16 +17,26 @@ Drop-in replacements for the reference's SSSD hot path:
                                <- ``verace_v1.modules.cham_memory`` (same names)
 * ``launch_cham_hip_update``   <- ``verace_v1.serving.triton_kernels.launch_cham_triton_update``
                                (CHAM holographic scan, holographic_dim <= 1024)
+* ``cham_step_``               -- in-place single-token CHAM step (opt-in)
+* ``ContinuousHolographicMemory`` <- ``verace_v1.modules.cham_memory.ContinuousHolographicMemory``
+* ``ManifoldContinuousMoE`` / ``SiTUGLU`` <- ``verace_v1.modules.mcmoe`` / ``.activations`` (torch ops)
+* ``VeraceV1Layer`` / ``VeraceV1Model`` / ``VeraceV1Config`` / ``DecodeState``
+                               -- the layer harness (``backbone.py:21-210``, ACDE
+                                  ``acd_engine.py:36-167``) with batched in-place decode
 * ``HAS_HIP``                  <- ``verace_v1.serving.triton_kernels.HAS_TRITON``
 
 All compute runs in ``libverace_sssd.so`` (C ABI: ``include/verace_sssd.h``).
 """
-from .hip_kernels import (HAS_HIP, SSSDScanFunction, launch_cham_hip_update,
+from .hip_kernels import (HAS_HIP, SSSDScanFunction, cham_step_, launch_cham_hip_update,
                           launch_sssd_hip_scan, launch_sssd_hip_scan_bwd,
                           launch_sssd_hip_scan_fused,
                           newton_schulz_unitary_retraction, parallel_newton_schulz_retraction,
                           sssd_scan, sssd_step_)
 from .sssd_attention import SSSDAttention
+from .cham_memory import ContinuousHolographicMemory
+from .mcmoe import ManifoldContinuousMoE, SiTUGLU
+from .backbone import (AdaptiveCognitiveDepthEngine, DecodeState, LayerDecodeState, VeraceV1Config,
+                       VeraceV1Layer, VeraceV1Model)
 from .state_cache import SlotTable, SSSDStateCache
 
 __all__ = [
@@ -41,6 +51,16 @@ __all__ = [
     "launch_sssd_hip_scan_fused",
     "launch_cham_hip_update",
     "sssd_step_",
+    "cham_step_",
+    "ContinuousHolographicMemory",
+    "ManifoldContinuousMoE",
+    "SiTUGLU",
+    "AdaptiveCognitiveDepthEngine",
+    "DecodeState",
+    "LayerDecodeState",
+    "VeraceV1Config",
+    "VeraceV1Layer",
+    "VeraceV1Model",
     "newton_schulz_unitary_retraction",
     "parallel_newton_schulz_retraction",
 ]

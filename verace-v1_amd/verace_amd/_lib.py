@@ -40,6 +40,8 @@ EXPORTED = (
     "vmi_cham_scan_fwd",
     "vmi_sssd_scan_bwd_workspace_bytes",
     "vmi_sssd_scan_bwd",
+    "vmi_cham_step_workspace_bytes",
+    "vmi_cham_step_inplace",
     "vmi_cham_ns_workspace_bytes",
     "vmi_cham_ns_retraction",
 )
@@ -101,6 +103,11 @@ def _declare(lib):
     lib.vmi_sssd_scan_bwd.argtypes = [vp, vp, vp, vp, i32, i32, vp, vp, i32, vp, vp, vp, vp, vp,
                                       vp, i64, i64, i64, i64, vp, sz, vp]
     lib.vmi_sssd_scan_bwd.restype = i32
+    lib.vmi_cham_step_workspace_bytes.argtypes = [i64, i64, ctypes.POINTER(sz)]
+    lib.vmi_cham_step_workspace_bytes.restype = i32
+    lib.vmi_cham_step_inplace.argtypes = [vp, vp, vp, vp, i32, i32, vp, vp, vp, vp, vp, i64, i64,
+                                          vp, sz, vp]
+    lib.vmi_cham_step_inplace.restype = i32
     lib.vmi_cham_ns_workspace_bytes.argtypes = [i64, i64, ctypes.POINTER(sz)]
     lib.vmi_cham_ns_workspace_bytes.restype = i32
     lib.vmi_cham_ns_retraction.argtypes = [vp, vp, vp, vp, i64, i64, i32, vp, sz, vp]

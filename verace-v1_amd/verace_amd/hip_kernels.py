@@ -374,6 +374,70 @@ def launch_cham_hip_update(
     return out, (hr, hi)
 
 
+def cham_step_(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    gamma: torch.Tensor,
+    hologram: Tuple[torch.Tensor, torch.Tensor],
+    readout: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+) -> torch.Tensor:
+    """In-place CHAM decode step: ``H <- U H`` (and ``R <- U R`` for a carried readout
+    state R = NS_3(H)); returns ``Re(NS_3(H') q)`` in q's dtype, [B, 1, h].
+
+    q, k, v: [B, 1, h] or [B, h]; gamma: [B, 1], [B] or [B, 1, 1]; hologram = (H_real,
+    H_imag) [B, h, h] float32 contiguous, updated in place; readout: the same shape, or None
+    when H is unitary (a sequence that started from the identity: NS_3(H) = H).  Only for
+    callers that own the state: the reference never mutates ``initial_hologram`` (the
+    generator's branches share it), so pass copies where it is shared.  Reference: the CHAM
+    forward at seq_len 1 (``cham_memory.py:117-238``) that the decode loop re-runs per token.
+    h must be a multiple of 4 (<= 1024); other h take the general scan and a retraction.
+    """
+    hr, hi = hologram
+    for name, t in (("q", q), ("H_real", hr), ("H_imag", hi)):
+        _require_device(t, name)
+    if hr.dtype != torch.float32 or hi.dtype != torch.float32 or not hr.is_contiguous() \
+            or not hi.is_contiguous() or hr.dim() != 3 or hr.shape != hi.shape:
+        raise RuntimeError("verace_amd: hologram must be two contiguous float32 [B, h, h] tensors")
+    B, h, _ = hr.shape
+    rr = ri = None
+    if readout is not None:
+        rr, ri = readout
+        for name, t in (("R_real", rr), ("R_imag", ri)):
+            _require_device(t, name)
+            if t.dtype != torch.float32 or not t.is_contiguous() or t.shape != hr.shape:
+                raise RuntimeError(f"verace_amd: {name} must be a contiguous float32 {tuple(hr.shape)} tensor")
+    q_c = q.reshape(B, 1, h).contiguous()
+    k_c = k.reshape(B, 1, h).to(q.dtype).contiguous()
+    v_c = v.reshape(B, 1, h).to(q.dtype).contiguous()
+    g_c = gamma.reshape(B).contiguous()
+    for name, t in (("k", k_c), ("v", v_c), ("gamma", g_c)):
+        _require_device(t, name)
+    if h % 4 != 0 or h > 1024:
+        # general route: the scan from the current state (it retracts for the readout), then
+        # the new raw state (and its retraction) written back in place
+        out, (nr, ni) = launch_cham_hip_update(q_c, k_c, v_c, g_c.reshape(B, 1), (hr, hi))
+        hr.copy_(nr)
+        hi.copy_(ni)
+        if readout is not None:
+            r2, i2 = _ns(nr, ni, 3)
+            rr.copy_(r2)
+            ri.copy_(i2)
+        return out
+    out = torch.empty_like(q_c)
+    lib = _lib.load()
+    ws_bytes = ctypes.c_size_t(0)
+    _lib.check(lib.vmi_cham_step_workspace_bytes(B, h, ctypes.byref(ws_bytes)),
+               "vmi_cham_step_workspace_bytes")
+    ws = torch.empty(ws_bytes.value, device=q.device, dtype=torch.uint8) if ws_bytes.value else None
+    _lib.check(lib.vmi_cham_step_inplace(_ptr(q_c), _ptr(k_c), _ptr(v_c), _ptr(g_c),
+                                         _lib.dtype_code(q_c.dtype), _lib.dtype_code(g_c.dtype),
+                                         _ptr(hr), _ptr(hi), _ptr(rr), _ptr(ri), _ptr(out), B, h,
+                                         _ptr(ws), ws_bytes.value, _lib.stream_handle(q.device)),
+               "vmi_cham_step_inplace")
+    return out
+
+
 def _ns(H_real: torch.Tensor, H_imag: torch.Tensor, steps: int) -> Tuple[torch.Tensor, torch.Tensor]:
     _require_device(H_real, "H_real")
     _require_device(H_imag, "H_imag")
