@@ -219,3 +219,16 @@ def test_cham_empty_sequence_passes_the_state_through(device, h):
     assert torch.equal(hr, H0[0]) and torch.equal(hi, H0[1])
     out, hr, hi = _run(device, q, k, v, gam)
     assert torch.equal(hr, torch.eye(h).expand(B, h, h)) and torch.count_nonzero(hi) == 0
+
+
+def test_wide_initial_hologram_default_size(device):
+    """h = 1024 (the reference's default) from a non-unitary initial hologram with T = 40 >= 17:
+    the route that retracts H_0 once (NS_3(H_0) on the fp32 MFMA) and carries R_t beside H_t,
+    against the fp64 oracle that retracts every H_t."""
+    B, T, h = 1, 40, 1024
+    print(f"[case] cham wide h{h} T{T} non-unitary initial hologram", flush=True)
+    g = torch.Generator().manual_seed(21)
+    a = torch.randn(B, h, h, generator=g, dtype=torch.float64) + 1j * torch.randn(B, h, h, generator=g, dtype=torch.float64)
+    u = torch.linalg.qr(a)[0] * (1.0 + 0.05 * torch.rand(B, 1, h, generator=g, dtype=torch.float64))
+    h0 = (u.real.float().contiguous(), u.imag.float().contiguous())
+    _check(device, B, T, h, 22, h0=h0, label="default h, initial hologram")

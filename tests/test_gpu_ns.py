@@ -55,3 +55,24 @@ def test_ns_output_is_unitary(device):
     Hc = (r.cpu().double() + 1j * i.cpu().double())
     err = (Hc.conj().transpose(-1, -2) @ Hc - torch.eye(n, dtype=torch.complex128)).abs().max()
     assert float(err) < 1e-4
+
+
+def test_ns_retraction_default_size(device):
+    """The reference's default chams_holographic_dim (config.py:35): n = 1024, batch 2,
+    against the fp64 oracle (1e-5)."""
+    from verace_amd import newton_schulz_unitary_retraction
+    n, batch = 1024, 2
+    print(f"[case] ns batch={batch} n={n}", flush=True)
+    g = torch.Generator().manual_seed(5)
+    scale = 0.4 / n ** 0.5
+    hr = torch.randn(batch, n, n, generator=g) * scale + torch.eye(n)
+    hi = torch.randn(batch, n, n, generator=g) * scale
+    got_r, got_i = newton_schulz_unitary_retraction(hr.to(device), hi.to(device))
+    torch.cuda.synchronize()
+    ref_r, ref_i = cham_ns.newton_schulz_retraction(hr.double(), hi.double())
+    er = float((got_r.cpu().double() - ref_r).abs().max())
+    ei = float((got_i.cpu().double() - ref_i).abs().max())
+    rel = float(torch.sqrt(((got_r.cpu().double() - ref_r) ** 2).sum() + ((got_i.cpu().double() - ref_i) ** 2).sum())
+                / torch.sqrt((ref_r ** 2).sum() + (ref_i ** 2).sum()))
+    print(f"  max abs err real={er:.2e} imag={ei:.2e} rel={rel:.2e}", flush=True)
+    assert er < 1e-5 and ei < 1e-5 and rel < 1e-5
