@@ -557,6 +557,164 @@ def pmc_summary(fetch_csv, write_csv, out_json):
     return res
 
 
+def _model_cfg():
+    from verace_amd import VeraceV1Config
+    return VeraceV1Config(vocab_size=32000, hidden_dim=1024, num_layers=12, num_heads=8, head_dim=128,
+                          chams_holographic_dim=1024)
+
+
+def _build_model(device):
+    """The FULL / DEC model (hidden 1024, 12 layers, H 8, D 128, vocab 32000, CHAM h = 1024),
+    random-init bf16 weights drawn on the device (seed 0)."""
+    import torch
+    from verace_amd import VeraceV1Model
+    torch.manual_seed(0)
+    torch.cuda.manual_seed(0)
+    with torch.device(device):
+        model = VeraceV1Model(_model_cfg())
+    return model.to(torch.bfloat16).eval()
+
+
+def bench_model_full(device, model, iters=3, warmup=1):
+    """FULL config: 12-layer fixed-depth prefill, B=4 x T=2048 random
+    token ids, bf16, SSSD + CHAM + M-CMoE per layer.  Whole forward timed with HIP events;
+    the sub-layer shares from a second, instrumented pass with events between the sub-layers."""
+    import torch
+    B, T = 4, 2048
+    g = torch.Generator().manual_seed(0)
+    ids = torch.randint(0, 32000, (B, T), generator=g).to(device)
+    stream = torch.cuda.current_stream(device)
+    with torch.no_grad():
+        for _ in range(warmup):
+            model(ids, use_adaptive_depth=False)
+        torch.cuda.synchronize()
+        per = []
+        for _ in range(iters):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            logits, _ = model(ids, use_adaptive_depth=False)
+            b.record(stream)
+            torch.cuda.synchronize()
+            per.append(a.elapsed_time(b))
+        finite = bool(torch.isfinite(logits.float()).all())
+        # instrumented pass: events around each sub-layer (same ops as VeraceV1Layer.forward)
+        ev = []
+        h = model.embed_tokens(ids)
+        drift = 0.0
+        for layer in model.layers:
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            e[0].record(stream)
+            o, st = layer.sssd_attn(layer.sssd_norm(h), return_state=True)
+            h = h + o
+            e[1].record(stream)
+            c, _ = layer.cham_memory(layer.cham_norm(h))
+            h = h + c
+            e[2].record(stream)
+            h = h + layer.mcmoe(layer.mcmoe_norm(h))
+            e[3].record(stream)
+            ev.append(e)
+            nrm = st.reshape(B, 8, -1).norm(dim=-1) / 128 ** 0.5
+            drift = max(drift, float((nrm - 1).abs().max()))
+        torch.cuda.synchronize()
+    shares = [sum(e[i].elapsed_time(e[i + 1]) for e in ev) for i in range(3)]
+    ms = statistics.median(per)
+    return {
+        "config": "FULL: 12 layers, hidden 1024, H 8, D 128, CHAM h 1024, vocab 32000, bf16, "
+                  "B=4 x T=2048, fixed depth (static loop), random-init weights",
+        "ms_median": round(ms, 3), "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+        "sssd_sublayers_ms": round(shares[0], 3), "cham_sublayers_ms": round(shares[1], 3),
+        "mcmoe_sublayers_ms": round(shares[2], 3), "logits_finite": finite,
+        "sssd_state_norm_drift": drift,
+    }
+
+
+def bench_model_decode(device, model):
+    """DEC config: batch 64, 12 layers, hidden 1024, H 8, D 128, CHAM
+    h 1024; states from a seeded 512-token prefill (ACDE, as the reference's generator), then
+    256 single-token steps with random ids, every layer's SSSD and CHAM state updated in place
+    (one SSSD and one CHAM step launch per layer for the whole batch).  Per-step latency from
+    HIP events; layer 0's SSSD states checked against the fp64 C oracle over the 256 steps
+    (two heads), every SSSD state's norm against its prefill value, and the CHAM states'
+    unitarity."""
+    import numpy as np
+    import torch
+    from oracle import sssd_closed
+    B, P, S = DEC["B"], DEC["prefill"], DEC["steps"]
+    g = torch.Generator().manual_seed(0)
+    ids = torch.randint(0, 32000, (B, P), generator=g).to(device)
+    g1 = torch.Generator().manual_seed(1)
+    steps_ids = torch.randint(0, 32000, (S, B, 1), generator=g1).to(device)
+    stream = torch.cuda.current_stream(device)
+    with torch.no_grad():
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        _, st = model.prefill(ids)
+        b.record(stream)
+        torch.cuda.synchronize()
+        prefill_ms = a.elapsed_time(b)
+        l0 = model.layers[0]
+        s0 = st.layers[0].sssd.clone()
+        n_pre = [x.sssd.reshape(B, 8, -1).norm(dim=-1).clone() for x in st.layers]
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(S)]
+        for i in range(S):
+            evs[i][0].record(stream)
+            model.decode_step(steps_ids[i], st)
+            evs[i][1].record(stream)
+        torch.cuda.synchronize()
+        per = [x.elapsed_time(y) for x, y in evs]
+        # layer 0's SSSD inputs of every step (its input is the embedding: recomputed here)
+        q, k, v, dl = l0.sssd_attn.project(l0.sssd_norm(model.embed_tokens(steps_ids[:, :, 0].t())))
+        # the same sub-layer steps in isolation: one SSSD / CHAM step launch per layer
+        x = torch.randn(B, 1, 1024, device=device).bfloat16()
+        st2 = model._fresh_layer_state(l0, B, device)
+        qq, kk, vv, dd = l0.sssd_attn.project(x)
+        cq, ck, cv, cg = l0.cham_memory.project(x)
+        from verace_amd import cham_step_, sssd_step_
+        t_s, t_c = [], []
+        for i in range(20):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            e[0].record(stream)
+            sssd_step_(qq, kk, vv, dd, st2.sssd)
+            e[1].record(stream)
+            cham_step_(cq, ck, cv, cg, st2.cham)
+            e[2].record(stream)
+            torch.cuda.synchronize()
+            t_s.append(e[0].elapsed_time(e[1]))
+            t_c.append(e[1].elapsed_time(e[2]))
+    sel = [(0, 0), (B - 1, 7)]
+    qn, kn, vn, dn = (t.float().cpu().numpy() for t in (q, k, v, dl))
+    worst = 0.0
+    for (bb, hh) in sel:
+        sl = (slice(bb, bb + 1), slice(None), slice(hh, hh + 1))
+        _, p64 = sssd_closed.sssd_scan_closed_c(qn[sl], kn[sl], vn[sl], dn[bb:bb + 1, :, hh:hh + 1],
+                                                s0[bb:bb + 1, hh:hh + 1].double().cpu().numpy())
+        got = st.layers[0].sssd[bb, hh].double().cpu().numpy()
+        worst = max(worst, float(np.linalg.norm(got - p64[0, 0]) / np.linalg.norm(p64[0, 0])))
+    drift = max(float((x.sssd.reshape(B, 8, -1).norm(dim=-1) / n0 - 1).abs().max())
+                for x, n0 in zip(st.layers, n_pre))
+    hr, hi = st.layers[0].cham
+    Hc = (hr[0].double() + 1j * hi[0].double())
+    unit = float((Hc.conj().t() @ Hc - torch.eye(1024, device=device, dtype=torch.complex128)).abs().max())
+    per_s = sorted(per)
+    sssd_bytes = algorithmic_bytes_step(B, 8, 128)
+    cham_bytes = B * (2 * 2 * 1024 * 1024 * 4 + 4 * 1024 * 2 + 2)
+    ms_c = statistics.median(t_c)
+    return {
+        "config": "DEC: batch 64, 12 layers, hidden 1024, H 8, D 128, CHAM h 1024, bf16, 512-token "
+                  "prefill (ACDE) then 256 single-token steps, states updated in place",
+        "prefill_ms": round(prefill_ms, 2),
+        "step_ms_median": round(statistics.median(per), 3),
+        "step_ms_p90": round(per_s[int(0.9 * (S - 1))], 3),
+        "tokens_per_s": round(B / (statistics.median(per) * 1e-3), 1),
+        "sssd_step_us_per_layer": round(1e3 * statistics.median(t_s), 2),
+        "cham_step_us_per_layer": round(1e3 * ms_c, 2),
+        "cham_step_hbm_frac": round(cham_bytes / (ms_c * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "parity": {"layer0_sssd_state_rel_vs_fp64": worst, "sssd_state_norm_drift": drift,
+                   "layer0_cham_unitarity_err": unit,
+                   "pass": bool(worst <= 2e-2 and drift <= 1e-4 and unit <= 1e-3)},
+    }
+
+
 def load_traffic():
     """HBM bytes per scan from the committed rocprofv3 --pmc summary, if present."""
     p = os.path.join(REPO_ROOT, "profiles", "pmc_traffic_op_scan.json")
@@ -576,6 +734,8 @@ def main():
     ap.add_argument("--no-long", action="store_true", help="skip the LONG (T=65536) scan timing")
     ap.add_argument("--no-module", action="store_true",
                     help="skip the FULL SSSD sub-layer (fused vs unfused projections) timing")
+    ap.add_argument("--no-model", action="store_true",
+                    help="skip the model-level FULL prefill and DEC decode timings")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc counter CSVs into "
                          "profiles/pmc_traffic_op_scan.json and exit")
@@ -656,6 +816,12 @@ def main():
         result["module_full"] = bench_module_full(device)
         result["cham"] = bench_cham(device)
         result["scan_backward"] = bench_backward(device)
+    if not args.no_model:
+        model = _build_model(device)
+        result["model_full"] = bench_model_full(device, model)
+        result["model_decode"] = bench_model_decode(device, model)
+        del model
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

@@ -17,8 +17,10 @@
 // Bound: HBM (each state is read once and written once: 16 h^2 bytes per item and state,
 // 8 flops per element).  Grid (h / 32 column blocks, B, number of states): columns evolve
 // independently (a_j, b_j are sums over rows of column j), so a workgroup owns 32 columns of
-// one state of one item: thread (rg, cg) holds rows rg + 64 m and columns 4 cg .. 4 cg + 3
-// (float4, eight lanes cover a 128-byte row piece).  The readout sums over columns, so the
+// one state of one item (512 threads): thread (rg, cg) holds rows rg + (512 / (CB/4)) m and
+// columns 4 cg .. 4 cg + 3 (float4; CB / 4 lanes cover a row piece of the block).  CB = 32
+// (128-byte row pieces) up to h = 512, CB = 16 above (8 rows of both parts per thread: 64
+// floats; 32 columns would need 128 and spill).  The readout sums over columns, so the
 // readout-state workgroups write per-block partial sums of Rr' q; cham_step_finish_kernel
 // adds them.
 #include "cham_common.h"
@@ -29,18 +31,28 @@ namespace chams {
 
 using cham::NCoef;
 
-constexpr int NT = 512;
-constexpr int CB = 32;          // columns per workgroup
-constexpr int NRG = NT / 8;     // row groups (8 column groups of 4 columns)
+constexpr int CB_MIN = 16;      // smallest column block (sizes the readout partials)
 
-template <typename IO, typename GT, int RPT>
+// EXACT: h == NT / 8 * RPT and h % 32 == 0, so every row and column of the block exists and
+// the loads and stores need no guards (branches around them made the compiler serialise the
+// loads and spill at 1024 threads).
+// (h is then a compile-time constant, so every address is a base plus an immediate).
+template <typename IO, typename GT, int NT, int CB, int RPT, bool EXACT>
 __global__ __launch_bounds__(NT) void cham_step_kernel(
     const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
     const GT* __restrict__ gamma, float* hr0, float* hi0, float* hr1, float* hi1,
-    float* __restrict__ part, int h, int nstates) {
+    float* __restrict__ part, int h_arg, int nstates) {
+  constexpr int CGN = CB / 4;        // column groups of 4 columns (float4)
+  const int h = EXACT ? NT / CGN * RPT : h_arg;
+  constexpr int NRG = NT / CGN;  // row groups
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int cg = tid & 7, rg = tid >> 3;
-  const int blk = blockIdx.x, b = blockIdx.y, z = blockIdx.z;
+  const int cg = tid & (CGN - 1), rg = tid / CGN;
+  // With 16-column blocks two blocks share each 128-byte line of a row.  Workgroups go to the
+  // 8 XCDs round robin by linear id, so blocks x and x + 8 land on the same XCD (and L2):
+  // they take the two halves of the same lines (column blocks 2c and 2c + 1).
+  const int bx = blockIdx.x;
+  const int blk = (CB == 16 && (gridDim.x & 15) == 0) ? ((bx & ~15) | ((bx & 7) << 1) | ((bx >> 3) & 1)) : bx;
+  const int b = blockIdx.y, z = blockIdx.z;
   const int nblk = gridDim.x;
   const int c0 = blk * CB + 4 * cg;
   const bool readout = z == nstates - 1;
@@ -49,22 +61,40 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
   const int64_t hh = static_cast<int64_t>(h) * h;
   const int64_t tb = static_cast<int64_t>(b) * h;  // this item's token row
 
-  __shared__ float4 s_red[NT / 64][CB][2];  // per wave: (ar, ai, br, bi) of each column... x2
+  __shared__ float4 s_red[NT / 64][CB];  // per wave: (ar, ai, br, bi) of each column
   __shared__ float s_dot[NT / 64][3];
 
-  // state rows rg + NRG m, columns c0 .. c0+3 (both parts); zero outside h
+  // state rows rg + NRG m, columns c0 .. c0+3 (both parts); zero outside h.  Addresses are
+  // the item's base (uniform) plus a 32-bit element offset (h^2 <= 2^20).
   float4 xr[RPT], xi[RPT];
   float kr[RPT], vr[RPT];
   const bool colok = c0 < h;  // h % 4 == 0 (checked by the host), so all four or none
+  float* __restrict__ br_ = sr + static_cast<int64_t>(b) * hh;
+  float* __restrict__ bi_ = si + static_cast<int64_t>(b) * hh;
+  const IO* __restrict__ kb = k + tb;
+  const IO* __restrict__ vb = v + tb;
+  const int off0 = rg * h + c0;
 #pragma unroll
   for (int m = 0; m < RPT; ++m) {
     const int r = rg + NRG * m;
-    const bool ok = colok && r < h;
-    const int64_t o = static_cast<int64_t>(b) * hh + static_cast<int64_t>(ok ? r : 0) * h + (ok ? c0 : 0);
-    xr[m] = ok ? *reinterpret_cast<const float4*>(sr + o) : make_float4(0.f, 0.f, 0.f, 0.f);
-    xi[m] = ok ? *reinterpret_cast<const float4*>(si + o) : make_float4(0.f, 0.f, 0.f, 0.f);
-    kr[m] = r < h ? io<IO>::load(k, tb + r) : 0.f;
-    vr[m] = r < h ? io<IO>::load(v, tb + r) : 0.f;
+    if constexpr (EXACT) {
+      xr[m] = *reinterpret_cast<const float4*>(br_ + off0 + m * NRG * h);
+      xi[m] = *reinterpret_cast<const float4*>(bi_ + off0 + m * NRG * h);
+      kr[m] = io<IO>::load(kb, r);
+      vr[m] = io<IO>::load(vb, r);
+    } else {
+      xr[m] = make_float4(0.f, 0.f, 0.f, 0.f);
+      xi[m] = xr[m];
+      kr[m] = vr[m] = 0.f;
+      if (r < h) {
+        if (colok) {
+          xr[m] = *reinterpret_cast<const float4*>(br_ + off0 + m * NRG * h);
+          xi[m] = *reinterpret_cast<const float4*>(bi_ + off0 + m * NRG * h);
+        }
+        kr[m] = io<IO>::load(kb, r);
+        vr[m] = io<IO>::load(vb, r);
+      }
+    }
   }
   const float g = io<GT>::load(gamma, b);
   float4 qc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -97,7 +127,7 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
   }
   // sum over the wave's 8 row groups (lane bits 3..5), then over the waves in LDS
 #pragma unroll
-  for (int off = 8; off <= 32; off <<= 1) {
+  for (int off = CGN; off <= 32; off <<= 1) {
     ar.x += __shfl_xor(ar.x, off); ar.y += __shfl_xor(ar.y, off);
     ar.z += __shfl_xor(ar.z, off); ar.w += __shfl_xor(ar.w, off);
     ai.x += __shfl_xor(ai.x, off); ai.y += __shfl_xor(ai.y, off);
@@ -113,17 +143,11 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
     vv += __shfl_xor(vv, off);
     kv += __shfl_xor(kv, off);
   }
-  if (lane < 8) {
-    float* dst = reinterpret_cast<float*>(&s_red[wave][4 * cg][0]);
-    // columns 4cg + e: (ar, ai, br, bi) packed as two float4 per column
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float* pa = &ar.x;
-      const float* pai = &ai.x;
-      const float* pb = &br.x;
-      const float* pbi = &bi.x;
-      dst[8 * e + 0] = pa[e]; dst[8 * e + 1] = pai[e]; dst[8 * e + 2] = pb[e]; dst[8 * e + 3] = pbi[e];
-    }
+  if (lane < CGN) {  // columns 4cg + e: (ar, ai, br, bi)
+    s_red[wave][4 * cg + 0] = make_float4(ar.x, ai.x, br.x, bi.x);
+    s_red[wave][4 * cg + 1] = make_float4(ar.y, ai.y, br.y, bi.y);
+    s_red[wave][4 * cg + 2] = make_float4(ar.z, ai.z, br.z, bi.z);
+    s_red[wave][4 * cg + 3] = make_float4(ar.w, ai.w, br.w, bi.w);
   }
   if (lane == 0) {
     s_dot[wave][0] = kk; s_dot[wave][1] = vv; s_dot[wave][2] = kv;
@@ -131,12 +155,12 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
   __syncthreads();
   float4 A[4];  // (ar, ai, br, bi) of columns 4cg + e, summed over all rows
 #pragma unroll
-  for (int e = 0; e < 4; ++e) A[e] = s_red[0][4 * cg + e][0];
+  for (int e = 0; e < 4; ++e) A[e] = s_red[0][4 * cg + e];
 #pragma unroll
   for (int w = 1; w < NT / 64; ++w)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float4 x = s_red[w][4 * cg + e][0];
+      const float4 x = s_red[w][4 * cg + e];
       A[e].x += x.x; A[e].y += x.y; A[e].z += x.z; A[e].w += x.w;
     }
   kk = s_dot[0][0]; vv = s_dot[0][1]; kv = s_dot[0][2];
@@ -174,10 +198,9 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
     yi.y = fmaf(kr[m], ci[1], fmaf(vr[m], di[1], yi.y));
     yi.z = fmaf(kr[m], ci[2], fmaf(vr[m], di[2], yi.z));
     yi.w = fmaf(kr[m], ci[3], fmaf(vr[m], di[3], yi.w));
-    if (colok && r < h) {
-      const int64_t o = static_cast<int64_t>(b) * hh + static_cast<int64_t>(r) * h + c0;
-      *reinterpret_cast<float4*>(sr + o) = yr;
-      *reinterpret_cast<float4*>(si + o) = yi;
+    if (EXACT || (colok && r < h)) {
+      *reinterpret_cast<float4*>(br_ + off0 + m * NRG * h) = yr;
+      *reinterpret_cast<float4*>(bi_ + off0 + m * NRG * h) = yi;
     }
     po[m] = fmaf(yr.x, qc.x, fmaf(yr.y, qc.y, fmaf(yr.z, qc.z, yr.w * qc.w)));
   }
@@ -185,17 +208,182 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
     // sum over the 8 column groups (lane bits 0..2): every lane of the group gets the row sum
 #pragma unroll
     for (int m = 0; m < RPT; ++m) {
-      po[m] += __shfl_xor(po[m], 1);
-      po[m] += __shfl_xor(po[m], 2);
-      po[m] += __shfl_xor(po[m], 4);
+#pragma unroll
+      for (int off = 1; off < CGN; off <<= 1) po[m] += __shfl_xor(po[m], off);
     }
     float* pp = part + (static_cast<int64_t>(b) * nblk + blk) * h;
 #pragma unroll
     for (int m = 0; m < RPT; ++m) {
       const int r = rg + NRG * m;
-      if (cg == (m & 7) && r < h) pp[r] = po[m];
+      if (cg == (m & (CGN - 1)) && (EXACT || r < h)) pp[r] = po[m];
     }
   }
+}
+
+// h = 1024: 32-column blocks (full 128-byte row pieces) of 512 threads, 16 rows per thread.
+// 16 rows of both parts (128 floats) do not fit in registers beside the rest, so rows
+// rg + 64 m for m >= 8 pass through LDS (128 KiB per workgroup): loaded into registers,
+// summed into the column partials, parked in LDS, and read back for the update.
+template <typename IO, typename GT>
+__global__ __launch_bounds__(512) void cham_step1024_kernel(
+    const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
+    const GT* __restrict__ gamma, float* hr0, float* hi0, float* hr1, float* hi1,
+    float* __restrict__ part, int nstates) {
+  constexpr int NT = 512, H = 1024, CB = 32, CGN = 8, NRG = 64, RPT = 16, RR = 8;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int cg = tid & (CGN - 1), rg = tid / CGN;
+  const int blk = blockIdx.x, b = blockIdx.y, z = blockIdx.z;
+  const int nblk = gridDim.x;
+  const int c0 = blk * CB + 4 * cg;
+  const bool readout = z == nstates - 1;
+  float* __restrict__ sr = (z == 0 ? hr0 : hr1) + static_cast<int64_t>(b) * H * H;
+  float* __restrict__ si = (z == 0 ? hi0 : hi1) + static_cast<int64_t>(b) * H * H;
+  const IO* __restrict__ kb = k + static_cast<int64_t>(b) * H;
+  const IO* __restrict__ vb = v + static_cast<int64_t>(b) * H;
+  const int off0 = rg * H + c0;
+
+  __shared__ float4 s_hold[RPT - RR][2][NT];  // rows m >= RR: real, imag
+  __shared__ float4 s_red[NT / 64][CB];
+  __shared__ float s_dot[NT / 64][3];
+
+  float4 xr[RR], xi[RR];
+  float kr[RPT], vr[RPT];
+#pragma unroll
+  for (int m = 0; m < RR; ++m) {
+    xr[m] = *reinterpret_cast<const float4*>(sr + off0 + m * NRG * H);
+    xi[m] = *reinterpret_cast<const float4*>(si + off0 + m * NRG * H);
+  }
+#pragma unroll
+  for (int m = 0; m < RPT; ++m) {
+    kr[m] = io<IO>::load(kb, rg + NRG * m);
+    vr[m] = io<IO>::load(vb, rg + NRG * m);
+  }
+  const float g = io<GT>::load(gamma, b);
+  float4 qc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (readout)
+    qc = make_float4(io<IO>::load(q, static_cast<int64_t>(b) * H + c0),
+                     io<IO>::load(q, static_cast<int64_t>(b) * H + c0 + 1),
+                     io<IO>::load(q, static_cast<int64_t>(b) * H + c0 + 2),
+                     io<IO>::load(q, static_cast<int64_t>(b) * H + c0 + 3));
+  float4 ar = make_float4(0.f, 0.f, 0.f, 0.f), ai = ar, br = ar, bi = ar;
+  auto acc = [&](float kx, float vx, const float4& yr, const float4& yi) {
+    ar.x = fmaf(kx, yr.x, ar.x); ar.y = fmaf(kx, yr.y, ar.y);
+    ar.z = fmaf(kx, yr.z, ar.z); ar.w = fmaf(kx, yr.w, ar.w);
+    ai.x = fmaf(kx, yi.x, ai.x); ai.y = fmaf(kx, yi.y, ai.y);
+    ai.z = fmaf(kx, yi.z, ai.z); ai.w = fmaf(kx, yi.w, ai.w);
+    br.x = fmaf(vx, yr.x, br.x); br.y = fmaf(vx, yr.y, br.y);
+    br.z = fmaf(vx, yr.z, br.z); br.w = fmaf(vx, yr.w, br.w);
+    bi.x = fmaf(vx, yi.x, bi.x); bi.y = fmaf(vx, yi.y, bi.y);
+    bi.z = fmaf(vx, yi.z, bi.z); bi.w = fmaf(vx, yi.w, bi.w);
+  };
+  __builtin_amdgcn_sched_barrier(0);
+  {  // rows m >= RR: through registers into the partials and LDS
+    float4 tr[RPT - RR], ti[RPT - RR];
+#pragma unroll
+    for (int m = RR; m < RPT; ++m) {
+      tr[m - RR] = *reinterpret_cast<const float4*>(sr + off0 + m * NRG * H);
+      ti[m - RR] = *reinterpret_cast<const float4*>(si + off0 + m * NRG * H);
+    }
+#pragma unroll
+    for (int m = 0; m < RR; ++m) acc(kr[m], vr[m], xr[m], xi[m]);
+#pragma unroll
+    for (int m = RR; m < RPT; ++m) {
+      acc(kr[m], vr[m], tr[m - RR], ti[m - RR]);
+      s_hold[m - RR][0][tid] = tr[m - RR];
+      s_hold[m - RR][1][tid] = ti[m - RR];
+    }
+  }
+  float kk = 0.f, vv = 0.f, kv = 0.f;
+  if (cg == 0) {
+#pragma unroll
+    for (int m = 0; m < RPT; ++m) {
+      kk = fmaf(kr[m], kr[m], kk);
+      vv = fmaf(vr[m], vr[m], vv);
+      kv = fmaf(kr[m], vr[m], kv);
+    }
+  }
+#pragma unroll
+  for (int off = CGN; off <= 32; off <<= 1) {
+    ar.x += __shfl_xor(ar.x, off); ar.y += __shfl_xor(ar.y, off);
+    ar.z += __shfl_xor(ar.z, off); ar.w += __shfl_xor(ar.w, off);
+    ai.x += __shfl_xor(ai.x, off); ai.y += __shfl_xor(ai.y, off);
+    ai.z += __shfl_xor(ai.z, off); ai.w += __shfl_xor(ai.w, off);
+    br.x += __shfl_xor(br.x, off); br.y += __shfl_xor(br.y, off);
+    br.z += __shfl_xor(br.z, off); br.w += __shfl_xor(br.w, off);
+    bi.x += __shfl_xor(bi.x, off); bi.y += __shfl_xor(bi.y, off);
+    bi.z += __shfl_xor(bi.z, off); bi.w += __shfl_xor(bi.w, off);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    kk += __shfl_xor(kk, off);
+    vv += __shfl_xor(vv, off);
+    kv += __shfl_xor(kv, off);
+  }
+  if (lane < CGN) {
+    s_red[wave][4 * cg + 0] = make_float4(ar.x, ai.x, br.x, bi.x);
+    s_red[wave][4 * cg + 1] = make_float4(ar.y, ai.y, br.y, bi.y);
+    s_red[wave][4 * cg + 2] = make_float4(ar.z, ai.z, br.z, bi.z);
+    s_red[wave][4 * cg + 3] = make_float4(ar.w, ai.w, br.w, bi.w);
+  }
+  if (lane == 0) {
+    s_dot[wave][0] = kk; s_dot[wave][1] = vv; s_dot[wave][2] = kv;
+  }
+  __syncthreads();
+  float4 A[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) A[e] = s_red[0][4 * cg + e];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float4 x = s_red[w][4 * cg + e];
+      A[e].x += x.x; A[e].y += x.y; A[e].z += x.z; A[e].w += x.w;
+    }
+  kk = s_dot[0][0]; vv = s_dot[0][1]; kv = s_dot[0][2];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) {
+    kk += s_dot[w][0]; vv += s_dot[w][1]; kv += s_dot[w][2];
+  }
+  bool ok;
+  const NCoef N = cham::cayley_n_guarded(g, kk, vv, kv, ok);
+  if (!ok) {
+#pragma unroll
+    for (int m = 0; m < RPT; ++m) kr[m] = vr[m] = 0.f;
+  }
+  float cr[4], ci[4], dr[4], di[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float4 s = A[e];
+    cr[e] = N.n11r * s.x - N.n11i * s.y + N.n12r * s.z - N.n12i * s.w;
+    ci[e] = N.n11r * s.y + N.n11i * s.x + N.n12r * s.w + N.n12i * s.z;
+    dr[e] = N.n12r * s.x - N.n12i * s.y + N.n22r * s.z - N.n22i * s.w;
+    di[e] = N.n12r * s.y + N.n12i * s.x + N.n22r * s.w + N.n22i * s.z;
+  }
+  float* pp = part + (static_cast<int64_t>(b) * nblk + blk) * H;
+  auto upd = [&](int m, float4 yr, float4 yi) {
+    yr.x = fmaf(kr[m], cr[0], fmaf(vr[m], dr[0], yr.x));
+    yr.y = fmaf(kr[m], cr[1], fmaf(vr[m], dr[1], yr.y));
+    yr.z = fmaf(kr[m], cr[2], fmaf(vr[m], dr[2], yr.z));
+    yr.w = fmaf(kr[m], cr[3], fmaf(vr[m], dr[3], yr.w));
+    yi.x = fmaf(kr[m], ci[0], fmaf(vr[m], di[0], yi.x));
+    yi.y = fmaf(kr[m], ci[1], fmaf(vr[m], di[1], yi.y));
+    yi.z = fmaf(kr[m], ci[2], fmaf(vr[m], di[2], yi.z));
+    yi.w = fmaf(kr[m], ci[3], fmaf(vr[m], di[3], yi.w));
+    *reinterpret_cast<float4*>(sr + off0 + m * NRG * H) = yr;
+    *reinterpret_cast<float4*>(si + off0 + m * NRG * H) = yi;
+    if (readout) {  // this row's readout partial, summed over the 8 column groups
+      float po = fmaf(yr.x, qc.x, fmaf(yr.y, qc.y, fmaf(yr.z, qc.z, yr.w * qc.w)));
+#pragma unroll
+      for (int off = 1; off < CGN; off <<= 1) po += __shfl_xor(po, off);
+      if (cg == (m & (CGN - 1))) pp[rg + NRG * m] = po;
+    }
+  };
+#pragma unroll
+  for (int m = 0; m < RR; ++m) upd(m, xr[m], xi[m]);
+  // keep the held rows' LDS reads after the register rows are stored (register pressure)
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int m = RR; m < RPT; ++m) upd(m, s_hold[m - RR][0][tid], s_hold[m - RR][1][tid]);
 }
 
 // out[b][i] = sum over the column blocks of the readout partials (io dtype)
@@ -216,20 +404,29 @@ template <typename IO, typename GT>
 hipError_t launch_t(const void* q, const void* k, const void* v, const void* gamma, float* hr,
                     float* hi, float* rr, float* ri, void* out, int B, int h, float* part,
                     hipStream_t stream) {
-  const int nblk = (h + CB - 1) / CB;
+  // h = 1024: the LDS-holding kernel with 32-column blocks; other h above 512: 16-column
+  // blocks of 512 threads, 8 rows each (32 columns would need 16 rows per thread and spill)
+  const int cb = (h > 512 && h != 1024) ? 16 : 32;
+  const int nblk = (h + cb - 1) / cb;
   const int nstates = rr ? 2 : 1;
   const dim3 grid(nblk, B, nstates);
   const IO* qq = static_cast<const IO*>(q);
   const IO* kq = static_cast<const IO*>(k);
   const IO* vq = static_cast<const IO*>(v);
   const GT* gg = static_cast<const GT*>(gamma);
-#define VMI_CS(RPT_) \
-  hipLaunchKernelGGL((cham_step_kernel<IO, GT, RPT_>), grid, dim3(NT), 0, stream, qq, kq, vq, gg, \
-                     hr, hi, rr, ri, part, h, nstates)
-  if (h <= 2 * NRG) VMI_CS(2);
-  else if (h <= 4 * NRG) VMI_CS(4);
-  else if (h <= 8 * NRG) VMI_CS(8);
-  else VMI_CS(16);
+#define VMI_CS(CB_, RPT_, EX_) \
+  hipLaunchKernelGGL((cham_step_kernel<IO, GT, 512, CB_, RPT_, EX_>), grid, dim3(512), 0, stream, \
+                     qq, kq, vq, gg, hr, hi, rr, ri, part, h, nstates)
+  if (h == 128) VMI_CS(32, 2, true);
+  else if (h < 128) VMI_CS(32, 2, false);
+  else if (h == 256) VMI_CS(32, 4, true);
+  else if (h < 256) VMI_CS(32, 4, false);
+  else if (h == 512) VMI_CS(32, 8, true);
+  else if (h < 512) VMI_CS(32, 8, false);
+  else if (h == 1024)
+    hipLaunchKernelGGL((cham_step1024_kernel<IO, GT>), grid, dim3(512), 0, stream, qq, kq, vq, gg,
+                       hr, hi, rr, ri, part, nstates);
+  else VMI_CS(16, 8, false);
 #undef VMI_CS
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -241,7 +438,7 @@ hipError_t launch_t(const void* q, const void* k, const void* v, const void* gam
 }  // namespace chams
 
 size_t cham_step_workspace_bytes(int64_t B, int64_t h) {
-  return static_cast<size_t>(B) * ((h + chams::CB - 1) / chams::CB) * h * sizeof(float);
+  return static_cast<size_t>(B) * ((h + chams::CB_MIN - 1) / chams::CB_MIN) * h * sizeof(float);
 }
 
 hipError_t launch_cham_step(const void* q, const void* k, const void* v, const void* gamma,
