@@ -86,6 +86,20 @@ int vmi_sssd_scan_fwd(const void* q, const void* k, const void* v,
                       int64_t B, int64_t T, int64_t H, int64_t D,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same prefill scan with no workspace argument and no allocation: the scan's workspace
+ * is a fixed 40 MiB device array of the library, one per GPU, held from the library's first
+ * use on that GPU until the process ends (enough for every plan of the OP, FULL, LONG and DEC
+ * shapes; plans needing more return VMI_ERR_WORKSPACE before anything is launched -- use
+ * vmi_sssd_scan_fwd for them).  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Calls on one GPU share its array, so calls that overlap on one
+ * GPU (several streams or host threads) race: order them.  Arguments and results as
+ * vmi_sssd_scan_fwd. */
+int vmi_sssd_scan_fwd_noalloc(const void* q, const void* k, const void* v,
+                              const void* delta, int io_dtype, int delta_dtype,
+                              const float* psi_in, void* out, float* psi_out,
+                              int64_t B, int64_t T, int64_t H, int64_t D, void* stream);
+
 /* Prefill scan on the raw projections, with the steps either side of the scan fused:
  * replaces sssd_attention.py:114-126 (F.normalize of q, k, v; delta = 0.1 *
  * sigmoid(w_delta x) * active_mask) and :177 (head_rmsnorm) around the scan.

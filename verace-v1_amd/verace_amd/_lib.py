@@ -23,6 +23,7 @@ EXPORTED = (
     "vmi_last_hip_error",
     "vmi_sssd_scan_workspace_bytes",
     "vmi_sssd_scan_fwd",
+    "vmi_sssd_scan_fwd_noalloc",
     "vmi_sssd_scan_fused_workspace_bytes",
     "vmi_sssd_scan_fused",
     "vmi_sssd_step_inplace",
@@ -70,6 +71,9 @@ def _declare(lib):
     lib.vmi_sssd_scan_fwd.argtypes = [vp, vp, vp, vp, i32, i32, vp, vp, vp, i64, i64, i64, i64,
                                       vp, sz, vp]
     lib.vmi_sssd_scan_fwd.restype = i32
+    lib.vmi_sssd_scan_fwd_noalloc.argtypes = [vp, vp, vp, vp, i32, i32, vp, vp, vp, i64, i64, i64,
+                                              i64, vp]
+    lib.vmi_sssd_scan_fwd_noalloc.restype = i32
     lib.vmi_sssd_scan_fused_workspace_bytes.argtypes = [i64, i64, i64, i64, i32, ctypes.POINTER(sz)]
     lib.vmi_sssd_scan_fused_workspace_bytes.restype = i32
     lib.vmi_sssd_scan_fused.argtypes = [vp, i64, i32, vp, vp, ctypes.c_float, vp, vp, vp, i64, i64,
