@@ -25,6 +25,10 @@ Drop-in replacements for the reference's SSSD hot path:
                                   ``acd_engine.py:36-167``) with batched in-place decode
 * ``HAS_HIP``                  <- ``verace_v1.serving.triton_kernels.HAS_TRITON``
 
+``torch.ops.verace.{sssd_scan, sssd_scan_bwd, sssd_step_, sssd_scan_fused, cham_scan, cham_step_,
+ns_retraction}`` are the same launchers registered as torch operators with fake kernels and
+autograd (``ops.py``), for FakeTensor / meta tracing and ``torch.compile``.
+
 All compute runs in ``libverace_sssd.so`` (C ABI: ``include/verace_sssd.h``).
 """
 from .hip_kernels import (HAS_HIP, SSSDScanFunction, cham_step_, launch_cham_hip_update,
@@ -32,6 +36,7 @@ from .hip_kernels import (HAS_HIP, SSSDScanFunction, cham_step_, launch_cham_hip
                           launch_sssd_hip_scan_fused,
                           newton_schulz_unitary_retraction, parallel_newton_schulz_retraction,
                           sssd_scan, sssd_step_)
+from . import ops  # noqa: F401  (torch.ops.verace.*: the launchers as traceable operators)
 from .sssd_attention import SSSDAttention
 from .cham_memory import ContinuousHolographicMemory
 from .mcmoe import ManifoldContinuousMoE, SiTUGLU

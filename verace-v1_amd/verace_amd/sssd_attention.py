@@ -26,8 +26,17 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import ops as _ops  # noqa: F401  (registers torch.ops.verace.*)
 from .hip_kernels import (fused_scan_supported, launch_sssd_hip_scan, launch_sssd_hip_scan_fused,
                           sssd_scan)
+
+
+def _traced(x: torch.Tensor) -> bool:
+    """True while torch.compile / FakeTensor / meta tracing runs this module: the scan then goes
+    through the registered torch.ops.verace operators (fake kernels, autograd) instead of the
+    ctypes launchers, so the graph does not break."""
+    from torch._subclasses.fake_tensor import FakeTensor
+    return torch.compiler.is_compiling() or isinstance(x, FakeTensor) or x.device.type == "meta"
 
 
 class SSSDAttention(nn.Module):
@@ -105,6 +114,8 @@ class SSSDAttention(nn.Module):
         return_state: bool = False,
         active_mask: Optional[torch.Tensor] = None,
     ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        if _traced(x):
+            return self._forward_traced(x, initial_state, return_state, active_mask)
         if not x.is_cuda:
             raise RuntimeError("verace_amd.SSSDAttention runs on a HIP device only; "
                                "move the module and inputs to the GPU")
@@ -136,6 +147,36 @@ class SSSDAttention(nn.Module):
         if return_state:
             return output, psi
         return output, None
+
+    def _forward_traced(self, x, initial_state, return_state, active_mask):
+        """``forward`` on the registered operators (the same routes: differentiable scan when
+        autograd needs it, the fused scan where it applies, else the unfused ops)."""
+        b, s, _ = x.shape
+        grad = torch.is_grad_enabled() and (
+            x.requires_grad or (initial_state is not None and initial_state.requires_grad))
+        rms_grad = (torch.is_grad_enabled() and self.head_rmsnorm.weight is not None
+                    and self.head_rmsnorm.weight.requires_grad)
+        if not grad and self._fused(x):
+            ws = [w.detach() for w in (self.w_q.weight, self.w_k.weight, self.w_v.weight,
+                                       self.w_delta.weight)]
+            pad = (-sum(w.shape[0] for w in ws)) % 256
+            if pad:
+                ws.append(ws[0].new_zeros(pad, ws[0].shape[1]))
+            proj = F.linear(x, torch.cat(ws, 0))
+            w = None if rms_grad else self.head_rmsnorm.weight
+            eps = None if w is None else self.head_rmsnorm.eps
+            mask = None if active_mask is None else active_mask.reshape(b, s)
+            o, psi = torch.ops.verace.sssd_scan_fused(proj, self.num_heads, self.head_dim, mask,
+                                                      None if w is None else w.detach().float(),
+                                                      eps, initial_state)
+            if rms_grad:
+                o = self.head_rmsnorm(o)
+        else:
+            q, k, v, delta = self.project(x, active_mask)
+            o, psi = torch.ops.verace.sssd_scan(q, k, v, delta, initial_state)
+            o = self.head_rmsnorm(o)
+        output = self.w_out(o.reshape(b, s, self.num_heads * self.head_dim))
+        return output, (psi if return_state else None)
 
     def forward_cached(self, x: torch.Tensor, cache, layer: int, handles,
                        active_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
