@@ -715,6 +715,74 @@ def bench_model_decode(device, model):
     }
 
 
+MFMA_KERNELS = [  # (label, substring of the kernel name in rocprofv3's CSVs, dense peak TFLOP/s)
+    ("scan pass A (chunk_kernel READOUT=0)", "sssd_chunk_kernelIDF16bNS_6bf16_tELb0ELb0E", MFMA_F16_PEAK_TFLOPS),
+    ("scan pass C (chunk_kernel READOUT=1)", "sssd_chunk_kernelIDF16bNS_6bf16_tELb1ELb0E", MFMA_F16_PEAK_TFLOPS),
+    ("scan pass B (carry_kernel)", "sssd_carry_kernel", MFMA_F16_PEAK_TFLOPS),
+    ("fused scan pass A", "sssd_chunk_kernelIDF16bNS_6bf16_tELb0ELb1E", MFMA_F16_PEAK_TFLOPS),
+    ("fused scan pass C", "sssd_chunk_kernelIDF16bNS_6bf16_tELb1ELb1E", MFMA_F16_PEAK_TFLOPS),
+    ("backward columns (bwdc_cols_kernel)", "bwdc_cols_kernel", MFMA_F16_PEAK_TFLOPS),
+    ("backward prep (bwdc_prep_kernel)", "bwdc_prep_kernel", 157.3),
+    ("CHAM NS GEMM (ns_gemm2_kernel)", "ns_gemm2_kernel", 157.3),
+    ("CHAM Z (wide_z_kernel)", "wide_z_kernel", 157.3),
+]
+
+
+def mfma_summary(counter_csv, trace_csv, out_json):
+    """Per-kernel MFMA counters from a rocprofv3 --pmc run (SQ_INSTS_VALU_MFMA_MOPS_{F16,BF16,
+    F32}, SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE, SQ_INSTS_MFMA / VALU / LDS) and the kernel
+    durations of a --kernel-trace run of the same command: MFMA flops per dispatch
+    (MOPS x 512), achieved TFLOP/s (flops / mean duration), and MFMA utilisation
+    (busy cycles / (GRBM_GUI_ACTIVE x 1024 SIMDs), rocprofv3's MfmaUtil)."""
+    import csv
+    sums, counts = {}, {}
+    for r in csv.DictReader(open(counter_csv)):
+        key = (r["Kernel_Name"], r["Counter_Name"])
+        sums[key] = sums.get(key, 0.0) + float(r["Counter_Value"])
+        if r["Counter_Name"] == "GRBM_GUI_ACTIVE":
+            counts[r["Kernel_Name"]] = counts.get(r["Kernel_Name"], 0) + 1
+    durs = {}
+    for r in csv.DictReader(open(trace_csv)):
+        durs.setdefault(r["Kernel_Name"], []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    res = {}
+    for label, sub, peak in MFMA_KERNELS:
+        names = [n for n in counts if sub in n]
+        if not names:
+            continue
+        n = names[0]
+        c = counts[n]
+        get = lambda cn: sums.get((n, cn), 0.0) / c
+        flops = 512 * (get("SQ_INSTS_VALU_MFMA_MOPS_F16") + get("SQ_INSTS_VALU_MFMA_MOPS_BF16")
+                       + get("SQ_INSTS_VALU_MFMA_MOPS_F32"))
+        tr = [d for k, v in durs.items() if sub in k for d in v]
+        mean_ns = statistics.mean(tr) if tr else None
+        util = 100 * get("SQ_VALU_MFMA_BUSY_CYCLES") / max(get("GRBM_GUI_ACTIVE") * 1024, 1)
+        res[label] = {
+            "dispatches": c, "mean_us": None if mean_ns is None else round(mean_ns / 1e3, 2),
+            "mfma_flops_per_dispatch": flops,
+            "mfma_tflops": None if not mean_ns else round(flops / mean_ns / 1e3, 1),
+            "peak_tflops": peak,
+            "mfma_frac_of_peak": None if not mean_ns else round(flops / mean_ns / 1e3 / peak, 4),
+            "mfma_busy_util_pct": round(util, 2),
+            "insts_mfma": get("SQ_INSTS_MFMA"), "insts_valu": get("SQ_INSTS_VALU"),
+            "insts_lds": get("SQ_INSTS_LDS"),
+        }
+    with open(out_json, "w") as f:
+        json.dump(res, f, indent=1)
+    return res
+
+
+def load_mfma_counters():
+    """Per-pass MFMA TFLOP/s of the OP scan from the committed rocprofv3 counter summary."""
+    p = os.path.join(REPO_ROOT, "profiles", "mfma_counters_op_scan.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        d = json.load(f)
+    return {k: {"mfma_tflops": v["mfma_tflops"], "frac_of_peak": v["mfma_frac_of_peak"],
+                "mean_us": v["mean_us"]} for k, v in d.items()}
+
+
 def load_traffic():
     """HBM bytes per scan from the committed rocprofv3 --pmc summary, if present."""
     p = os.path.join(REPO_ROOT, "profiles", "pmc_traffic_op_scan.json")
@@ -739,6 +807,11 @@ def main():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc counter CSVs into "
                          "profiles/pmc_traffic_op_scan.json and exit")
+    ap.add_argument("--mfma-summary", nargs=2, metavar=("COUNTER_CSV", "TRACE_CSV"),
+                    help="summarise a rocprofv3 --pmc MFMA counter run and a --kernel-trace run "
+                         "of the same command into profiles/<--mfma-out> and exit")
+    ap.add_argument("--mfma-out", default="mfma_counters_op_scan.json",
+                    help="file name under profiles/ for --mfma-summary")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the scan, run torch copies of COPY_PROBE_BYTES (calibration "
                          "kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -746,6 +819,10 @@ def main():
     if args.pmc_summary:
         out = os.path.join(REPO_ROOT, "profiles", "pmc_traffic_op_scan.json")
         print(json.dumps(pmc_summary(args.pmc_summary[0], args.pmc_summary[1], out), indent=1))
+        return
+    if args.mfma_summary:
+        out = os.path.join(REPO_ROOT, "profiles", args.mfma_out)
+        print(json.dumps(mfma_summary(args.mfma_summary[0], args.mfma_summary[1], out), indent=1))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
@@ -791,6 +868,10 @@ def main():
             # (a, b = [k v]^T Psi, the rank-2 update, Psi q) against the dense f16 MFMA peak
             # the scan's products run on
             "mfma": {
+                # counter-backed figures (rocprofv3 SQ_INSTS_VALU_MFMA_MOPS_*, committed in
+                # profiles/mfma_counters_op_scan.json and mfma_counters.md) are reported beside
+                # this algorithmic one as "counters"
+                "counters": load_mfma_counters(),
                 "algorithmic_flops": 10 * D * D * B * T * H,
                 "tflops": round(10 * D * D * B * T * H / (ms * 1e-3) / 1e12, 2),
                 "peak_tflops": MFMA_F16_PEAK_TFLOPS,
@@ -798,6 +879,9 @@ def main():
             },
         },
         "parity": parity,
+        # the chunk scan rounds the state, W and Z to f16 once per 16-token chunk (fp32
+        # accumulation; every MFMA accumulates in fp32); measured drift in "parity"
+        "state_operand_precision": "f16 per 16-token chunk, fp32 accumulate",
         "wall_s_timed_region": round(wall, 3),
     }
     if args.copy_probe:
