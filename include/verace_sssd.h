@@ -193,6 +193,25 @@ int vmi_state_cache_step(vmi_state_cache* cache, int64_t layer, const int64_t* h
                          const void* delta, int io_dtype, int delta_dtype, void* out,
                          void* stream);
 
+/* The CHAM half of the cached state: holo_pool [num_layers, num_slots, 2, h, h] float32 (the
+ * caller's; slot s of layer l holds the raw hologram's real plane, then its imaginary plane)
+ * becomes part of the cache, so a handle's (sssd_state, cham_hologram) tuple of
+ * acd_engine.py:88-92 lives in one slot of each pool.  vmi_state_cache_cham_step runs the
+ * in-place CHAM decode step (as vmi_cham_step_inplace) over the hologram slots with the slot
+ * decisions of the layer's last vmi_state_cache_step: call it with the same handles in the
+ * same order after that layer's SSSD step (the CHAM sub-layer's inputs come from the SSSD
+ * sub-layer's output, backbone.py:83-93); other handle lists return VMI_ERR_INVALID_ARG.
+ * A handle with no slot yet starts from the identity.  Every cached hologram is taken to have
+ * started from the identity (unitary, so the readout NS_3(H) = H; write NS_3-retracted pairs
+ * only if that holds).  q, k, v, out: [n, 1, h] io_dtype; gamma: [n] gamma_dtype; h % 4 == 0,
+ * h <= 1024.  Workspace from vmi_state_cache_cham_workspace_bytes. */
+int vmi_state_cache_attach_hologram(vmi_state_cache* cache, int64_t h, float* holo_pool);
+int vmi_state_cache_cham_workspace_bytes(int64_t n, int64_t h, size_t* bytes);
+int vmi_state_cache_cham_step(vmi_state_cache* cache, int64_t layer, const int64_t* handles,
+                              int64_t n, const void* q, const void* k, const void* v,
+                              const void* gamma, int io_dtype, int gamma_dtype, void* out,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
 /* Backward of the scan (training).  Replaces the eager autograd through
  * sssd_attention.py:144-175 that the reference's training loop differentiates
  * (pretrain.py:164-195): given the forward's inputs, its final state psi_T

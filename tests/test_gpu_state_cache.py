@@ -168,3 +168,90 @@ def test_cache_step_batch_above_one_launch(device, D):
     assert torch.equal(o, o_ref)
     assert torch.equal(cache.read(0, hs), ref)
     assert cache.table.free_slots(0) == 500 - 300   # the 150 shared slots were freed
+
+
+def test_cache_tree_search_against_oracle_with_holograms(device):
+    """Each tree-search branch (hyper_generate.py:97-121) against the oracle run from its
+    parent's state: a 2-layer cache holding both halves of the reference's per-layer tuple
+    (sssd_state [H, D, D] and the CHAM hologram, acd_engine.py:88-92).  Sequences are
+    prefilled (states written), forked into branches that share the parent's slots, and every
+    branch takes its own tokens for two steps (SSSD step, then the CHAM step of the same layer
+    and handles).  Each branch's outputs and final states must equal the fp64 closed-form SSSD
+    scan (oracle.sssd_closed) and the fp64 CHAM closed form (oracle.cham_scan) run from the
+    parent's state over that branch's tokens, and the parents' own states must be untouched.
+    Bars: bf16 I/O 2e-2 (outputs), fp32 states 1e-5."""
+    from oracle import cham_scan, sssd_closed
+    from verace_amd import SSSDStateCache
+    print("[case] cache tree search vs oracle, with holograms", flush=True)
+    L, N, H, D, h = 2, 64, 4, 128, 64
+    n_seq, n_br, steps = 3, 3, 2
+    cache = SSSDStateCache(L, N, H, D, device=device, hologram_dim=h)
+    g = torch.Generator().manual_seed(40)
+    parents = cache.new(n_seq)
+    psi0 = {l: _orth(n_seq, H, D, seed=50 + l) for l in range(L)}
+    holo0 = {}
+    for l in range(L):
+        a = torch.randn(n_seq, h, h, generator=g, dtype=torch.float64) + \
+            1j * torch.randn(n_seq, h, h, generator=g, dtype=torch.float64)
+        u = torch.linalg.qr(a)[0]
+        holo0[l] = (u.real.float().contiguous(), u.imag.float().contiguous())
+        cache.write(l, parents, psi0[l].to(device), (holo0[l][0].to(device), holo0[l][1].to(device)))
+    branches = {p: cache.fork(p, n_br) for p in parents}
+    order = [b for p in parents for b in branches[p]]
+    nb = len(order)
+    # per-branch tokens for every step and layer
+    toks = {}
+    for s in range(steps):
+        for l in range(L):
+            q, k, v, d = _tokens(nb, H, D, seed=1000 + 10 * s + l)
+            cq = F.normalize(torch.randn(nb, 1, h, generator=g), dim=-1).bfloat16()
+            ck = F.normalize(torch.randn(nb, 1, h, generator=g), dim=-1).bfloat16()
+            cv = F.normalize(torch.randn(nb, 1, h, generator=g), dim=-1).bfloat16()
+            cg = (0.1 * torch.sigmoid(torch.randn(nb, generator=g))).bfloat16()
+            toks[(s, l)] = (q, k, v, d, cq, ck, cv, cg)
+    outs = {}
+    hs = np.array(order, dtype=np.int64)
+    for s in range(steps):
+        for l in range(L):
+            q, k, v, d, cq, ck, cv, cg = (t.to(device) for t in toks[(s, l)])
+            o = cache.step(l, q, k, v, d, hs)
+            co = cache.cham_step(l, cq, ck, cv, cg, hs)
+            outs[(s, l)] = (o.float().cpu(), co.float().cpu())
+    torch.cuda.synchronize()
+    worst = {"o": 0.0, "psi": 0.0, "co": 0.0, "holo": 0.0}
+
+    def rel(a, b):
+        a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+        return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+    for l in range(L):
+        st = cache.read(l, order).cpu()
+        hr, hi = (t.cpu() for t in cache.read_holograms(l, order))
+        for i, bh in enumerate(order):
+            pi = parents.index(next(p for p in parents if bh in branches[p]))
+            sel = lambda t: torch.stack([toks[(s, l)][t][i] for s in range(steps)], 0).unsqueeze(0)
+            q, k, v, d = (sel(j).float().numpy().reshape(1, steps, H, -1) if j < 3 else
+                          sel(j).float().numpy().reshape(1, steps, H) for j in range(4))
+            o64, p64 = sssd_closed.sssd_scan_closed_np(q, k, v, d, psi0[l][pi:pi + 1].double().numpy())
+            got_o = torch.stack([outs[(s, l)][0][i, 0] for s in range(steps)], 0).numpy()
+            worst["o"] = max(worst["o"], rel(got_o, o64[0]))
+            worst["psi"] = max(worst["psi"], rel(st[i].numpy(), p64[0]))
+            cq, ck, cv = (torch.stack([toks[(s, l)][4 + j][i, 0] for s in range(steps)], 0)
+                          .double().numpy()[None] for j in range(3))
+            cg = np.array([[float(toks[(s, l)][7][i]) for s in range(steps)]])
+            rec, (sr, si) = cham_scan.cham_scan_closed(cq, ck, cv, cg, holo0[l][0][pi:pi + 1].double().numpy(),
+                                                      holo0[l][1][pi:pi + 1].double().numpy())
+            got_c = torch.stack([outs[(s, l)][1][i, 0] for s in range(steps)], 0).numpy()
+            worst["co"] = max(worst["co"], rel(got_c, rec[0]))
+            worst["holo"] = max(worst["holo"], rel(hr[i].numpy(), sr[0]), rel(hi[i].numpy(), si[0]))
+        # the parents' states are untouched (their branches wrote fresh slots)
+        assert torch.equal(cache.read(l, parents).cpu(), psi0[l])
+        pr, pim = (t.cpu() for t in cache.read_holograms(l, parents))
+        assert torch.equal(pr, holo0[l][0]) and torch.equal(pim, holo0[l][1])
+    print("  " + " ".join(f"{k}={v:.2e}" for k, v in worst.items()), flush=True)
+    assert worst["o"] <= 2e-2 and worst["co"] <= 2e-2
+    assert worst["psi"] <= 1e-5 and worst["holo"] <= 1e-5
+    # a CHAM step whose handles differ from the layer's last SSSD step is refused
+    with pytest.raises(ValueError):
+        q, k, v, d, cq, ck, cv, cg = (t.to(device) for t in toks[(0, 0)])
+        cache.step(0, q, k, v, d, hs)
+        cache.cham_step(0, cq[:2], ck[:2], cv[:2], cg[:2], hs[:2])

@@ -33,15 +33,60 @@ using cham::NCoef;
 
 constexpr int CB_MIN = 16;      // smallest column block (sizes the readout partials)
 
+// Where item b's state lives.  DenseItems: plane arrays [B, h, h] (real and imaginary
+// separate).  SlotItems: the per-layer hologram pool of a decode state cache, slot s at
+// pool + 2 s h^2 (real plane, then imaginary); item b reads slot in_slot[b] (-1: the
+// identity) and writes slot out_slot[b] (copy-on-write when they differ), slots in the
+// kernel arguments as for the SSSD step (vmi::SlotArgs).
+struct DenseItems {
+  static constexpr bool kSlotted = false;
+};
+struct SlotItems {
+  static constexpr bool kSlotted = true;
+  int32_t in_slot[kMaxSlotArgs];
+  int32_t out_slot[kMaxSlotArgs];
+};
+
+struct ItemPtrs {
+  const float* in_r;
+  const float* in_i;
+  float* out_r;
+  float* out_i;
+  bool identity;  // slotted item with no slot yet: the state is I (real), 0 (imaginary)
+};
+template <typename Map>
+__device__ __forceinline__ ItemPtrs item_ptrs(const Map& map, float* re, float* im, int b,
+                                              int64_t hh) {
+  ItemPtrs p;
+  if constexpr (Map::kSlotted) {
+    const int si = map.in_slot[b], so = map.out_slot[b];
+    p.identity = si < 0;
+    p.in_r = re + 2 * static_cast<int64_t>(si < 0 ? 0 : si) * hh;
+    p.in_i = p.in_r + hh;
+    p.out_r = re + 2 * static_cast<int64_t>(so) * hh;
+    p.out_i = p.out_r + hh;
+  } else {
+    (void)map;
+    p.identity = false;
+    p.in_r = p.out_r = re + static_cast<int64_t>(b) * hh;
+    p.in_i = p.out_i = im + static_cast<int64_t>(b) * hh;
+  }
+  return p;
+}
+__device__ __forceinline__ float4 eye4(int r, int c0) {
+  return make_float4(r == c0 ? 1.f : 0.f, r == c0 + 1 ? 1.f : 0.f, r == c0 + 2 ? 1.f : 0.f,
+                     r == c0 + 3 ? 1.f : 0.f);
+}
+
 // EXACT: h == NT / 8 * RPT and h % 32 == 0, so every row and column of the block exists and
 // the loads and stores need no guards (branches around them made the compiler serialise the
 // loads and spill at 1024 threads).
 // (h is then a compile-time constant, so every address is a base plus an immediate).
-template <typename IO, typename GT, int NT, int CB, int RPT, bool EXACT>
+template <typename IO, typename GT, int NT, int CB, int RPT, bool EXACT, typename Map>
 __global__ __launch_bounds__(NT) void cham_step_kernel(
     const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
     const GT* __restrict__ gamma, float* hr0, float* hi0, float* hr1, float* hi1,
-    float* __restrict__ part, int h_arg, int nstates) {
+    float* __restrict__ part, int h_arg, int nstates, const Map map) {
   constexpr int CGN = CB / 4;        // column groups of 4 columns (float4)
   const int h = EXACT ? NT / CGN * RPT : h_arg;
   constexpr int NRG = NT / CGN;  // row groups
@@ -69,17 +114,21 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
   float4 xr[RPT], xi[RPT];
   float kr[RPT], vr[RPT];
   const bool colok = c0 < h;  // h % 4 == 0 (checked by the host), so all four or none
-  float* __restrict__ br_ = sr + static_cast<int64_t>(b) * hh;
-  float* __restrict__ bi_ = si + static_cast<int64_t>(b) * hh;
+  const ItemPtrs ip = item_ptrs(map, sr, si, b, hh);
   const IO* __restrict__ kb = k + tb;
   const IO* __restrict__ vb = v + tb;
   const int off0 = rg * h + c0;
 #pragma unroll
   for (int m = 0; m < RPT; ++m) {
     const int r = rg + NRG * m;
-    if constexpr (EXACT) {
-      xr[m] = *reinterpret_cast<const float4*>(br_ + off0 + m * NRG * h);
-      xi[m] = *reinterpret_cast<const float4*>(bi_ + off0 + m * NRG * h);
+    if (Map::kSlotted && ip.identity) {  // uniform over the workgroup
+      xr[m] = (EXACT || (colok && r < h)) ? eye4(r, c0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      xi[m] = make_float4(0.f, 0.f, 0.f, 0.f);
+      kr[m] = (EXACT || r < h) ? io<IO>::load(kb, r) : 0.f;
+      vr[m] = (EXACT || r < h) ? io<IO>::load(vb, r) : 0.f;
+    } else if constexpr (EXACT) {
+      xr[m] = *reinterpret_cast<const float4*>(ip.in_r + off0 + m * NRG * h);
+      xi[m] = *reinterpret_cast<const float4*>(ip.in_i + off0 + m * NRG * h);
       kr[m] = io<IO>::load(kb, r);
       vr[m] = io<IO>::load(vb, r);
     } else {
@@ -88,8 +137,8 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
       kr[m] = vr[m] = 0.f;
       if (r < h) {
         if (colok) {
-          xr[m] = *reinterpret_cast<const float4*>(br_ + off0 + m * NRG * h);
-          xi[m] = *reinterpret_cast<const float4*>(bi_ + off0 + m * NRG * h);
+          xr[m] = *reinterpret_cast<const float4*>(ip.in_r + off0 + m * NRG * h);
+          xi[m] = *reinterpret_cast<const float4*>(ip.in_i + off0 + m * NRG * h);
         }
         kr[m] = io<IO>::load(kb, r);
         vr[m] = io<IO>::load(vb, r);
@@ -199,8 +248,8 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
     yi.z = fmaf(kr[m], ci[2], fmaf(vr[m], di[2], yi.z));
     yi.w = fmaf(kr[m], ci[3], fmaf(vr[m], di[3], yi.w));
     if (EXACT || (colok && r < h)) {
-      *reinterpret_cast<float4*>(br_ + off0 + m * NRG * h) = yr;
-      *reinterpret_cast<float4*>(bi_ + off0 + m * NRG * h) = yi;
+      *reinterpret_cast<float4*>(ip.out_r + off0 + m * NRG * h) = yr;
+      *reinterpret_cast<float4*>(ip.out_i + off0 + m * NRG * h) = yi;
     }
     po[m] = fmaf(yr.x, qc.x, fmaf(yr.y, qc.y, fmaf(yr.z, qc.z, yr.w * qc.w)));
   }
@@ -224,11 +273,11 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
 // 16 rows of both parts (128 floats) do not fit in registers beside the rest, so rows
 // rg + 64 m for m >= 8 pass through LDS (128 KiB per workgroup): loaded into registers,
 // summed into the column partials, parked in LDS, and read back for the update.
-template <typename IO, typename GT>
+template <typename IO, typename GT, typename Map>
 __global__ __launch_bounds__(512) void cham_step1024_kernel(
     const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
     const GT* __restrict__ gamma, float* hr0, float* hi0, float* hr1, float* hi1,
-    float* __restrict__ part, int nstates) {
+    float* __restrict__ part, int nstates, const Map map) {
   constexpr int NT = 512, H = 1024, CB = 32, CGN = 8, NRG = 64, RPT = 16, RR = 8;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cg = tid & (CGN - 1), rg = tid / CGN;
@@ -236,8 +285,12 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
   const int nblk = gridDim.x;
   const int c0 = blk * CB + 4 * cg;
   const bool readout = z == nstates - 1;
-  float* __restrict__ sr = (z == 0 ? hr0 : hr1) + static_cast<int64_t>(b) * H * H;
-  float* __restrict__ si = (z == 0 ? hi0 : hi1) + static_cast<int64_t>(b) * H * H;
+  const ItemPtrs ip = item_ptrs(map, z == 0 ? hr0 : hr1, z == 0 ? hi0 : hi1, b,
+                                static_cast<int64_t>(H) * H);
+  const float* __restrict__ sr = ip.in_r;
+  const float* __restrict__ si = ip.in_i;
+  float* __restrict__ wr = ip.out_r;
+  float* __restrict__ wi = ip.out_i;
   const IO* __restrict__ kb = k + static_cast<int64_t>(b) * H;
   const IO* __restrict__ vb = v + static_cast<int64_t>(b) * H;
   const int off0 = rg * H + c0;
@@ -250,8 +303,13 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
   float kr[RPT], vr[RPT];
 #pragma unroll
   for (int m = 0; m < RR; ++m) {
-    xr[m] = *reinterpret_cast<const float4*>(sr + off0 + m * NRG * H);
-    xi[m] = *reinterpret_cast<const float4*>(si + off0 + m * NRG * H);
+    if (Map::kSlotted && ip.identity) {
+      xr[m] = eye4(rg + NRG * m, c0);
+      xi[m] = make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+      xr[m] = *reinterpret_cast<const float4*>(sr + off0 + m * NRG * H);
+      xi[m] = *reinterpret_cast<const float4*>(si + off0 + m * NRG * H);
+    }
   }
 #pragma unroll
   for (int m = 0; m < RPT; ++m) {
@@ -281,8 +339,13 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
     float4 tr[RPT - RR], ti[RPT - RR];
 #pragma unroll
     for (int m = RR; m < RPT; ++m) {
-      tr[m - RR] = *reinterpret_cast<const float4*>(sr + off0 + m * NRG * H);
-      ti[m - RR] = *reinterpret_cast<const float4*>(si + off0 + m * NRG * H);
+      if (Map::kSlotted && ip.identity) {
+        tr[m - RR] = eye4(rg + NRG * m, c0);
+        ti[m - RR] = make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        tr[m - RR] = *reinterpret_cast<const float4*>(sr + off0 + m * NRG * H);
+        ti[m - RR] = *reinterpret_cast<const float4*>(si + off0 + m * NRG * H);
+      }
     }
 #pragma unroll
     for (int m = 0; m < RR; ++m) acc(kr[m], vr[m], xr[m], xi[m]);
@@ -369,8 +432,8 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
     yi.y = fmaf(kr[m], ci[1], fmaf(vr[m], di[1], yi.y));
     yi.z = fmaf(kr[m], ci[2], fmaf(vr[m], di[2], yi.z));
     yi.w = fmaf(kr[m], ci[3], fmaf(vr[m], di[3], yi.w));
-    *reinterpret_cast<float4*>(sr + off0 + m * NRG * H) = yr;
-    *reinterpret_cast<float4*>(si + off0 + m * NRG * H) = yi;
+    *reinterpret_cast<float4*>(wr + off0 + m * NRG * H) = yr;
+    *reinterpret_cast<float4*>(wi + off0 + m * NRG * H) = yi;
     if (readout) {  // this row's readout partial, summed over the 8 column groups
       float po = fmaf(yr.x, qc.x, fmaf(yr.y, qc.y, fmaf(yr.z, qc.z, yr.w * qc.w)));
 #pragma unroll
@@ -400,10 +463,10 @@ __global__ __launch_bounds__(256) void cham_step_finish_kernel(const float* __re
   io<IO>::store(out, static_cast<int64_t>(b) * h + i, s);
 }
 
-template <typename IO, typename GT>
+template <typename IO, typename GT, typename Map>
 hipError_t launch_t(const void* q, const void* k, const void* v, const void* gamma, float* hr,
                     float* hi, float* rr, float* ri, void* out, int B, int h, float* part,
-                    hipStream_t stream) {
+                    const Map& map, hipStream_t stream) {
   // h = 1024: the LDS-holding kernel with 32-column blocks; other h above 512: 16-column
   // blocks of 512 threads, 8 rows each (32 columns would need 16 rows per thread and spill)
   const int cb = (h > 512 && h != 1024) ? 16 : 32;
@@ -415,8 +478,8 @@ hipError_t launch_t(const void* q, const void* k, const void* v, const void* gam
   const IO* vq = static_cast<const IO*>(v);
   const GT* gg = static_cast<const GT*>(gamma);
 #define VMI_CS(CB_, RPT_, EX_) \
-  hipLaunchKernelGGL((cham_step_kernel<IO, GT, 512, CB_, RPT_, EX_>), grid, dim3(512), 0, stream, \
-                     qq, kq, vq, gg, hr, hi, rr, ri, part, h, nstates)
+  hipLaunchKernelGGL((cham_step_kernel<IO, GT, 512, CB_, RPT_, EX_, Map>), grid, dim3(512), 0, \
+                     stream, qq, kq, vq, gg, hr, hi, rr, ri, part, h, nstates, map)
   if (h == 128) VMI_CS(32, 2, true);
   else if (h < 128) VMI_CS(32, 2, false);
   else if (h == 256) VMI_CS(32, 4, true);
@@ -424,8 +487,8 @@ hipError_t launch_t(const void* q, const void* k, const void* v, const void* gam
   else if (h == 512) VMI_CS(32, 8, true);
   else if (h < 512) VMI_CS(32, 8, false);
   else if (h == 1024)
-    hipLaunchKernelGGL((cham_step1024_kernel<IO, GT>), grid, dim3(512), 0, stream, qq, kq, vq, gg,
-                       hr, hi, rr, ri, part, nstates);
+    hipLaunchKernelGGL((cham_step1024_kernel<IO, GT, Map>), grid, dim3(512), 0, stream, qq, kq, vq,
+                       gg, hr, hi, rr, ri, part, nstates, map);
   else VMI_CS(16, 8, false);
 #undef VMI_CS
   hipError_t e = hipGetLastError();
@@ -441,21 +504,46 @@ size_t cham_step_workspace_bytes(int64_t B, int64_t h) {
   return static_cast<size_t>(B) * ((h + chams::CB_MIN - 1) / chams::CB_MIN) * h * sizeof(float);
 }
 
-hipError_t launch_cham_step(const void* q, const void* k, const void* v, const void* gamma,
-                            int io_dtype, int gamma_dtype, float* hr, float* hi, float* rr,
-                            float* ri, void* out, int B, int h, void* workspace,
-                            hipStream_t stream) {
+template <typename Map>
+hipError_t launch_cham_step_map(const void* q, const void* k, const void* v, const void* gamma,
+                                int io_dtype, int gamma_dtype, float* hr, float* hi, float* rr,
+                                float* ri, void* out, int B, int h, void* workspace, const Map& map,
+                                hipStream_t stream) {
   float* part = static_cast<float*>(workspace);
 #define VMI_GT(IO_)                                                                              \
   if (gamma_dtype == VMI_F32)                                                                  \
-    return chams::launch_t<IO_, float>(q, k, v, gamma, hr, hi, rr, ri, out, B, h, part, stream); \
+    return chams::launch_t<IO_, float, Map>(q, k, v, gamma, hr, hi, rr, ri, out, B, h, part, map, \
+                                            stream);                                           \
   if (gamma_dtype == VMI_BF16)                                                                 \
-    return chams::launch_t<IO_, bf16_t>(q, k, v, gamma, hr, hi, rr, ri, out, B, h, part, stream); \
-  return chams::launch_t<IO_, f16_t>(q, k, v, gamma, hr, hi, rr, ri, out, B, h, part, stream);
+    return chams::launch_t<IO_, bf16_t, Map>(q, k, v, gamma, hr, hi, rr, ri, out, B, h, part, map, \
+                                             stream);                                          \
+  return chams::launch_t<IO_, f16_t, Map>(q, k, v, gamma, hr, hi, rr, ri, out, B, h, part, map,   \
+                                          stream);
   if (io_dtype == VMI_F32) { VMI_GT(float) }
   if (io_dtype == VMI_BF16) { VMI_GT(bf16_t) }
   VMI_GT(f16_t)
 #undef VMI_GT
+}
+
+hipError_t launch_cham_step(const void* q, const void* k, const void* v, const void* gamma,
+                            int io_dtype, int gamma_dtype, float* hr, float* hi, float* rr,
+                            float* ri, void* out, int B, int h, void* workspace,
+                            hipStream_t stream) {
+  return launch_cham_step_map(q, k, v, gamma, io_dtype, gamma_dtype, hr, hi, rr, ri, out, B, h,
+                              workspace, chams::DenseItems{}, stream);
+}
+
+hipError_t launch_cham_step_slots(const void* q, const void* k, const void* v, const void* gamma,
+                                  int io_dtype, int gamma_dtype, float* pool, const int32_t* in_slot,
+                                  const int32_t* out_slot, void* out, int B, int h, void* workspace,
+                                  hipStream_t stream) {
+  chams::SlotItems map;
+  for (int i = 0; i < B; ++i) {
+    map.in_slot[i] = in_slot[i];
+    map.out_slot[i] = out_slot[i];
+  }
+  return launch_cham_step_map(q, k, v, gamma, io_dtype, gamma_dtype, pool, pool, nullptr, nullptr,
+                              out, B, h, workspace, map, stream);
 }
 
 }  // namespace vmi

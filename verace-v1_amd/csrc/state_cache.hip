@@ -38,6 +38,14 @@ struct vmi_state_cache {
   // scratch of the last plan (host)
   std::vector<int32_t> src, dst;
   std::vector<char> inplace;
+  // the CHAM half of each layer's state (vmi_state_cache_attach_hologram): pool
+  // [L, N, 2, h, h] fp32, slot s of layer l at holo + (l N + s) 2 h^2; the hologram of a
+  // handle lives in the same slot as its SSSD state, and a layer's CHAM step applies the
+  // slot decisions of that layer's last SSSD step (same handles, same order)
+  int64_t h = 0;
+  float* holo = nullptr;
+  std::vector<std::vector<int64_t>> last_handles;  // per layer
+  std::vector<std::vector<int32_t>> last_src, last_dst;
 };
 
 namespace {
@@ -130,6 +138,9 @@ int vmi_state_cache_create(int64_t num_layers, int64_t num_slots, int64_t H, int
   c->D = D;
   c->pool = pool;
   c->refs.assign(num_layers * num_slots, 0);
+  c->last_handles.resize(num_layers);
+  c->last_src.resize(num_layers);
+  c->last_dst.resize(num_layers);
   c->free.resize(num_layers);
   for (auto& f : c->free)
     for (int64_t s = num_slots - 1; s >= 0; --s) f.push_back(static_cast<int32_t>(s));
@@ -215,6 +226,9 @@ int vmi_state_cache_step(vmi_state_cache* c, int64_t layer, const int64_t* handl
   if (n * c->H > INT32_MAX) return VMI_ERR_INVALID_ARG;
   const int st = plan(c, layer, handles, n);
   if (st != VMI_OK) return st;
+  c->last_handles[layer].assign(handles, handles + n);
+  c->last_src[layer] = c->src;
+  c->last_dst[layer] = c->dst;
   const int64_t H = c->H, D = c->D;
   const size_t io_bytes = io_dtype == VMI_F32 ? 4 : 2;
   const size_t d_bytes = delta_dtype == VMI_F32 ? 4 : 2;
@@ -242,6 +256,59 @@ int vmi_state_cache_step(vmi_state_cache* c, int64_t layer, const int64_t* handl
     else
       e = vmi::launch_sssd_seq(qb, kb, vb, db, io_dtype, delta_dtype, pool, ob, pool, nb, 1,
                                static_cast<int>(H), static_cast<int>(D), s, map);
+    if (e != hipSuccess) return vmi::hip_status(e);
+  }
+  return VMI_OK;
+}
+
+int vmi_state_cache_attach_hologram(vmi_state_cache* c, int64_t h, float* holo_pool) {
+  if (c == nullptr || h < 1 || holo_pool == nullptr) return VMI_ERR_INVALID_ARG;
+  if (h > 1024 || h % 4 != 0) return VMI_ERR_UNSUPPORTED;
+  c->h = h;
+  c->holo = holo_pool;
+  return VMI_OK;
+}
+
+int vmi_state_cache_cham_workspace_bytes(int64_t n, int64_t h, size_t* bytes) {
+  if (bytes == nullptr || n < 0 || h < 1) return VMI_ERR_INVALID_ARG;
+  const int64_t nb = n < vmi::kMaxSlotArgs ? n : vmi::kMaxSlotArgs;
+  *bytes = vmi::cham_step_workspace_bytes(nb, h);
+  return VMI_OK;
+}
+
+int vmi_state_cache_cham_step(vmi_state_cache* c, int64_t layer, const int64_t* handles,
+                              int64_t n, const void* q, const void* k, const void* v,
+                              const void* gamma, int io_dtype, int gamma_dtype, void* out,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  if (c == nullptr || c->holo == nullptr || layer < 0 || layer >= c->L || n < 0)
+    return VMI_ERR_INVALID_ARG;
+  if (io_dtype != VMI_F32 && io_dtype != VMI_BF16 && io_dtype != VMI_F16) return VMI_ERR_INVALID_ARG;
+  if (gamma_dtype != VMI_F32 && gamma_dtype != VMI_BF16 && gamma_dtype != VMI_F16)
+    return VMI_ERR_INVALID_ARG;
+  // the same handles, in the same order, as this layer's last SSSD step
+  const auto& lh = c->last_handles[layer];
+  if (static_cast<int64_t>(lh.size()) != n) return VMI_ERR_INVALID_ARG;
+  for (int64_t b = 0; b < n; ++b)
+    if (handles == nullptr || lh[b] != handles[b]) return VMI_ERR_INVALID_ARG;
+  if (n == 0) return VMI_OK;
+  if (q == nullptr || k == nullptr || v == nullptr || gamma == nullptr || out == nullptr)
+    return VMI_ERR_INVALID_ARG;
+  size_t need = 0;
+  vmi_state_cache_cham_workspace_bytes(n, c->h, &need);
+  if (workspace == nullptr || workspace_bytes < need) return VMI_ERR_WORKSPACE;
+  const int64_t h = c->h;
+  const size_t io_bytes = io_dtype == VMI_F32 ? 4 : 2;
+  const size_t g_bytes = gamma_dtype == VMI_F32 ? 4 : 2;
+  float* pool = c->holo + layer * c->N * 2 * h * h;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int64_t b0 = 0; b0 < n; b0 += vmi::kMaxSlotArgs) {
+    const int nb = static_cast<int>(n - b0 < vmi::kMaxSlotArgs ? n - b0 : vmi::kMaxSlotArgs);
+    const size_t tok = static_cast<size_t>(b0) * h * io_bytes;
+    const hipError_t e = vmi::launch_cham_step_slots(
+        static_cast<const char*>(q) + tok, static_cast<const char*>(k) + tok,
+        static_cast<const char*>(v) + tok, static_cast<const char*>(gamma) + b0 * g_bytes, io_dtype,
+        gamma_dtype, pool, c->last_src[layer].data() + b0, c->last_dst[layer].data() + b0,
+        static_cast<char*>(out) + tok, nb, static_cast<int>(h), workspace, s);
     if (e != hipSuccess) return vmi::hip_status(e);
   }
   return VMI_OK;

@@ -128,6 +128,15 @@ hipError_t launch_cham_step(const void* q, const void* k, const void* v, const v
                             float* ri, void* out, int B, int h, void* workspace,
                             hipStream_t stream);
 
+// The same over the hologram pool of a decode state cache ([N, 2, h, h] per layer: slot s's
+// real plane at pool + 2 s h^2, imaginary plane after it), in_slot / out_slot host arrays of
+// B <= kMaxSlotArgs items (-1 in: the identity); no readout state (every cached hologram
+// started from the identity, so NS_3(H) = H).
+hipError_t launch_cham_step_slots(const void* q, const void* k, const void* v, const void* gamma,
+                                  int io_dtype, int gamma_dtype, float* pool, const int32_t* in_slot,
+                                  const int32_t* out_slot, void* out, int B, int h, void* workspace,
+                                  hipStream_t stream);
+
 // cham_wide.hip: the same scan for 128 < h <= kChamMaxDim.
 size_t cham_wide_workspace_bytes(int64_t B, int64_t T, int64_t h);
 hipError_t launch_cham_wide(const void* q, const void* k, const void* v, const void* gamma,

@@ -37,6 +37,9 @@ EXPORTED = (
     "vmi_state_cache_slots",
     "vmi_state_cache_refs",
     "vmi_state_cache_step",
+    "vmi_state_cache_attach_hologram",
+    "vmi_state_cache_cham_workspace_bytes",
+    "vmi_state_cache_cham_step",
     "vmi_cham_scan_workspace_bytes",
     "vmi_cham_scan_fwd",
     "vmi_sssd_scan_bwd_workspace_bytes",
@@ -95,7 +98,12 @@ def _declare(lib):
     lib.vmi_state_cache_slots.argtypes = [vp, i64, pi64, i64, pi32]
     lib.vmi_state_cache_refs.argtypes = [vp, i64, pi32, pi64]
     lib.vmi_state_cache_step.argtypes = [vp, i64, pi64, i64, vp, vp, vp, vp, i32, i32, vp, vp]
-    for name in ("create", "destroy", "new", "fork", "release", "plan", "slots", "refs", "step"):
+    lib.vmi_state_cache_attach_hologram.argtypes = [vp, i64, vp]
+    lib.vmi_state_cache_cham_workspace_bytes.argtypes = [i64, i64, ctypes.POINTER(sz)]
+    lib.vmi_state_cache_cham_step.argtypes = [vp, i64, pi64, i64, vp, vp, vp, vp, i32, i32, vp, vp,
+                                              sz, vp]
+    for name in ("create", "destroy", "new", "fork", "release", "plan", "slots", "refs", "step",
+                 "attach_hologram", "cham_workspace_bytes", "cham_step"):
         getattr(lib, "vmi_state_cache_" + name).restype = i32
     lib.vmi_cham_scan_workspace_bytes.argtypes = [i64, i64, i64, ctypes.POINTER(sz)]
     lib.vmi_cham_scan_workspace_bytes.restype = i32

@@ -134,13 +134,20 @@ class SlotTable:
 class SSSDStateCache:
     """``[num_layers, num_slots, H, D, D]`` fp32 states on one device, addressed by handles.
 
+    With ``hologram_dim`` the cache also holds each handle's CHAM hologram (the second half
+    of the reference's ``(sssd_state, cham_hologram)`` tuple) in ``holograms``
+    ``[num_layers, num_slots, 2, h, h]`` (real plane, imaginary plane) under the same slot as
+    its SSSD state: :meth:`cham_step` steps them in place after :meth:`step` of the same layer
+    and handles.  Cached holograms are taken to have started from the identity (unitary, so
+    their Newton-Schulz readout is the hologram itself).
+
     All launches go to the current stream of ``device``; the steps of one cache must stay
     on one stream.  D = 128 runs the persistent decode-step kernel, other D up to 256 the
     token-sequential kernel.
     """
 
     def __init__(self, num_layers: int, num_slots: int, num_heads: int, head_dim: int,
-                 device: Optional[torch.device] = None):
+                 device: Optional[torch.device] = None, hologram_dim: Optional[int] = None):
         device = torch.device(device if device is not None else "cuda")
         if device.type != "cuda":
             raise RuntimeError("verace_amd: the state cache lives on a HIP device")
@@ -151,6 +158,14 @@ class SSSDStateCache:
                                   dtype=torch.float32, device=device)
         self.table = SlotTable(num_layers, num_slots, num_heads, head_dim,
                                self.states.data_ptr())
+        self.hologram_dim = hologram_dim
+        self.holograms = None
+        if hologram_dim is not None:
+            self.holograms = torch.zeros(num_layers, num_slots, 2, hologram_dim, hologram_dim,
+                                         dtype=torch.float32, device=device)
+            _check(self.table._lib.vmi_state_cache_attach_hologram(
+                self.table._h, hologram_dim, ctypes.c_void_p(self.holograms.data_ptr())),
+                "vmi_state_cache_attach_hologram")
 
     # -- handles (host only) -------------------------------------------------------
     def new(self, n: int = 1) -> List[int]:
@@ -189,13 +204,73 @@ class SSSDStateCache:
             "vmi_state_cache_step")
         return out
 
-    def write(self, layer: int, handles: Sequence[int], states: torch.Tensor) -> None:
-        """Store whole states [B, H, D, D] (e.g. the final states of a prefill scan)."""
+    def cham_step(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                  gamma: torch.Tensor, handles) -> torch.Tensor:
+        """The in-place CHAM decode step of ``layer`` for the same ``handles`` (same order) as
+        the preceding :meth:`step` of that layer: each hologram moves with its SSSD state's
+        slot (copy-on-write included).  q, k, v: [B, 1, h] or [B, h]; gamma: [B] or [B, 1].
+        Returns Re(NS_3(H') q) [B, 1, h] in q's dtype."""
+        if self.holograms is None:
+            raise RuntimeError("verace_amd: this cache holds no holograms (hologram_dim=None)")
+        h = self.hologram_dim
+        hs = handles if isinstance(handles, np.ndarray) and handles.dtype == np.int64 \
+            else _handles(handles)
+        B = len(hs)
+        q_c = q.reshape(B, 1, h).contiguous()
+        k_c = k.reshape(B, 1, h).to(q.dtype).contiguous()
+        v_c = v.reshape(B, 1, h).to(q.dtype).contiguous()
+        g_c = gamma.reshape(B).contiguous()
+        out = torch.empty_like(q_c)
+        lib = self.table._lib
+        ws_bytes = ctypes.c_size_t(0)
+        _check(lib.vmi_state_cache_cham_workspace_bytes(B, h, ctypes.byref(ws_bytes)),
+               "vmi_state_cache_cham_workspace_bytes")
+        ws = torch.empty(max(ws_bytes.value, 1), device=self.device, dtype=torch.uint8)
+        P = ctypes.c_void_p
+        _check(lib.vmi_state_cache_cham_step(
+            self.table._h, layer, hs.ctypes.data_as(_I64P), B, P(q_c.data_ptr()), P(k_c.data_ptr()),
+            P(v_c.data_ptr()), P(g_c.data_ptr()), _lib.dtype_code(q_c.dtype),
+            _lib.dtype_code(g_c.dtype), P(out.data_ptr()), P(ws.data_ptr()), ws_bytes.value,
+            _lib.stream_handle(self.device)), "vmi_state_cache_cham_step")
+        return out
+
+    def write(self, layer: int, handles: Sequence[int], states: torch.Tensor,
+              holograms: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> None:
+        """Store whole states [B, H, D, D] (e.g. the final states of a prefill scan) and, for
+        a cache with holograms, the raw holograms (H_real, H_imag) [B, h, h] (identity where
+        not given)."""
         dst = self.table.plan_write(layer, handles)
         if len(dst):
             idx = torch.from_numpy(dst.astype(np.int64)).to(self.device)
             self.states[layer].index_copy_(0, idx, states.to(torch.float32).reshape(
                 len(dst), self.num_heads, self.head_dim, self.head_dim))
+            if self.holograms is not None:
+                h = self.hologram_dim
+                if holograms is None:
+                    hr = torch.eye(h, device=self.device).expand(len(dst), h, h)
+                    hi = torch.zeros(len(dst), h, h, device=self.device)
+                else:
+                    hr, hi = holograms
+                pair = torch.stack([hr.to(torch.float32).reshape(len(dst), h, h),
+                                    hi.to(torch.float32).reshape(len(dst), h, h)], 1)
+                self.holograms[layer].index_copy_(0, idx, pair)
+
+    def read_holograms(self, layer: int, handles: Sequence[int]):
+        """(H_real, H_imag) [B, h, h] of ``handles`` at ``layer`` (identity where never written)."""
+        if self.holograms is None:
+            raise RuntimeError("verace_amd: this cache holds no holograms (hologram_dim=None)")
+        slots = self.table.slots(layer, handles).astype(np.int64)
+        h = self.hologram_dim
+        hr = torch.eye(h, dtype=torch.float32, device=self.device).expand(len(slots), h, h).contiguous()
+        hi = torch.zeros(len(slots), h, h, dtype=torch.float32, device=self.device)
+        have = np.nonzero(slots >= 0)[0]
+        if len(have):
+            src = torch.from_numpy(slots[have]).to(self.device)
+            dst = torch.from_numpy(have).to(self.device)
+            sel = self.holograms[layer].index_select(0, src)
+            hr[dst] = sel[:, 0]
+            hi[dst] = sel[:, 1]
+        return hr, hi
 
     def read(self, layer: int, handles: Sequence[int]) -> torch.Tensor:
         """States [B, H, D, D] of ``handles`` at ``layer`` (identity where never written)."""
