@@ -655,6 +655,9 @@ def bench_model_decode(device, model):
         l0 = model.layers[0]
         s0 = st.layers[0].sssd.clone()
         n_pre = [x.sssd.reshape(B, 8, -1).norm(dim=-1).clone() for x in st.layers]
+        from verace_amd import DecodeGraph, DecodeState, LayerDecodeState
+        st_g = DecodeState([LayerDecodeState(x.sssd.clone(), (x.cham[0].clone(), x.cham[1].clone()), None)
+                            for x in st.layers])
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(S)]
         for i in range(S):
             evs[i][0].record(stream)
@@ -662,6 +665,18 @@ def bench_model_decode(device, model):
             evs[i][1].record(stream)
         torch.cuda.synchronize()
         per = [x.elapsed_time(y) for x, y in evs]
+        # the same 256 steps replayed from one captured HIP graph (DecodeGraph), from a copy
+        # of the prefill states: its final states must equal the eager loop's
+        graph = DecodeGraph(model, st_g, B)
+        for i in range(S):
+            evs[i][0].record(stream)
+            graph.step(steps_ids[i])
+            evs[i][1].record(stream)
+        torch.cuda.synchronize()
+        per_g = [x.elapsed_time(y) for x, y in evs]
+        graph_dev = max(float(((a.sssd - b.sssd).abs().max())) for a, b in zip(st_g.layers, st.layers))
+        graph_dev = max(graph_dev, max(float((a.cham[0] - b.cham[0]).abs().max()) for a, b in zip(st_g.layers, st.layers)))
+        del graph, st_g
         # layer 0's SSSD inputs of every step (its input is the embedding: recomputed here)
         q, k, v, dl = l0.sssd_attn.project(l0.sssd_norm(model.embed_tokens(steps_ids[:, :, 0].t())))
         # the same sub-layer steps in isolation: one SSSD / CHAM step launch per layer
@@ -706,12 +721,15 @@ def bench_model_decode(device, model):
         "step_ms_median": round(statistics.median(per), 3),
         "step_ms_p90": round(per_s[int(0.9 * (S - 1))], 3),
         "tokens_per_s": round(B / (statistics.median(per) * 1e-3), 1),
+        "graph_step_ms_median": round(statistics.median(per_g), 3),
+        "graph_step_ms_p90": round(sorted(per_g)[int(0.9 * (S - 1))], 3),
+        "graph_tokens_per_s": round(B / (statistics.median(per_g) * 1e-3), 1),
         "sssd_step_us_per_layer": round(1e3 * statistics.median(t_s), 2),
         "cham_step_us_per_layer": round(1e3 * ms_c, 2),
         "cham_step_hbm_frac": round(cham_bytes / (ms_c * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "parity": {"layer0_sssd_state_rel_vs_fp64": worst, "sssd_state_norm_drift": drift,
-                   "layer0_cham_unitarity_err": unit,
-                   "pass": bool(worst <= 2e-2 and drift <= 1e-4 and unit <= 1e-3)},
+                   "layer0_cham_unitarity_err": unit, "graph_vs_eager_state_maxdiff": graph_dev,
+                   "pass": bool(worst <= 2e-2 and drift <= 1e-4 and unit <= 1e-3 and graph_dev <= 1e-5)},
     }
 
 

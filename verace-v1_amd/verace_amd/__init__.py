@@ -40,8 +40,8 @@ from . import ops  # noqa: F401  (torch.ops.verace.*: the launchers as traceable
 from .sssd_attention import SSSDAttention
 from .cham_memory import ContinuousHolographicMemory
 from .mcmoe import ManifoldContinuousMoE, SiTUGLU
-from .backbone import (AdaptiveCognitiveDepthEngine, DecodeState, LayerDecodeState, VeraceV1Config,
-                       VeraceV1Layer, VeraceV1Model)
+from .backbone import (AdaptiveCognitiveDepthEngine, DecodeGraph, DecodeState, LayerDecodeState,
+                       VeraceV1Config, VeraceV1Layer, VeraceV1Model)
 from .state_cache import SlotTable, SSSDStateCache
 
 __all__ = [
@@ -62,6 +62,7 @@ __all__ = [
     "SiTUGLU",
     "AdaptiveCognitiveDepthEngine",
     "DecodeState",
+    "DecodeGraph",
     "LayerDecodeState",
     "VeraceV1Config",
     "VeraceV1Layer",

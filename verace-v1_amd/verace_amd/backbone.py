@@ -130,9 +130,12 @@ class AdaptiveCognitiveDepthEngine(nn.Module):
         return torch.sigmoid(self.w_halting(h_l)).squeeze(-1)
 
     def run(self, layers, h_in: torch.Tensor, max_depth: int, min_depth: int,
-            initial_layer_states=None, step_states: Optional["DecodeState"] = None):
+            initial_layer_states=None, step_states: Optional["DecodeState"] = None,
+            static_control: bool = False):
         """acd_engine.py:36-167 on the whole batch (see the module docstring).  With
         ``step_states`` (T = 1) the layers take their in-place step instead of the forward.
+        ``static_control`` takes no decision from device values (every layer runs, always with
+        the active mask; the results are the same), so the loop can be captured in a HIP graph.
         Returns (final_h, depth_counts, layer_states as per-layer lists of per-item tuples,
         or None with step_states)."""
         b, s, d = h_in.shape
@@ -148,11 +151,11 @@ class AdaptiveCognitiveDepthEngine(nn.Module):
                            and l < len(initial_layer_states) and initial_layer_states[l] is not None
                            else [None] * b) for l in range(n_layers)]
         for l_idx in range(n_layers):
-            if not bool(active.any()):
+            if not static_control and not bool(active.any()):
                 break
             layer = layers[l_idx]
             item_on = active.any(dim=1)                              # items with work here
-            mask = None if bool(active.all()) else active
+            mask = active if static_control or not bool(active.all()) else None
             if step_states is not None:
                 out = layer.step_(h_curr, step_states.layers[l_idx], mask)
             else:
@@ -177,7 +180,7 @@ class AdaptiveCognitiveDepthEngine(nn.Module):
             acc = new_acc
             active = still
             h_curr = h_next
-        if bool(active.any()):
+        if static_control or bool(active.any()):
             rem = (1.0 - acc).clamp(min=0.0)
             final_h = final_h + (rem * active.to(h_in.dtype)).unsqueeze(-1) * h_curr
             depth = depth + rem * active.to(h_in.dtype)
@@ -324,7 +327,8 @@ class VeraceV1Model(nn.Module):
                     st.layers.append(self._fresh_layer_state(layer, b, x.device))
         return self.lm_head(self.final_norm(final_h)), st
 
-    def decode_step(self, next_ids: torch.Tensor, state: DecodeState, static_depth: bool = False):
+    def decode_step(self, next_ids: torch.Tensor, state: DecodeState, static_depth: bool = False,
+                    static_control: bool = False):
         """One token per item (next_ids [B, 1]); the states are updated in place.  The same
         function as ``forward(next_ids, layer_states=...)`` (ACDE) or the static loop."""
         x = self.embed_tokens(next_ids)
@@ -335,5 +339,42 @@ class VeraceV1Model(nn.Module):
             final_h = h
         else:
             final_h, _, _ = self.acd_engine.run(self.layers, x, self.config.max_cognitive_depth,
-                                                self.config.min_cognitive_depth, step_states=state)
+                                                self.config.min_cognitive_depth, step_states=state,
+                                                static_control=static_control)
         return self.lm_head(self.final_norm(final_h))
+
+
+class DecodeGraph:
+    """``decode_step`` captured once in a HIP graph (torch.cuda.CUDAGraph) and replayed per
+    token: the ~40 small launches per layer of a batch-64 decode step (projections, norms,
+    M-CMoE, halting) are otherwise bound by host launch cost.  The graph reads the next token
+    ids from :attr:`ids` and writes the logits into :attr:`logits`; the states of ``state`` are
+    updated in place by every replay.  Warm-up runs (needed before capture) use a copy of the
+    states, so ``state`` is not advanced by the construction."""
+
+    def __init__(self, model: VeraceV1Model, state: DecodeState, batch: int,
+                 static_depth: bool = False, warmup: int = 2):
+        dev = state.layers[0].sssd.device
+        self.ids = torch.zeros(batch, 1, dtype=torch.long, device=dev)
+        scratch = DecodeState([LayerDecodeState(
+            l.sssd.clone(), (l.cham[0].clone(), l.cham[1].clone()),
+            None if l.cham_readout is None else (l.cham_readout[0].clone(), l.cham_readout[1].clone()))
+            for l in state.layers])
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                model.decode_step(self.ids, scratch, static_depth, static_control=True)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        del scratch
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = model.decode_step(self.ids, state, static_depth, static_control=True)
+
+    def step(self, next_ids: torch.Tensor) -> torch.Tensor:
+        """Advance every item by one token; returns the logits [B, 1, vocab] (the graph's
+        output buffer, overwritten by the next step)."""
+        self.ids.copy_(next_ids)
+        self.graph.replay()
+        return self.logits
