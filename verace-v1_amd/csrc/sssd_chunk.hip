@@ -196,11 +196,22 @@ template <typename E>
 __device__ __forceinline__ typename mfma_t<E>::v8 lds8(const E* p) {
   return *reinterpret_cast<const typename mfma_t<E>::v8*>(p);
 }
+// Two 8-byte reads issued as two ds_read_b64.  Plain loads would be fused by the compiler
+// into ds_read2_b64, which gfx950 serves far slower for these operand patterns (measured with
+// SQ_LDS_IDX_ACTIVE / SQ_LDS_BANK_CONFLICT: 16 LDS cycles per read2 of the W operand,
+// half of them bank conflicts, against 2 + 2 for the two single reads); volatile LDS
+// accesses are never fused.
+template <typename E>
+__device__ __forceinline__ typename mfma_t<E>::v4 lds4_single(const E* p) {
+  typedef typename mfma_t<E>::v4 V4;
+  typedef __attribute__((address_space(3))) const volatile V4 lds_v4;
+  return *((lds_v4*)(p));
+}
 template <typename E>
 __device__ __forceinline__ typename mfma_t<E>::v8 lds4x2(const E* p0, const E* p1) {
   typedef typename mfma_t<E>::v4 V4;
   typedef typename mfma_t<E>::v8 V8;
-  return cat8<V4, V8>(lds4<E>(p0), lds4<E>(p1));
+  return cat8<V4, V8>(lds4_single<E>(p0), lds4_single<E>(p1));
 }
 
 // Transposing LDS read (ds_read_b64_tr_b16).  Within each 16-lane group, lane 4i + r
@@ -376,8 +387,8 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   //   it = n-3  phase 1: Gram matrix (MFMA), Cayley blocks, diagonal blocks of T~
   //   it = n-2  phase 2: off-diagonal blocks of T~ (kept in registers; the 16x16 block on MFMA)
   //   it = n-1  phase 3: k, v, q rows -> tok[n % 3], T~ (hi + lo) -> tt[n & 1]
-  // with 8 the same steps run as load, Gram + Cayley blocks, diagonal blocks, three
-  // off-diagonal steps, an empty phase and the write (it = n-8 .. n-1).
+  // with 8 the same steps run as load, f16 conversion (fused: k, v normalisation), Gram +
+  // Cayley blocks, diagonal blocks, three off-diagonal steps and the write (it = n-8 .. n-1).
   // tok[n % 3] last held chunk n-3, whose readout ended in iteration n-2, and tt[n & 1]
   // last held chunk n-2, so the write overwrites nothing still in use.  The scratch of
   // a chunk is pscr[n & 1] with 4 producers (chunk n+2, the next one to use it, starts
@@ -426,6 +437,10 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   // zero the tokens past the end; fused mode: normalise the k, v rows (to f16)
   auto p_prep = [&](Regs& r, int n, PScratch& P) {
     const int t0 = (chunk0 + n) * C;
+    if constexpr (!FUSED && NPW == 8) {  // the 8-phase schedule converts here, a phase
+#pragma unroll                          // before the Gram matrix
+      for (int ks = 0; ks < 8; ++ks) r.kv[ks] = to_f16x8<IO>(r.kv[ks]);
+    }
     if (t0 + C > a.T) {  // last, partial chunk
       const uint4 z = make_uint4(0, 0, 0, 0);
       if (t0 + (l32 >> 1) >= a.T) {
@@ -466,7 +481,7 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   // factor I + U T~ U^T stays exactly consistent with its Gram matrix; Cayley blocks
   auto p_gram = [&](Regs& r, int n, PScratch& P) {
     const int t0 = (chunk0 + n) * C;
-    if constexpr (!FUSED) {
+    if constexpr (!FUSED && NPW != 8) {
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) r.kv[ks] = to_f16x8<IO>(r.kv[ks]);
     }
@@ -616,9 +631,16 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
         r.q[m] = to_f16x8_scaled<IO>(r.q[m], rsqrtf(fmaxf(s2, 1e-24f)));
       }
     }
+    // Each 16-byte piece as two ds_write_b64: rows are 8-byte aligned (264-byte pitch), and a
+    // ds_write_b128 of this pattern measured 5x the LDS cycles of the two 8-byte writes.
     E* tdst = tb + rho_slot(l32) * U_LD;
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    typedef __attribute__((address_space(3))) volatile u32x2 lds_u2;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) *reinterpret_cast<uint4*>(tdst + 16 * ks + 8 * g) = r.kv[ks];
+    for (int ks = 0; ks < 8; ++ks) {
+      *((lds_u2*)(tdst + 16 * ks + 8 * g)) = u32x2{r.kv[ks].x, r.kv[ks].y};
+      *((lds_u2*)(tdst + 16 * ks + 8 * g + 4)) = u32x2{r.kv[ks].z, r.kv[ks].w};
+    }
     if (READOUT) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
@@ -680,15 +702,7 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
           } else {
             p_write(r, n, tv, cv);
           }
-        } else if constexpr (!FUSED) {
-          if (phase == 0) p_load(r, n);
-          else if (phase == 1) { p_prep(r, n, P); p_gram(r, n, P); }
-          else if (phase == 2) p_diag(P);
-          else if (phase == 3) od_1a(P, tv);
-          else if (phase == 4) od_1b(P, tv);
-          else if (phase == 5) od_c(P, cv);
-          else if (phase == 7) p_write(r, n, tv, cv);
-        } else {  // the k, v normalisation takes the otherwise empty slot
+        } else {  // 8 phases: the f16 conversion (fused: the k, v normalisation) has its own
           if (phase == 0) p_load(r, n);
           else if (phase == 1) p_prep(r, n, P);
           else if (phase == 2) p_gram(r, n, P);
