@@ -419,15 +419,18 @@ def bench_cham(device, iters=5, warmup=2):
             "valu_tflops": round(flops / (us * 1e-6) / 1e12, 2),
             "valu_frac": round(flops / (us * 1e-6) / 78.6e12, 4),
         }
-    # the reference's default holographic_dim (1024): prefill from the identity, and one
-    # decode token for 64 sequences with their held holograms (R_0 = NS_3(H_0) per call)
-    for name, (Bw, Tw, init_w) in (("h1024_identity_B4_T2048", (4, 2048, False)),
-                                   ("h1024_decode_B64_T1", (64, 1, True))):
+    # the reference's default holographic_dim (1024): prefill from the identity (fp32 inputs:
+    # the token-sequential column route; bf16 inputs, as the model's projections give them:
+    # the chunked matrix-core route), and one decode token for 64 sequences with their held
+    # holograms (R_0 = NS_3(H_0) per call)
+    for name, (Bw, Tw, init_w, dt) in (("h1024_identity_B4_T2048", (4, 2048, False, torch.float32)),
+                                       ("h1024_identity_B4_T2048_bf16", (4, 2048, False, torch.bfloat16)),
+                                       ("h1024_decode_B64_T1", (64, 1, True, torch.float32))):
         hw = 1024
-        qw = nrm(torch.randn(Bw, Tw, hw, generator=g), dim=-1).to(device)
-        kw = nrm(torch.randn(Bw, Tw, hw, generator=g), dim=-1).to(device)
-        vw = nrm(torch.randn(Bw, Tw, hw, generator=g), dim=-1).to(device)
-        gw = (0.1 * torch.sigmoid(torch.randn(Bw, Tw, generator=g))).to(device)
+        qw = nrm(torch.randn(Bw, Tw, hw, generator=g), dim=-1).to(dt).to(device)
+        kw = nrm(torch.randn(Bw, Tw, hw, generator=g), dim=-1).to(dt).to(device)
+        vw = nrm(torch.randn(Bw, Tw, hw, generator=g), dim=-1).to(dt).to(device)
+        gw = (0.1 * torch.sigmoid(torch.randn(Bw, Tw, generator=g))).to(dt).to(device)
         iw = None
         if init_w:
             Qw = torch.linalg.qr(torch.complex(torch.randn(Bw, hw, hw), torch.randn(Bw, hw, hw)))[0]

@@ -18,6 +18,8 @@
 //      of chunk n (R_c its start state);
 //   4. wide_apply_kernel: per token, x = z_t, then x <- U_j x for the chunk's tokens
 //      j <= t (x = R_t q_t) and rec_t = Re(x).
+#include <type_traits>
+
 #include "cham_common.h"
 #include "vmi_dispatch.h"
 
@@ -541,20 +543,22 @@ __global__ __launch_bounds__(256) void wide_vec_init_kernel(const IO* __restrict
 int padded(int h) { return h <= 256 ? 256 : (h <= 512 ? 512 : 1024); }
 
 struct WideWs {
-  float *coef, *snap, *Z, *r0r, *r0i, *ns, *vec;
+  float *coef, *snap, *Z, *r0r, *r0i, *ns, *vec, *mm;
   size_t floats;
 };
-// (the short route with an initial hologram uses coef, Z and vec; the long one all but vec)
+// (the short route with an initial hologram uses coef, Z and vec; the long one all but vec;
+// mm: the per-chunk factors of the matrix-core state carry, cham_mfma.hip)
 WideWs carve(void* base, int64_t B, int64_t T, int64_t h) {
   const int64_t HP = padded(static_cast<int>(h));
   const int64_t nch = (T + C2 - 1) / C2;
-  const int64_t sizes[7] = {B * T * NCF, B * nch * 2 * h * HP, B * nch * 2 * C2 * HP,
-                            B * h * h, B * h * h, 6 * B * h * h, 4 * B * MVT * 2 * HP};
+  const int64_t sizes[8] = {B * T * NCF, B * nch * 2 * h * HP, B * nch * 2 * C2 * HP,
+                            B * h * h, B * h * h, 6 * B * h * h, 4 * B * MVT * 2 * HP,
+                            static_cast<int64_t>((cham_mfma_workspace_bytes(B, T, h) + 3) / 4)};
   WideWs w;
   float* p = static_cast<float*>(base);
-  float** dst[7] = {&w.coef, &w.snap, &w.Z, &w.r0r, &w.r0i, &w.ns, &w.vec};
+  float** dst[8] = {&w.coef, &w.snap, &w.Z, &w.r0r, &w.r0i, &w.ns, &w.vec, &w.mm};
   size_t off = 0;
-  for (int i = 0; i < 7; ++i) {
+  for (int i = 0; i < 8; ++i) {
     *dst[i] = p ? p + off : nullptr;
     off += (sizes[i] + 63) / 64 * 64;  // 256-byte aligned pieces
   }
@@ -606,11 +610,19 @@ hipError_t launch_rpl(const void* q, const void* k, const void* v, const float* 
   const int nch = (T + C2 - 1) / C2;
   const bool shortr = h0r && T <= MVT;
   const int nstates = h0r && nch > 0 && !shortr ? 2 : 1;
-  hipLaunchKernelGGL((wide_cols_kernel<IO, LPC, RPL>), dim3(B, (h + CPG - 1) / CPG, nstates),
-                     dim3(CNT), 0, stream, static_cast<const IO*>(k), static_cast<const IO*>(v),
-                     w.coef, h0r, h0i, w.r0r, w.r0i, w.snap, hr_out, hi_out, T, h, nstates,
-                     shortr ? 0 : 1);
-  hipError_t e = hipGetLastError();
+  constexpr int io_code = std::is_same<IO, bf16_t>::value ? VMI_BF16
+                        : (std::is_same<IO, f16_t>::value ? VMI_F16 : VMI_F32);
+  hipError_t e;
+  if (cham_mfma_usable(io_code, h, k, v)) {  // chunked carry on the matrix cores
+    e = launch_cham_mfma_cols(k, v, io_code, w.coef, h0r, h0i, w.r0r, w.r0i, w.snap, hr_out,
+                              hi_out, B, T, h, HP, nstates, shortr ? 0 : 1, C2, w.mm, stream);
+  } else {
+    hipLaunchKernelGGL((wide_cols_kernel<IO, LPC, RPL>), dim3(B, (h + CPG - 1) / CPG, nstates),
+                       dim3(CNT), 0, stream, static_cast<const IO*>(k), static_cast<const IO*>(v),
+                       w.coef, h0r, h0i, w.r0r, w.r0i, w.snap, hr_out, hi_out, T, h, nstates,
+                       shortr ? 0 : 1);
+    e = hipGetLastError();
+  }
   if (e != hipSuccess || nch == 0) return e;
   if (shortr) {
     e = short_readout<IO>(q, h0r, h0i, B, T, h, HP, w, stream);

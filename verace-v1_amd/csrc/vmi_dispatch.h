@@ -144,6 +144,16 @@ hipError_t launch_cham_wide(const void* q, const void* k, const void* v, const v
                             void* out, float* hr_out, float* hi_out, int B, int T, int h,
                             void* workspace, hipStream_t stream);
 
+// cham_mfma.hip: the wide route's state carry on the matrix cores (16-bit k, v, h % 8 == 0,
+// 16-byte aligned k, v; entries of k, v below 65504 in magnitude, as L2-normalised rows are).
+bool cham_mfma_usable(int io_dtype, int h, const void* k, const void* v);
+size_t cham_mfma_workspace_bytes(int64_t B, int64_t T, int64_t h);
+hipError_t launch_cham_mfma_cols(const void* k, const void* v, int io_dtype, const float* coef,
+                                 const float* i0r, const float* i0i, const float* i1r,
+                                 const float* i1i, float* snap, float* fr, float* fi, int B,
+                                 int T, int h, int hp, int nstates, int snap_on, int c2, void* ws,
+                                 hipStream_t stream);
+
 // sssd_bwd.hip: backward of the scan (dq, dk, dv, ddelta, dPsi_0 from dOut, dPsi_T).
 bool sssd_bwd_supported(int64_t D);
 size_t sssd_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D);
