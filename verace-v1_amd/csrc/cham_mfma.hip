@@ -91,7 +91,9 @@ template <> __device__ __forceinline__ V4 to_f16x4<bf16_t>(uint2 raw, bool guard
   return r;
 }
 
-// fp32 -> (hi, lo) f16 pair with packed conversions (round to nearest): x = hi + lo to ~2^-22
+// fp32 -> (hi, lo) f16 pair (round to nearest): x = hi + lo to ~2^-22.  hi by a packed
+// conversion per two values; lo = x - hi is exact in fp32 and is rounded to f16 by one
+// mixed-precision FMA per value (x * 1.0 - hi, hi read as f16 from its half of the register).
 __device__ __forceinline__ void split8p(const float* x, V8& hi, V8& lo) {
   typedef float f2 __attribute__((ext_vector_type(2)));
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -99,8 +101,13 @@ __device__ __forceinline__ void split8p(const float* x, V8& hi, V8& lo) {
   for (int p = 0; p < 4; ++p) {
     const f2 xv = {x[2 * p], x[2 * p + 1]};
     const h2 hv = __builtin_convertvector(xv, h2);
-    const f2 lv = xv - __builtin_convertvector(hv, f2);
-    const h2 lw = __builtin_convertvector(lv, h2);
+    const uint32_t hb = __builtin_bit_cast(uint32_t, hv);
+    uint32_t lb;
+    asm("v_fma_mixlo_f16 %0, %1, 1.0, -%3 op_sel_hi:[0,0,1]\n\t"
+        "v_fma_mixhi_f16 %0, %2, 1.0, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+        : "=&v"(lb)
+        : "v"(xv[0]), "v"(xv[1]), "v"(hb));
+    const h2 lw = __builtin_bit_cast(h2, lb);
     hi[2 * p] = hv[0];
     hi[2 * p + 1] = hv[1];
     lo[2 * p] = lw[0];
@@ -114,7 +121,7 @@ __global__ __launch_bounds__(64) void cm_prep_kernel(const IO* __restrict__ k,
                                                      const IO* __restrict__ v,
                                                      const float* __restrict__ coef,
                                                      E* __restrict__ tt, E* __restrict__ yk,
-                                                     E* __restrict__ yv, int T, int h) {
+                                                     E* __restrict__ yv, int T, int h, int hp) {
   __shared__ float G[RK][RK + 1];
   __shared__ float Nc[CT][NCF];
   __shared__ float Tf[2][RK][RK + 1];
@@ -126,10 +133,10 @@ __global__ __launch_bounds__(64) void cm_prep_kernel(const IO* __restrict__ k,
   const bool tok_ok = tok < T;
   const int64_t row = static_cast<int64_t>(b) * T + (tok_ok ? tok : 0);
   const IO* src = ((l32 & 1) ? v : k) + row * h;
-  E* dst = ((l32 & 1) ? yv : yk) + row * h;
+  E* dst = ((l32 & 1) ? yv : yk) + row * hp;  // rows padded to hp with zeros
   f32x16 acc = {};
-  const int nks = (h + 15) / 16;  // the same trip count in both half-waves (MFMA is wave-wide)
-  for (int ks = 0; ks < nks; ++ks) {
+  const int nks = (h + 15) / 16;  // the same trip counts in both half-waves (MFMA is wave-wide)
+  for (int ks = 0; ks < hp / 16; ++ks) {
     const int f0 = 16 * ks + 8 * g;  // h % 8 == 0: a piece is wholly inside or outside
     uint2 r0 = make_uint2(0, 0), r1 = make_uint2(0, 0);
     if (tok_ok && f0 < h) {
@@ -137,8 +144,8 @@ __global__ __launch_bounds__(64) void cm_prep_kernel(const IO* __restrict__ k,
       r1 = *reinterpret_cast<const uint2*>(src + f0 + 4);
     }
     const V8 x = cat8<V4, V8>(to_f16x4<IO>(r0, true), to_f16x4<IO>(r1, true));
-    if (tok_ok && f0 < h) *reinterpret_cast<V8*>(dst + f0) = x;
-    acc = MM::mma32(x, x, acc);
+    if (tok_ok) *reinterpret_cast<V8*>(dst + f0) = x;
+    if (ks < nks) acc = MM::mma32(x, x, acc);
   }
 #pragma unroll
   for (int r = 0; r < 16; ++r) G[8 * (r >> 2) + 4 * g + (r & 3)][l32] = acc[r];
@@ -317,12 +324,14 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
 
   // ---- Y of a chunk, as the A operand of W = Y^T H: lane (rho = l32, g), tile rt, K-step ks
   // holds rows r0w + 32 rt + 16 ks + 4 g + {0..3} and + 8 + {0..3} of rank row rho
-  // (k or v of token t0 + rho / 2, f16 from the prep kernel); loaded a chunk ahead.
-  uint2 yraw[TPW][2][2];
-  auto load_y = [&](int m) {
-    const int tok = m * CT + (l32 >> 1);
-    const bool ok = m < nc && tok < T;
-    const E* src = ((l32 & 1) ? v : k) + (static_cast<int64_t>(b) * T + (ok ? tok : 0)) * h;
+  // (k or v of token t0 + rho / 2, f16 from the prep kernel, rows padded to HP with zeros);
+  // loaded a chunk ahead.  Tokens past the end read token T - 1 instead: their rows and
+  // columns of T are zero, so any finite values there leave W's used rows, Z and H unchanged.
+  typedef uint2 YBuf[TPW][2][2];
+  typedef V8 TBuf[2][2];
+  auto load_y = [&](int m, YBuf& yraw) {
+    const int tok = min((m < nc ? m : nc - 1) * CT + (l32 >> 1), T - 1);
+    const E* src = ((l32 & 1) ? v : k) + (static_cast<int64_t>(b) * T + tok) * HP;
 #pragma unroll
     for (int rt = 0; rt < TPW; ++rt)
 #pragma unroll
@@ -330,7 +339,7 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
           const int f = r0w + 32 * rt + 16 * ks + 8 * hf + 4 * g;
-          yraw[rt][ks][hf] = (ok && f < h) ? *reinterpret_cast<const uint2*>(src + f) : make_uint2(0, 0);
+          yraw[rt][ks][hf] = *reinterpret_cast<const uint2*>(src + f);
         }
   };
   // update operand offsets (transposing reads of the wave's Y block): rows
@@ -343,8 +352,7 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
   // part wave / 2, K-steps kst = 0, 1, hi and lo), loaded a chunk ahead
   const int zpart = (wave >> 1) & 1;
   const int mrow = 16 * (wave & 1) + l16;
-  V8 tnext[2][2];
-  auto load_t = [&](int m) {
+  auto load_t = [&](int m, TBuf& tnext) {
     if (wave >= 4) return;
     const E* tb = tt + (static_cast<int64_t>(b) * nc + (m < nc ? m : 0)) * TT_STRIDE;
 #pragma unroll
@@ -356,24 +364,22 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
       tnext[kst][1] = *reinterpret_cast<const V8*>(ar + RK * RK);
     }
   };
-  load_y(0);
-  load_t(0);
-  for (int m = 0; m < nc; ++m) {
-    if (m % cpc == 0) write_snap(m / cpc);
-    V8 tcur[2][2];
-#pragma unroll
-    for (int kst = 0; kst < 2; ++kst) {
-      tcur[kst][0] = tnext[kst][0];
-      tcur[kst][1] = tnext[kst][1];
-    }
-    load_t(m + 1);
+  // one chunk; (yraw, tcur) hold its prefetched operands, (ynext, tnext) receive the next
+  // chunk's (two buffer sets used alternately, so no register copies between iterations)
+  auto chunk = [&](int m, YBuf& yraw, TBuf& tcur, YBuf& ynext, TBuf& tnext) {
     V8 ya[TPW][2];
 #pragma unroll
     for (int rt = 0; rt < TPW; ++rt)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
         ya[rt][ks] = cat8<V4, V8>(__builtin_bit_cast(V4, yraw[rt][ks][0]), __builtin_bit_cast(V4, yraw[rt][ks][1]));
-    load_y(m + 1);  // next chunk (zeros past the end)
+    // the snapshot stores go after this chunk's operands have arrived, so that waiting for
+    // those loads never waits for the stores
+    asm volatile("" ::: "memory");
+    if (m % cpc == 0) write_snap(m / cpc);
+    asm volatile("" ::: "memory");
+    load_t(m + 1, tnext);
+    load_y(m + 1, ynext);
     // the wave's Y rows into LDS for the update's transposing reads
 #pragma unroll
     for (int rt = 0; rt < TPW; ++rt)
@@ -475,6 +481,14 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
     // the next chunk's Y writes and W partials reuse yt / wpart: every wave's reads of this
     // chunk's ones must be done (the Z' reads above end before the next barrier anyway)
     __syncthreads();
+  };
+  YBuf ya0, ya1;
+  TBuf ta0, ta1;
+  load_y(0, ya0);
+  load_t(0, ta0);
+  for (int m = 0; m < nc; m += 2) {
+    chunk(m, ya0, ta0, ya1, ta1);
+    if (m + 1 < nc) chunk(m + 1, ya1, ta1, ya0, ta0);
   }
   // ---- final raw state (z == 0): row-major planes through LDS column tiles
   if (z == 0) {
@@ -507,10 +521,11 @@ hipError_t launch_typed(const IO* k, const IO* v, const float* coef, const float
                         int c2, void* ws, hipStream_t stream) {
   const int nc = (T + CT - 1) / CT;
   E* tt = static_cast<E*>(ws);
-  E* yk = tt + static_cast<int64_t>(B) * nc * TT_STRIDE;  // f16 k, v ([B][T][h] each)
-  E* yv = yk + static_cast<int64_t>(B) * T * h;
+  E* yk = tt + static_cast<int64_t>(B) * nc * TT_STRIDE;  // f16 k, v ([B][T][HP] each)
+  E* yv = yk + static_cast<int64_t>(B) * T * (NWV * 32 * TPW);
   if (nc > 0) {
-    hipLaunchKernelGGL((cm_prep_kernel<IO>), dim3(nc, B), dim3(64), 0, stream, k, v, coef, tt, yk, yv, T, h);
+    hipLaunchKernelGGL((cm_prep_kernel<IO>), dim3(nc, B), dim3(64), 0, stream, k, v, coef, tt, yk, yv, T, h,
+                       NWV * 32 * TPW);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -522,10 +537,11 @@ hipError_t launch_typed(const IO* k, const IO* v, const float* coef, const float
 
 }  // namespace chamm
 
-// Workspace of the MFMA state carry (T per chunk, the f16 k and v), in bytes.
-size_t cham_mfma_workspace_bytes(int64_t B, int64_t T, int64_t h) {
+// Workspace of the MFMA state carry (T per chunk, the f16 k and v with rows padded to hp), in
+// bytes; hp = 256, 512 or 1024, the padded height of the wide route.
+size_t cham_mfma_workspace_bytes(int64_t B, int64_t T, int64_t hp) {
   const int64_t nc = (T + chamm::CT - 1) / chamm::CT;
-  return static_cast<size_t>(B * nc * chamm::TT_STRIDE + 2 * B * T * h) * sizeof(_Float16) + 256;
+  return static_cast<size_t>(B * nc * chamm::TT_STRIDE + 2 * B * T * hp) * sizeof(_Float16) + 256;
 }
 
 bool cham_mfma_usable(int io_dtype, int h, const void* k, const void* v) {

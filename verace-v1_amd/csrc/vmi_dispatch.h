@@ -147,7 +147,7 @@ hipError_t launch_cham_wide(const void* q, const void* k, const void* v, const v
 // cham_mfma.hip: the wide route's state carry on the matrix cores (16-bit k, v, h % 8 == 0,
 // 16-byte aligned k, v; entries of k, v below 65504 in magnitude, as L2-normalised rows are).
 bool cham_mfma_usable(int io_dtype, int h, const void* k, const void* v);
-size_t cham_mfma_workspace_bytes(int64_t B, int64_t T, int64_t h);
+size_t cham_mfma_workspace_bytes(int64_t B, int64_t T, int64_t hp);  // hp: padded h
 hipError_t launch_cham_mfma_cols(const void* k, const void* v, int io_dtype, const float* coef,
                                  const float* i0r, const float* i0i, const float* i1r,
                                  const float* i1i, float* snap, float* fr, float* fi, int B,
