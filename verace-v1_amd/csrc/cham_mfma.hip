@@ -13,7 +13,9 @@
 // Launches (before the readout kernels of cham_wide.hip, which read the snapshots written
 // here exactly as they read the token-sequential kernel's):
 //   1. cm_prep_kernel, one wave per (chunk, sequence): k, v converted to f16 (non-finite
-//      elements zeroed) and stored for the column kernel, G on the MFMA from them, then T by
+//      elements zeroed) and stored in the column kernel's MFMA operand layout (each
+//      16-feature block of the chunk's 32 rank rows as 64 lanes x 16 bytes, so every operand
+//      load is a contiguous 1 KB), G on the MFMA from them, then T by
 //      forward substitution over the 16 tokens (lane = column of T), stored as f16 hi + lo
 //      parts of Re T and Im T.
 //   2. cm_cols_kernel, workgroup (16 columns, sequence, state): 8 waves, wave w owns rows
@@ -120,8 +122,8 @@ template <typename IO>
 __global__ __launch_bounds__(64) void cm_prep_kernel(const IO* __restrict__ k,
                                                      const IO* __restrict__ v,
                                                      const float* __restrict__ coef,
-                                                     E* __restrict__ tt, E* __restrict__ yk,
-                                                     E* __restrict__ yv, int T, int h, int hp) {
+                                                     E* __restrict__ tt, E* __restrict__ yop,
+                                                     int T, int h, int hp) {
   __shared__ float G[RK][RK + 1];
   __shared__ float Nc[CT][NCF];
   __shared__ float Tf[2][RK][RK + 1];
@@ -133,18 +135,19 @@ __global__ __launch_bounds__(64) void cm_prep_kernel(const IO* __restrict__ k,
   const bool tok_ok = tok < T;
   const int64_t row = static_cast<int64_t>(b) * T + (tok_ok ? tok : 0);
   const IO* src = ((l32 & 1) ? v : k) + row * h;
-  E* dst = ((l32 & 1) ? yv : yk) + row * hp;  // rows padded to hp with zeros
+  // operand block kb of this chunk: lane (rho, g) holds features 16 kb + 4 g + {0..3} and
+  // 16 kb + 8 + 4 g + {0..3} of rank row rho (the K order of the column kernel's state tiles;
+  // G sums over every feature, so any order serves it); blocks past h and tokens past T are 0
+  E* dst = yop + (static_cast<int64_t>(b) * nc + m) * (hp / 16) * 512 + lane * 8;
   f32x16 acc = {};
   const int nks = (h + 15) / 16;  // the same trip counts in both half-waves (MFMA is wave-wide)
   for (int ks = 0; ks < hp / 16; ++ks) {
-    const int f0 = 16 * ks + 8 * g;  // h % 8 == 0: a piece is wholly inside or outside
+    const int f0 = 16 * ks + 4 * g, f1 = f0 + 8;  // h % 4 == 0: a piece is wholly in or out
     uint2 r0 = make_uint2(0, 0), r1 = make_uint2(0, 0);
-    if (tok_ok && f0 < h) {
-      r0 = *reinterpret_cast<const uint2*>(src + f0);
-      r1 = *reinterpret_cast<const uint2*>(src + f0 + 4);
-    }
+    if (tok_ok && f0 < h) r0 = *reinterpret_cast<const uint2*>(src + f0);
+    if (tok_ok && f1 < h) r1 = *reinterpret_cast<const uint2*>(src + f1);
     const V8 x = cat8<V4, V8>(to_f16x4<IO>(r0, true), to_f16x4<IO>(r1, true));
-    if (tok_ok) *reinterpret_cast<V8*>(dst + f0) = x;
+    *reinterpret_cast<V8*>(dst + ks * 512) = x;
     if (ks < nks) acc = MM::mma32(x, x, acc);
   }
 #pragma unroll
@@ -225,7 +228,7 @@ struct alignas(16) ColsSmem {
 // snap: [B][nch][2][h][HP] as in cham_wide.hip (chunk-start readout state every C2 tokens).
 template <int TPW>
 __global__ __launch_bounds__(NTH) void cm_cols_kernel(
-    const E* __restrict__ k, const E* __restrict__ v, const E* __restrict__ tt,
+    const E* __restrict__ yop, const E* __restrict__ tt,
     const float* __restrict__ i0r, const float* __restrict__ i0i,
     const float* __restrict__ i1r, const float* __restrict__ i1i, float* __restrict__ snap,
     float* __restrict__ fr, float* __restrict__ fi, int T, int h, int nstates, int snap_on,
@@ -323,24 +326,18 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
   };
 
   // ---- Y of a chunk, as the A operand of W = Y^T H: lane (rho = l32, g), tile rt, K-step ks
-  // holds rows r0w + 32 rt + 16 ks + 4 g + {0..3} and + 8 + {0..3} of rank row rho
-  // (k or v of token t0 + rho / 2, f16 from the prep kernel, rows padded to HP with zeros);
-  // loaded a chunk ahead.  Tokens past the end read token T - 1 instead: their rows and
-  // columns of T are zero, so any finite values there leave W's used rows, Z and H unchanged.
-  typedef uint2 YBuf[TPW][2][2];
+  // holds rows r0w + 32 rt + 16 ks + 4 g + {0..3} and + 8 + {0..3} of rank row rho (k or v of
+  // token t0 + rho / 2): operand block (r0w + 32 rt + 16 ks) / 16 of the prep kernel's layout,
+  // one contiguous 16-byte piece per lane; loaded a chunk ahead.
+  typedef V8 YBuf[TPW][2];
   typedef V8 TBuf[2][2];
   auto load_y = [&](int m, YBuf& yraw) {
-    const int tok = min((m < nc ? m : nc - 1) * CT + (l32 >> 1), T - 1);
-    const E* src = ((l32 & 1) ? v : k) + (static_cast<int64_t>(b) * T + tok) * HP;
+    const E* src = yop + (static_cast<int64_t>(b) * nc + (m < nc ? m : nc - 1)) * (HP / 16) * 512 +
+                   (r0w / 16) * 512 + lane * 8;
 #pragma unroll
     for (int rt = 0; rt < TPW; ++rt)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int f = r0w + 32 * rt + 16 * ks + 8 * hf + 4 * g;
-          yraw[rt][ks][hf] = *reinterpret_cast<const uint2*>(src + f);
-        }
+      for (int ks = 0; ks < 2; ++ks) yraw[rt][ks] = *reinterpret_cast<const V8*>(src + (2 * rt + ks) * 512);
   };
   // update operand offsets (transposing reads of the wave's Y block): rows
   // rho = 16 ks + 8 hh + 4 g + i, local rows 32 rt + 16 (lane / 16 & 1) + 4 r
@@ -372,7 +369,7 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
     for (int rt = 0; rt < TPW; ++rt)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-        ya[rt][ks] = cat8<V4, V8>(__builtin_bit_cast(V4, yraw[rt][ks][0]), __builtin_bit_cast(V4, yraw[rt][ks][1]));
+        ya[rt][ks] = yraw[rt][ks];
     // the snapshot stores go after this chunk's operands have arrived, so that waiting for
     // those loads never waits for the stores
     asm volatile("" ::: "memory");
@@ -521,27 +518,26 @@ hipError_t launch_typed(const IO* k, const IO* v, const float* coef, const float
                         int c2, void* ws, hipStream_t stream) {
   const int nc = (T + CT - 1) / CT;
   E* tt = static_cast<E*>(ws);
-  E* yk = tt + static_cast<int64_t>(B) * nc * TT_STRIDE;  // f16 k, v ([B][T][HP] each)
-  E* yv = yk + static_cast<int64_t>(B) * T * (NWV * 32 * TPW);
+  E* yop = tt + static_cast<int64_t>(B) * nc * TT_STRIDE;  // [B][nc][HP / 16][64][8] f16
   if (nc > 0) {
-    hipLaunchKernelGGL((cm_prep_kernel<IO>), dim3(nc, B), dim3(64), 0, stream, k, v, coef, tt, yk, yv, T, h,
+    hipLaunchKernelGGL((cm_prep_kernel<IO>), dim3(nc, B), dim3(64), 0, stream, k, v, coef, tt, yop, T, h,
                        NWV * 32 * TPW);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL((cm_cols_kernel<TPW>), dim3((h + COLS - 1) / COLS, B, nstates), dim3(NTH), 0,
-                     stream, yk, yv, tt, i0r, i0i, i1r, i1i, snap, fr, fi, T, h, nstates,
+                     stream, yop, tt, i0r, i0i, i1r, i1i, snap, fr, fi, T, h, nstates,
                      snap_on, c2);
   return hipGetLastError();
 }
 
 }  // namespace chamm
 
-// Workspace of the MFMA state carry (T per chunk, the f16 k and v with rows padded to hp), in
-// bytes; hp = 256, 512 or 1024, the padded height of the wide route.
+// Workspace of the MFMA state carry (T per chunk, the f16 k and v of every chunk in operand
+// layout, hp features each), in bytes; hp = 256, 512 or 1024, the padded height of the wide route.
 size_t cham_mfma_workspace_bytes(int64_t B, int64_t T, int64_t hp) {
   const int64_t nc = (T + chamm::CT - 1) / chamm::CT;
-  return static_cast<size_t>(B * nc * chamm::TT_STRIDE + 2 * B * T * hp) * sizeof(_Float16) + 256;
+  return static_cast<size_t>(B * nc * (chamm::TT_STRIDE + chamm::RK * hp)) * sizeof(_Float16) + 256;
 }
 
 bool cham_mfma_usable(int io_dtype, int h, const void* k, const void* v) {
