@@ -331,13 +331,14 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
   // one contiguous 16-byte piece per lane; loaded a chunk ahead.
   typedef V8 YBuf[TPW][2];
   typedef V8 TBuf[2][2];
-  auto load_y = [&](int m, YBuf& yraw) {
+  // tile rt of the next chunk's operands; the tiles are requested at four points of the chunk
+  // (tile rt after barrier rt) so that the loads do not queue up behind each other
+  auto load_y = [&](int m, YBuf& yraw, int rt) {
+    if (rt >= TPW) return;
     const E* src = yop + (static_cast<int64_t>(b) * nc + (m < nc ? m : nc - 1)) * (HP / 16) * 512 +
                    (r0w / 16) * 512 + lane * 8;
 #pragma unroll
-    for (int rt = 0; rt < TPW; ++rt)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) yraw[rt][ks] = *reinterpret_cast<const V8*>(src + (2 * rt + ks) * 512);
+    for (int ks = 0; ks < 2; ++ks) yraw[rt][ks] = *reinterpret_cast<const V8*>(src + (2 * rt + ks) * 512);
   };
   // update operand offsets (transposing reads of the wave's Y block): rows
   // rho = 16 ks + 8 hh + 4 g + i, local rows 32 rt + 16 (lane / 16 & 1) + 4 r
@@ -376,7 +377,7 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
     if (m % cpc == 0) write_snap(m / cpc);
     asm volatile("" ::: "memory");
     load_t(m + 1, tnext);
-    load_y(m + 1, ynext);
+    load_y(m + 1, ynext, 0);
     // the wave's Y rows into LDS for the update's transposing reads
 #pragma unroll
     for (int rt = 0; rt < TPW; ++rt)
@@ -405,6 +406,7 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
       *reinterpret_cast<float4*>(&sm.wpart[wave][l32][8 * q + 4 * g]) =
           make_float4(wacc[4 * q], wacc[4 * q + 1], wacc[4 * q + 2], wacc[4 * q + 3]);
     __syncthreads();
+    load_y(m + 1, ynext, 1);
     // reduction: wave w sums columns n = 4w .. 4w + 3 (lane: n = 4w + lane / 16, rho pair 2 (lane % 16))
     {
       const int n = 4 * wave + (lane >> 4), rp = 2 * (lane & 15);
@@ -418,6 +420,7 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
       *reinterpret_cast<float2*>(&sm.wred[n][rp]) = s;
     }
     __syncthreads();
+    load_y(m + 1, ynext, 2);
     // Z = T W on waves 0..3: [Zr; Zi] (64 x 16) = [[Tr, -Ti], [Ti, Tr]] (64 x 64) [Wr; Wi];
     // wave wz computes rows 16 wz .. 16 wz + 15 (part wz / 2, rho 16 (wz & 1) + ..)
     if (wave < 4) {
@@ -456,6 +459,7 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
       *reinterpret_cast<V4*>(&sm.zl[n][rho0]) = zl4;
     }
     __syncthreads();
+    load_y(m + 1, ynext, 3);
     // H += Y Z': A = Y rows (transposing reads), B = Z' rows rho = 16 ks + 8 (i/4) + 4 g + i%4
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -481,7 +485,8 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
   };
   YBuf ya0, ya1;
   TBuf ta0, ta1;
-  load_y(0, ya0);
+#pragma unroll
+  for (int rt = 0; rt < TPW; ++rt) load_y(0, ya0, rt);
   load_t(0, ta0);
   for (int m = 0; m < nc; m += 2) {
     chunk(m, ya0, ta0, ya1, ta1);
