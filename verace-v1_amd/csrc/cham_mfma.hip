@@ -225,12 +225,17 @@ struct alignas(16) ColsSmem {
 // Workgroup (column block cb, sequence b, state z).  Lane (n = lane % 32, g = lane / 32)
 // of wave w holds, in tile rt, rows w RPW + 32 rt + 8 (r/4) + 4 g + r%4 of MFMA column n:
 // the real part of state column c0 + n for n < 16, the imaginary part of c0 + n - 16 else.
-// snap: [B][nch][2][h][HP] as in cham_wide.hip (chunk-start readout state every C2 tokens).
-template <int TPW>
+// Readout snapshots (the state at the start of every c2 tokens):
+//   S16 = false: fp32 [B][nch][2][h][HP] as in cham_wide.hip;
+//   S16 = true (identity start, every entry of the state at most 1 in magnitude): f16 in the
+//   A-operand layout of cm_read_kernel, [B][nch][part][HP / 32][HP / 16][64][8]: block
+//   (part, it, kb) lane (m, g) holds part's rows 32 it + m, columns
+//   16 kb + 8 (i/4) + 4 g + i%4 (i < 8), so this workgroup writes the blocks kb = cb.
+template <int TPW, bool S16>
 __global__ __launch_bounds__(NTH) void cm_cols_kernel(
     const E* __restrict__ yop, const E* __restrict__ tt,
     const float* __restrict__ i0r, const float* __restrict__ i0i,
-    const float* __restrict__ i1r, const float* __restrict__ i1i, float* __restrict__ snap,
+    const float* __restrict__ i1r, const float* __restrict__ i1i, void* __restrict__ snapv,
     float* __restrict__ fr, float* __restrict__ fi, int T, int h, int nstates, int snap_on,
     int c2) {
   constexpr int RPW = 32 * TPW, HP = NWV * RPW;
@@ -313,7 +318,8 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
   const bool snaps = snap_on && z == nstates - 1;
   auto write_snap = [&](int n) {
     if (!snaps || !colok) return;
-    float* d = snap + ((static_cast<int64_t>(b) * nch + n) * 2 + part) * h * HP + static_cast<int64_t>(col) * HP;
+    float* d = static_cast<float*>(snapv) + ((static_cast<int64_t>(b) * nch + n) * 2 + part) * h * HP +
+               static_cast<int64_t>(col) * HP;
 #pragma unroll
     for (int rt = 0; rt < TPW; ++rt)
 #pragma unroll
@@ -346,6 +352,36 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
   const int offU = rho_slot(4 * g + (l16 >> 2)) * Y_LD + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
   E* const ywr = ytw + rho_slot(l32) * Y_LD + 4 * g;
 
+  // f16 snapshot in operand layout: the wave's rows go through its own Y block in LDS (state
+  // column n in place of rank row n) and come back transposed by the update's reads, so every
+  // store is a contiguous 1 KB.  The wave's later Y writes follow these reads in its own LDS
+  // queue, so they cannot overtake them.
+  auto write_snap16 = [&](int n) {
+#pragma unroll
+    for (int rt = 0; rt < TPW; ++rt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        V4 hv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hv[e] = static_cast<E>(hs[rt][4 * q + e] * inv_ssc);
+        *reinterpret_cast<V4*>(ywr + 32 * rt + 8 * q) = hv;
+      }
+    E* d = static_cast<E*>(snapv) + static_cast<int64_t>(b * nch + n) * 2 * (HP / 32) * (HP / 16) * 512 +
+           (static_cast<int64_t>(r0w / 32) * (HP / 16) + blockIdx.x) * 512 + lane * 8;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)  // ks = part (columns 16 ks .. 16 ks + 15 of the block)
+#pragma unroll
+      for (int rt = 0; rt < TPW; ++rt) {
+        typedef short i16x4 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+        const E* pp = ytw + offU + ks * Y_LD + 32 * rt;
+        const V4 a0 = __builtin_bit_cast(V4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(pp)));
+        const V4 a1 = __builtin_bit_cast(V4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(pp + 2 * Y_LD)));
+        *reinterpret_cast<V8*>(d + (static_cast<int64_t>(ks) * (HP / 32) * (HP / 16) + rt * (HP / 16)) * 512) =
+            cat8<V4, V8>(a0, a1);
+      }
+  };
+
   // T operands of the Z waves (A of [[Re T, -Im T], [Im T, Re T]], rows 16 (wave & 1) + l16 of
   // part wave / 2, K-steps kst = 0, 1, hi and lo), loaded a chunk ahead
   const int zpart = (wave >> 1) & 1;
@@ -374,7 +410,13 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
     // the snapshot stores go after this chunk's operands have arrived, so that waiting for
     // those loads never waits for the stores
     asm volatile("" ::: "memory");
-    if (m % cpc == 0) write_snap(m / cpc);
+    if (m % cpc == 0) {
+      if constexpr (S16) {
+        if (snaps) write_snap16(m / cpc);
+      } else {
+        write_snap(m / cpc);
+      }
+    }
     asm volatile("" ::: "memory");
     load_t(m + 1, tnext);
     load_y(m + 1, ynext, 0);
@@ -479,9 +521,10 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
         hs[rt] = MM::mma32(ay, bl, hs[rt]);
       }
     }
-    // the next chunk's Y writes and W partials reuse yt / wpart: every wave's reads of this
-    // chunk's ones must be done (the Z' reads above end before the next barrier anyway)
-    __syncthreads();
+    // no barrier here: yt is per wave, the next W partials are written after barriers 2 and 3
+    // (every wave's reads of this chunk's partials are done by then), and the next Z' and W
+    // reductions are written after the next barrier 1, which every wave reaches only once
+    // its update has read this chunk's Z'
   };
   YBuf ya0, ya1;
   TBuf ta0, ta1;
@@ -492,6 +535,7 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
     chunk(m, ya0, ta0, ya1, ta1);
     if (m + 1 < nc) chunk(m + 1, ya1, ta1, ya0, ta0);
   }
+  __syncthreads();  // the tile below overlays Z' and the Y blocks of the last update
   // ---- final raw state (z == 0): row-major planes through LDS column tiles
   if (z == 0) {
     float* tile = &sm.wpart[0][0][0];
@@ -516,6 +560,310 @@ __global__ __launch_bounds__(NTH) void cm_cols_kernel(
   }
 }
 
+// ---------------------------------------------------------------- 3: readout from the identity
+// With no initial hologram every readout state is H_t itself, a product of unitary factors, so
+// its entries are at most 1 in magnitude and f16 snapshots of it lose only relative precision
+// 2^-11 (the output is rounded to 16 bits anyway).  Workgroup = 32 consecutive tokens of one
+// sequence (X = their readout vectors, rows of both parts as fp32 MFMA accumulators, laid out
+// like the column kernel's state with tokens in place of columns):
+//   0. q' = tau_t q_t in f16 (tau_t a power of two putting max |q_t| in [16, 32), so that X and
+//      the products below stay far inside the f16 range) as B operands in LDS;
+//   1. X = S q' with S the snapshot at the start of the token's 128-token block
+//      (v_mfma_f32_32x32x16_f16; A operands stream from the snapshot, one 1 KB block per load);
+//   2. for every 16-token chunk c of the block up to the group's last token: X += Y_c Z,
+//      Z = mask(T_c Y_c^T X) (the chunk factor I + Y T Y^T of cm_cols_kernel; a token of chunk c
+//      keeps the rank rows of tokens up to itself, a token of a later chunk all of them, a token
+//      of an earlier chunk none), with single f16 operands;
+//   3. rec_t = Re(x_t) / tau_t through LDS to contiguous rows of the output.
+constexpr int RG = 32;    // tokens per readout workgroup
+constexpr int C2M = 128;  // tokens per f16 snapshot
+constexpr int WP_LD = 68; // floats per token row of the W partials ([wave][token][part, rho])
+
+template <int TPW>
+struct alignas(16) ReadSmem {
+  static constexpr int HP = NWV * 32 * TPW;
+  union {
+    E qb[HP / 16][64][8];  // phase 1
+    struct {
+      float wpart[NWV][RG][WP_LD];
+      float wred[RG][WP_LD];
+      E zs[2][RG][Z_LD];
+    } p2;                  // phase 2
+    uint16_t ot[RG][HP + 8];  // phase 3
+  } u;
+  E yt[NWV][RK][Y_LD];
+  float tau[RG];
+};
+
+template <typename IO> __device__ __forceinline__ void unpack8(uint4 r, float* f);
+template <> __device__ __forceinline__ void unpack8<bf16_t>(uint4 r, float* f) {
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+template <> __device__ __forceinline__ void unpack8<f16_t>(uint4 r, float* f) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const h2 v = __builtin_bit_cast(h2, w[i]);
+    f[2 * i] = static_cast<float>(v[0]);
+    f[2 * i + 1] = static_cast<float>(v[1]);
+  }
+}
+template <typename IO> __device__ __forceinline__ uint16_t pack_io(float x);
+template <> __device__ __forceinline__ uint16_t pack_io<bf16_t>(float x) { return f32_to_bf16(x); }
+template <> __device__ __forceinline__ uint16_t pack_io<f16_t>(float x) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+
+template <typename IO, int TPW>
+__global__ __launch_bounds__(NTH) void cm_read_kernel(const IO* __restrict__ q,
+                                                      const E* __restrict__ snap,
+                                                      const E* __restrict__ yop,
+                                                      const E* __restrict__ tt,
+                                                      IO* __restrict__ out, int B, int T, int h) {
+  constexpr int RPW = 32 * TPW, HP = NWV * RPW, NKB = HP / 16;
+  __shared__ ReadSmem<TPW> sm;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, g = lane >> 5, l16 = lane & 15, g4 = lane >> 4;
+  // work item: consecutive items (the groups of one snapshot) on one XCD (workgroup i runs on
+  // XCD i % 8), so the snapshot they share is read into that XCD's L2 once
+  const int ngrp = (T + RG - 1) / RG, total = B * ngrp, per = (total + 7) / 8;
+  const int item = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (item >= total) return;  // the whole workgroup
+  const int b = item / ngrp, t0 = (item % ngrp) * RG;
+  const int nc = (T + CT - 1) / CT, nsn = (T + C2M - 1) / C2M, sn = t0 / C2M;
+  const int r0w = wave * RPW;
+
+  // ---- 0: q' as B operands: block kb, lane (t, g) holds features 16 kb + 8 (i/4) + 4 g + i%4
+  {
+    constexpr int FPT = HP / 16, NP = FPT / 8;  // features and 8-element pieces per thread
+    const int t = tid >> 4, s = tid & 15;       // 16 threads per token
+    const int tok = t0 + t;
+    const IO* src = q + (static_cast<int64_t>(b) * T + (tok < T ? tok : 0)) * h;
+    float x[NP][8];
+    float mx = 0.f;
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+      const int f = s * FPT + 8 * u;  // h % 8 == 0: a piece is wholly in or out
+      const uint4 raw = (tok < T && f < h) ? *reinterpret_cast<const uint4*>(src + f) : make_uint4(0, 0, 0, 0);
+      unpack8<IO>(raw, x[u]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(x[u][e]));
+    }
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    int ex = 5;
+    if (mx > 0.f && mx <= 3.0e38f) {
+      (void)frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
+    }
+    const float tau = ldexpf(1.f, 5 - ex);  // tau mx in [16, 32); 1 for zero / non-finite rows
+    if (s == 0) sm.tau[t] = tau;
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+      const int f = s * FPT + 8 * u, kb = f >> 4, hf = (f >> 3) & 1;
+      V4 lo, hi;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lo[e] = static_cast<E>(x[u][e] * tau);
+        hi[e] = static_cast<E>(x[u][4 + e] * tau);
+      }
+      *reinterpret_cast<V4*>(&sm.u.qb[kb][t][4 * hf]) = lo;
+      *reinterpret_cast<V4*>(&sm.u.qb[kb][t + 32][4 * hf]) = hi;
+    }
+  }
+  __syncthreads();
+
+  // ---- 1: X = S q' over the column blocks kb of the snapshot (blocks past h were not written)
+  f32x16 X[2][TPW];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int rt = 0; rt < TPW; ++rt) X[p][rt] = f32x16{};
+  {
+    const int nkb = (h + 15) / 16;
+    const E* sb = snap + static_cast<int64_t>(b * nsn + sn) * 2 * (HP / 32) * NKB * 512 +
+                  static_cast<int64_t>(r0w / 32) * NKB * 512 + lane * 8;
+    typedef V8 ABuf[2][TPW];
+    auto load_a = [&](int kb, ABuf& a) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int rt = 0; rt < TPW; ++rt)
+          a[p][rt] = *reinterpret_cast<const V8*>(sb + (static_cast<int64_t>(p * (HP / 32) + rt) * NKB + kb) * 512);
+    };
+    auto step = [&](int kb, ABuf& a) {
+      const V8 bq = *reinterpret_cast<const V8*>(&sm.u.qb[kb][lane][0]);
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int rt = 0; rt < TPW; ++rt) X[p][rt] = MM::mma32(a[p][rt], bq, X[p][rt]);
+    };
+    ABuf a0, a1;
+    load_a(0, a0);
+    for (int kb = 0; kb < nkb; kb += 2) {
+      if (kb + 1 < nkb) load_a(kb + 1, a1);
+      step(kb, a0);
+      if (kb + 1 < nkb) {
+        if (kb + 2 < nkb) load_a(kb + 2, a0);
+        step(kb + 1, a1);
+      }
+    }
+  }
+  __syncthreads();  // phase 2 overlays the B operands
+
+  // ---- 2: the chunk factors of the block up to the group's last token
+  E* const ytw = &sm.yt[wave][0][0];
+  const int offU = rho_slot(4 * g + (l16 >> 2)) * Y_LD + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
+  E* const ywr = ytw + rho_slot(l32) * Y_LD + 4 * g;
+  const int zpart = (wave >> 1) & 1, mrow = 16 * (wave & 1) + l16, ztok = 16 * (wave >> 2);
+  const int cb = sn * (C2M / CT), ce = min(nc - 1, (t0 + RG - 1) / CT);
+  V8 ya[TPW][2];
+  V8 ta[2];
+  auto load_y = [&](int c) {
+    const E* src = yop + (static_cast<int64_t>(b) * nc + c) * NKB * 512 + (r0w / 16) * 512 + lane * 8;
+#pragma unroll
+    for (int rt = 0; rt < TPW; ++rt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) ya[rt][ks] = *reinterpret_cast<const V8*>(src + (2 * rt + ks) * 512);
+  };
+  auto load_t = [&](int c) {  // hi parts of T's real form, rows mrow of part zpart
+    const E* tb = tt + (static_cast<int64_t>(b) * nc + c) * TT_STRIDE;
+#pragma unroll
+    for (int kst = 0; kst < 2; ++kst) {
+      const int mat = (zpart == 0) == (kst == 0) ? 0 : 2;  // 0: Re T, 2: Im T
+      ta[kst] = *reinterpret_cast<const V8*>(tb + mat * RK * RK + mrow * RK + 8 * g4);
+    }
+  };
+  load_y(cb);
+  load_t(cb);
+  for (int c = cb; c <= ce; ++c) {
+    // Y rows into the wave's LDS block for the update's transposing reads
+#pragma unroll
+    for (int rt = 0; rt < TPW; ++rt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        *reinterpret_cast<V4*>(ywr + 32 * rt + 16 * ks) = __builtin_shufflevector(ya[rt][ks], ya[rt][ks], 0, 1, 2, 3);
+        *reinterpret_cast<V4*>(ywr + 32 * rt + 16 * ks + 8) = __builtin_shufflevector(ya[rt][ks], ya[rt][ks], 4, 5, 6, 7);
+      }
+    // W partials = Y^T X over this wave's rows, both parts
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      f32x16 wacc = {};
+#pragma unroll
+      for (int rt = 0; rt < TPW; ++rt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          V8 xb;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) xb[i] = static_cast<E>(X[p][rt][8 * ks + i]);
+          wacc = MM::mma32(ya[rt][ks], xb, wacc);
+        }
+      // lane (t, g) holds W_p[8 (r/4) + 4 g + r%4][t]
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq)
+        *reinterpret_cast<float4*>(&sm.u.p2.wpart[wave][l32][32 * p + 8 * qq + 4 * g]) =
+            make_float4(wacc[4 * qq], wacc[4 * qq + 1], wacc[4 * qq + 2], wacc[4 * qq + 3]);
+    }
+    if (c < ce) load_y(c + 1);  // ya is in LDS and consumed: fetch the next chunk's
+    __syncthreads();
+    {  // reduction: thread -> token tid / 16, rows 4 (tid % 16) .. + 3
+      const int t = tid >> 4, r4 = 4 * (tid & 15);
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int w = 0; w < NWV; ++w) {
+        const float4 x = *reinterpret_cast<const float4*>(&sm.u.p2.wpart[w][t][r4]);
+        acc.x += x.x;
+        acc.y += x.y;
+        acc.z += x.z;
+        acc.w += x.w;
+      }
+      *reinterpret_cast<float4*>(&sm.u.p2.wred[t][r4]) = acc;
+    }
+    __syncthreads();
+    {  // Z tile: rows (zpart, 16 (wave & 1) .. + 15), tokens ztok .. ztok + 15
+      f32x4 zacc = {};
+#pragma unroll
+      for (int kst = 0; kst < 2; ++kst) {
+        V8 a = ta[kst];
+        if (zpart == 0 && kst == 1) a = -a;
+        const float* wsrc = &sm.u.p2.wred[ztok + l16][32 * kst + 8 * g4];
+        const float4 w0 = *reinterpret_cast<const float4*>(wsrc);
+        const float4 w1 = *reinterpret_cast<const float4*>(wsrc + 4);
+        const V8 bw = {static_cast<E>(w0.x), static_cast<E>(w0.y), static_cast<E>(w0.z), static_cast<E>(w0.w),
+                       static_cast<E>(w1.x), static_cast<E>(w1.y), static_cast<E>(w1.z), static_cast<E>(w1.w)};
+        zacc = MM::mma16(a, bw, zacc);
+      }
+      if (c < ce) load_t(c + 1);
+      // lane (token ztok + l16, g4): rho = 16 (wave & 1) + 4 g4 + r
+      const int tl = ztok + l16, tg = t0 + tl, ct = tg / CT;
+      V4 zv;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rho = 16 * (wave & 1) + 4 * g4 + r;
+        const bool keep = ct > c || (ct == c && c * CT + (rho >> 1) <= tg);
+        zv[r] = keep ? static_cast<E>(zacc[r] * (1.f / TSCALE)) : static_cast<E>(0.f);
+      }
+      *reinterpret_cast<V4*>(&sm.u.p2.zs[zpart][tl][16 * (wave & 1) + 4 * g4]) = zv;
+    }
+    __syncthreads();
+    // X_p += Y Z_p: A = Y rows (transposing reads), B = Z_p rows rho = 16 ks + 8 (i/4) + 4 g + i%4
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      V8 ay[TPW];
+#pragma unroll
+      for (int rt = 0; rt < TPW; ++rt) {
+        typedef short i16x4 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+        const E* pp = ytw + offU + ks * Y_LD + 32 * rt;
+        const V4 a0 = __builtin_bit_cast(V4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(pp)));
+        const V4 a1 = __builtin_bit_cast(V4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(pp + 2 * Y_LD)));
+        ay[rt] = cat8<V4, V8>(a0, a1);
+      }
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const E* zp = &sm.u.p2.zs[p][l32][16 * ks + 4 * g];
+        const V8 bz = cat8<V4, V8>(*reinterpret_cast<const V4*>(zp), *reinterpret_cast<const V4*>(zp + 8));
+#pragma unroll
+        for (int rt = 0; rt < TPW; ++rt) X[p][rt] = MM::mma32(ay[rt], bz, X[p][rt]);
+      }
+    }
+    // no barrier: the next partials / reduction / Z' are written after barriers that every
+    // wave reaches only once it has finished reading this chunk's (as in cm_cols_kernel)
+  }
+  __syncthreads();  // the output rows overlay Z'
+
+  // ---- 3: rec_t = Re(x_t) / tau_t, transposed through LDS to contiguous output rows
+  {
+    const float it = 1.f / sm.tau[l32];
+#pragma unroll
+    for (int rt = 0; rt < TPW; ++rt)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int row = r0w + 32 * rt + 8 * qq + 4 * g;
+        uint2 pk;
+        pk.x = static_cast<uint32_t>(pack_io<IO>(X[0][rt][4 * qq] * it)) |
+               (static_cast<uint32_t>(pack_io<IO>(X[0][rt][4 * qq + 1] * it)) << 16);
+        pk.y = static_cast<uint32_t>(pack_io<IO>(X[0][rt][4 * qq + 2] * it)) |
+               (static_cast<uint32_t>(pack_io<IO>(X[0][rt][4 * qq + 3] * it)) << 16);
+        *reinterpret_cast<uint2*>(&sm.u.ot[l32][row]) = pk;
+      }
+  }
+  __syncthreads();
+  {
+    const int t = tid >> 4, s = tid & 15, tok = t0 + t;
+    if (tok < T) {
+      IO* dst = out + (static_cast<int64_t>(b) * T + tok) * h;
+      for (int f = 8 * s; f < h; f += 128)
+        *reinterpret_cast<uint4*>(dst + f) = *reinterpret_cast<const uint4*>(&sm.u.ot[t][f]);
+    }
+  }
+}
+
 template <typename IO, int TPW>
 hipError_t launch_typed(const IO* k, const IO* v, const float* coef, const float* i0r,
                         const float* i0i, const float* i1r, const float* i1i, float* snap,
@@ -530,9 +878,33 @@ hipError_t launch_typed(const IO* k, const IO* v, const float* coef, const float
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((cm_cols_kernel<TPW>), dim3((h + COLS - 1) / COLS, B, nstates), dim3(NTH), 0,
+  hipLaunchKernelGGL((cm_cols_kernel<TPW, false>), dim3((h + COLS - 1) / COLS, B, nstates), dim3(NTH), 0,
                      stream, yop, tt, i0r, i0i, i1r, i1i, snap, fr, fi, T, h, nstates,
                      snap_on, c2);
+  return hipGetLastError();
+}
+
+// identity start: state carry with f16 snapshots every C2M tokens, then the chunked readout
+template <typename IO, int TPW>
+hipError_t launch_scan16(const IO* q, const IO* k, const IO* v, const float* coef, void* snap,
+                         IO* out, float* fr, float* fi, int B, int T, int h, void* ws,
+                         hipStream_t stream) {
+  const int nc = (T + CT - 1) / CT;
+  if (nc == 0) return hipSuccess;
+  E* tt = static_cast<E*>(ws);
+  E* yop = tt + static_cast<int64_t>(B) * nc * TT_STRIDE;
+  hipLaunchKernelGGL((cm_prep_kernel<IO>), dim3(nc, B), dim3(64), 0, stream, k, v, coef, tt, yop, T, h,
+                     NWV * 32 * TPW);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((cm_cols_kernel<TPW, true>), dim3((h + COLS - 1) / COLS, B, 1), dim3(NTH), 0,
+                     stream, yop, tt, nullptr, nullptr, nullptr, nullptr, snap, fr, fi, T, h, 1, 1,
+                     C2M);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int total = B * ((T + RG - 1) / RG);
+  hipLaunchKernelGGL((cm_read_kernel<IO, TPW>), dim3(8 * ((total + 7) / 8)), dim3(NTH), 0, stream, q,
+                     static_cast<const E*>(snap), yop, tt, out, B, T, h);
   return hipGetLastError();
 }
 
@@ -543,6 +915,28 @@ hipError_t launch_typed(const IO* k, const IO* v, const float* coef, const float
 size_t cham_mfma_workspace_bytes(int64_t B, int64_t T, int64_t hp) {
   const int64_t nc = (T + chamm::CT - 1) / chamm::CT;
   return static_cast<size_t>(B * nc * (chamm::TT_STRIDE + chamm::RK * hp)) * sizeof(_Float16) + 256;
+}
+
+size_t cham_mfma_snap16_bytes(int64_t B, int64_t T, int64_t hp) {
+  return static_cast<size_t>(B * ((T + chamm::C2M - 1) / chamm::C2M) * 2 * hp * hp) * sizeof(_Float16);
+}
+
+hipError_t launch_cham_mfma_scan(const void* q, const void* k, const void* v, int io_dtype,
+                                 const float* coef, void* snap, void* out, float* fr, float* fi,
+                                 int B, int T, int h, int hp, void* ws, hipStream_t stream) {
+#define VMI_CS(IO, TPW)                                                                          \
+  return chamm::launch_scan16<IO, TPW>(static_cast<const IO*>(q), static_cast<const IO*>(k),      \
+                                       static_cast<const IO*>(v), coef, snap, static_cast<IO*>(out), \
+                                       fr, fi, B, T, h, ws, stream)
+  if (io_dtype == VMI_BF16) {
+    if (hp == 256) VMI_CS(bf16_t, 1);
+    if (hp == 512) VMI_CS(bf16_t, 2);
+    VMI_CS(bf16_t, 4);
+  }
+  if (hp == 256) VMI_CS(f16_t, 1);
+  if (hp == 512) VMI_CS(f16_t, 2);
+  VMI_CS(f16_t, 4);
+#undef VMI_CS
 }
 
 bool cham_mfma_usable(int io_dtype, int h, const void* k, const void* v) {

@@ -613,7 +613,16 @@ hipError_t launch_rpl(const void* q, const void* k, const void* v, const float* 
   constexpr int io_code = std::is_same<IO, bf16_t>::value ? VMI_BF16
                         : (std::is_same<IO, f16_t>::value ? VMI_F16 : VMI_F32);
   hipError_t e;
-  if (cham_mfma_usable(io_code, h, k, v)) {  // chunked carry on the matrix cores
+  const bool mm = cham_mfma_usable(io_code, h, k, v);
+  if (mm && !h0r && (reinterpret_cast<uintptr_t>(q) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+    // identity start: chunked carry and chunked readout on the matrix cores (f16 snapshots
+    // in the snapshot region, which is at least as large: 2 HP^2 f16 per 128 tokens against
+    // 2 h HP fp32 per 64)
+    return launch_cham_mfma_scan(q, k, v, io_code, w.coef, w.snap, out, hr_out, hi_out, B, T, h,
+                                 HP, w.mm, stream);
+  }
+  if (mm) {  // chunked carry on the matrix cores
     e = launch_cham_mfma_cols(k, v, io_code, w.coef, h0r, h0i, w.r0r, w.r0i, w.snap, hr_out,
                               hi_out, B, T, h, HP, nstates, shortr ? 0 : 1, C2, w.mm, stream);
   } else {

@@ -148,6 +148,13 @@ hipError_t launch_cham_wide(const void* q, const void* k, const void* v, const v
 // 16-byte aligned k, v; entries of k, v below 65504 in magnitude, as L2-normalised rows are).
 bool cham_mfma_usable(int io_dtype, int h, const void* k, const void* v);
 size_t cham_mfma_workspace_bytes(int64_t B, int64_t T, int64_t hp);  // hp: padded h
+// identity start (no initial hologram): the whole scan, state carry with f16 snapshots in the
+// `snap` buffer (cham_mfma_snap16_bytes) and the chunked readout into `out`; q and out 16-byte
+// aligned besides cham_mfma_usable's conditions
+size_t cham_mfma_snap16_bytes(int64_t B, int64_t T, int64_t hp);
+hipError_t launch_cham_mfma_scan(const void* q, const void* k, const void* v, int io_dtype,
+                                 const float* coef, void* snap, void* out, float* fr, float* fi,
+                                 int B, int T, int h, int hp, void* ws, hipStream_t stream);
 hipError_t launch_cham_mfma_cols(const void* k, const void* v, int io_dtype, const float* coef,
                                  const float* i0r, const float* i0i, const float* i1r,
                                  const float* i1i, float* snap, float* fr, float* fi, int B,
