@@ -168,3 +168,83 @@ def test_tiny_model_batched_inplace_decode(device, tiny):
     w1 = _check_states(st.to_layer_states(), z, "states_step", none_is_identity=True)
     print(f"  logits prefill={e:.2e} step={e1:.2e} states={w1:.2e}", flush=True)
     assert e <= 1e-5 and e1 <= 1e-5 and w1 <= 1e-5
+
+
+def test_full_config_layer(device):
+    """One layer of the FULL config (hidden 1024, H 8, D 128, CHAM h 1024,
+    M-CMoE rank 32 x 64 components, random-init bf16 weights, B4 x T2048, identity start; layer
+    index 1, so no block-residual snapshot) through the HIP path (backbone.py:53-101), checked
+    against the fp64 oracles on slices small enough for the host:
+      * SSSD sub-layer, item 0, all 2048 tokens and 8 heads: q, k, v, delta from the captured
+        sub-layer input in fp32 (sssd_attention.py:114-126), the fp64 closed-form scan, head
+        RMSNorm and w_out; module output and final state within 2e-2 (bf16 with fp32 state),
+        every item's state norm within 1e-4 of sqrt(D);
+      * CHAM sub-layer, item 0, first 64 tokens (cham_memory.py:128-243 on the fp64 closed
+        form with the matrix-free NS_3 readout): output within 2e-2; every item's final raw
+        hologram keeps ||H||_F = sqrt(h) within 1e-4 (unitary factors from the identity).
+    """
+    import torch.nn.functional as F
+    from oracle import cham_scan, sssd_closed
+    from verace_amd.backbone import VeraceV1Config, VeraceV1Layer
+
+    print("[case] FULL-config layer B4 T2048 hidden 1024 bf16", flush=True)
+    torch.manual_seed(0)
+    cfg = VeraceV1Config(vocab_size=32000)
+    layer = VeraceV1Layer(1, cfg).to(device=device, dtype=torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(4, 2048, cfg.hidden_dim, generator=g).to(device=device, dtype=torch.bfloat16)
+    cap = {}
+
+    def grab(name):
+        def fn(mod, args, kwargs, out):
+            cap[name] = (args[0].detach(), out)
+        return fn
+
+    hooks = [layer.sssd_attn.register_forward_hook(grab("sssd"), with_kwargs=True),
+             layer.cham_memory.register_forward_hook(grab("cham"), with_kwargs=True)]
+    with torch.no_grad():
+        h_out, _, psi, (hr, hi) = layer(x)
+    torch.cuda.synchronize()
+    for hk in hooks:
+        hk.remove()
+    assert torch.isfinite(h_out).all()
+
+    # ---- SSSD sub-layer, item 0
+    a = layer.sssd_attn
+    xs, (ys, _) = cap["sssd"]
+    W = {n: p.detach().float().cpu() for n, p in a.state_dict().items()}
+    x0 = xs[0:1].float().cpu()
+    H, D = cfg.num_heads, cfg.head_dim
+    q = F.normalize(F.linear(x0, W["w_q.weight"]).view(1, -1, H, D), dim=-1)
+    k = F.normalize(F.linear(x0, W["w_k.weight"]).view(1, -1, H, D), dim=-1)
+    v = F.normalize(F.linear(x0, W["w_v.weight"]).view(1, -1, H, D), dim=-1)
+    dl = 0.1 * torch.sigmoid(F.linear(x0, W["w_delta.weight"]))
+    o64, p64 = sssd_closed.sssd_scan_closed_c(q.numpy(), k.numpy(), v.numpy(), dl.numpy())
+    o_norm = F.rms_norm(torch.from_numpy(o64).float(), (D,), W["head_rmsnorm.weight"])
+    y_ref = F.linear(o_norm.reshape(1, -1, H * D), W["w_out.weight"])
+    ey = _rel(ys[0:1].float().cpu(), y_ref)
+    ep = _rel(psi[0:1].cpu(), p64)
+    nrm = psi.double().reshape(psi.shape[0], H, -1).norm(dim=-1).cpu().numpy()
+    en = float(np.abs(nrm / np.sqrt(D) - 1).max())
+    print(f"  SSSD item 0: rel y={ey:.2e} state={ep:.2e}; state norm drift (all items) {en:.2e}",
+          flush=True)
+    assert ey <= 2e-2 and ep <= 2e-2 and en <= 1e-4
+
+    # ---- CHAM sub-layer, item 0, first 64 tokens
+    c = layer.cham_memory
+    xc, (yc, _) = cap["cham"]
+    Wc = {n: p.detach().float().cpu() for n, p in c.state_dict().items()}
+    x0 = xc[0:1, :64].float().cpu()
+    qc = F.normalize(F.linear(x0, Wc["w_q.weight"]), dim=-1)
+    kc = F.normalize(F.linear(x0, Wc["w_k.weight"]), dim=-1)
+    vc = F.normalize(F.silu(F.linear(x0, Wc["w_v.weight"])), dim=-1)
+    gc = 0.1 * torch.sigmoid(F.linear(x0, Wc["w_gamma.weight"])).squeeze(-1)
+    rec, _ = cham_scan.cham_scan_closed(qc.numpy(), kc.numpy(), vc.numpy(), gc.numpy())
+    yc_ref = F.rms_norm(F.linear(torch.from_numpy(rec).float(), Wc["w_out.weight"]),
+                        (cfg.hidden_dim,), Wc["norm.weight"], eps=c.norm.eps)
+    eyc = _rel(yc[0:1, :64].float().cpu(), yc_ref)
+    hn = torch.sqrt(hr.double().pow(2).sum((-2, -1)) + hi.double().pow(2).sum((-2, -1))).cpu().numpy()
+    ehn = float(np.abs(hn / np.sqrt(cfg.chams_holographic_dim) - 1).max())
+    print(f"  CHAM item 0, 64 tokens: rel y={eyc:.2e}; hologram norm drift (all items) {ehn:.2e}",
+          flush=True)
+    assert eyc <= 2e-2 and ehn <= 1e-4
