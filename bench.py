@@ -883,6 +883,10 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": load_traffic(),
+            # measured once with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE) over
+            # `bench.py --copy-probe`, not in this run; the scaling is in the JSON itself
+            "traffic_source": "profiles/pmc_traffic_op_scan.json (rocprofv3 --pmc run of this "
+                              "kernel, copy-calibrated)",
             "algorithmic_bytes": nbytes,
             "kernel": "whole scan (all launches of one vmi_sssd_scan_fwd call)",
             # the matrix-core side of the same time: 10 D^2 algorithmic flop per token-head
