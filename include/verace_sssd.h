@@ -220,9 +220,10 @@ int vmi_state_cache_cham_step(vmi_state_cache* cache, int64_t layer, const int64
  *   dq, dk, dv : [B,T,H,D] io_dtype;  d_delta : [B,T,H] delta_dtype;
  *   d_psi0     : [B,H,D,D] fp32 = dL/d initial_state (NULL: not needed).
  * The states are rebuilt in reverse from psi_T (every factor is exactly
- * orthogonal), so nothing but psi_T is kept from the forward.  D = 64 or 128
- * (otherwise VMI_ERR_UNSUPPORTED); workspace from vmi_sssd_scan_bwd_workspace_bytes
- * (per-token partial sums: B T H (D/16)(2D + 8) floats). */
+ * orthogonal), so nothing but psi_T is kept from the forward.  1 <= D <= 256
+ * (otherwise VMI_ERR_UNSUPPORTED): D = 64 and 128 with T >= 32 run the chunked
+ * matrix-core backward, every other case the per-token reverse pass; workspace from
+ * vmi_sssd_scan_bwd_workspace_bytes. */
 int vmi_sssd_scan_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, size_t* bytes);
 int vmi_sssd_scan_bwd(const void* q, const void* k, const void* v, const void* delta,
                       int io_dtype, int delta_dtype, const float* psi_T, const void* d_out,

@@ -55,6 +55,12 @@ def _oracle(q, k, v, d, psi0, w_o, w_s, with_state_grad):
     (1, 1, 1, 128, torch.float32, True, False),
     (2, 33, 3, 128, torch.float16, False, False),
     (1, 50, 2, 64, torch.bfloat16, True, True),
+    # head dims other than 64 / 128 (the per-token reverse pass at any T, padded inside)
+    (2, 40, 2, 96, torch.float32, True, True),
+    (1, 20, 3, 48, torch.float32, False, True),
+    (1, 35, 1, 200, torch.bfloat16, True, True),
+    (1, 12, 2, 256, torch.float32, True, True),
+    (2, 9, 2, 17, torch.float32, True, True),
 ])
 def test_scan_backward_matches_oracle(device, B, T, H, D, dtype, init, sgrad):
     from verace_amd import SSSDScanFunction

@@ -83,8 +83,8 @@ int vmi_sssd_scan_fwd(const void* q, const void* k, const void* v, const void* d
 int vmi_sssd_scan_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, size_t* bytes) {
   if (bytes == nullptr || B < 0 || T < 0 || H < 0 || D < 1) return VMI_ERR_INVALID_ARG;
   if (!vmi::sssd_bwd_supported(D)) return VMI_ERR_UNSUPPORTED;
-  *bytes = T >= vmi::kBwdChunkMinT ? vmi::sssd_bwd_chunk_workspace_bytes(B, T, H, D)
-                                   : vmi::sssd_bwd_workspace_bytes(B, T, H, D);
+  *bytes = vmi::use_bwd_chunk(T, D) ? vmi::sssd_bwd_chunk_workspace_bytes(B, T, H, D)
+                                    : vmi::sssd_bwd_workspace_bytes(B, T, H, D);
   return VMI_OK;
 }
 
@@ -107,7 +107,7 @@ int vmi_sssd_scan_bwd(const void* q, const void* k, const void* v, const void* d
   if (d_psi0 != nullptr && (ranges_overlap(d_psi0, state_bytes, psi_T, state_bytes) ||
                             (d_psi_T != nullptr && ranges_overlap(d_psi0, state_bytes, d_psi_T, state_bytes))))
     return VMI_ERR_ALIAS;
-  const bool chunked = T >= vmi::kBwdChunkMinT;
+  const bool chunked = vmi::use_bwd_chunk(T, D);
   const size_t need = chunked ? vmi::sssd_bwd_chunk_workspace_bytes(B, T, H, D)
                               : vmi::sssd_bwd_workspace_bytes(B, T, H, D);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return VMI_ERR_WORKSPACE;

@@ -39,7 +39,9 @@ constexpr int LPC = 32;           // lanes per column
 constexpr int CPW = 64 / LPC;     // columns per wave
 constexpr int NWV = NT / 64;      // waves
 
-template <int D> struct Part { static constexpr int size = 2 * D + 8; };  // dU rows, dM, pad
+// DP: head_dim padded to a multiple of 32 (32, 64, 128, 256); the runtime D <= DP rows and
+// columns are real, the padding rows and columns are zeros and contribute nothing.
+template <int DP> struct Part { static constexpr int size = 2 * DP + 8; };  // dU rows, dM, pad
 
 // sum over the LPC lanes of a column, result in all of them
 __device__ __forceinline__ float col_sum(float x) {
@@ -47,40 +49,44 @@ __device__ __forceinline__ float col_sum(float x) {
   return LPC == 64 ? half_pair_sum(x) : x;
 }
 
-template <typename IO, typename GO, int D>
+template <typename IO, typename GO, int DP>
 __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
     const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
     const void* __restrict__ delta, int delta_dtype, const float* __restrict__ psi_T,
     const GO* __restrict__ dout, const float* __restrict__ dpsi_T, IO* __restrict__ dq,
-    float* __restrict__ dpsi0, float* __restrict__ part, int T, int H) {
-  constexpr int RPT = D / LPC;  // rows per thread
-  constexpr int PS = Part<D>::size;
-  constexpr int NBLK = D / CB;
+    float* __restrict__ dpsi0, float* __restrict__ part, int T, int H, int D) {
+  constexpr int RPT = DP / LPC;  // rows per thread
+  constexpr int PS = Part<DP>::size;
+  constexpr int NBLK = DP / CB;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int rg = lane & (LPC - 1);
   const int cl = CPW * wave + lane / LPC;  // column within the block
   const int blk = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, hd = bh % H;
-  const int j = blk * CB + cl;            // state column
+  const int j = blk * CB + cl;            // state column (padding when j >= D)
+  const bool jv = j < D;
   const int64_t DD = static_cast<int64_t>(D) * D;
 
-  __shared__ float sk[2][SB][D], sv[2][SB][D], sdo[2][SB][D];
+  __shared__ float sk[2][SB][DP], sv[2][SB][DP], sdo[2][SB][DP];
   __shared__ float sq[2][SB][CB];
   __shared__ float sco[2][SB][8];  // m00 m01 m10 m11 kk kv vv -
   __shared__ float sdl[2][SB];
-  __shared__ float sred[2][NWV][2 * D + 4];  // per-wave partials, double-buffered
+  __shared__ float sred[2][NWV][2 * DP + 4];  // per-wave partials, double-buffered
 
   // state columns: psi = Psi^(T)[:, j], lam = dL/dPsi_T[:, j]
   float psi[RPT], lam[RPT];
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
-    const int64_t o = bh * DD + static_cast<int64_t>(rg + LPC * r) * D + j;
-    psi[r] = psi_T[o];
-    lam[r] = dpsi_T ? dpsi_T[o] : 0.f;
+    const int row = rg + LPC * r;
+    const bool ok = jv && row < D;
+    const int64_t o = ok ? bh * DD + static_cast<int64_t>(row) * D + j : 0;
+    psi[r] = ok ? psi_T[o] : 0.f;
+    lam[r] = (ok && dpsi_T) ? dpsi_T[o] : 0.f;
   }
 
-  // stage s holds tokens t = T - 1 - (SB s + i), i < SB (descending); tokens < 0 are zeros
-  constexpr int EPT = SB * D / NT;
+  // stage s holds tokens t = T - 1 - (SB s + i), i < SB (descending); tokens < 0 and
+  // padding features are zeros
+  constexpr int EPT = SB * DP / NT;
   float rk[EPT], rv[EPT], rdo[EPT];
   float rq = 0.f, rd = 0.f;
   auto tok_index = [&](int t) { return (static_cast<int64_t>(b) * T + t) * H + hd; };
@@ -88,15 +94,16 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       const int x = tid + NT * e;
-      const int t = T - 1 - (SB * s + x / D);
-      const int64_t o = t >= 0 ? tok_index(t) * D + x % D : 0;
+      const int t = T - 1 - (SB * s + x / DP);
+      const int64_t o = (t >= 0 && x % DP < D) ? tok_index(t) * D + x % DP : 0;
       rk[e] = io<IO>::load(k, o);
       rv[e] = io<IO>::load(v, o);
       rdo[e] = io<GO>::load(dout, o);
     }
     {
       const int t = T - 1 - (SB * s + tid / CB);
-      rq = (tid < SB * CB && t >= 0) ? io<IO>::load(q, tok_index(t) * D + blk * CB + tid % CB) : 0.f;
+      rq = (tid < SB * CB && t >= 0 && blk * CB + tid % CB < D)
+               ? io<IO>::load(q, tok_index(t) * D + blk * CB + tid % CB) : 0.f;
     }
     {
       const int t = T - 1 - (SB * s + tid);
@@ -108,10 +115,10 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
       const int x = tid + NT * e;
-      const bool ok = T - 1 - (SB * s + x / D) >= 0;
-      sk[buf][x / D][x % D] = ok ? rk[e] : 0.f;
-      sv[buf][x / D][x % D] = ok ? rv[e] : 0.f;
-      sdo[buf][x / D][x % D] = ok ? rdo[e] : 0.f;
+      const bool ok = T - 1 - (SB * s + x / DP) >= 0 && x % DP < D;
+      sk[buf][x / DP][x % DP] = ok ? rk[e] : 0.f;
+      sv[buf][x / DP][x % DP] = ok ? rv[e] : 0.f;
+      sdo[buf][x / DP][x % DP] = ok ? rdo[e] : 0.f;
     }
     if (tid < SB * CB) sq[buf][tid / CB][tid % CB] = rq;
     if (tid < SB) sdl[buf][tid] = rd;
@@ -186,7 +193,7 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
       dqs = col_sum(dqs);
       B0 = col_sum(B0);
       B1 = col_sum(B1);
-      if (rg == 0) io<IO>::store(dq, tok_index(t) * D + j, dqs);
+      if (rg == 0 && jv) io<IO>::store(dq, tok_index(t) * D + j, dqs);
       // Psi^(t) = R^T Psi^(t+1): alpha = M^T (U^T psi);  A = U^T Psi^(t) = U^T psi + G alpha
       const float al0 = m00 * a1 + m10 * b1, al1 = m01 * a1 + m11 * b1;
       const float A0 = a1 + kk * al0 + kv * al1, A1 = b1 + kv * al0 + vv * al1;
@@ -218,11 +225,11 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
           sred[par][wave][2 * (rg + LPC * r)] = u0[r];
           sred[par][wave][2 * (rg + LPC * r) + 1] = u1[r];
         }
-        if (lane < 4) sred[par][wave][2 * D + lane] = dm[lane];
+        if (lane < 4) sred[par][wave][2 * DP + lane] = dm[lane];
       }
       __syncthreads();
       float* pp = part + ((static_cast<int64_t>(bh) * T + t) * NBLK + blk) * PS;
-      for (int x = tid; x < 2 * D + 4; x += NT) {
+      for (int x = tid; x < 2 * DP + 4; x += NT) {
         float acc = sred[par][0][x];
 #pragma unroll
         for (int w = 1; w < NWV; ++w) acc += sred[par][w][x];
@@ -233,9 +240,12 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
     if (s + 1 < nst) commit(s + 1);  // buffer (s + 1) & 1 was last read in stage s - 1
     __syncthreads();
   }
-  if (dpsi0) {
+  if (dpsi0 && jv) {
 #pragma unroll
-    for (int r = 0; r < RPT; ++r) dpsi0[bh * DD + static_cast<int64_t>(rg + LPC * r) * D + j] = lam[r];
+    for (int r = 0; r < RPT; ++r) {
+      const int row = rg + LPC * r;
+      if (row < D) dpsi0[bh * DD + static_cast<int64_t>(row) * D + j] = lam[r];
+    }
   }
 }
 
@@ -243,14 +253,14 @@ __global__ __launch_bounds__(NT) void sssd_bwd_cols_kernel(
 //   M = c N,  N = [[-P vv, P kv - h], [P kv + h, -P kk]],  P = h^2,  h = delta / 2,
 //   c = 2 / (1 + P g),  g = kk vv - kv^2,
 // then kk = k.k, vv = v.v, kv = k.v:  dk = dU_0 + 2 dkk k + dkv v,  dv = dU_1 + 2 dvv v + dkv k.
-template <typename IO, int D>
+template <typename IO, int DP>
 __global__ __launch_bounds__(256) void sssd_bwd_reduce_kernel(
     const IO* __restrict__ k, const IO* __restrict__ v, const void* __restrict__ delta,
     int delta_dtype, const float* __restrict__ part, IO* __restrict__ dk, IO* __restrict__ dv,
-    void* __restrict__ ddelta, int T, int H, int BHT) {
-  constexpr int PS = Part<D>::size;
-  constexpr int NBLK = D / CB;
-  constexpr int RL = (D + 63) / 64;  // rows per lane
+    void* __restrict__ ddelta, int T, int H, int BHT, int D) {
+  constexpr int PS = Part<DP>::size;
+  constexpr int NBLK = DP / CB;
+  constexpr int RL = (DP + 63) / 64;  // rows per lane
   const int lane = threadIdx.x & 63;
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (w >= BHT) return;  // whole wave
@@ -287,10 +297,10 @@ __global__ __launch_bounds__(256) void sssd_bwd_reduce_kernel(
   float d00 = 0.f, d01 = 0.f, d10 = 0.f, d11 = 0.f;
 #pragma unroll
   for (int n = 0; n < NBLK; ++n) {
-    d00 += pp[n * PS + 2 * D];
-    d01 += pp[n * PS + 2 * D + 1];
-    d10 += pp[n * PS + 2 * D + 2];
-    d11 += pp[n * PS + 2 * D + 3];
+    d00 += pp[n * PS + 2 * DP];
+    d01 += pp[n * PS + 2 * DP + 1];
+    d10 += pp[n * PS + 2 * DP + 2];
+    d11 += pp[n * PS + 2 * DP + 3];
   }
   const float dl = load_scalar(delta, delta_dtype, ti);
   // a token with a non-finite Cayley factor was the identity in the forward: no gradient
@@ -328,22 +338,22 @@ __global__ __launch_bounds__(256) void sssd_bwd_reduce_kernel(
   }
 }
 
-template <typename IO, typename GO, int D>
+template <typename IO, typename GO, int DP>
 hipError_t launch_d(const void* q, const void* k, const void* v, const void* delta,
                     int delta_dtype, const float* psi_T, const void* dout, const float* dpsi_T,
                     void* dq, void* dk, void* dv, void* ddelta, float* dpsi0, int B, int T,
-                    int H, void* ws, hipStream_t stream) {
+                    int H, int D, void* ws, hipStream_t stream) {
   float* part = static_cast<float*>(ws);
-  hipLaunchKernelGGL((sssd_bwd_cols_kernel<IO, GO, D>), dim3(D / CB, B * H), dim3(NT), 0, stream,
+  hipLaunchKernelGGL((sssd_bwd_cols_kernel<IO, GO, DP>), dim3(DP / CB, B * H), dim3(NT), 0, stream,
                      static_cast<const IO*>(q), static_cast<const IO*>(k),
                      static_cast<const IO*>(v), delta, delta_dtype, psi_T,
-                     static_cast<const GO*>(dout), dpsi_T, static_cast<IO*>(dq), dpsi0, part, T, H);
+                     static_cast<const GO*>(dout), dpsi_T, static_cast<IO*>(dq), dpsi0, part, T, H, D);
   hipError_t e = hipGetLastError();
   const int BHT = B * H * T;
   if (e != hipSuccess || BHT == 0) return e;
-  hipLaunchKernelGGL((sssd_bwd_reduce_kernel<IO, D>), dim3((BHT + 3) / 4), dim3(256), 0, stream,
+  hipLaunchKernelGGL((sssd_bwd_reduce_kernel<IO, DP>), dim3((BHT + 3) / 4), dim3(256), 0, stream,
                      static_cast<const IO*>(k), static_cast<const IO*>(v), delta, delta_dtype,
-                     part, static_cast<IO*>(dk), static_cast<IO*>(dv), ddelta, T, H, BHT);
+                     part, static_cast<IO*>(dk), static_cast<IO*>(dv), ddelta, T, H, BHT, D);
   return hipGetLastError();
 }
 
@@ -352,11 +362,14 @@ hipError_t launch_go(const void* q, const void* k, const void* v, const void* de
                      int delta_dtype, const float* psi_T, const void* dout, const float* dpsi_T,
                      void* dq, void* dk, void* dv, void* ddelta, float* dpsi0, int B, int T,
                      int H, int D, void* ws, hipStream_t stream) {
-  if (D == 64)
-    return launch_d<IO, GO, 64>(q, k, v, delta, delta_dtype, psi_T, dout, dpsi_T, dq, dk, dv,
-                                ddelta, dpsi0, B, T, H, ws, stream);
-  return launch_d<IO, GO, 128>(q, k, v, delta, delta_dtype, psi_T, dout, dpsi_T, dq, dk, dv,
-                               ddelta, dpsi0, B, T, H, ws, stream);
+#define VMI_BWD_D(DP)                                                                      \
+  return launch_d<IO, GO, DP>(q, k, v, delta, delta_dtype, psi_T, dout, dpsi_T, dq, dk, dv, \
+                              ddelta, dpsi0, B, T, H, D, ws, stream)
+  if (D <= 32) VMI_BWD_D(32);
+  if (D <= 64) VMI_BWD_D(64);
+  if (D <= 128) VMI_BWD_D(128);
+  VMI_BWD_D(256);
+#undef VMI_BWD_D
 }
 
 template <typename IO>
@@ -376,10 +389,11 @@ hipError_t launch_io(const void* q, const void* k, const void* v, const void* de
 
 }  // namespace bwd
 
-bool sssd_bwd_supported(int64_t D) { return D == 64 || D == 128; }
+bool sssd_bwd_supported(int64_t D) { return D >= 1 && D <= 256; }
 
 size_t sssd_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D) {
-  return static_cast<size_t>(B * H * T * (D / bwd::CB)) * (2 * D + 8) * sizeof(float);
+  const int64_t DP = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
+  return static_cast<size_t>(B * H * T * (DP / bwd::CB)) * (2 * DP + 8) * sizeof(float);
 }
 
 hipError_t launch_sssd_bwd(const void* q, const void* k, const void* v, const void* delta,

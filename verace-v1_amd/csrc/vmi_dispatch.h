@@ -161,7 +161,8 @@ hipError_t launch_cham_mfma_cols(const void* k, const void* v, int io_dtype, con
                                  int T, int h, int hp, int nstates, int snap_on, int c2, void* ws,
                                  hipStream_t stream);
 
-// sssd_bwd.hip: backward of the scan (dq, dk, dv, ddelta, dPsi_0 from dOut, dPsi_T).
+// sssd_bwd.hip: backward of the scan (dq, dk, dv, ddelta, dPsi_0 from dOut, dPsi_T), any
+// head_dim up to 256 (the per-token reverse pass; padded to a multiple of 32 inside).
 bool sssd_bwd_supported(int64_t D);
 size_t sssd_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D);
 hipError_t launch_sssd_bwd(const void* q, const void* k, const void* v, const void* delta,
@@ -171,8 +172,11 @@ hipError_t launch_sssd_bwd(const void* q, const void* k, const void* v, const vo
                            hipStream_t stream);
 
 // sssd_bwd_chunk.hip: the same backward in chunks of 16 tokens on the fp32 MFMA
-// (used for T >= kBwdChunkMinT).
+// (used for T >= kBwdChunkMinT at head_dim 64 and 128; other head dims take sssd_bwd.hip).
 constexpr int64_t kBwdChunkMinT = 32;
+inline bool use_bwd_chunk(int64_t T, int64_t D) {
+  return T >= kBwdChunkMinT && (D == 64 || D == 128);
+}
 size_t sssd_bwd_chunk_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D);
 hipError_t launch_sssd_bwd_chunk(const void* q, const void* k, const void* v, const void* delta,
                                  int io_dtype, int delta_dtype, const float* psi_T,

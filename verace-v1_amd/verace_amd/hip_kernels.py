@@ -169,9 +169,9 @@ class SSSDScanFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, delta, initial_state):
-        if q.shape[-1] not in (64, 128):  # fail here rather than in the backward
+        if not 1 <= q.shape[-1] <= 256:  # fail here rather than in the backward
             raise RuntimeError(f"verace_amd: no backward kernel for head_dim {q.shape[-1]} "
-                               "(built for 64 and 128)")
+                               "(built for 1 .. 256)")
         out, psi = launch_sssd_hip_scan(q, k, v, delta, initial_state)
         ctx.save_for_backward(q, k, v, delta, psi)
         ctx.init_dtype = None if initial_state is None else initial_state.dtype
