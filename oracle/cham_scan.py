@@ -86,8 +86,9 @@ def ns_apply(H, x, steps=3):
     return H @ f(steps, x.astype(np.complex128))
 
 
-def cham_scan_closed(q, k, v, gamma, H0r=None, H0i=None, ns_steps=3):
-    """Same outputs as cham_scan_eager, by the closed form and the matrix-free readout."""
+def cham_scan_closed(q, k, v, gamma, H0r=None, H0i=None, ns_steps=3, readout=True):
+    """Same outputs as cham_scan_eager, by the closed form and the matrix-free readout.
+    readout=False skips the readout (rec stays zero): the raw state alone, by the same loop."""
     q, k, v, gamma = (np.asarray(x, dtype=np.float64) for x in (q, k, v, gamma))
     B, T, h = q.shape
     rec = np.zeros((B, T, h))
@@ -100,6 +101,7 @@ def cham_scan_closed(q, k, v, gamma, H0r=None, H0i=None, ns_steps=3):
             W = np.stack([k[b, t], v[b, t]], 1)
             N = cham_cayley_closed(k[b, t], v[b, t], gamma[b, t])
             H = H + W @ (N @ (W.T @ H))
-            rec[b, t] = ns_apply(H, q[b, t], ns_steps).real
+            if readout:
+                rec[b, t] = ns_apply(H, q[b, t], ns_steps).real
         Hr_out[b], Hi_out[b] = H.real, H.imag
     return rec, (Hr_out, Hi_out)

@@ -53,7 +53,26 @@ def main(ref_root: str) -> None:
     from verace_v1.config import VeraceV1Config  # noqa: E402
 
     blobs = {}
-    torch.set_num_threads(8)
+    torch.set_num_threads(4)
+
+    # torch.linalg.solve on a *batch* of complex64 matrices stalls in this container's CPU
+    # build (oneMKL reports "Parameter 6 was incorrect on entry to CLASWP" and a batch entry
+    # of 1024 x 1024 takes over 100 s, against 0.07 s for the same matrix on its own).  The
+    # reference's CHAM path (cham_memory.py:52-95) solves [b, s, h, h] batches at h = 1024, so
+    # complex batches go through one call of the same routine per matrix; real batches (the
+    # SSSD path) are left alone.
+    solve = torch.linalg.solve
+
+    def solve_per_matrix(A, B, *args, **kwargs):
+        if A.is_complex() and A.dim() > 2 and not args and not kwargs:
+            lead = torch.broadcast_shapes(A.shape[:-2], B.shape[:-2])
+            Ab = A.expand(*lead, *A.shape[-2:]).reshape(-1, *A.shape[-2:])
+            Bb = B.expand(*lead, *B.shape[-2:]).reshape(-1, *B.shape[-2:])
+            out = torch.stack([solve(Ab[i], Bb[i]) for i in range(Ab.shape[0])])
+            return out.reshape(*lead, *out.shape[-2:])
+        return solve(A, B, *args, **kwargs)
+
+    torch.linalg.solve = solve_per_matrix
 
     # ---- record the RNG state right after the vision encoder is built
     orig_vis = bb.VeraceVisionEncoder
@@ -98,6 +117,7 @@ def main(ref_root: str) -> None:
                     rec["h_real"] = hr.detach().numpy().copy()
                     rec["h_imag"] = hi.detach().numpy().copy()
                 calls[kind].append(rec)
+                print(f"[gen] {kind} call {len(calls[kind])} (layer {layer}) recorded", flush=True)
             return fn
 
         hooks = []

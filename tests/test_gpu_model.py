@@ -41,7 +41,27 @@ def cpu_model(device):
     return m.to(device).eval(), z
 
 
+def _sssd_state_fp64(attn, x, init):
+    """Final state of SSSDAttention on x by the fp64 closed-form oracle (projections in fp64)."""
+    import torch.nn.functional as F
+    from oracle import sssd_closed
+    W = {n: p.detach().double().cpu() for n, p in attn.state_dict().items()}
+    x = torch.from_numpy(np.asarray(x)).double()
+    H, D = attn.num_heads, attn.head_dim
+    q = F.normalize(F.linear(x, W["w_q.weight"]).view(x.shape[0], -1, H, D), dim=-1)
+    k = F.normalize(F.linear(x, W["w_k.weight"]).view(x.shape[0], -1, H, D), dim=-1)
+    v = F.normalize(F.linear(x, W["w_v.weight"]).view(x.shape[0], -1, H, D), dim=-1)
+    dl = 0.1 * torch.sigmoid(F.linear(x, W["w_delta.weight"]))
+    _, p64 = sssd_closed.sssd_scan_closed_c(q.numpy(), k.numpy(), v.numpy(), dl.numpy(),
+                                            None if init is None else np.asarray(init, np.float64))
+    return p64
+
+
 def test_cpu_config_sssd_layers(device, cpu_model):
+    """Outputs against the reference's own outputs at the fp32 bar (1e-5).  The final state
+    is held to 1e-5 against the fp64 closed form.  Against the reference's fp32 eager state,
+    the bar widens by that state's own distance from fp64 (1.2e-5 here, from its LU solves and
+    Blelloch products), as the SURVEY's adjudication rule prescribes where fp32 eager drifts."""
     m, z = cpu_model
     n = int(z["cpu/sssd_calls"])
     assert n == 4  # 2 layers x 2 batch items (ACDE runs the layers per item)
@@ -49,18 +69,42 @@ def test_cpu_config_sssd_layers(device, cpu_model):
         layer = int(z[f"cpu/sssd/{j}/layer"])
         print(f"[case] cpu-config SSSD call {j} layer {layer}", flush=True)
         x = torch.from_numpy(z[f"cpu/sssd/{j}/x"]).to(device)
-        init = None
-        if f"cpu/sssd/{j}/init" in z.files:
-            init = torch.from_numpy(z[f"cpu/sssd/{j}/init"]).to(device)
+        init_np = z[f"cpu/sssd/{j}/init"] if f"cpu/sssd/{j}/init" in z.files else None
+        init = None if init_np is None else torch.from_numpy(init_np).to(device)
         with torch.no_grad():
             y, st = m.layers[layer].sssd_attn(x, initial_state=init, return_state=True)
         torch.cuda.synchronize()
-        ey, es = _rel(y.cpu(), z[f"cpu/sssd/{j}/y"]), _rel(st.cpu(), z[f"cpu/sssd/{j}/state"])
-        print(f"  rel y={ey:.2e} state={es:.2e}", flush=True)
-        assert ey <= 1e-5 and es <= 1e-5
+        p64 = _sssd_state_fp64(m.layers[layer].sssd_attn, z[f"cpu/sssd/{j}/x"], init_np)
+        ref_st = z[f"cpu/sssd/{j}/state"]
+        ey = _rel(y.cpu(), z[f"cpu/sssd/{j}/y"])
+        es64, es_ref, ref_own = _rel(st.cpu(), p64), _rel(st.cpu(), ref_st), _rel(ref_st, p64)
+        print(f"  rel y={ey:.2e}; state vs fp64={es64:.2e}, vs reference={es_ref:.2e} "
+              f"(reference vs fp64 {ref_own:.2e})", flush=True)
+        assert ey <= 1e-5 and es64 <= 1e-5 and es_ref <= 1e-5 + ref_own
+
+
+def _cham_state_fp64(cham, x):
+    """Final raw hologram of ContinuousHolographicMemory on x (one item) by the fp64 closed
+    form (projections in fp64, cham_memory.py:128-155; no readout)."""
+    import torch.nn.functional as F
+    from oracle import cham_scan
+    W = {n: p.detach().double().cpu() for n, p in cham.state_dict().items()}
+    x = torch.from_numpy(np.asarray(x)).double()
+    q = F.normalize(F.linear(x, W["w_q.weight"]), dim=-1)
+    k = F.normalize(F.linear(x, W["w_k.weight"]), dim=-1)
+    v = F.normalize(F.silu(F.linear(x, W["w_v.weight"])), dim=-1)
+    g = 0.1 * torch.sigmoid(F.linear(x, W["w_gamma.weight"])).squeeze(-1)
+    _, (hr, hi) = cham_scan.cham_scan_closed(q.numpy(), k.numpy(), v.numpy(), g.numpy(),
+                                             readout=False)
+    return hr, hi
 
 
 def test_cpu_config_cham_layers(device, cpu_model):
+    """Outputs and the raw state's leading 32 x 32 block against the reference's own (1e-5).
+    The state norm is held to 1e-5 against the fp64 closed form.  Against the reference's fp32
+    eager norm, the bar widens by that norm's own distance from fp64 (its solves, prefix scan
+    and products in fp32; the reference's comment puts its unitarity drift after 256 tokens
+    at ~1e-4)."""
     m, z = cpu_model
     n = int(z["cpu/cham_calls"])
     assert n == 4
@@ -73,10 +117,17 @@ def test_cpu_config_cham_layers(device, cpu_model):
         torch.cuda.synchronize()
         ey = _rel(y.cpu(), z[f"cpu/cham/{j}/y"])
         er = _rel(hr[0, :32, :32].cpu(), z[f"cpu/cham/{j}/h_real/slice"])
+        hr64, _ = _cham_state_fp64(m.layers[layer].cham_memory, z[f"cpu/cham/{j}/x"])
+        n64 = float(np.linalg.norm(hr64))
+        n_ref = float(z[f"cpu/cham/{j}/h_real/norm"])
         nr = float(hr.double().norm())
-        en = abs(nr - float(z[f"cpu/cham/{j}/h_real/norm"])) / float(z[f"cpu/cham/{j}/h_real/norm"])
-        print(f"  rel y={ey:.2e} state slice={er:.2e} norm={en:.2e}", flush=True)
-        assert ey <= 1e-5 and er <= 1e-5 and en <= 1e-5
+        en64, en_ref, ref_own = abs(nr - n64) / n64, abs(nr - n_ref) / n_ref, abs(n_ref - n64) / n64
+        es64 = _rel(hr[0].double().cpu(), hr64[0])
+        print(f"  rel y={ey:.2e} state slice={er:.2e}; state vs fp64={es64:.2e}; ||H_real|| vs "
+              f"fp64={en64:.2e}, vs reference={en_ref:.2e} (reference vs fp64 {ref_own:.2e})",
+              flush=True)
+        assert ey <= 1e-5 and er <= 1e-5 and es64 <= 1e-5 and en64 <= 1e-5
+        assert en_ref <= 1e-5 + ref_own
 
 
 def test_cpu_config_model_logits(device, cpu_model):
@@ -96,7 +147,17 @@ def test_cpu_config_model_logits(device, cpu_model):
     print(f"  logits head={e_head:.2e} sum={e_sum:.2e} sq={e_sq:.2e} argmax agree={agree:.4f} "
           f"states={e_st:.2e}", flush=True)
     assert np.array_equal(depth.cpu().numpy(), z["cpu/depth"])
-    assert e_head <= 1e-4 and e_sum <= 1e-4 and e_sq <= 1e-4 and e_st <= 1e-5
+    # final SSSD states: 1e-5 against the fp64 closed form run on the reference's per-call
+    # inputs (the same calls, in the same order); against the reference's fp32 eager states
+    # the bar widens by their own distance from fp64 (see test_cpu_config_sssd_layers)
+    p64 = np.stack([np.stack([_sssd_state_fp64(m.layers[l].sssd_attn, z[f"cpu/sssd/{2 * l + i}/x"],
+                                               None)[0] for i in range(2)]) for l in range(2)])
+    p64 = p64.reshape(z["cpu/sssd_states"].shape)
+    assert all(int(z[f"cpu/sssd/{2 * l + i}/layer"]) == l for l in range(2) for i in range(2))
+    e64, ref_own = _rel(st, p64), _rel(z["cpu/sssd_states"], p64)
+    print(f"  states vs fp64={e64:.2e} (reference vs fp64 {ref_own:.2e})", flush=True)
+    assert e_head <= 1e-4 and e_sum <= 1e-4 and e_sq <= 1e-4
+    assert e64 <= 1e-5 and e_st <= 1e-5 + ref_own
     assert agree >= 0.99
 
 
@@ -144,7 +205,9 @@ def test_tiny_model_acde_static_and_step(device, tiny):
     ed = float(np.abs(depth.cpu().numpy() - z["tiny/depth"]).max())
     ed1 = float(np.abs(depth1.cpu().numpy() - z["tiny/depth_step"]).max())
     w0, w1 = _check_states(states, z, "states"), _check_states(states1, z, "states_step")
-    halted = float((z["tiny/depth"] < 4).mean())
+    # depth = N(t) + R(t) (acd_engine.py:67-79): a token still active after all 4 layers
+    # counts 4 plus its remainder (> 4); one that halted earlier counts at most 4
+    halted = float((z["tiny/depth"] <= 4 + 1e-6).mean())
     print(f"  logits acde={e:.2e} step={e1:.2e} static={es:.2e} depth err={ed:.1e}/{ed1:.1e} "
           f"states={w0:.2e}/{w1:.2e} (fraction of tokens halting early {halted:.2f})", flush=True)
     assert 0.0 < halted < 1.0  # the per-item gathered path ran

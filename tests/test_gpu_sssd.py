@@ -256,9 +256,10 @@ def test_module_matches_reference_golden(device):
 
 def test_module_rejects_cpu_and_grad_without_backward(device):
     """CPU inputs raise; inputs that require grad raise in the forward when no backward
-    kernel exists for the head_dim (16 here), instead of failing later in backward()."""
+    kernel exists for the head_dim (the backward covers 1 .. 256; 264 here), instead of
+    failing later in backward()."""
     from verace_amd import SSSDAttention
-    m = SSSDAttention(hidden_dim=32, num_heads=2, head_dim=16)
+    m = SSSDAttention(hidden_dim=32, num_heads=1, head_dim=264)
     with pytest.raises(RuntimeError):
         m(torch.randn(1, 4, 32))
     m = m.to(device)
