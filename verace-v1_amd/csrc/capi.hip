@@ -1,10 +1,14 @@
 // extern "C" entry points of libverace_sssd.so (declared in include/verace_sssd.h).
 // Argument checking and dispatch only; the kernels live in sssd_*.hip / cham_*.hip.
+#include <atomic>
+
 #include "vmi_common.h"
 #include "vmi_dispatch.h"
 
 namespace {
 thread_local int g_last_hip_error = 0;
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];  // 0: not queried yet
 }  // namespace
 
 namespace vmi {
@@ -12,6 +16,25 @@ int hip_status(hipError_t e) {
   if (e == hipSuccess) return VMI_OK;
   g_last_hip_error = static_cast<int>(e);
   return VMI_ERR_HIP;
+}
+
+hipError_t device_cu_count(int* cus) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int c = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *cus = c;
+      return hipSuccess;
+    }
+  }
+  int c = 0;
+  e = hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  if (dev >= 0 && dev < kMaxDevices) g_cu_count[dev].store(c, std::memory_order_relaxed);
+  *cus = c;
+  return hipSuccess;
 }
 }  // namespace vmi
 

@@ -127,8 +127,8 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
       kr[m] = (EXACT || r < h) ? io<IO>::load(kb, r) : 0.f;
       vr[m] = (EXACT || r < h) ? io<IO>::load(vb, r) : 0.f;
     } else if constexpr (EXACT) {
-      xr[m] = *reinterpret_cast<const float4*>(ip.in_r + off0 + m * NRG * h);
-      xi[m] = *reinterpret_cast<const float4*>(ip.in_i + off0 + m * NRG * h);
+      xr[m] = ld_stream4(ip.in_r + off0 + m * NRG * h);
+      xi[m] = ld_stream4(ip.in_i + off0 + m * NRG * h);
       kr[m] = io<IO>::load(kb, r);
       vr[m] = io<IO>::load(vb, r);
     } else {
@@ -137,8 +137,8 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
       kr[m] = vr[m] = 0.f;
       if (r < h) {
         if (colok) {
-          xr[m] = *reinterpret_cast<const float4*>(ip.in_r + off0 + m * NRG * h);
-          xi[m] = *reinterpret_cast<const float4*>(ip.in_i + off0 + m * NRG * h);
+          xr[m] = ld_stream4(ip.in_r + off0 + m * NRG * h);
+          xi[m] = ld_stream4(ip.in_i + off0 + m * NRG * h);
         }
         kr[m] = io<IO>::load(kb, r);
         vr[m] = io<IO>::load(vb, r);
@@ -248,8 +248,8 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
     yi.z = fmaf(kr[m], ci[2], fmaf(vr[m], di[2], yi.z));
     yi.w = fmaf(kr[m], ci[3], fmaf(vr[m], di[3], yi.w));
     if (EXACT || (colok && r < h)) {
-      *reinterpret_cast<float4*>(ip.out_r + off0 + m * NRG * h) = yr;
-      *reinterpret_cast<float4*>(ip.out_i + off0 + m * NRG * h) = yi;
+      st_stream4(ip.out_r + off0 + m * NRG * h, yr);
+      st_stream4(ip.out_i + off0 + m * NRG * h, yi);
     }
     po[m] = fmaf(yr.x, qc.x, fmaf(yr.y, qc.y, fmaf(yr.z, qc.z, yr.w * qc.w)));
   }
@@ -307,8 +307,8 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
       xr[m] = eye4(rg + NRG * m, c0);
       xi[m] = make_float4(0.f, 0.f, 0.f, 0.f);
     } else {
-      xr[m] = *reinterpret_cast<const float4*>(sr + off0 + m * NRG * H);
-      xi[m] = *reinterpret_cast<const float4*>(si + off0 + m * NRG * H);
+      xr[m] = ld_stream4(sr + off0 + m * NRG * H);
+      xi[m] = ld_stream4(si + off0 + m * NRG * H);
     }
   }
 #pragma unroll
@@ -343,8 +343,8 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
         tr[m - RR] = eye4(rg + NRG * m, c0);
         ti[m - RR] = make_float4(0.f, 0.f, 0.f, 0.f);
       } else {
-        tr[m - RR] = *reinterpret_cast<const float4*>(sr + off0 + m * NRG * H);
-        ti[m - RR] = *reinterpret_cast<const float4*>(si + off0 + m * NRG * H);
+        tr[m - RR] = ld_stream4(sr + off0 + m * NRG * H);
+        ti[m - RR] = ld_stream4(si + off0 + m * NRG * H);
       }
     }
 #pragma unroll
@@ -432,8 +432,8 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
     yi.y = fmaf(kr[m], ci[1], fmaf(vr[m], di[1], yi.y));
     yi.z = fmaf(kr[m], ci[2], fmaf(vr[m], di[2], yi.z));
     yi.w = fmaf(kr[m], ci[3], fmaf(vr[m], di[3], yi.w));
-    *reinterpret_cast<float4*>(wr + off0 + m * NRG * H) = yr;
-    *reinterpret_cast<float4*>(wi + off0 + m * NRG * H) = yi;
+    st_stream4(wr + off0 + m * NRG * H, yr);
+    st_stream4(wi + off0 + m * NRG * H, yi);
     if (readout) {  // this row's readout partial, summed over the 8 column groups
       float po = fmaf(yr.x, qc.x, fmaf(yr.y, qc.y, fmaf(yr.z, qc.z, yr.w * qc.w)));
 #pragma unroll

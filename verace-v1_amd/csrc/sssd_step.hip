@@ -59,7 +59,7 @@ __global__ __launch_bounds__(NT) void sssd_step128_kernel(
     if (si >= 0) {
       const float* src = psi_in + si * DD + c0;
 #pragma unroll
-      for (int m = 0; m < RPT; ++m) st[m] = *reinterpret_cast<const float4*>(src + (rg + 8 * m) * D);
+      for (int m = 0; m < RPT; ++m) st[m] = ld_stream4(src + (rg + 8 * m) * D);
     } else {
 #pragma unroll
       for (int m = 0; m < RPT; ++m) {
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(NT) void sssd_step128_kernel(
       x.y = fmaf(kr[m], al.y, fmaf(vr[m], be.y, x.y));
       x.z = fmaf(kr[m], al.z, fmaf(vr[m], be.z, x.z));
       x.w = fmaf(kr[m], al.w, fmaf(vr[m], be.w, x.w));
-      if (!Map::kSlotted || di >= 0) *reinterpret_cast<float4*>(dst + (rg + 8 * m) * D) = x;
+      if (!Map::kSlotted || di >= 0) st_stream4(dst + (rg + 8 * m) * D, x);
       po[m] = fmaf(x.x, qc.x, fmaf(x.y, qc.y, fmaf(x.z, qc.z, x.w * qc.w)));
     }
     // reduce-scatter po[] over the 32 lanes (cg) of this half-wave: after the
@@ -212,10 +212,8 @@ template <typename IO, typename Map>
 hipError_t launch_typed(const void* q, const void* k, const void* v, const void* delta,
                         int delta_dtype, const float* psi_in, void* out, float* psi_out,
                         const Map& map, int BH, int H, hipStream_t stream) {
-  int dev = 0, cus = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  int cus = 0;
+  hipError_t e = device_cu_count(&cus);
   if (e != hipSuccess) return e;
   const int grid = BH < cus ? BH : cus;
   hipLaunchKernelGGL((sssd_step128_kernel<IO, Map>), dim3(grid), dim3(NT), 0, stream,

@@ -10,6 +10,10 @@ namespace vmi {
 // capi.hip: maps a HIP error to VMI_ERR_HIP and records it for vmi_last_hip_error().
 int hip_status(hipError_t e);
 
+// capi.hip: the compute-unit count of the current device, queried once per device and
+// cached (launchers that size their grid by it make no runtime query per launch).
+hipError_t device_cu_count(int* cus);
+
 // Where the [D, D] state of head bh = b*H + h (batch item b, head h) lives, as an index
 // into psi_in / psi_out in units of D*D floats:
 //   DenseStates  index bh (the reference layout [B, H, D, D]);
