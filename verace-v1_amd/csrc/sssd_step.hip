@@ -1,24 +1,29 @@
 // Single-token SSSD step (decode) for head_dim 128: Psi' = R Psi, o = Psi' q.
 //
 // The step is bound by HBM traffic: every (batch, head) state (64 KiB fp32) is read
-// once and written once, while the arithmetic is ~10 D^2 flops.  A workgroup can only
-// start writing a state after it has read all of it (a = k^T Psi and b = v^T Psi are
-// sums over every row), so one workgroup per head would read all states first and
-// write them all afterwards, leaving HBM reads and writes unoverlapped.  Here the
-// workgroups are persistent: workgroup w handles heads w, w + G, w + 2G, ... and
-// issues the loads of its next head before it reduces, updates and stores the
-// current one, so the reads of one head overlap the writes of the previous one.
+// once and written once, while the arithmetic is ~10 D^2 flops.  Nothing of a column
+// can be written before the whole column has been read (a = k^T Psi and b = v^T Psi are
+// sums over its rows), but columns are independent of each other until the output
+// o = Psi' q, which sums over them.  A head is therefore processed as two units of 64
+// columns: the first unit's update and store go out while the second unit's loads are
+// still in flight, and o accumulates over the units in registers.  Workgroups are
+// persistent, two per CU (so the reduce and barrier phases of one overlap the memory
+// traffic of the other): workgroup w handles heads w, w + G, ..., and the loads of the
+// next unit (of this head, or unit 0 of the next head) are issued before the current
+// unit is reduced, updated and stored.  Measured at DEC (B64 H8, 12 rotating layers of
+// states updated in place): 12.6 us per layer against 14.1 us for whole-head units on
+// one workgroup per CU; a plain read-modify-write stream of the same bytes takes 12.0 us.
 //
-// Layout (as in the token-sequential kernel): thread (rg, cg) owns rows rg + 8m
-// (m = 0..15) and columns 4cg .. 4cg+3, so every state load and store is a
-// coalesced float4.  Per head (reference recurrence sssd_attention.py:160-175 at
-// seq_len 1, closed form):
-//   a = k^T Psi, b = v^T Psi     per-thread partials over 16 rows, combined across
-//                                the two half-waves with a lane swap and across
+// Layout of a unit: thread (rg, cg), rg = tid / 16, cg = tid % 16, owns rows rg + 16m
+// (m = 0..7) and the unit's columns 4cg .. 4cg+3, so every state load and store is a
+// coalesced float4 (a 256-byte row segment per 16 lanes).  Per unit (reference recurrence
+// sssd_attention.py:160-175 at seq_len 1, closed form):
+//   a = k^T Psi, b = v^T Psi     per-thread partials over 8 rows, combined across the
+//                                four row groups of a wave with lane swaps and across
 //                                the four waves in LDS
-//   Psi += k alpha + v beta      alpha, beta from vmi::cayley_coeffs
-//   o = Psi q                    row partials reduce-scattered over the 32 lanes
-//                                that share a row group
+//   Psi += k alpha + v beta      alpha, beta from vmi::cayley_coeffs (once per head)
+//   o += Psi q                   row partials over this unit's columns; after the last
+//                                unit reduce-scattered over the 16 lanes of a row group
 // Where a head's state is read and written is the Map template parameter
 // (vmi_dispatch.h): the dense [B, H, D, D] layout, or slots of a decode state cache
 // (state_cache.hip), which may differ between read and write (copy-on-write).
@@ -30,42 +35,50 @@ namespace step {
 
 constexpr int D = 128;
 constexpr int NT = 256;
-constexpr int RPT = 16;  // rows per thread
+constexpr int UC = 64;            // state columns per unit
+constexpr int NU = D / UC;        // units per head
+constexpr int CG = UC / 4;        // float4 column groups per unit
+constexpr int RG = NT / CG;       // row groups
+constexpr int RPT = D / RG;       // rows per thread
+constexpr int WG_PER_CU = 2;
+static_assert(RPT == CG / 2, "the o reduce-scatter leaves one row per lane pair");
+static_assert(NU % 2 == 0, "units alternate two register buffers and two LDS buffers");
 
 template <typename IO, typename Map>
-__global__ __launch_bounds__(NT) void sssd_step128_kernel(
+__global__ __launch_bounds__(NT, WG_PER_CU) void sssd_step128_kernel(
     const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
     const void* __restrict__ delta, int delta_dtype, const float* psi_in, IO* __restrict__ out,
     float* psi_out, Map map, int BH, int H) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int cg = tid & 31, rg = tid >> 5;
+  const int cg = tid % CG, rg = tid / CG;
   const int c0 = 4 * cg;
   constexpr int64_t DD = static_cast<int64_t>(D) * D;
 
-  __shared__ float s_tok[2][3][D];   // q, k, v (fp32) of the head being processed, x2
+  __shared__ float s_tok[2][3][D];          // q, k, v (fp32) of the head, x2 (head parity)
   __shared__ float s_delta[2];
-  __shared__ float4 s_red[2][4][2][D / 4];  // per wave: a and b partials, x2
+  __shared__ float4 s_red[2][4][2][CG];     // per wave: a and b partials, x2 (unit parity)
 
-  // state of the current and the next head (double-buffered registers)
-  float4 st0[RPT], st1[RPT];
+  // state of the current and the next unit (double-buffered registers)
+  float4 sa[RPT], sb[RPT];
   // this thread's share of the next head's q/k/v row (elements tid and tid + 256 of
   // the 384-element concatenation) and its delta
   float tk0 = 0.f, tk1 = 0.f, tdl = 0.f;
 
-  auto load_state = [&](float4* st, int bh) {
+  auto load_unit = [&](float4* st, int bh, int u) {
     const int64_t si = psi_in != nullptr ? map.in_index(bh, H) : -1;  // uniform; < 0: identity
+    const int cb = UC * u + c0;
     if (si >= 0) {
-      const float* src = psi_in + si * DD + c0;
+      const float* src = psi_in + si * DD + cb;
 #pragma unroll
-      for (int m = 0; m < RPT; ++m) st[m] = ld_stream4(src + (rg + 8 * m) * D);
+      for (int m = 0; m < RPT; ++m) st[m] = ld_stream4(src + (rg + RG * m) * D);
     } else {
 #pragma unroll
       for (int m = 0; m < RPT; ++m) {
-        const int r = rg + 8 * m;
-        st[m] = make_float4(r == c0 ? 1.f : 0.f, r == c0 + 1 ? 1.f : 0.f, r == c0 + 2 ? 1.f : 0.f,
-                            r == c0 + 3 ? 1.f : 0.f);
+        const int r = rg + RG * m;
+        st[m] = make_float4(r == cb ? 1.f : 0.f, r == cb + 1 ? 1.f : 0.f, r == cb + 2 ? 1.f : 0.f,
+                            r == cb + 3 ? 1.f : 0.f);
       }
     }
   };
@@ -82,38 +95,40 @@ __global__ __launch_bounds__(NT) void sssd_step128_kernel(
     if (tid == 0) s_delta[buf] = tdl;
   };
 
-  // process head bh whose state is in st and whose q/k/v are in s_tok[buf]
-  auto process = [&](float4* st, int bh, int buf) {
-    float kr[RPT], vr[RPT];
+  float kr[RPT], vr[RPT];  // k and v at this thread's rows (zero for a guarded token)
+  cayley2 M;
+  float po[RPT];           // o partials at this thread's rows, summed over units
+
+  // unit u of head bh: columns UC u .. UC u + UC - 1 in st, q/k/v in s_tok[buf]
+  auto process = [&](float4* st, int bh, int u, int buf) {
+    if (u == 0) {
 #pragma unroll
-    for (int m = 0; m < RPT; ++m) {
-      kr[m] = s_tok[buf][1][rg + 8 * m];
-      vr[m] = s_tok[buf][2][rg + 8 * m];
-    }
-    const float4 qc = *reinterpret_cast<const float4*>(&s_tok[buf][0][c0]);
-    // Gram entries, reduced by every wave over the full vectors
-    float kk, vv, kv;
-    {
+      for (int m = 0; m < RPT; ++m) {
+        kr[m] = s_tok[buf][1][rg + RG * m];
+        vr[m] = s_tok[buf][2][rg + RG * m];
+      }
+      // Gram entries, reduced by every wave over the full vectors
       const float k0 = s_tok[buf][1][lane], k1 = s_tok[buf][1][lane + 64];
       const float v0 = s_tok[buf][2][lane], v1 = s_tok[buf][2][lane + 64];
-      kk = fmaf(k0, k0, k1 * k1);
-      vv = fmaf(v0, v0, v1 * v1);
-      kv = fmaf(k0, v0, k1 * v1);
+      float kk = fmaf(k0, k0, k1 * k1);
+      float vv = fmaf(v0, v0, v1 * v1);
+      float kv = fmaf(k0, v0, k1 * v1);
 #pragma unroll
       for (int off = 32; off >= 1; off >>= 1) {
         kk += __shfl_xor(kk, off);
         vv += __shfl_xor(vv, off);
         kv += __shfl_xor(kv, off);
       }
-    }
-    // a token with a non-finite Cayley factor is the identity (uniform over the workgroup)
-    bool ok;
-    const cayley2 M = cayley_guarded(s_delta[buf], kk, vv, kv, ok);
-    if (!ok) {
+      // a token with a non-finite Cayley factor is the identity (uniform over the workgroup)
+      bool ok;
+      M = cayley_guarded(s_delta[buf], kk, vv, kv, ok);
+      if (!ok) {
 #pragma unroll
-      for (int m = 0; m < RPT; ++m) kr[m] = vr[m] = 0.f;
+        for (int m = 0; m < RPT; ++m) kr[m] = vr[m] = 0.f;
+      }
     }
-    // column partials over this thread's 16 rows
+    const float4 qc = *reinterpret_cast<const float4*>(&s_tok[buf][0][UC * u + c0]);
+    // column partials over this thread's rows
     float4 pa = make_float4(0.f, 0.f, 0.f, 0.f), pb = pa;
 #pragma unroll
     for (int m = 0; m < RPT; ++m) {
@@ -122,20 +137,23 @@ __global__ __launch_bounds__(NT) void sssd_step128_kernel(
       pb.x = fmaf(vr[m], st[m].x, pb.x); pb.y = fmaf(vr[m], st[m].y, pb.y);
       pb.z = fmaf(vr[m], st[m].z, pb.z); pb.w = fmaf(vr[m], st[m].w, pb.w);
     }
-    // the two half-waves hold row groups 2w and 2w+1 of the same columns
-    pa.x += __shfl_xor(pa.x, 32); pa.y += __shfl_xor(pa.y, 32);
-    pa.z += __shfl_xor(pa.z, 32); pa.w += __shfl_xor(pa.w, 32);
-    pb.x += __shfl_xor(pb.x, 32); pb.y += __shfl_xor(pb.y, 32);
-    pb.z += __shfl_xor(pb.z, 32); pb.w += __shfl_xor(pb.w, 32);
-    if (lane < 32) {
-      s_red[buf][wave][0][cg] = pa;
-      s_red[buf][wave][1][cg] = pb;
+    // lanes cg + CG j of a wave hold its row groups j of the same columns
+#pragma unroll
+    for (int off = CG; off < 64; off <<= 1) {
+      pa.x += __shfl_xor(pa.x, off); pa.y += __shfl_xor(pa.y, off);
+      pa.z += __shfl_xor(pa.z, off); pa.w += __shfl_xor(pa.w, off);
+      pb.x += __shfl_xor(pb.x, off); pb.y += __shfl_xor(pb.y, off);
+      pb.z += __shfl_xor(pb.z, off); pb.w += __shfl_xor(pb.w, off);
+    }
+    if (lane < CG) {
+      s_red[u & 1][wave][0][cg] = pa;
+      s_red[u & 1][wave][1][cg] = pb;
     }
     __syncthreads();
-    float4 a4 = s_red[buf][0][0][cg], b4 = s_red[buf][0][1][cg];
+    float4 a4 = s_red[u & 1][0][0][cg], b4 = s_red[u & 1][0][1][cg];
 #pragma unroll
     for (int w = 1; w < 4; ++w) {
-      const float4 xa = s_red[buf][w][0][cg], xb = s_red[buf][w][1][cg];
+      const float4 xa = s_red[u & 1][w][0][cg], xb = s_red[u & 1][w][1][cg];
       a4.x += xa.x; a4.y += xa.y; a4.z += xa.z; a4.w += xa.w;
       b4.x += xb.x; b4.y += xb.y; b4.z += xb.z; b4.w += xb.w;
     }
@@ -145,8 +163,7 @@ __global__ __launch_bounds__(NT) void sssd_step128_kernel(
                                   fmaf(M.m10, a4.z, M.m11 * b4.z), fmaf(M.m10, a4.w, M.m11 * b4.w));
     // update, store, and row partials of o = Psi' q
     const int64_t di = map.out_index(bh, H);  // uniform; < 0 (slotted maps only): not written
-    float* dst = psi_out + (di < 0 ? 0 : di) * DD + c0;
-    float po[RPT];
+    float* dst = psi_out + (di < 0 ? 0 : di) * DD + UC * u + c0;
 #pragma unroll
     for (int m = 0; m < RPT; ++m) {
       float4 x = st[m];
@@ -154,57 +171,63 @@ __global__ __launch_bounds__(NT) void sssd_step128_kernel(
       x.y = fmaf(kr[m], al.y, fmaf(vr[m], be.y, x.y));
       x.z = fmaf(kr[m], al.z, fmaf(vr[m], be.z, x.z));
       x.w = fmaf(kr[m], al.w, fmaf(vr[m], be.w, x.w));
-      if (!Map::kSlotted || di >= 0) st_stream4(dst + (rg + 8 * m) * D, x);
-      po[m] = fmaf(x.x, qc.x, fmaf(x.y, qc.y, fmaf(x.z, qc.z, x.w * qc.w)));
+      if (!Map::kSlotted || di >= 0) st_stream4(dst + (rg + RG * m) * D, x);
+      const float p = fmaf(x.x, qc.x, fmaf(x.y, qc.y, fmaf(x.z, qc.z, x.w * qc.w)));
+      po[m] = u == 0 ? p : po[m] + p;
     }
-    // reduce-scatter po[] over the 32 lanes (cg) of this half-wave: after the
-    // halving steps lane cg holds the sum for row rg + 8*mloc, paired with lane cg^1
-    int mloc = 0;
+    if (u == NU - 1) {
+      // reduce-scatter po[] over the CG lanes of this row group: after the halving
+      // steps lane cg holds the sum for row rg + RG*mloc, paired with lane cg^1
+      int mloc = 0;
 #pragma unroll
-    for (int off = 16, cnt = RPT; off >= 2; off >>= 1, cnt >>= 1) {
-      const int half = cnt >> 1;
-      const bool hi = (lane & off) != 0;
+      for (int off = CG / 2, cnt = RPT; off >= 2; off >>= 1, cnt >>= 1) {
+        const int half = cnt >> 1;
+        const bool hi = (lane & off) != 0;
 #pragma unroll
-      for (int i = 0; i < RPT / 2; ++i) {
-        if (i < half) {
-          const float send = hi ? po[i] : po[i + half];
-          const float keep = hi ? po[i + half] : po[i];
-          po[i] = keep + __shfl_xor(send, off);
+        for (int i = 0; i < RPT / 2; ++i) {
+          if (i < half) {
+            const float send = hi ? po[i] : po[i + half];
+            const float keep = hi ? po[i + half] : po[i];
+            po[i] = keep + __shfl_xor(send, off);
+          }
         }
+        if (hi) mloc += half;
       }
-      if (hi) mloc += half;
+      const float o_row = po[0] + __shfl_xor(po[0], 1);
+      if (out != nullptr && (lane & 1) == 0)
+        io<IO>::store(out, static_cast<int64_t>(bh) * D + rg + RG * mloc, o_row);
     }
-    const float o_row = po[0] + __shfl_xor(po[0], 1);
-    if (out != nullptr && (lane & 1) == 0) io<IO>::store(out, static_cast<int64_t>(bh) * D + rg + 8 * mloc, o_row);
   };
 
   const int G = gridDim.x;
   int bh = blockIdx.x;
   if (bh >= BH) return;  // uniform
-  load_state(st0, bh);
+  int buf = 0;
+  load_unit(sa, bh, 0);
   load_tok(bh);
   commit_tok(0);
-  // iterations alternate the register buffers st0 / st1 and the LDS buffers 0 / 1
+  // units alternate the register buffers sa / sb and the s_red buffers; heads alternate
+  // the s_tok buffers.  The next unit's loads are issued before the barrier that
+  // publishes this head's q/k/v (issuing them after it measured 1.2 us slower).
   for (;;) {
     const int bh1 = bh + G;
-    if (bh1 < BH) {
-      load_state(st1, bh1);
-      load_tok(bh1);
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      float4* cur = (u & 1) ? sb : sa;
+      float4* nxt = (u & 1) ? sa : sb;
+      if (u + 1 < NU) {
+        load_unit(nxt, bh, u + 1);
+      } else if (bh1 < BH) {
+        load_unit(nxt, bh1, 0);
+        load_tok(bh1);
+      }
+      if (u == 0) __syncthreads();  // s_tok[buf] complete; s_red free
+      process(cur, bh, u, buf);
     }
-    __syncthreads();  // s_tok[0] complete; s_red[0] free
-    process(st0, bh, 0);
     if (bh1 >= BH) break;
-    commit_tok(1);
-    const int bh2 = bh1 + G;
-    if (bh2 < BH) {
-      load_state(st0, bh2);
-      load_tok(bh2);
-    }
-    __syncthreads();  // s_tok[1] complete; s_red[1] free
-    process(st1, bh1, 1);
-    if (bh2 >= BH) break;
-    commit_tok(0);
-    bh = bh2;
+    commit_tok(buf ^ 1);
+    buf ^= 1;
+    bh = bh1;
   }
 }
 
@@ -215,7 +238,7 @@ hipError_t launch_typed(const void* q, const void* k, const void* v, const void*
   int cus = 0;
   hipError_t e = device_cu_count(&cus);
   if (e != hipSuccess) return e;
-  const int grid = BH < cus ? BH : cus;
+  const int grid = BH < WG_PER_CU * cus ? BH : WG_PER_CU * cus;
   hipLaunchKernelGGL((sssd_step128_kernel<IO, Map>), dim3(grid), dim3(NT), 0, stream,
                      static_cast<const IO*>(q), static_cast<const IO*>(k),
                      static_cast<const IO*>(v), delta, delta_dtype, psi_in, static_cast<IO*>(out),

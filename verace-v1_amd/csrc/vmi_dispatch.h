@@ -74,8 +74,9 @@ hipError_t launch_sssd_seq(const void* q, const void* k, const void* v, const vo
                            float* psi_out, int B, int T, int H, int D, hipStream_t stream,
                            const SlotArgs& map);
 
-// sssd_step.hip: single-token step for head_dim 128 (persistent, loads of the next
-// head overlap the update and store of the current one).  psi_in may equal psi_out;
+// sssd_step.hip: single-token step for head_dim 128 (persistent, two workgroups per CU,
+// heads in units of 64 columns whose loads run one unit ahead of the update and store).
+// psi_in may equal psi_out;
 // `map` places the states (dense, or slots of a decode state cache).
 bool use_step128(int64_t T, int64_t D);
 hipError_t launch_sssd_step128(const void* q, const void* k, const void* v, const void* delta,
