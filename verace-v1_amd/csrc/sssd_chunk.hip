@@ -1013,54 +1013,59 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
 }
 
 // The segment start states: X = psi0 (identity if null), then X <- F_f X for the pass A
-// factors f = 0 .. nf-1 in order, storing start_s = X after every fstride-th factor
-// (fstride = 1: F_f = P_f; 2: F_2s, F_2s+1 are the two parts of segment s).
+// factors f = 0 .. nf-1 in order, storing start_s = X after every FSTRIDE-th factor
+// (FSTRIDE = 1: F_f = P_f; 2: F_2s, F_2s+1 are the two parts of segment s).
 // Left products act on the columns independently, so the chain of one sequence is
-// split over CARRY_SPLIT workgroups of CARRY_COLS columns each.  Every factor is read
-// with coalesced loads two products ahead and staged in LDS as a bf16 hi + lo pair;
-// the running columns X are kept in LDS the same way (transposed).  Wave (rb, ch)
-// produces rows 32rb .. 32rb+31 and columns 32ch .. 32ch+31 of the workgroup's block
-// with bf16x3 MFMA (hi*hi + hi*lo + lo*hi, fp32-faithful).
-constexpr int CARRY_SPLIT = 2;
-constexpr int CARRY_COLS = D / CARRY_SPLIT;         // 64
-constexpr int CARRY_WAVES = (D / 32) * (CARRY_COLS / 32);  // 8
-constexpr int CARRY_NT = CARRY_WAVES * 64;
+// split over CARRY_SPLIT workgroups of CARRY_COLS columns each (grid (BH, CARRY_SPLIT):
+// with BH a multiple of 8 the blocks of one sequence share an XCD, hence its L2 copy of
+// every factor).  Two roles per workgroup:
+//   producer waves load factor f + 1 (coalesced float4, one product ahead) and stage it
+//                  in LDS as a bf16 hi + lo pair (double-buffered) while
+//   consumer waves multiply factor f into the running columns X (kept in LDS the same
+//                  way, transposed): wave w produces rows 32w .. 32w+31 with bf16x3 MFMA
+//                  (hi*hi + hi*lo + lo*hi, fp32-faithful), then writes them back to X.
+// Both roles pass the same two LDS-only barriers per product.  (Staging on the same waves
+// as the products, one buffer, two column blocks per sequence: 18.2 us at OP.)
+constexpr int CARRY_SPLIT = 4;
+constexpr int CARRY_COLS = D / CARRY_SPLIT;          // 32
+constexpr int CARRY_CW = D / 32;                     // consumer waves (32 rows each)
+constexpr int CARRY_PW = 8;                          // producer waves
+constexpr int CARRY_NT = (CARRY_CW + CARRY_PW) * 64;
+constexpr int CARRY_PT = CARRY_PW * 64;
 constexpr int CP_LD = D + 8;   // bf16 per LDS row of a factor and of X^T (272 B)
-constexpr int CARRY_F4 = D * D / 4 / CARRY_NT;  // float4 of a factor per thread
+constexpr int CARRY_F4 = D * D / 4 / CARRY_PT;      // float4 of a factor per producer thread
+static_assert(CARRY_COLS == 32, "one 32-column MFMA tile per consumer wave");
 
+template <int FSTRIDE>
 __global__ __launch_bounds__(CARRY_NT) void sssd_carry_kernel(const float* psi0, const float* F,
-                                                              float* starts, int BH, int nf,
-                                                              int fstride) {
+                                                              float* starts, int BH, int nf) {
+  static_assert(FSTRIDE == 1 || FSTRIDE == 2, "one or two factors per segment");
   typedef mfma_t<__bf16> MM;
   typedef MM::v8 V8;
-  __shared__ __bf16 phi[D * CP_LD], plo[D * CP_LD];                    // factor, row-major
+  __shared__ __bf16 phi[2][D * CP_LD], plo[2][D * CP_LD];              // factor, row-major
   __shared__ __bf16 xhi[CARRY_COLS * CP_LD], xlo[CARRY_COLS * CP_LD];  // X^T: [n][k]
   const int bh = blockIdx.x, cb = blockIdx.y;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, g = lane >> 5;
-  const int rb = wave & 3, ch = wave >> 2;
   const int64_t DD = static_cast<int64_t>(D) * D;
-  auto put = [](__bf16* hi, __bf16* lo, int off, float x) {
-    const __bf16 h = static_cast<__bf16>(x);
-    hi[off] = h;
-    lo[off] = static_cast<__bf16>(x - static_cast<float>(h));
-  };
-  for (int e = tid; e < CARRY_COLS * D; e += CARRY_NT) {
-    const int row = e / CARRY_COLS, n = e - row * CARRY_COLS, colg = CARRY_COLS * cb + n;
-    put(xhi, xlo, n * CP_LD + row, psi0 ? psi0[bh * DD + row * D + colg] : (row == colg ? 1.f : 0.f));
-  }
-  typedef float4 Share[CARRY_F4];  // a thread's share of a factor: float4 index tid + NT*m
-  auto fetch = [&](Share& pf, int f) {
-    if (f >= nf) return;
+  if (nf <= 0) return;  // uniform
+  // producers: factor f + 1 is staged during product f, from registers loaded two
+  // products ahead (two register buffers; every fetch and stage is issued, clamped to the
+  // last factor past the end, so the waits count a fixed sequence of loads)
+  const int pt = tid - CARRY_CW * 64;
+  float4 pa[CARRY_F4], pb[CARRY_F4];
+  auto fetch = [&](float4* pf, int f) {  // 0 <= f < nf
     const float4* src = reinterpret_cast<const float4*>(F + (static_cast<int64_t>(f) * BH + bh) * DD);
 #pragma unroll
-    for (int m = 0; m < CARRY_F4; ++m) pf[m] = src[tid + CARRY_NT * m];
+    for (int m = 0; m < CARRY_F4; ++m) pf[m] = src[pt + CARRY_PT * m];
   };
-  auto step = [&](Share& pf, int f) {  // X <- F_f X
+  auto stage = [&](const float4* pf, int buf) {  // 8-byte stores of hi and lo
+    // not hoisted into the previous product's phase (it would wait for loads early)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int m = 0; m < CARRY_F4; ++m) {  // stage F_f as hi + lo (8-byte stores)
-      const int e = 4 * (tid + CARRY_NT * m);
+    for (int m = 0; m < CARRY_F4; ++m) {
+      const int e = 4 * (pt + CARRY_PT * m);
       const int row = e / D, c0 = e - row * D;
       const float xv[4] = {pf[m].x, pf[m].y, pf[m].z, pf[m].w};
       bf16x4 h4, l4;
@@ -1069,57 +1074,103 @@ __global__ __launch_bounds__(CARRY_NT) void sssd_carry_kernel(const float* psi0,
         h4[i] = static_cast<__bf16>(xv[i]);
         l4[i] = static_cast<__bf16>(xv[i] - static_cast<float>(h4[i]));
       }
-      *reinterpret_cast<bf16x4*>(&phi[row * CP_LD + c0]) = h4;
-      *reinterpret_cast<bf16x4*>(&plo[row * CP_LD + c0]) = l4;
-    }
-    __syncthreads();  // factor staged; X (initial or from the previous product) complete
-    fetch(pf, f + 2);
-    // Y = F[32rb .. +31][:] X[:][32ch .. +31]; A row = l32, B column = l32, k-slots
-    // 16ks + 8g + 0..7 in both operands
-    // three independent accumulator chains (hi hi, hi lo, lo hi) interleave in the MFMA
-    // pipeline instead of one chain of 24 dependent products
-    f32x16 Y = {}, Y1 = {}, Y2 = {};
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      const int ka = 16 * ks + 8 * g;
-      const V8 ah = *reinterpret_cast<const V8*>(&phi[(32 * rb + l32) * CP_LD + ka]);
-      const V8 al = *reinterpret_cast<const V8*>(&plo[(32 * rb + l32) * CP_LD + ka]);
-      const V8 bh8 = *reinterpret_cast<const V8*>(&xhi[(32 * ch + l32) * CP_LD + ka]);
-      const V8 bl8 = *reinterpret_cast<const V8*>(&xlo[(32 * ch + l32) * CP_LD + ka]);
-      Y = MM::mma32(ah, bh8, Y);
-      Y1 = MM::mma32(ah, bl8, Y1);
-      Y2 = MM::mma32(al, bh8, Y2);
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) Y[r] += Y1[r] + Y2[r];
-    __syncthreads();  // every wave has read the factor and X before they are replaced
-    // Y: lane (g, l32) holds rows 32rb + 8(r/4) + 4g + r%4 of column 32ch + l32
-    const int colw = 32 * ch + l32;
-    float* dst = (f + 1) % fstride == 0
-                     ? starts + (static_cast<int64_t>((f + 1) / fstride - 1) * BH + bh) * DD +
-                           CARRY_COLS * cb + colw
-                     : nullptr;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {  // rows 32rb + 8i + 4g + 0..3: 4 consecutive k of X^T
-      const int row0 = 32 * rb + 8 * i + 4 * g;
-      bf16x4 h4, l4;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float y = Y[4 * i + r];
-        if (dst) dst[(row0 + r) * D] = y;
-        h4[r] = static_cast<__bf16>(y);
-        l4[r] = static_cast<__bf16>(y - static_cast<float>(h4[r]));
-      }
-      *reinterpret_cast<bf16x4*>(&xhi[colw * CP_LD + row0]) = h4;
-      *reinterpret_cast<bf16x4*>(&xlo[colw * CP_LD + row0]) = l4;
+      *reinterpret_cast<bf16x4*>(&phi[buf][row * CP_LD + c0]) = h4;
+      *reinterpret_cast<bf16x4*>(&plo[buf][row * CP_LD + c0]) = l4;
     }
   };
-  Share p0, p1;
-  fetch(p0, 0);
-  fetch(p1, 1);
-  for (int f = 0; f < nf; f += 2) {
-    step(p0, f);
-    if (f + 1 < nf) step(p1, f + 1);
+  const bool producer = wave >= CARRY_CW;  // uniform per wave
+  if (producer) {
+    fetch(pa, 0);
+    fetch(pb, nf > 1 ? 1 : 0);
+  }
+  // X = the block's columns of psi0, transposed (identity if null)
+  if (psi0) {
+    for (int e = tid; e < CARRY_COLS * D; e += CARRY_NT) {
+      const int row = e / CARRY_COLS, n = e - row * CARRY_COLS;
+      const float x = psi0[bh * DD + row * D + CARRY_COLS * cb + n];
+      const __bf16 h = static_cast<__bf16>(x);
+      xhi[n * CP_LD + row] = h;
+      xlo[n * CP_LD + row] = static_cast<__bf16>(x - static_cast<float>(h));
+    }
+  } else {
+    constexpr int WPR = CP_LD / 4;  // 8-byte words per X^T row (padding included)
+    for (int w = tid; w < CARRY_COLS * WPR; w += CARRY_NT) {
+      const int n = w / WPR, k0 = 4 * (w - n * WPR), diag = CARRY_COLS * cb + n;
+      bf16x4 h4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) h4[i] = static_cast<__bf16>(k0 + i == diag ? 1.f : 0.f);
+      *reinterpret_cast<bf16x4*>(&xhi[n * CP_LD + k0]) = h4;
+      *reinterpret_cast<bf16x4*>(&xlo[n * CP_LD + k0]) = bf16x4{};
+    }
+  }
+  if (producer) {
+    stage(pa, 0);
+    fetch(pa, nf > 2 ? 2 : nf - 1);
+    lds_barrier();  // factor 0 staged, X complete
+    int f = 0;
+    for (; f + 1 < nf; f += 2) {
+      // product f reads buffer 0: stage factor f+1 into buffer 1
+      stage(pb, 1);
+      fetch(pb, f + 3 < nf ? f + 3 : nf - 1);
+      lds_barrier();  // product f has read its factor and X
+      lds_barrier();  // X updated; factor f+1 staged
+      // product f+1 reads buffer 1: stage factor f+2 (the last one again past the end)
+      // into buffer 0, read by product f before the barrier above
+      stage(pa, 0);
+      fetch(pa, f + 4 < nf ? f + 4 : nf - 1);
+      lds_barrier();
+      lds_barrier();
+    }
+    if (f < nf) {  // odd nf: the last product stages nothing
+      lds_barrier();
+      lds_barrier();
+    }
+  } else {
+    // consumers: X <- F_f X, rows 32 wave .. 32 wave + 31 of the block's columns
+    lds_barrier();
+    for (int f = 0; f < nf; ++f) {
+      const int buf = f & 1;
+      // A row = l32, B column = l32, k-slots 16ks + 8g + 0..7 in both operands; three
+      // independent accumulator chains (hi hi, hi lo, lo hi) interleave in the MFMA pipe
+      f32x16 Y = {}, Y1 = {}, Y2 = {};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const int ka = 16 * ks + 8 * g;
+        const V8 ah = *reinterpret_cast<const V8*>(&phi[buf][(32 * wave + l32) * CP_LD + ka]);
+        const V8 al = *reinterpret_cast<const V8*>(&plo[buf][(32 * wave + l32) * CP_LD + ka]);
+        const V8 bh8 = *reinterpret_cast<const V8*>(&xhi[l32 * CP_LD + ka]);
+        const V8 bl8 = *reinterpret_cast<const V8*>(&xlo[l32 * CP_LD + ka]);
+        Y = MM::mma32(ah, bh8, Y);
+        Y1 = MM::mma32(ah, bl8, Y1);
+        Y2 = MM::mma32(al, bh8, Y2);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) Y[r] += Y1[r] + Y2[r];
+      lds_barrier();  // every wave has read the factor and X before X is replaced
+      // Y: lane (g, l32) holds rows 32 wave + 8(r/4) + 4g + r%4 of column l32
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {  // rows 32 wave + 8i + 4g + 0..3: 4 consecutive k of X^T
+        const int row0 = 32 * wave + 8 * i + 4 * g;
+        bf16x4 h4, l4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float y = Y[4 * i + r];
+          h4[r] = static_cast<__bf16>(y);
+          l4[r] = static_cast<__bf16>(y - static_cast<float>(h4[r]));
+        }
+        *reinterpret_cast<bf16x4*>(&xhi[l32 * CP_LD + row0]) = h4;
+        *reinterpret_cast<bf16x4*>(&xlo[l32 * CP_LD + row0]) = l4;
+      }
+      if ((f + 1) % FSTRIDE == 0) {  // uniform: a segment start is complete
+        float* dst = starts + (static_cast<int64_t>((f + 1) / FSTRIDE - 1) * BH + bh) * DD +
+                     CARRY_COLS * cb + l32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dst[(32 * wave + 8 * i + 4 * g + r) * D] = Y[4 * i + r];
+      }
+      lds_barrier();  // X updated (and the next factor staged)
+    }
   }
 }
 
@@ -1198,9 +1249,12 @@ hipError_t run_chunked_args(chunk::Args a, const float* psi_in, void* out, float
                        dim3(chunk::Cfg<false>::NT), 0, stream, pa);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(chunk::sssd_carry_kernel, dim3(BH, chunk::CARRY_SPLIT),
-                       dim3(chunk::CARRY_NT), 0, stream,
-                       psi_in, P, starts, BH, p.nfactors, p.fstride);
+    if (p.fstride == 2)
+      hipLaunchKernelGGL(chunk::sssd_carry_kernel<2>, dim3(BH, chunk::CARRY_SPLIT),
+                         dim3(chunk::CARRY_NT), 0, stream, psi_in, P, starts, BH, p.nfactors);
+    else
+      hipLaunchKernelGGL(chunk::sssd_carry_kernel<1>, dim3(BH, chunk::CARRY_SPLIT),
+                         dim3(chunk::CARRY_NT), 0, stream, psi_in, P, starts, BH, p.nfactors);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
