@@ -57,31 +57,70 @@ def make_inputs(B, T, H, D, seed, dtype, device):
 
 
 def bench_scan(args, device):
+    """OP: the scan of B8 T4096 H8 D128 bf16 inputs from the identity, K timed steps.
+
+    A step is one vmi_sssd_scan_fwd call through the C ABI with prebuilt arguments and
+    preallocated outputs and workspace, as a serving loop calls it; two input sets of
+    ~200 MB each alternate, so the 256 MB MALL holds nothing useful from the previous step.
+    Events on the kernels' stream bracket every call.  The torch-facing
+    launch_sssd_hip_scan (argument checks and three allocations per call) is timed the same
+    way afterwards and reported beside it: its host time per call can exceed the scan's
+    device time on a slow host CPU, and then the events would time the host.
+    """
+    import ctypes
     import torch
-    from verace_amd import launch_sssd_hip_scan
+    from verace_amd import _lib, launch_sssd_hip_scan
     B, T, H, D = OP["B"], OP["T"], OP["H"], OP["D"]
     sets = []
     for s in range(2):
         cpu, dev = make_inputs(B, T, H, D, seed=s, dtype=torch.bfloat16, device=device)
         sets.append((cpu, dev))
     stream = torch.cuda.current_stream(device)
+    lib = _lib.load()
+    code = _lib.dtype_code(torch.bfloat16)
+    ws_bytes = ctypes.c_size_t(0)
+    _lib.check(lib.vmi_sssd_scan_workspace_bytes(B, T, H, D, code, ctypes.byref(ws_bytes)),
+               "vmi_sssd_scan_workspace_bytes")
+    sh = _lib.stream_handle(device)
+    vp = ctypes.c_void_p
+    bufs, argl = [], []
+    for _, (q, k, v, d) in sets:
+        out = torch.empty_like(q)
+        psi = torch.empty(B, H, D, D, device=device, dtype=torch.float32)
+        ws = torch.empty(max(ws_bytes.value, 1), device=device, dtype=torch.uint8)
+        bufs.append((out, psi, ws))
+        argl.append((vp(q.data_ptr()), vp(k.data_ptr()), vp(v.data_ptr()), vp(d.data_ptr()), code,
+                     code, None, vp(out.data_ptr()), vp(psi.data_ptr()), B, T, H, D,
+                     vp(ws.data_ptr()), ws_bytes.value, sh))
+    call = lib.vmi_sssd_scan_fwd
+
+    def timed(step, n):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(n)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(n):
+            evs[i][0].record(stream)
+            step(i)
+            evs[i][1].record(stream)
+        torch.cuda.synchronize()
+        return [a.elapsed_time(b) for a, b in evs], time.perf_counter() - t0
+
+    def capi_step(i):
+        st = call(*argl[i % 2])
+        if st != 0:
+            raise RuntimeError(f"vmi_sssd_scan_fwd failed: {st}")
+
     for i in range(args.warmup):
-        launch_sssd_hip_scan(*sets[i % 2][1])
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    outs = None
-    for i in range(args.steps):
-        evs[i][0].record(stream)
-        outs = launch_sssd_hip_scan(*sets[i % 2][1])
-        evs[i][1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per = [a.elapsed_time(b) for a, b in evs]  # ms
+        capi_step(i)
+    per, wall = timed(capi_step, args.steps)
+    outs = bufs[(args.steps - 1) % 2][:2]
     # parity spot check of the last step against the fp64 C oracle (two (b, h) slices)
     parity = check_scan(sets[(args.steps - 1) % 2][0], outs, B, H)
-    return per, wall, parity
+    for i in range(2):
+        launch_sssd_hip_scan(*sets[i % 2][1])
+    api, _ = timed(lambda i: launch_sssd_hip_scan(*sets[i % 2][1]), args.steps)
+    return per, wall, parity, api
 
 
 def check_scan(cpu_inputs, outs, B, H):
@@ -852,7 +891,7 @@ def main():
 
     import torch
     device = torch.device("cuda:0")
-    per, wall, parity = bench_scan(args, device)
+    per, wall, parity, api = bench_scan(args, device)
     B, T, H, D = OP["B"], OP["T"], OP["H"], OP["D"]
     tokens = B * T
     ms = statistics.median(per)
@@ -908,6 +947,10 @@ def main():
         # accumulation; every MFMA accumulates in fp32); measured drift in "parity"
         "state_operand_precision": "f16 per 16-token chunk, fp32 accumulate",
         "wall_s_timed_region": round(wall, 3),
+        # the same K scans through the torch-facing launch_sssd_hip_scan (argument checks and
+        # output / workspace allocation per call): host time included where it exceeds the scan
+        "torch_api_ms_per_step": round(sum(api) / len(api), 4),
+        "timing": "C-ABI vmi_sssd_scan_fwd calls with prebuilt arguments, events around each call",
     }
     if args.copy_probe:
         src = torch.ones(COPY_PROBE_BYTES // 4, device=device)
