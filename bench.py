@@ -719,8 +719,24 @@ def bench_model_decode(device, model):
         graph_dev = max(float(((a.sssd - b.sssd).abs().max())) for a, b in zip(st_g.layers, st.layers))
         graph_dev = max(graph_dev, max(float((a.cham[0] - b.cham[0]).abs().max()) for a, b in zip(st_g.layers, st.layers)))
         del graph, st_g
-        # layer 0's SSSD inputs of every step (its input is the embedding: recomputed here)
-        q, k, v, dl = l0.sssd_attn.project(l0.sssd_norm(model.embed_tokens(steps_ids[:, :, 0].t())))
+        # layer 0's SSSD inputs of every step (its input is the embedding: recomputed here).
+        # The fused decode step normalises the bf16 stacked projection in fp32, so the oracle
+        # starts from that projection (normalised in fp64 on the host); the unfused step takes
+        # project()'s bf16 q, k, v, delta.
+        xin = l0.sssd_norm(model.embed_tokens(steps_ids[:, :, 0].t()))
+        fused_step = l0.sssd_attn._fused_step(xin[:, :1])
+        if fused_step:
+            proj = torch.nn.functional.linear(xin, l0.sssd_attn._stacked_weight()).double().cpu()
+            HD = 8 * 128
+
+            def unit(t):
+                t = t.reshape(B, S, 8, 128)
+                return t / t.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+
+            q, k, v = unit(proj[..., :HD]), unit(proj[..., HD:2 * HD]), unit(proj[..., 2 * HD:3 * HD])
+            dl = 0.1 * torch.sigmoid(proj[..., 3 * HD:3 * HD + 8])
+        else:
+            q, k, v, dl = l0.sssd_attn.project(xin)
         # the same sub-layer steps in isolation: one SSSD / CHAM step launch per layer
         x = torch.randn(B, 1, 1024, device=device).bfloat16()
         st2 = model._fresh_layer_state(l0, B, device)
@@ -739,7 +755,7 @@ def bench_model_decode(device, model):
             t_s.append(e[0].elapsed_time(e[1]))
             t_c.append(e[1].elapsed_time(e[2]))
     sel = [(0, 0), (B - 1, 7)]
-    qn, kn, vn, dn = (t.float().cpu().numpy() for t in (q, k, v, dl))
+    qn, kn, vn, dn = (t.double().cpu().numpy() for t in (q, k, v, dl))
     worst = 0.0
     for (bb, hh) in sel:
         sl = (slice(bb, bb + 1), slice(None), slice(hh, hh + 1))
@@ -769,6 +785,7 @@ def bench_model_decode(device, model):
         "sssd_step_us_per_layer": round(1e3 * statistics.median(t_s), 2),
         "cham_step_us_per_layer": round(1e3 * ms_c, 2),
         "cham_step_hbm_frac": round(cham_bytes / (ms_c * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "sssd_step_fused": bool(fused_step),
         "parity": {"layer0_sssd_state_rel_vs_fp64": worst, "sssd_state_norm_drift": drift,
                    "layer0_cham_unitarity_err": unit, "graph_vs_eager_state_maxdiff": graph_dev,
                    "pass": bool(worst <= 2e-2 and drift <= 1e-4 and unit <= 1e-3 and graph_dev <= 1e-5)},

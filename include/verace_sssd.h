@@ -136,6 +136,23 @@ int vmi_sssd_step_inplace(const void* q, const void* k, const void* v,
                           float* psi, void* out,
                           int64_t B, int64_t H, int64_t D, void* stream);
 
+/* vmi_sssd_step_inplace fused with the projections either side of it (as vmi_sssd_scan_fused
+ * for the prefill): the decode step of the reference's forward at seq_len 1 from the
+ * projections on (sssd_attention.py:114-126 before the scan, :177 after it, called from
+ * acd_engine.py:116-121 and hyper_generate.py:59-63).
+ *   proj : [B, proj_stride] io_dtype, row b = x_b [W_q; W_k; W_v; W_delta]^T raw (q of head h
+ *          at h D, k at H D + h D, v at 2 H D + h D, the delta logit at 3 H D + h);
+ *          proj_stride >= 3 H D + H;
+ *   q, k, v are L2-normalised in the kernel (F.normalize, eps 1e-12) and
+ *   delta = 0.1 sigmoid(logit) * mask[b] (mask: [B] uint8, null = every item active);
+ *   psi : [B, H, D, D] float32, updated in place;
+ *   out : [B, 1, H, D] io_dtype = head_rmsnorm(o) = o rsqrt(mean(o^2) + rms_eps) rms_weight
+ *         when rms_weight ([D] float32) is given, else o.
+ * D = 128 (otherwise VMI_ERR_UNSUPPORTED: run the unfused ops and vmi_sssd_step_inplace). */
+int vmi_sssd_step_fused(const void* proj, int64_t proj_stride, int io_dtype, const uint8_t* mask,
+                        const float* rms_weight, float rms_eps, float* psi, void* out,
+                        int64_t B, int64_t H, int64_t D, void* stream);
+
 /* One decode step over the slots of a state cache (copy-on-write decode):
  *   item b reads state slot in_slot[b] (or the identity when in_slot[b] == -1),
  *   writes R * state to slot out_slot[b], and out[b] = (R * state) q[b].

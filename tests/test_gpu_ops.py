@@ -35,6 +35,10 @@ def test_opcheck_scan_step_cham_ns(device):
                           (qc[:, :1], qc[:, :1], qc[:, :1], g[:, :1], H.clone(), torch.zeros_like(H),
                            None, None))
     torch.library.opcheck(torch.ops.verace.ns_retraction.default, (H + 0.01, H * 0, 3))
+    proj = torch.randn(3, 1, 3 * 2 * 128 + 2, device=device).to(torch.bfloat16)
+    st128 = torch.linalg.qr(torch.randn(3, 2, 128, 128))[0].contiguous().to(device)
+    torch.library.opcheck(torch.ops.verace.sssd_step_fused_.default,
+                          (proj, 2, 128, st128.clone(), None, torch.ones(128, device=device), None))
 
 
 def test_ops_equal_launchers_and_autograd(device):

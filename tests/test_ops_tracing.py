@@ -20,6 +20,9 @@ def test_fake_kernels_give_reference_layouts():
     proj = torch.empty(2, 40, 3 * 4 * 128 + 4, device="meta", dtype=torch.bfloat16)
     o, s = torch.ops.verace.sssd_scan_fused(proj, 4, 128, None, None, None, None)
     assert o.shape == (2, 40, 4, 128) and s.shape == (2, 4, 128, 128)
+    st128 = torch.empty(2, 4, 128, 128, device="meta")
+    o1 = torch.ops.verace.sssd_step_fused_(proj[:, :1], 4, 128, st128, None, None, None)
+    assert o1.shape == (2, 1, 4, 128) and o1.dtype == torch.bfloat16
     qc = torch.empty(3, 7, 32, device="meta")
     g = torch.empty(3, 7, device="meta")
     out, hr, hi = torch.ops.verace.cham_scan(qc, qc, qc, g, None, None)

@@ -201,6 +201,21 @@ int vmi_sssd_step_inplace(const void* q, const void* k, const void* v, const voi
                                          static_cast<int>(D), s));
 }
 
+int vmi_sssd_step_fused(const void* proj, int64_t proj_stride, int io_dtype, const uint8_t* mask,
+                        const float* rms_weight, float rms_eps, float* psi, void* out, int64_t B,
+                        int64_t H, int64_t D, void* stream) {
+  if (!valid_dtype(io_dtype)) return VMI_ERR_INVALID_ARG;
+  if (B < 0 || H < 0 || D < 1 || !(rms_eps >= 0.0f)) return VMI_ERR_INVALID_ARG;
+  if (!vmi::use_step128(1, D)) return VMI_ERR_UNSUPPORTED;
+  if (B * H > INT32_MAX) return VMI_ERR_INVALID_ARG;
+  if (proj == nullptr || psi == nullptr || proj_stride < 3 * H * D + H) return VMI_ERR_INVALID_ARG;
+  if (B == 0 || H == 0) return VMI_OK;
+  return hip_status(vmi::launch_sssd_step128_fused(proj, proj_stride, io_dtype, mask, rms_weight,
+                                                   rms_eps, psi, out, static_cast<int>(B),
+                                                   static_cast<int>(H),
+                                                   static_cast<hipStream_t>(stream)));
+}
+
 int vmi_sssd_step_slots(const void* q, const void* k, const void* v, const void* delta,
                         int io_dtype, int delta_dtype, float* states, int64_t num_slots,
                         const int32_t* in_slot, const int32_t* out_slot, void* out, int64_t B,

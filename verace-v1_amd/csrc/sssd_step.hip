@@ -44,11 +44,25 @@ constexpr int WG_PER_CU = 2;
 static_assert(RPT == CG / 2, "the o reduce-scatter leaves one row per lane pair");
 static_assert(NU % 2 == 0, "units alternate two register buffers and two LDS buffers");
 
-template <typename IO, typename Map>
+// Fused decode step (FUSED = true; reference sssd_attention.py:114-126 and :177 at seq_len 1):
+// q, k, v and the delta logit of item b are read from row b of the stacked projection
+// proj = x [W_q; W_k; W_v; W_delta]^T (passed as q; row stride `stride` elements): q of head
+// h at h D, k at H D + h D, v at 2 H D + h D, the logit at 3 H D + h.  q, k, v are
+// L2-normalised in the kernel (F.normalize: x / max(|x|, 1e-12), in fp32), delta =
+// 0.1 sigmoid(logit) mask[b], and with rms_w the output is head_rmsnorm(o) =
+// o rsqrt(mean(o^2) + rms_eps) rms_w.
+struct StepFused {
+  int64_t stride;
+  const uint8_t* mask;  // per item (null: every item active)
+  const float* rms_w;   // [D] (null: o stored as computed)
+  float rms_eps;
+};
+
+template <typename IO, typename Map, bool FUSED>
 __global__ __launch_bounds__(NT, WG_PER_CU) void sssd_step128_kernel(
     const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
     const void* __restrict__ delta, int delta_dtype, const float* psi_in, IO* __restrict__ out,
-    float* psi_out, Map map, int BH, int H) {
+    float* psi_out, Map map, int BH, int H, StepFused fz) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -59,12 +73,13 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void sssd_step128_kernel(
   __shared__ float s_tok[2][3][D];          // q, k, v (fp32) of the head, x2 (head parity)
   __shared__ float s_delta[2];
   __shared__ float4 s_red[2][4][2][CG];     // per wave: a and b partials, x2 (unit parity)
+  __shared__ float s_rms[4];                // fused RMSNorm: per-wave sums of o^2
 
   // state of the current and the next unit (double-buffered registers)
   float4 sa[RPT], sb[RPT];
   // this thread's share of the next head's q/k/v row (elements tid and tid + 256 of
   // the 384-element concatenation) and its delta
-  float tk0 = 0.f, tk1 = 0.f, tdl = 0.f;
+  float tk0 = 0.f, tk1 = 0.f, tdl = 0.f, tmk = 1.f;
 
   auto load_unit = [&](float4* st, int bh, int u) {
     const int64_t si = psi_in != nullptr ? map.in_index(bh, H) : -1;  // uniform; < 0: identity
@@ -83,19 +98,33 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void sssd_step128_kernel(
     }
   };
   auto load_tok = [&](int bh) {
-    // element e of [q | k | v] for head bh lives at bh*D + (e % D) of array e / D
-    const int64_t base = static_cast<int64_t>(bh) * D;
-    tk0 = io<IO>::load(tid < D ? q : k, base + (tid & (D - 1)));
-    if (tid < D) tk1 = io<IO>::load(v, base + tid);
-    if (tid == 0) tdl = load_scalar(delta, delta_dtype, bh);
+    if constexpr (FUSED) {
+      const int b = bh / H, hh = bh - b * H;
+      const int64_t row = static_cast<int64_t>(b) * fz.stride + static_cast<int64_t>(hh) * D;
+      const int64_t HD = static_cast<int64_t>(H) * D;
+      tk0 = io<IO>::load(q, row + (tid < D ? 0 : HD) + (tid & (D - 1)));
+      if (tid < D) tk1 = io<IO>::load(q, row + 2 * HD + tid);
+      if (tid == 0) {
+        tdl = io<IO>::load(q, static_cast<int64_t>(b) * fz.stride + 3 * HD + hh);
+        tmk = fz.mask != nullptr ? static_cast<float>(fz.mask[b]) : 1.f;
+      }
+    } else {
+      // element e of [q | k | v] for head bh lives at bh*D + (e % D) of array e / D
+      const int64_t base = static_cast<int64_t>(bh) * D;
+      tk0 = io<IO>::load(tid < D ? q : k, base + (tid & (D - 1)));
+      if (tid < D) tk1 = io<IO>::load(v, base + tid);
+      if (tid == 0) tdl = load_scalar(delta, delta_dtype, bh);
+    }
   };
   auto commit_tok = [&](int buf) {
     (&s_tok[buf][0][0])[tid] = tk0;
     if (tid < D) s_tok[buf][2][tid] = tk1;
-    if (tid == 0) s_delta[buf] = tdl;
+    // fused: 0.1 sigmoid(logit) * mask (a NaN logit stays NaN, so the guard below applies)
+    if (tid == 0) s_delta[buf] = FUSED ? 0.1f / (1.f + expf(-tdl)) * tmk : tdl;
   };
 
   float kr[RPT], vr[RPT];  // k and v at this thread's rows (zero for a guarded token)
+  float qn = 1.f;          // fused: 1 / |q|
   cayley2 M;
   float po[RPT];           // o partials at this thread's rows, summed over units
 
@@ -113,11 +142,29 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void sssd_step128_kernel(
       float kk = fmaf(k0, k0, k1 * k1);
       float vv = fmaf(v0, v0, v1 * v1);
       float kv = fmaf(k0, v0, k1 * v1);
+      float qq = 0.f;
+      if constexpr (FUSED) {
+        const float q0 = s_tok[buf][0][lane], q1 = s_tok[buf][0][lane + 64];
+        qq = fmaf(q0, q0, q1 * q1);
+      }
 #pragma unroll
       for (int off = 32; off >= 1; off >>= 1) {
         kk += __shfl_xor(kk, off);
         vv += __shfl_xor(vv, off);
         kv += __shfl_xor(kv, off);
+        if constexpr (FUSED) qq += __shfl_xor(qq, off);
+      }
+      if constexpr (FUSED) {  // the Gram entries and rows of the normalised k, v
+        const float nk = 1.f / fmaxf(sqrtf(kk), 1e-12f), nv = 1.f / fmaxf(sqrtf(vv), 1e-12f);
+        qn = 1.f / fmaxf(sqrtf(qq), 1e-12f);
+        kv = kv * nk * nv;
+        kk = kk * nk * nk;
+        vv = vv * nv * nv;
+#pragma unroll
+        for (int m = 0; m < RPT; ++m) {
+          kr[m] *= nk;
+          vr[m] *= nv;
+        }
       }
       // a token with a non-finite Cayley factor is the identity (uniform over the workgroup)
       bool ok;
@@ -127,7 +174,10 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void sssd_step128_kernel(
         for (int m = 0; m < RPT; ++m) kr[m] = vr[m] = 0.f;
       }
     }
-    const float4 qc = *reinterpret_cast<const float4*>(&s_tok[buf][0][UC * u + c0]);
+    float4 qc = *reinterpret_cast<const float4*>(&s_tok[buf][0][UC * u + c0]);
+    if constexpr (FUSED) {
+      qc.x *= qn; qc.y *= qn; qc.z *= qn; qc.w *= qn;
+    }
     // column partials over this thread's rows
     float4 pa = make_float4(0.f, 0.f, 0.f, 0.f), pb = pa;
 #pragma unroll
@@ -193,9 +243,21 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void sssd_step128_kernel(
         }
         if (hi) mloc += half;
       }
-      const float o_row = po[0] + __shfl_xor(po[0], 1);
+      float o_row = po[0] + __shfl_xor(po[0], 1);
+      const int row = rg + RG * mloc;  // each row held by exactly one even lane
+      if constexpr (FUSED) {
+        if (fz.rms_w != nullptr) {  // uniform: head RMSNorm over the head's D rows
+          float ss = (lane & 1) == 0 ? o_row * o_row : 0.f;
+#pragma unroll
+          for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+          if (lane == 0) s_rms[wave] = ss;
+          __syncthreads();
+          const float tot = (s_rms[0] + s_rms[1]) + (s_rms[2] + s_rms[3]);
+          o_row *= rsqrtf(tot * (1.f / D) + fz.rms_eps) * fz.rms_w[row];
+        }
+      }
       if (out != nullptr && (lane & 1) == 0)
-        io<IO>::store(out, static_cast<int64_t>(bh) * D + rg + RG * mloc, o_row);
+        io<IO>::store(out, static_cast<int64_t>(bh) * D + row, o_row);
     }
   };
 
@@ -231,18 +293,19 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void sssd_step128_kernel(
   }
 }
 
-template <typename IO, typename Map>
+template <typename IO, typename Map, bool FUSED = false>
 hipError_t launch_typed(const void* q, const void* k, const void* v, const void* delta,
                         int delta_dtype, const float* psi_in, void* out, float* psi_out,
-                        const Map& map, int BH, int H, hipStream_t stream) {
+                        const Map& map, int BH, int H, hipStream_t stream,
+                        const StepFused& fz = StepFused{}) {
   int cus = 0;
   hipError_t e = device_cu_count(&cus);
   if (e != hipSuccess) return e;
   const int grid = BH < WG_PER_CU * cus ? BH : WG_PER_CU * cus;
-  hipLaunchKernelGGL((sssd_step128_kernel<IO, Map>), dim3(grid), dim3(NT), 0, stream,
+  hipLaunchKernelGGL((sssd_step128_kernel<IO, Map, FUSED>), dim3(grid), dim3(NT), 0, stream,
                      static_cast<const IO*>(q), static_cast<const IO*>(k),
                      static_cast<const IO*>(v), delta, delta_dtype, psi_in, static_cast<IO*>(out),
-                     psi_out, map, BH, H);
+                     psi_out, map, BH, H, fz);
   return hipGetLastError();
 }
 
@@ -264,6 +327,22 @@ hipError_t launch_map(const void* q, const void* k, const void* v, const void* d
 }  // namespace step
 
 bool use_step128(int64_t T, int64_t D) { return T == 1 && D == step::D; }
+
+hipError_t launch_sssd_step128_fused(const void* proj, int64_t proj_stride, int io_dtype,
+                                     const uint8_t* mask, const float* rms_w, float rms_eps,
+                                     float* psi, void* out, int B, int H, hipStream_t stream) {
+  const step::StepFused fz{proj_stride, mask, rms_w, rms_eps};
+  const int BH = B * H;
+  if (io_dtype == VMI_F32)
+    return step::launch_typed<float, DenseStates, true>(proj, proj, proj, nullptr, VMI_F32, psi,
+                                                        out, psi, DenseStates{}, BH, H, stream, fz);
+  if (io_dtype == VMI_BF16)
+    return step::launch_typed<bf16_t, DenseStates, true>(proj, proj, proj, nullptr, VMI_BF16, psi,
+                                                         out, psi, DenseStates{}, BH, H, stream,
+                                                         fz);
+  return step::launch_typed<f16_t, DenseStates, true>(proj, proj, proj, nullptr, VMI_F16, psi, out,
+                                                      psi, DenseStates{}, BH, H, stream, fz);
+}
 
 hipError_t launch_sssd_step128(const void* q, const void* k, const void* v, const void* delta,
                                int io_dtype, int delta_dtype, const float* psi_in, void* out,

@@ -91,6 +91,13 @@ hipError_t launch_sssd_step128(const void* q, const void* k, const void* v, cons
                                float* psi_out, const SlotArgs& map, int B, int H,
                                hipStream_t stream);
 
+// The same step fused with the projections around it (head_dim 128, states in place):
+// proj [B, stride] raw (x [W_q; W_k; W_v; W_delta]^T, one row per item); q, k, v normalised and
+// delta = 0.1 sigmoid(.) * mask in the kernel; out = head_rmsnorm(o) when rms_w is given.
+hipError_t launch_sssd_step128_fused(const void* proj, int64_t proj_stride, int io_dtype,
+                                     const uint8_t* mask, const float* rms_w, float rms_eps,
+                                     float* psi, void* out, int B, int H, hipStream_t stream);
+
 // sssd_scan.hip: picks the kernel family for a prefill scan.
 size_t scan_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int io_dtype);
 hipError_t dispatch_scan(const void* q, const void* k, const void* v, const void* delta,

@@ -10,6 +10,9 @@ Drop-in replacements for the reference's SSSD hot path:
 * ``launch_sssd_hip_scan_fused`` -- the scan with the projections' normalisation, delta,
                                   mask and head RMSNorm fused in (on x @ [W_q; W_k; W_v; W_delta].T)
 * ``sssd_step_``               -- in-place single-token decode step (opt-in)
+* ``sssd_step_fused_``         -- the same step with the projections' normalisation, delta,
+                                  mask and head RMSNorm fused in (on one row of the stacked
+                                  projection per item)
 * ``SSSDStateCache``           -- per-layer decode state pools with copy-on-write
                                   branches (replaces the ``layer_states`` lists of
                                   ``acd_engine.py`` / ``hyper_generate.py``)
@@ -35,7 +38,7 @@ from .hip_kernels import (HAS_HIP, SSSDScanFunction, cham_step_, launch_cham_hip
                           launch_sssd_hip_scan, launch_sssd_hip_scan_bwd,
                           launch_sssd_hip_scan_fused,
                           newton_schulz_unitary_retraction, parallel_newton_schulz_retraction,
-                          sssd_scan, sssd_step_)
+                          sssd_scan, sssd_step_, sssd_step_fused_)
 from . import ops  # noqa: F401  (torch.ops.verace.*: the launchers as traceable operators)
 from .sssd_attention import SSSDAttention
 from .cham_memory import ContinuousHolographicMemory
@@ -56,6 +59,7 @@ __all__ = [
     "launch_sssd_hip_scan_fused",
     "launch_cham_hip_update",
     "sssd_step_",
+    "sssd_step_fused_",
     "cham_step_",
     "ContinuousHolographicMemory",
     "ManifoldContinuousMoE",

@@ -27,6 +27,7 @@ EXPORTED = (
     "vmi_sssd_scan_fused_workspace_bytes",
     "vmi_sssd_scan_fused",
     "vmi_sssd_step_inplace",
+    "vmi_sssd_step_fused",
     "vmi_sssd_step_slots",
     "vmi_state_cache_create",
     "vmi_state_cache_destroy",
@@ -83,6 +84,9 @@ def _declare(lib):
                                         i64, i64, vp, sz, vp]
     lib.vmi_sssd_scan_fused.restype = i32
     lib.vmi_sssd_step_inplace.argtypes = [vp, vp, vp, vp, i32, i32, vp, vp, i64, i64, i64, vp]
+    lib.vmi_sssd_step_fused.argtypes = [vp, i64, i32, vp, vp, ctypes.c_float, vp, vp, i64, i64, i64,
+                                        vp]
+    lib.vmi_sssd_step_fused.restype = i32
     lib.vmi_sssd_step_inplace.restype = i32
     lib.vmi_sssd_step_slots.argtypes = [vp, vp, vp, vp, i32, i32, vp, i64, vp, vp, vp, i64, i64,
                                         i64, vp]

@@ -37,7 +37,7 @@ import torch
 import torch.nn as nn
 
 from .cham_memory import ContinuousHolographicMemory
-from .hip_kernels import sssd_step_, newton_schulz_unitary_retraction
+from .hip_kernels import newton_schulz_unitary_retraction
 from .mcmoe import ManifoldContinuousMoE
 from .sssd_attention import SSSDAttention
 
@@ -104,12 +104,7 @@ class VeraceV1Layer(nn.Module):
         """One token per item (h_in [B, 1, hidden]) with this layer's states updated in
         place; the same sub-layers as :meth:`forward` (no block residual: a decode call's
         layers never receive a snapshot, see the module docstring)."""
-        b = h_in.shape[0]
-        a = self.sssd_attn
-        q, k, v, delta = a.project(self.sssd_norm(h_in), active_mask)
-        o = sssd_step_(q, k, v, delta, st.sssd)
-        o_norm = a.head_rmsnorm(o).reshape(b, 1, a.num_heads * a.head_dim)
-        h_mid1 = h_in + a.w_out(o_norm)
+        h_mid1 = h_in + self.sssd_attn.step_(self.sssd_norm(h_in), st.sssd, active_mask)
         cham_out = self.cham_memory.step_(self.cham_norm(h_mid1), st.cham, st.cham_readout, active_mask)
         h_mid2 = h_mid1 + cham_out
         return h_mid2 + self.mcmoe(self.mcmoe_norm(h_mid2))

@@ -316,6 +316,63 @@ def sssd_step_(
     return out
 
 
+def fused_step_supported(x_dtype: torch.dtype, head_dim: int) -> bool:
+    """Whether :func:`sssd_step_fused_` runs these shapes (head_dim 128, any I/O dtype)."""
+    return x_dtype in (torch.bfloat16, torch.float16, torch.float32) and head_dim == 128
+
+
+def sssd_step_fused_(
+    proj: torch.Tensor,
+    num_heads: int,
+    head_dim: int,
+    state: torch.Tensor,
+    active_mask: Optional[torch.Tensor] = None,
+    rms_weight: Optional[torch.Tensor] = None,
+    rms_eps: Optional[float] = None,
+) -> torch.Tensor:
+    """:func:`sssd_step_` with the steps either side of it fused (``sssd_attention.py:114-126``
+    and ``:177`` at seq_len 1): ``proj`` [B, 1, >= 3HD + H] (or [B, >= 3HD + H]) is
+    ``x @ [W_q; W_k; W_v; W_delta].T`` (raw); q, k, v are L2-normalised, ``delta = 0.1 *
+    sigmoid(.) * active_mask`` is formed and, with ``rms_weight``, the output is
+    ``head_rmsnorm(o)`` (``rms_eps`` None = the eps torch's ``nn.RMSNorm`` adds by default),
+    all inside the kernel.  ``state`` [B, H, D, D] float32 contiguous is updated in place.
+    Returns out [B, 1, H, D] in proj's dtype.  head_dim other than 128 raises."""
+    _require_device(proj, "proj")
+    _require_device(state, "state")
+    H, D = num_heads, head_dim
+    if not fused_step_supported(proj.dtype, D):
+        raise RuntimeError("verace_amd: the fused decode step needs head_dim 128")
+    if state.dtype != torch.float32 or not state.is_contiguous():
+        raise RuntimeError("verace_amd: state must be a contiguous float32 tensor")
+    b = proj.shape[0]
+    if tuple(state.shape) != (b, H, D, D):
+        raise RuntimeError(f"verace_amd: state must be {(b, H, D, D)}, got {tuple(state.shape)}")
+    p2 = proj.reshape(b, proj.shape[-1])
+    if proj.dim() == 3 and proj.shape[1] != 1:
+        raise RuntimeError(f"verace_amd: proj must hold one token per item, got {tuple(proj.shape)}")
+    if p2.shape[1] < 3 * H * D + H:
+        raise RuntimeError(f"verace_amd: proj has {p2.shape[1]} columns, needs >= {3 * H * D + H}")
+    if p2.stride(1) != 1:
+        p2 = p2.contiguous()
+    mask = None
+    if active_mask is not None:
+        _require_device(active_mask, "active_mask")
+        mask = active_mask.reshape(b).to(torch.uint8).contiguous()
+    w = None
+    eps = 0.0
+    if rms_weight is not None:
+        _require_device(rms_weight, "rms_weight")
+        w = rms_weight.to(torch.float32).contiguous()
+        eps = rms_default_eps(proj.dtype) if rms_eps is None else float(rms_eps)
+    out = torch.empty(b, 1, H, D, device=proj.device, dtype=proj.dtype)
+    lib = _lib.load()
+    _lib.check(lib.vmi_sssd_step_fused(_ptr(p2), p2.stride(0), _lib.dtype_code(proj.dtype),
+                                       _ptr(mask), _ptr(w), eps, _ptr(state), _ptr(out), b, H, D,
+                                       _lib.stream_handle(proj.device)),
+               "vmi_sssd_step_fused")
+    return out
+
+
 def launch_cham_hip_update(
     q: torch.Tensor,
     k: torch.Tensor,

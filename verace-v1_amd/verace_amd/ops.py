@@ -9,6 +9,8 @@ Replaces, for tracing purposes, the reference's Triton launcher ``launch_sssd_tr
   differentiable through ``verace::sssd_scan_bwd`` (:func:`launch_sssd_hip_scan_bwd`).
 * ``verace::sssd_step_(q, k, v, delta, state!) -> out`` -- :func:`sssd_step_` (mutates state).
 * ``verace::sssd_scan_fused(proj, H, D, mask?, rms_weight?, rms_eps, state?) -> (out, state_T)``.
+* ``verace::sssd_step_fused_(proj, H, D, state!, mask?, rms_weight?, rms_eps) -> out`` --
+  :func:`sssd_step_fused_` (mutates state).
 * ``verace::cham_scan(q, k, v, gamma, h0_real?, h0_imag?) -> (out, h_real, h_imag)``.
 * ``verace::cham_step_(q, k, v, gamma, h_real!, h_imag!, r_real!?, r_imag!?) -> out``.
 * ``verace::ns_retraction(h_real, h_imag, steps) -> (real, imag)``.
@@ -89,6 +91,18 @@ def sssd_step_(q: Tensor, k: Tensor, v: Tensor, delta: Tensor, state: Tensor) ->
 def _sssd_step_fake(q, k, v, delta, state):
     B, H, D, _ = state.shape
     return q.new_empty((B, 1, H, D))
+
+
+@torch.library.custom_op("verace::sssd_step_fused_", mutates_args=("state",))
+def sssd_step_fused_(proj: Tensor, num_heads: int, head_dim: int, state: Tensor,
+                     active_mask: Optional[Tensor], rms_weight: Optional[Tensor],
+                     rms_eps: Optional[float]) -> Tensor:
+    return hk.sssd_step_fused_(proj, num_heads, head_dim, state, active_mask, rms_weight, rms_eps)
+
+
+@sssd_step_fused_.register_fake
+def _sssd_step_fused_fake(proj, num_heads, head_dim, state, active_mask, rms_weight, rms_eps):
+    return proj.new_empty((proj.shape[0], 1, num_heads, head_dim))
 
 
 @torch.library.custom_op("verace::sssd_scan_fused", mutates_args=())

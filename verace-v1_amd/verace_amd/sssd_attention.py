@@ -27,8 +27,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops as _ops  # noqa: F401  (registers torch.ops.verace.*)
-from .hip_kernels import (fused_scan_supported, launch_sssd_hip_scan, launch_sssd_hip_scan_fused,
-                          sssd_scan)
+from .hip_kernels import (fused_scan_supported, fused_step_supported, launch_sssd_hip_scan,
+                          launch_sssd_hip_scan_fused, sssd_scan, sssd_step_, sssd_step_fused_)
 
 
 def _traced(x: torch.Tensor) -> bool:
@@ -177,6 +177,38 @@ class SSSDAttention(nn.Module):
             o = self.head_rmsnorm(o)
         output = self.w_out(o.reshape(b, s, self.num_heads * self.head_dim))
         return output, (psi if return_state else None)
+
+    def step_(self, x: torch.Tensor, state: torch.Tensor,
+              active_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """``forward`` at seq_len 1 with the state updated in place: x [B, 1, hidden], state
+        [B, H, D, D] float32 (the reference's incremental call, ``acd_engine.py:116-121`` /
+        ``hyper_generate.py:59-63``, which returns a fresh state instead).  Returns the sub-layer
+        output [B, 1, hidden].  Where the fused prefill would run (same dtypes, head_dim 128)
+        the projections' normalisation, delta, mask and head RMSNorm run inside the step
+        kernel on one stacked projection GEMM; otherwise the reference's op sequence."""
+        b = x.shape[0]
+        H, D = self.num_heads, self.head_dim
+        if self._fused_step(x):
+            rms_grad = (torch.is_grad_enabled() and self.head_rmsnorm.weight is not None
+                        and self.head_rmsnorm.weight.requires_grad)
+            w = None
+            if not rms_grad:
+                w = self.head_rmsnorm.weight
+                w = torch.ones(D, device=x.device) if w is None else w.detach()
+            o = sssd_step_fused_(F.linear(x, self._stacked_weight()), H, D, state, active_mask, w,
+                                 self.head_rmsnorm.eps)
+            if rms_grad:
+                o = self.head_rmsnorm(o)
+        else:
+            q, k, v, delta = self.project(x, active_mask)
+            o = self.head_rmsnorm(sssd_step_(q, k, v, delta, state))
+        return self.w_out(o.reshape(b, 1, H * D))
+
+    def _fused_step(self, x: torch.Tensor) -> bool:
+        return (self.fuse_projections and x.shape[1] == 1
+                and fused_step_supported(x.dtype, self.head_dim)
+                and all(w.dtype == x.dtype for w in (self.w_q.weight, self.w_k.weight,
+                                                      self.w_v.weight, self.w_delta.weight)))
 
     def forward_cached(self, x: torch.Tensor, cache, layer: int, handles,
                        active_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
