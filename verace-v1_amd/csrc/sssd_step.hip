@@ -126,6 +126,17 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void sssd_step128_kernel(
   float kr[RPT], vr[RPT];  // k and v at this thread's rows (zero for a guarded token)
   float qn = 1.f;          // fused: 1 / |q|
   cayley2 M;
+  // the o row this lane ends up holding after the reduce-scatter below (rg + RG * mrow,
+  // in the even lanes); fused: its RMSNorm weight, loaded once here (loaded after a head's
+  // state stores, its wait would also wait for those stores)
+  int mrow = 0;
+#pragma unroll
+  for (int off = CG / 2, cnt = RPT; off >= 2; off >>= 1, cnt >>= 1)
+    if (lane & off) mrow += cnt >> 1;
+  float rw = 1.f;
+  if constexpr (FUSED) {
+    if (fz.rms_w != nullptr) rw = fz.rms_w[rg + RG * mrow];
+  }
   float po[RPT];           // o partials at this thread's rows, summed over units
 
   // unit u of head bh: columns UC u .. UC u + UC - 1 in st, q/k/v in s_tok[buf]
@@ -227,8 +238,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void sssd_step128_kernel(
     }
     if (u == NU - 1) {
       // reduce-scatter po[] over the CG lanes of this row group: after the halving
-      // steps lane cg holds the sum for row rg + RG*mloc, paired with lane cg^1
-      int mloc = 0;
+      // steps lane cg holds the sum for row rg + RG*mrow, paired with lane cg^1
 #pragma unroll
       for (int off = CG / 2, cnt = RPT; off >= 2; off >>= 1, cnt >>= 1) {
         const int half = cnt >> 1;
@@ -241,10 +251,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void sssd_step128_kernel(
             po[i] = keep + __shfl_xor(send, off);
           }
         }
-        if (hi) mloc += half;
       }
       float o_row = po[0] + __shfl_xor(po[0], 1);
-      const int row = rg + RG * mloc;  // each row held by exactly one even lane
+      const int row = rg + RG * mrow;  // each row held by exactly one even lane
       if constexpr (FUSED) {
         if (fz.rms_w != nullptr) {  // uniform: head RMSNorm over the head's D rows
           float ss = (lane & 1) == 0 ? o_row * o_row : 0.f;
@@ -253,7 +262,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void sssd_step128_kernel(
           if (lane == 0) s_rms[wave] = ss;
           __syncthreads();
           const float tot = (s_rms[0] + s_rms[1]) + (s_rms[2] + s_rms[3]);
-          o_row *= rsqrtf(tot * (1.f / D) + fz.rms_eps) * fz.rms_w[row];
+          o_row *= rsqrtf(tot * (1.f / D) + fz.rms_eps) * rw;
         }
       }
       if (out != nullptr && (lane & 1) == 0)
