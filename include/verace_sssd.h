@@ -289,6 +289,22 @@ int vmi_cham_step_inplace(const void* q, const void* k, const void* v, const voi
                           float* r_real, float* r_imag, void* out, int64_t B, int64_t h,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* vmi_cham_step_inplace fused with the projections before it: the CHAM decode step of the
+ * reference's forward at seq_len 1 from the projections on (cham_memory.py:128-155 before the
+ * scan, called per token from acd_engine.py:116-121 and hyper_generate.py:59-63).
+ *   proj : [B, proj_stride] io_dtype, row b = x_b [W_q; W_k; W_v; W_gamma]^T raw (q at 0, k at
+ *          h, v at 2h, the gamma logit at 3h); proj_stride >= 3h + 1;
+ *   in the kernel v = silu(v), q, k, v are L2-normalised (F.normalize, eps 1e-12) and
+ *   gamma = 0.1 sigmoid(logit) * mask[b] (mask: [B] uint8, null = every item active);
+ *   h_real, h_imag (and r_real, r_imag): as vmi_cham_step_inplace, updated in place;
+ *   out : [B, 1, h] io_dtype = Re(NS_3(H') q).
+ * h = 1024 (otherwise VMI_ERR_UNSUPPORTED: run the unfused ops and vmi_cham_step_inplace).
+ * Workspace from vmi_cham_step_workspace_bytes. */
+int vmi_cham_step_fused(const void* proj, int64_t proj_stride, int io_dtype, const uint8_t* mask,
+                        float* h_real, float* h_imag, float* r_real, float* r_imag, void* out,
+                        int64_t B, int64_t h, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
 /* Newton-Schulz unitary retraction of a batch of complex matrices
  * H = Hr + i Hi, `steps` iterations of H <- 0.5 H (3I - H^H H), both halves
  * of every iteration computed from the pre-update H.

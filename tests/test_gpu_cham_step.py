@@ -111,3 +111,32 @@ def test_cham_step_rejects_bad_arguments(device):
         cham_step_(q, q, q, g, (hr, hi), (hr[:1].contiguous(), hi[:1].contiguous()))  # readout shape
     with pytest.raises(RuntimeError):
         cham_step_(q.cpu(), q, q, g, (hr, hi))                   # device
+
+
+@pytest.mark.parametrize("h", [64, 1024])
+def test_cham_step_nonfinite_token_is_identity(device, h):
+    """A NaN or Inf in an item's k or v, or a NaN gamma, makes its token U = I (the reference's
+    guard, cham_memory.py:68-95): that item's state is unchanged bit for bit although the column
+    sums were formed with the non-finite row; the other items follow the oracle."""
+    from verace_amd import cham_step_
+    print(f"[case] cham step non-finite h{h}", flush=True)
+    B = 4
+    g = torch.Generator().manual_seed(70 + h)
+    q, k, v, gam = _tokens(B, 1, h, g, torch.float32)
+    k[0, 0, 5] = float("nan")
+    v[1, 0, h - 1] = float("inf")
+    gam[2, 0] = float("nan")
+    a = torch.randn(B, h, h, generator=g, dtype=torch.float64) + 1j * torch.randn(B, h, h, generator=g, dtype=torch.float64)
+    u = torch.linalg.qr(a)[0]
+    h0r, h0i = u.real.float().contiguous(), u.imag.float().contiguous()
+    hr, hi = h0r.to(device), h0i.to(device)
+    o = cham_step_(q.to(device), k.to(device), v.to(device), gam.to(device), (hr, hi))
+    torch.cuda.synchronize()
+    for b in (0, 1, 2):
+        assert torch.equal(hr[b].cpu(), h0r[b]) and torch.equal(hi[b].cpu(), h0i[b])
+    assert torch.isfinite(o).all()
+    ref, (sr, si) = cham_scan.cham_scan_closed(q[3:].double().numpy(), k[3:].double().numpy(),
+                                              v[3:].double().numpy(), gam[3:].double().numpy(),
+                                              h0r[3:].double().numpy(), h0i[3:].double().numpy())
+    assert max(_rel(hr[3:].cpu(), sr), _rel(hi[3:].cpu(), si)) <= 1e-5
+    assert _rel(o[3:].float().cpu(), ref) <= 1e-5

@@ -30,6 +30,10 @@ def test_fake_kernels_give_reference_layouts():
     H = torch.empty(3, 32, 32, device="meta")
     assert torch.ops.verace.cham_step_(qc[:, :1], qc[:, :1], qc[:, :1], g[:, :1], H, H.clone(),
                                        None, None).shape == (3, 1, 32)
+    projc = torch.empty(3, 1, 3 * 1024 + 1, device="meta", dtype=torch.bfloat16)
+    H1 = torch.empty(3, 1024, 1024, device="meta")
+    oc = torch.ops.verace.cham_step_fused_(projc, 1024, H1, H1.clone(), None, None, None)
+    assert oc.shape == (3, 1, 1024) and oc.dtype == torch.bfloat16
     r, i = torch.ops.verace.ns_retraction(H, H, 3)
     assert r.shape == H.shape
     dq, dk, dv, dd, dp = torch.ops.verace.sssd_scan_bwd(q, q, q, d, st, q, None, True)

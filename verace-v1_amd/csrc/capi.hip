@@ -308,6 +308,32 @@ int vmi_cham_step_inplace(const void* q, const void* k, const void* v, const voi
                                           static_cast<hipStream_t>(stream)));
 }
 
+int vmi_cham_step_fused(const void* proj, int64_t proj_stride, int io_dtype, const uint8_t* mask,
+                        float* h_real, float* h_imag, float* r_real, float* r_imag, void* out,
+                        int64_t B, int64_t h, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  if (!valid_dtype(io_dtype)) return VMI_ERR_INVALID_ARG;
+  if (B < 0 || h < 1 || B > 65535) return VMI_ERR_INVALID_ARG;
+  if (!vmi::cham_step_fused_supported(h)) return VMI_ERR_UNSUPPORTED;
+  if ((r_real == nullptr) != (r_imag == nullptr)) return VMI_ERR_INVALID_ARG;
+  if (proj_stride < 3 * h + 1) return VMI_ERR_INVALID_ARG;
+  if (B > 0 && (proj == nullptr || out == nullptr || h_real == nullptr || h_imag == nullptr))
+    return VMI_ERR_INVALID_ARG;
+  const size_t sb = static_cast<size_t>(B) * h * h * sizeof(float);
+  if (B > 0 && ranges_overlap(h_real, sb, h_imag, sb)) return VMI_ERR_ALIAS;
+  if (r_real != nullptr &&
+      (ranges_overlap(r_real, sb, r_imag, sb) || ranges_overlap(r_real, sb, h_real, sb) ||
+       ranges_overlap(r_real, sb, h_imag, sb) || ranges_overlap(r_imag, sb, h_real, sb) ||
+       ranges_overlap(r_imag, sb, h_imag, sb)))
+    return VMI_ERR_ALIAS;
+  const size_t need = vmi::cham_step_workspace_bytes(B, h);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return VMI_ERR_WORKSPACE;
+  if (B == 0) return VMI_OK;
+  return hip_status(vmi::launch_cham_step_fused(proj, proj_stride, io_dtype, mask, h_real, h_imag,
+                                                r_real, r_imag, out, static_cast<int>(B), workspace,
+                                                static_cast<hipStream_t>(stream)));
+}
+
 int vmi_cham_ns_workspace_bytes(int64_t batch, int64_t n, size_t* bytes) {
   if (bytes == nullptr || batch < 0 || n < 1) return VMI_ERR_INVALID_ARG;
   *bytes = vmi::ns_workspace_bytes(batch, n);

@@ -232,6 +232,8 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
     ci[e] = N.n11r * s.y + N.n11i * s.x + N.n12r * s.w + N.n12i * s.z;
     dr[e] = N.n12r * s.x - N.n12i * s.y + N.n22r * s.z - N.n22i * s.w;
     di[e] = N.n12r * s.y + N.n12i * s.x + N.n22r * s.w + N.n22i * s.z;
+    // identity token: the column sums were taken with the non-finite rows (NaN * 0 is NaN)
+    if (!ok) cr[e] = ci[e] = dr[e] = di[e] = 0.f;
   }
   // update, store, readout partials
   float po[RPT];
@@ -273,11 +275,22 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
 // 16 rows of both parts (128 floats) do not fit in registers beside the rest, so rows
 // rg + 64 m for m >= 8 pass through LDS (128 KiB per workgroup): loaded into registers,
 // summed into the column partials, parked in LDS, and read back for the update.
-template <typename IO, typename GT, typename Map>
+// Fused mode (FUSED = true; reference cham_memory.py:128-155 at seq_len 1): q, k, v and the
+// gamma logit of item b come from row b of the stacked projection proj = x [W_q; W_k; W_v;
+// W_gamma]^T (passed as q; row stride `stride` elements): q at 0, k at h, v at 2h, the logit
+// at 3h.  The kernel forms v = silu(v), normalises q, k, v (F.normalize: x / max(|x|, 1e-12),
+// in fp32: the column sums are taken with the raw rows and scaled by the norms afterwards)
+// and gamma = 0.1 sigmoid(logit) mask[b].
+struct ChamFused {
+  int64_t stride;
+  const uint8_t* mask;  // per item (null: every item active)
+};
+
+template <typename IO, typename GT, typename Map, bool FUSED = false>
 __global__ __launch_bounds__(512) void cham_step1024_kernel(
     const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
     const GT* __restrict__ gamma, float* hr0, float* hi0, float* hr1, float* hi1,
-    float* __restrict__ part, int nstates, const Map map) {
+    float* __restrict__ part, int nstates, const Map map, ChamFused fz) {
   constexpr int NT = 512, H = 1024, CB = 32, CGN = 8, NRG = 64, RPT = 16, RR = 8;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cg = tid & (CGN - 1), rg = tid / CGN;
@@ -291,13 +304,16 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
   const float* __restrict__ si = ip.in_i;
   float* __restrict__ wr = ip.out_r;
   float* __restrict__ wi = ip.out_i;
-  const IO* __restrict__ kb = k + static_cast<int64_t>(b) * H;
-  const IO* __restrict__ vb = v + static_cast<int64_t>(b) * H;
+  // item b's token row: q, k, v (fused: the three blocks of its projection row)
+  const IO* __restrict__ qb = FUSED ? q + static_cast<int64_t>(b) * fz.stride
+                                    : q + static_cast<int64_t>(b) * H;
+  const IO* __restrict__ kb = FUSED ? qb + H : k + static_cast<int64_t>(b) * H;
+  const IO* __restrict__ vb = FUSED ? qb + 2 * H : v + static_cast<int64_t>(b) * H;
   const int off0 = rg * H + c0;
 
   __shared__ float4 s_hold[RPT - RR][2][NT];  // rows m >= RR: real, imag
   __shared__ float4 s_red[NT / 64][CB];
-  __shared__ float s_dot[NT / 64][3];
+  __shared__ float s_dot[NT / 64][4];
 
   float4 xr[RR], xi[RR];
   float kr[RPT], vr[RPT];
@@ -315,14 +331,22 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
   for (int m = 0; m < RPT; ++m) {
     kr[m] = io<IO>::load(kb, rg + NRG * m);
     vr[m] = io<IO>::load(vb, rg + NRG * m);
+    if constexpr (FUSED) vr[m] = vr[m] / (1.f + expf(-vr[m]));  // silu
   }
-  const float g = io<GT>::load(gamma, b);
+  float g;
+  float qq = 0.f;  // fused: this thread's share of |q|^2 (entries tid and tid + 512)
+  if constexpr (FUSED) {
+    const float logit = io<IO>::load(qb, 3 * H);
+    g = 0.1f / (1.f + expf(-logit)) * (fz.mask != nullptr ? static_cast<float>(fz.mask[b]) : 1.f);
+    const float q0 = io<IO>::load(qb, tid), q1 = io<IO>::load(qb, tid + NT);
+    qq = fmaf(q0, q0, q1 * q1);
+  } else {
+    g = io<GT>::load(gamma, b);
+  }
   float4 qc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (readout)
-    qc = make_float4(io<IO>::load(q, static_cast<int64_t>(b) * H + c0),
-                     io<IO>::load(q, static_cast<int64_t>(b) * H + c0 + 1),
-                     io<IO>::load(q, static_cast<int64_t>(b) * H + c0 + 2),
-                     io<IO>::load(q, static_cast<int64_t>(b) * H + c0 + 3));
+    qc = make_float4(io<IO>::load(qb, c0), io<IO>::load(qb, c0 + 1), io<IO>::load(qb, c0 + 2),
+                     io<IO>::load(qb, c0 + 3));
   float4 ar = make_float4(0.f, 0.f, 0.f, 0.f), ai = ar, br = ar, bi = ar;
   auto acc = [&](float kx, float vx, const float4& yr, const float4& yi) {
     ar.x = fmaf(kx, yr.x, ar.x); ar.y = fmaf(kx, yr.y, ar.y);
@@ -381,6 +405,7 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
     kk += __shfl_xor(kk, off);
     vv += __shfl_xor(vv, off);
     kv += __shfl_xor(kv, off);
+    if constexpr (FUSED) qq += __shfl_xor(qq, off);
   }
   if (lane < CGN) {
     s_red[wave][4 * cg + 0] = make_float4(ar.x, ai.x, br.x, bi.x);
@@ -389,7 +414,7 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
     s_red[wave][4 * cg + 3] = make_float4(ar.w, ai.w, br.w, bi.w);
   }
   if (lane == 0) {
-    s_dot[wave][0] = kk; s_dot[wave][1] = vv; s_dot[wave][2] = kv;
+    s_dot[wave][0] = kk; s_dot[wave][1] = vv; s_dot[wave][2] = kv; s_dot[wave][3] = qq;
   }
   __syncthreads();
   float4 A[4];
@@ -402,10 +427,27 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
       const float4 x = s_red[w][4 * cg + e];
       A[e].x += x.x; A[e].y += x.y; A[e].z += x.z; A[e].w += x.w;
     }
-  kk = s_dot[0][0]; vv = s_dot[0][1]; kv = s_dot[0][2];
+  kk = s_dot[0][0]; vv = s_dot[0][1]; kv = s_dot[0][2]; qq = s_dot[0][3];
 #pragma unroll
   for (int w = 1; w < NT / 64; ++w) {
-    kk += s_dot[w][0]; vv += s_dot[w][1]; kv += s_dot[w][2];
+    kk += s_dot[w][0]; vv += s_dot[w][1]; kv += s_dot[w][2]; qq += s_dot[w][3];
+  }
+  if constexpr (FUSED) {  // the sums of the normalised rows: scale by the norms
+    const float nk = 1.f / fmaxf(sqrtf(kk), 1e-12f), nv = 1.f / fmaxf(sqrtf(vv), 1e-12f);
+    const float nq = 1.f / fmaxf(sqrtf(qq), 1e-12f);
+    kv = kv * nk * nv;
+    kk = kk * nk * nk;
+    vv = vv * nv * nv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      A[e].x *= nk; A[e].y *= nk; A[e].z *= nv; A[e].w *= nv;
+    }
+#pragma unroll
+    for (int m = 0; m < RPT; ++m) {
+      kr[m] *= nk;
+      vr[m] *= nv;
+    }
+    qc.x *= nq; qc.y *= nq; qc.z *= nq; qc.w *= nq;
   }
   bool ok;
   const NCoef N = cham::cayley_n_guarded(g, kk, vv, kv, ok);
@@ -421,6 +463,8 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
     ci[e] = N.n11r * s.y + N.n11i * s.x + N.n12r * s.w + N.n12i * s.z;
     dr[e] = N.n12r * s.x - N.n12i * s.y + N.n22r * s.z - N.n22i * s.w;
     di[e] = N.n12r * s.y + N.n12i * s.x + N.n22r * s.w + N.n22i * s.z;
+    // identity token: the column sums were taken with the non-finite rows (NaN * 0 is NaN)
+    if (!ok) cr[e] = ci[e] = dr[e] = di[e] = 0.f;
   }
   float* pp = part + (static_cast<int64_t>(b) * nblk + blk) * H;
   auto upd = [&](int m, float4 yr, float4 yi) {
@@ -488,7 +532,7 @@ hipError_t launch_t(const void* q, const void* k, const void* v, const void* gam
   else if (h < 512) VMI_CS(32, 8, false);
   else if (h == 1024)
     hipLaunchKernelGGL((cham_step1024_kernel<IO, GT, Map>), grid, dim3(512), 0, stream, qq, kq, vq,
-                       gg, hr, hi, rr, ri, part, nstates, map);
+                       gg, hr, hi, rr, ri, part, nstates, map, ChamFused{});
   else VMI_CS(16, 8, false);
 #undef VMI_CS
   hipError_t e = hipGetLastError();
@@ -498,7 +542,40 @@ hipError_t launch_t(const void* q, const void* k, const void* v, const void* gam
   return hipGetLastError();
 }
 
+template <typename IO>
+hipError_t launch_fused_t(const void* proj, int64_t stride, const uint8_t* mask, float* hr,
+                         float* hi, float* rr, float* ri, void* out, int B, float* part,
+                         hipStream_t stream) {
+  constexpr int h = 1024, nblk = h / 32;
+  const int nstates = rr ? 2 : 1;
+  const IO* p = static_cast<const IO*>(proj);
+  hipLaunchKernelGGL((cham_step1024_kernel<IO, IO, DenseItems, true>), dim3(nblk, B, nstates),
+                     dim3(512), 0, stream, p, p, p, p, hr, hi, rr, ri, part, nstates,
+                     DenseItems{}, ChamFused{stride, mask});
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((cham_step_finish_kernel<IO>), dim3((h + 255) / 256, B), dim3(256), 0, stream,
+                     part, static_cast<IO*>(out), h, nblk);
+  return hipGetLastError();
+}
+
 }  // namespace chams
+
+bool cham_step_fused_supported(int64_t h) { return h == 1024; }
+
+hipError_t launch_cham_step_fused(const void* proj, int64_t proj_stride, int io_dtype,
+                                  const uint8_t* mask, float* hr, float* hi, float* rr, float* ri,
+                                  void* out, int B, void* workspace, hipStream_t stream) {
+  float* part = static_cast<float*>(workspace);
+  if (io_dtype == VMI_F32)
+    return chams::launch_fused_t<float>(proj, proj_stride, mask, hr, hi, rr, ri, out, B, part,
+                                        stream);
+  if (io_dtype == VMI_BF16)
+    return chams::launch_fused_t<bf16_t>(proj, proj_stride, mask, hr, hi, rr, ri, out, B, part,
+                                         stream);
+  return chams::launch_fused_t<f16_t>(proj, proj_stride, mask, hr, hi, rr, ri, out, B, part,
+                                      stream);
+}
 
 size_t cham_step_workspace_bytes(int64_t B, int64_t h) {
   return static_cast<size_t>(B) * ((h + chams::CB_MIN - 1) / chams::CB_MIN) * h * sizeof(float);

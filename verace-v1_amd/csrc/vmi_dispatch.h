@@ -140,6 +140,14 @@ hipError_t launch_cham_step(const void* q, const void* k, const void* v, const v
                             float* ri, void* out, int B, int h, void* workspace,
                             hipStream_t stream);
 
+// The same fused with the projections before it (h = 1024, dense states): proj [B, stride] raw
+// (x [W_q; W_k; W_v; W_gamma]^T, one row per item); v = silu(.), q, k, v normalised and gamma =
+// 0.1 sigmoid(.) * mask in the kernel.  Workspace as cham_step_workspace_bytes(B, 1024).
+bool cham_step_fused_supported(int64_t h);
+hipError_t launch_cham_step_fused(const void* proj, int64_t proj_stride, int io_dtype,
+                                  const uint8_t* mask, float* hr, float* hi, float* rr, float* ri,
+                                  void* out, int B, void* workspace, hipStream_t stream);
+
 // The same over the hologram pool of a decode state cache ([N, 2, h, h] per layer: slot s's
 // real plane at pool + 2 s h^2, imaginary plane after it), in_slot / out_slot host arrays of
 // B <= kMaxSlotArgs items (-1 in: the identity); no readout state (every cached hologram

@@ -21,6 +21,7 @@ Drop-in replacements for the reference's SSSD hot path:
 * ``launch_cham_hip_update``   <- ``verace_v1.serving.triton_kernels.launch_cham_triton_update``
                                (CHAM holographic scan, holographic_dim <= 1024)
 * ``cham_step_``               -- in-place single-token CHAM step (opt-in)
+* ``cham_step_fused_``         -- the same step with silu, the normalisations and gamma fused in
 * ``ContinuousHolographicMemory`` <- ``verace_v1.modules.cham_memory.ContinuousHolographicMemory``
 * ``ManifoldContinuousMoE`` / ``SiTUGLU`` <- ``verace_v1.modules.mcmoe`` / ``.activations`` (torch ops)
 * ``VeraceV1Layer`` / ``VeraceV1Model`` / ``VeraceV1Config`` / ``DecodeState``
@@ -34,7 +35,8 @@ autograd (``ops.py``), for FakeTensor / meta tracing and ``torch.compile``.
 
 All compute runs in ``libverace_sssd.so`` (C ABI: ``include/verace_sssd.h``).
 """
-from .hip_kernels import (HAS_HIP, SSSDScanFunction, cham_step_, launch_cham_hip_update,
+from .hip_kernels import (HAS_HIP, SSSDScanFunction, cham_step_, cham_step_fused_,
+                          launch_cham_hip_update,
                           launch_sssd_hip_scan, launch_sssd_hip_scan_bwd,
                           launch_sssd_hip_scan_fused,
                           newton_schulz_unitary_retraction, parallel_newton_schulz_retraction,
@@ -61,6 +63,7 @@ __all__ = [
     "sssd_step_",
     "sssd_step_fused_",
     "cham_step_",
+    "cham_step_fused_",
     "ContinuousHolographicMemory",
     "ManifoldContinuousMoE",
     "SiTUGLU",

@@ -12,7 +12,9 @@ Newton-Schulz readout ``Re(NS_3(H_t) q_t)``), then ``norm(w_out(.))``.  The raw 
 ``(H_real, H_imag)`` is returned, never retracted.
 
 :meth:`step_` is the opt-in in-place single-token step for callers that own the state (a
-decode loop): the reference re-runs the forward at seq_len 1 and returns a fresh state.
+decode loop): the reference re-runs the forward at seq_len 1 and returns a fresh state.  At
+holographic_dim 1024 it runs the projections as one GEMM on the stacked weights and lets the
+step kernel form silu(v), the normalisations and gamma (:func:`cham_step_fused_`).
 """
 from __future__ import annotations
 
@@ -22,7 +24,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .hip_kernels import cham_step_, launch_cham_hip_update
+from .hip_kernels import cham_step_, cham_step_fused_, launch_cham_hip_update
 
 
 class ContinuousHolographicMemory(nn.Module):
@@ -36,6 +38,29 @@ class ContinuousHolographicMemory(nn.Module):
         self.w_gamma = nn.Linear(hidden_dim, 1, bias=False)
         self.w_out = nn.Linear(holographic_dim, hidden_dim, bias=False)
         self.norm = nn.RMSNorm(hidden_dim)
+        self.fuse_projections = True  # False: the decode step always takes the unfused ops
+        self._proj_key = None
+        self._proj_cat = None
+
+    def _stacked_weight(self) -> torch.Tensor:
+        """[W_q; W_k; W_v; W_gamma] as one [3h + 1, hidden] weight, rebuilt whenever one of the
+        four changes (storage or in-place update), zero rows padding it to a multiple of 256 (the
+        GEMM library's kernel choice for odd N is much slower)."""
+        ws = (self.w_q.weight, self.w_k.weight, self.w_v.weight, self.w_gamma.weight)
+        key = tuple((w.data_ptr(), w._version, w.dtype) for w in ws)
+        if self._proj_key != key:
+            cat = torch.cat([w.detach() for w in ws], 0)
+            pad = (-cat.shape[0]) % 256
+            if pad:
+                cat = torch.cat([cat, cat.new_zeros(pad, cat.shape[1])], 0)
+            self._proj_cat, self._proj_key = cat, key
+        return self._proj_cat
+
+    def _fused_step(self, x: torch.Tensor) -> bool:
+        return (self.fuse_projections and x.shape[1] == 1 and self.holographic_dim == 1024
+                and x.dtype in (torch.bfloat16, torch.float16, torch.float32)
+                and all(w.dtype == x.dtype for w in (self.w_q.weight, self.w_k.weight,
+                                                      self.w_v.weight, self.w_gamma.weight)))
 
     def project(self, x: torch.Tensor, active_mask: Optional[torch.Tensor] = None):
         """q, k, v [B, T, h] and gamma [B, T] as the reference builds them (:128-155)."""
@@ -73,6 +98,10 @@ class ContinuousHolographicMemory(nn.Module):
         [B, h, h] float32 updated in place.  ``readout`` is the readout state
         R = NS_3(H) carried beside H (updated in place too) when H is not unitary; None
         when H came from the identity start (then NS_3(H) = H).  Returns y [B, 1, hidden]."""
-        q, k, v, gamma = self.project(x, active_mask)
-        rec = cham_step_(q, k, v, gamma, hologram, readout)
+        if self._fused_step(x):  # one projection GEMM; normalisation and gamma in the kernel
+            rec = cham_step_fused_(F.linear(x, self._stacked_weight()), self.holographic_dim,
+                                   hologram, readout, active_mask)
+        else:
+            q, k, v, gamma = self.project(x, active_mask)
+            rec = cham_step_(q, k, v, gamma, hologram, readout)
         return self.norm(self.w_out(rec.to(self.w_out.weight.dtype)))

@@ -431,6 +431,63 @@ def launch_cham_hip_update(
     return out, (hr, hi)
 
 
+def cham_step_fused_(
+    proj: torch.Tensor,
+    holographic_dim: int,
+    hologram: Tuple[torch.Tensor, torch.Tensor],
+    readout: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+    active_mask: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """:func:`cham_step_` with the projections' post-processing fused (``cham_memory.py:128-155``
+    at seq_len 1): ``proj`` [B, 1, >= 3h + 1] (or [B, >= 3h + 1]) is ``x @ [W_q; W_k; W_v;
+    W_gamma].T`` (raw); ``v = silu(.)``, q, k, v are L2-normalised and ``gamma = 0.1 *
+    sigmoid(.) * active_mask`` inside the kernel.  hologram / readout as :func:`cham_step_`,
+    updated in place.  Returns ``Re(NS_3(H') q)`` [B, 1, h] in proj's dtype.  Only
+    holographic_dim 1024 (the reference's default) runs fused; other sizes raise."""
+    _require_device(proj, "proj")
+    hr, hi = hologram
+    h = holographic_dim
+    for name, t in (("H_real", hr), ("H_imag", hi)):
+        _require_device(t, name)
+    if hr.dtype != torch.float32 or hi.dtype != torch.float32 or not hr.is_contiguous() \
+            or not hi.is_contiguous() or hr.dim() != 3 or hr.shape != hi.shape:
+        raise RuntimeError("verace_amd: hologram must be two contiguous float32 [B, h, h] tensors")
+    B = hr.shape[0]
+    if tuple(hr.shape) != (B, h, h) or proj.shape[0] != B:
+        raise RuntimeError(f"verace_amd: hologram {tuple(hr.shape)} does not match proj {tuple(proj.shape)}")
+    if h != 1024:
+        raise RuntimeError("verace_amd: the fused CHAM step needs holographic_dim 1024")
+    rr = ri = None
+    if readout is not None:
+        rr, ri = readout
+        for name, t in (("R_real", rr), ("R_imag", ri)):
+            _require_device(t, name)
+            if t.dtype != torch.float32 or not t.is_contiguous() or t.shape != hr.shape:
+                raise RuntimeError(f"verace_amd: {name} must be a contiguous float32 {tuple(hr.shape)} tensor")
+    if proj.dim() == 3 and proj.shape[1] != 1:
+        raise RuntimeError(f"verace_amd: proj must hold one token per item, got {tuple(proj.shape)}")
+    p2 = proj.reshape(B, proj.shape[-1])
+    if p2.shape[1] < 3 * h + 1:
+        raise RuntimeError(f"verace_amd: proj has {p2.shape[1]} columns, needs >= {3 * h + 1}")
+    if p2.stride(1) != 1:
+        p2 = p2.contiguous()
+    mask = None
+    if active_mask is not None:
+        _require_device(active_mask, "active_mask")
+        mask = active_mask.reshape(B).to(torch.uint8).contiguous()
+    out = torch.empty(B, 1, h, device=proj.device, dtype=proj.dtype)
+    lib = _lib.load()
+    ws_bytes = ctypes.c_size_t(0)
+    _lib.check(lib.vmi_cham_step_workspace_bytes(B, h, ctypes.byref(ws_bytes)),
+               "vmi_cham_step_workspace_bytes")
+    ws = torch.empty(ws_bytes.value, device=proj.device, dtype=torch.uint8) if ws_bytes.value else None
+    _lib.check(lib.vmi_cham_step_fused(_ptr(p2), p2.stride(0), _lib.dtype_code(proj.dtype), _ptr(mask),
+                                       _ptr(hr), _ptr(hi), _ptr(rr), _ptr(ri), _ptr(out), B, h,
+                                       _ptr(ws), ws_bytes.value, _lib.stream_handle(proj.device)),
+               "vmi_cham_step_fused")
+    return out
+
+
 def cham_step_(
     q: torch.Tensor,
     k: torch.Tensor,

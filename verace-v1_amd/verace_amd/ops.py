@@ -13,6 +13,8 @@ Replaces, for tracing purposes, the reference's Triton launcher ``launch_sssd_tr
   :func:`sssd_step_fused_` (mutates state).
 * ``verace::cham_scan(q, k, v, gamma, h0_real?, h0_imag?) -> (out, h_real, h_imag)``.
 * ``verace::cham_step_(q, k, v, gamma, h_real!, h_imag!, r_real!?, r_imag!?) -> out``.
+* ``verace::cham_step_fused_(proj, h, h_real!, h_imag!, r_real!?, r_imag!?, mask?) -> out`` --
+  :func:`cham_step_fused_` (mutates the states).
 * ``verace::ns_retraction(h_real, h_imag, steps) -> (real, imag)``.
 
 The eager module path calls the launchers directly (no dispatcher overhead in a decode loop);
@@ -146,6 +148,20 @@ def cham_step_(q: Tensor, k: Tensor, v: Tensor, gamma: Tensor, h_real: Tensor, h
 def _cham_step_fake(q, k, v, gamma, h_real, h_imag, r_real, r_imag):
     B, h, _ = h_real.shape
     return q.new_empty((B, 1, h))
+
+
+@torch.library.custom_op("verace::cham_step_fused_",
+                         mutates_args=("h_real", "h_imag", "r_real", "r_imag"))
+def cham_step_fused_(proj: Tensor, holographic_dim: int, h_real: Tensor, h_imag: Tensor,
+                     r_real: Optional[Tensor], r_imag: Optional[Tensor],
+                     active_mask: Optional[Tensor]) -> Tensor:
+    readout = None if r_real is None else (r_real, r_imag)
+    return hk.cham_step_fused_(proj, holographic_dim, (h_real, h_imag), readout, active_mask)
+
+
+@cham_step_fused_.register_fake
+def _cham_step_fused_fake(proj, holographic_dim, h_real, h_imag, r_real, r_imag, active_mask):
+    return proj.new_empty((proj.shape[0], 1, holographic_dim))
 
 
 @torch.library.custom_op("verace::ns_retraction", mutates_args=())
