@@ -289,6 +289,22 @@ int vmi_cham_step_inplace(const void* q, const void* k, const void* v, const voi
                           float* r_real, float* r_imag, void* out, int64_t B, int64_t h,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* vmi_cham_scan_fwd from the identity fused with the projections before it (the reference's
+ * CHAM forward with no initial hologram, cham_memory.py:128-155 then :167-238, as the model's
+ * prefill calls it):
+ *   proj : [B, T, proj_stride] io_dtype (BF16 or F16), row (b, t) = x_{b,t} [W_q; W_k; W_v;
+ *          W_gamma]^T raw (q at 0, k at h, v at 2h, the gamma logit at 3h); proj_stride >= 3h + 1
+ *          and a multiple of 8; proj and out 16-byte aligned;
+ *   in the kernels v = silu(v), q, k, v are L2-normalised (F.normalize, eps 1e-12) and
+ *   gamma = 0.1 sigmoid(logit) * mask[b, t] (mask: [B, T] uint8, null = every token active);
+ *   out : [B, T, h] io_dtype = Re(NS_3(H_t) q_t) (= Re(H_t q_t): H_t is unitary);
+ *   h_real_out, h_imag_out : [B, h, h] float32, the raw final state.
+ * 128 < h <= 1024 with h % 8 == 0 (otherwise VMI_ERR_UNSUPPORTED: run the unfused ops and
+ * vmi_cham_scan_fwd).  Workspace from vmi_cham_scan_workspace_bytes. */
+int vmi_cham_scan_fused(const void* proj, int64_t proj_stride, int io_dtype, const uint8_t* mask,
+                        void* out, float* h_real_out, float* h_imag_out, int64_t B, int64_t T,
+                        int64_t h, void* workspace, size_t workspace_bytes, void* stream);
+
 /* vmi_cham_step_inplace fused with the projections before it: the CHAM decode step of the
  * reference's forward at seq_len 1 from the projections on (cham_memory.py:128-155 before the
  * scan, called per token from acd_engine.py:116-121 and hyper_generate.py:59-63).

@@ -39,6 +39,8 @@ def test_opcheck_scan_step_cham_ns(device):
     st128 = torch.linalg.qr(torch.randn(3, 2, 128, 128))[0].contiguous().to(device)
     projc = torch.randn(2, 1, 3 * 1024 + 1, device=device).to(torch.bfloat16)
     Hc = torch.eye(1024, device=device).expand(2, -1, -1).contiguous()
+    torch.library.opcheck(torch.ops.verace.cham_scan_fused.default,
+                          (torch.randn(2, 20, 3 * 256 + 1, device=device).to(torch.bfloat16), 256, None))
     torch.library.opcheck(torch.ops.verace.cham_step_fused_.default,
                           (projc, 1024, Hc.clone(), torch.zeros_like(Hc), None, None, None))
     torch.library.opcheck(torch.ops.verace.sssd_step_fused_.default,

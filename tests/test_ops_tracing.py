@@ -32,6 +32,8 @@ def test_fake_kernels_give_reference_layouts():
                                        None, None).shape == (3, 1, 32)
     projc = torch.empty(3, 1, 3 * 1024 + 1, device="meta", dtype=torch.bfloat16)
     H1 = torch.empty(3, 1024, 1024, device="meta")
+    o2, r2, i2 = torch.ops.verace.cham_scan_fused(projc.expand(3, 5, -1), 1024, None)
+    assert o2.shape == (3, 5, 1024) and r2.shape == (3, 1024, 1024) and i2.dtype == torch.float32
     oc = torch.ops.verace.cham_step_fused_(projc, 1024, H1, H1.clone(), None, None, None)
     assert oc.shape == (3, 1, 1024) and oc.dtype == torch.bfloat16
     r, i = torch.ops.verace.ns_retraction(H, H, 3)

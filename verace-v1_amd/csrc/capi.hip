@@ -274,6 +274,30 @@ int vmi_cham_scan_fwd(const void* q, const void* k, const void* v, const void* g
                                           static_cast<int>(h), workspace, s));
 }
 
+int vmi_cham_scan_fused(const void* proj, int64_t proj_stride, int io_dtype, const uint8_t* mask,
+                        void* out, float* h_real_out, float* h_imag_out, int64_t B, int64_t T,
+                        int64_t h, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!valid_dtype(io_dtype)) return VMI_ERR_INVALID_ARG;
+  if (B < 0 || T < 0 || h < 1 || B * T > INT32_MAX) return VMI_ERR_INVALID_ARG;
+  if (!vmi::cham_fused_scan_supported(io_dtype, h)) return VMI_ERR_UNSUPPORTED;
+  if (h_real_out == nullptr || h_imag_out == nullptr) return VMI_ERR_INVALID_ARG;
+  // 16-byte vector loads of q rows and 8-byte loads of k, v rows: stride a multiple of 8
+  // elements, the base and the output 16-byte aligned
+  if (proj_stride < 3 * h + 1 || proj_stride % 8 != 0) return VMI_ERR_INVALID_ARG;
+  if (T > 0 && (proj == nullptr || out == nullptr || reinterpret_cast<uintptr_t>(proj) % 16 != 0 ||
+                reinterpret_cast<uintptr_t>(out) % 16 != 0))
+    return VMI_ERR_INVALID_ARG;
+  const size_t sb = static_cast<size_t>(B) * h * h * sizeof(float);
+  if (B > 0 && ranges_overlap(h_real_out, sb, h_imag_out, sb)) return VMI_ERR_ALIAS;
+  const size_t need = vmi::cham_scan_workspace_bytes(B, T, h);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return VMI_ERR_WORKSPACE;
+  if (B == 0) return VMI_OK;
+  return hip_status(vmi::launch_cham_wide_fused(proj, proj_stride, io_dtype, mask, out, h_real_out,
+                                                h_imag_out, static_cast<int>(B),
+                                                static_cast<int>(T), static_cast<int>(h),
+                                                workspace, static_cast<hipStream_t>(stream)));
+}
+
 int vmi_cham_step_workspace_bytes(int64_t B, int64_t h, size_t* bytes) {
   if (bytes == nullptr || B < 0 || h < 1) return VMI_ERR_INVALID_ARG;
   if (h > 1024 || h % 4 != 0) return VMI_ERR_UNSUPPORTED;

@@ -74,5 +74,16 @@ __device__ __forceinline__ typename raw<T>::type ldraw(const T* p, int64_t i) {
   return reinterpret_cast<const typename raw<T>::type*>(p)[i];
 }
 
+// Fused projections (kernels fed the stacked projection x [W_q; W_k; W_v; W_gamma]^T instead of
+// q, k, v, gamma; reference cham_memory.py:128-155): v = silu(v), and the normalised value of a
+// k or v element as the carry's f16 operands hold it (the coefficient kernel forms the Gram
+// entries from exactly these values, so every token's factor is unitary for the vectors the
+// carry multiplies).  Non-finite values read as 0; their token is guarded as the identity.
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+__device__ __forceinline__ _Float16 fused_f16(float x, float scale) {
+  const float y = x * scale;
+  return __builtin_isfinite(y) ? static_cast<_Float16>(y) : static_cast<_Float16>(0.f);
+}
+
 }  // namespace cham
 }  // namespace vmi

@@ -93,6 +93,20 @@ template <> __device__ __forceinline__ V4 to_f16x4<bf16_t>(uint2 raw, bool guard
   return r;
 }
 
+// 4 raw 16-bit inputs -> fp32
+template <typename IO> __device__ __forceinline__ void unpack4(uint2 raw, float* f);
+template <> __device__ __forceinline__ void unpack4<bf16_t>(uint2 raw, float* f) {
+  f[0] = __uint_as_float(raw.x << 16);
+  f[1] = __uint_as_float(raw.x & 0xffff0000u);
+  f[2] = __uint_as_float(raw.y << 16);
+  f[3] = __uint_as_float(raw.y & 0xffff0000u);
+}
+template <> __device__ __forceinline__ void unpack4<f16_t>(uint2 raw, float* f) {
+  const V4 h = __builtin_bit_cast(V4, raw);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) f[i] = static_cast<float>(h[i]);
+}
+
 // fp32 -> (hi, lo) f16 pair (round to nearest): x = hi + lo to ~2^-22.  hi by a packed
 // conversion per two values; lo = x - hi is exact in fp32 and is rounded to f16 by one
 // mixed-precision FMA per value (x * 1.0 - hi, hi read as f16 from its half of the register).
@@ -118,12 +132,16 @@ __device__ __forceinline__ void split8p(const float* x, V8& hi, V8& lo) {
 }
 
 // ---------------------------------------------------------------- 1: G and T per chunk
-template <typename IO>
+// FUSED: k and v are read from the stacked projection (passed as k; row b*T + t of `stride`
+// elements: k at h, v at 2h), v through silu, both scaled by the norms the fused coefficient
+// kernel stored (coef floats 6 and 7) and rounded by cham::fused_f16, as that kernel did for
+// the Gram entries of its coefficients.
+template <typename IO, bool FUSED = false>
 __global__ __launch_bounds__(64) void cm_prep_kernel(const IO* __restrict__ k,
                                                      const IO* __restrict__ v,
                                                      const float* __restrict__ coef,
                                                      E* __restrict__ tt, E* __restrict__ yop,
-                                                     int T, int h, int hp) {
+                                                     int T, int h, int hp, int64_t stride = 0) {
   __shared__ float G[RK][RK + 1];
   __shared__ float Nc[CT][NCF];
   __shared__ float Tf[2][RK][RK + 1];
@@ -134,7 +152,8 @@ __global__ __launch_bounds__(64) void cm_prep_kernel(const IO* __restrict__ k,
   const int tok = t0 + (l32 >> 1);
   const bool tok_ok = tok < T;
   const int64_t row = static_cast<int64_t>(b) * T + (tok_ok ? tok : 0);
-  const IO* src = ((l32 & 1) ? v : k) + row * h;
+  const IO* src = FUSED ? k + row * stride + ((l32 & 1) ? 2 * h : h) : ((l32 & 1) ? v : k) + row * h;
+  const float scale = FUSED ? coef[row * NCF + 6 + (l32 & 1)] : 1.f;
   // operand block kb of this chunk: lane (rho, g) holds features 16 kb + 4 g + {0..3} and
   // 16 kb + 8 + 4 g + {0..3} of rank row rho (the K order of the column kernel's state tiles;
   // G sums over every feature, so any order serves it); blocks past h and tokens past T are 0
@@ -146,7 +165,27 @@ __global__ __launch_bounds__(64) void cm_prep_kernel(const IO* __restrict__ k,
     uint2 r0 = make_uint2(0, 0), r1 = make_uint2(0, 0);
     if (tok_ok && f0 < h) r0 = *reinterpret_cast<const uint2*>(src + f0);
     if (tok_ok && f1 < h) r1 = *reinterpret_cast<const uint2*>(src + f1);
-    const V8 x = cat8<V4, V8>(to_f16x4<IO>(r0, true), to_f16x4<IO>(r1, true));
+    V8 x;
+    if constexpr (FUSED) {
+      float f[8];
+      unpack4<IO>(r0, f);
+      unpack4<IO>(r1, f + 4);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float y = (l32 & 1) ? cham::silu_f(f[i]) : f[i];
+        x[i] = cham::fused_f16(y, scale);
+      }
+      if (!(tok_ok && f0 < h)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = static_cast<E>(0.f);
+      }
+      if (!(tok_ok && f1 < h)) {
+#pragma unroll
+        for (int i = 4; i < 8; ++i) x[i] = static_cast<E>(0.f);
+      }
+    } else {
+      x = cat8<V4, V8>(to_f16x4<IO>(r0, true), to_f16x4<IO>(r1, true));
+    }
     *reinterpret_cast<V8*>(dst + ks * 512) = x;
     if (ks < nks) acc = MM::mma32(x, x, acc);
   }
@@ -620,12 +659,15 @@ template <> __device__ __forceinline__ uint16_t pack_io<f16_t>(float x) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
 }
 
-template <typename IO, int TPW>
+// FUSED: q is read from the stacked projection (row b*T + t of `stride` elements, q at 0) and
+// L2-normalised here (F.normalize, eps 1e-12) before the power-of-two scaling.
+template <typename IO, int TPW, bool FUSED = false>
 __global__ __launch_bounds__(NTH) void cm_read_kernel(const IO* __restrict__ q,
                                                       const E* __restrict__ snap,
                                                       const E* __restrict__ yop,
                                                       const E* __restrict__ tt,
-                                                      IO* __restrict__ out, int B, int T, int h) {
+                                                      IO* __restrict__ out, int B, int T, int h,
+                                                      int64_t stride = 0) {
   constexpr int RPW = 32 * TPW, HP = NWV * RPW, NKB = HP / 16;
   __shared__ ReadSmem<TPW> sm;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -644,19 +686,33 @@ __global__ __launch_bounds__(NTH) void cm_read_kernel(const IO* __restrict__ q,
     constexpr int FPT = HP / 16, NP = FPT / 8;  // features and 8-element pieces per thread
     const int t = tid >> 4, s = tid & 15;       // 16 threads per token
     const int tok = t0 + t;
-    const IO* src = q + (static_cast<int64_t>(b) * T + (tok < T ? tok : 0)) * h;
+    const IO* src = q + (static_cast<int64_t>(b) * T + (tok < T ? tok : 0)) * (FUSED ? stride : h);
     float x[NP][8];
-    float mx = 0.f;
+    float mx = 0.f, ss = 0.f;
 #pragma unroll
     for (int u = 0; u < NP; ++u) {
       const int f = s * FPT + 8 * u;  // h % 8 == 0: a piece is wholly in or out
       const uint4 raw = (tok < T && f < h) ? *reinterpret_cast<const uint4*>(src + f) : make_uint4(0, 0, 0, 0);
       unpack8<IO>(raw, x[u]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(x[u][e]));
+      for (int e = 0; e < 8; ++e) {
+        mx = fmaxf(mx, fabsf(x[u][e]));
+        if constexpr (FUSED) ss = fmaf(x[u][e], x[u][e], ss);
+      }
     }
 #pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    for (int o = 8; o >= 1; o >>= 1) {
+      mx = fmaxf(mx, __shfl_xor(mx, o));
+      if constexpr (FUSED) ss += __shfl_xor(ss, o);
+    }
+    if constexpr (FUSED) {  // the token's 16 threads hold its whole row: normalise it
+      const float nq = 1.f / fmaxf(sqrtf(ss), 1e-12f);
+      mx *= nq;
+#pragma unroll
+      for (int u = 0; u < NP; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[u][e] *= nq;
+    }
     int ex = 5;
     if (mx > 0.f && mx <= 3.0e38f) {
       (void)frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
@@ -888,13 +944,17 @@ hipError_t launch_typed(const IO* k, const IO* v, const float* coef, const float
 template <typename IO, int TPW>
 hipError_t launch_scan16(const IO* q, const IO* k, const IO* v, const float* coef, void* snap,
                          IO* out, float* fr, float* fi, int B, int T, int h, void* ws,
-                         hipStream_t stream) {
+                         hipStream_t stream, bool fused = false, int64_t stride = 0) {
   const int nc = (T + CT - 1) / CT;
   if (nc == 0) return hipSuccess;
   E* tt = static_cast<E*>(ws);
   E* yop = tt + static_cast<int64_t>(B) * nc * TT_STRIDE;
-  hipLaunchKernelGGL((cm_prep_kernel<IO>), dim3(nc, B), dim3(64), 0, stream, k, v, coef, tt, yop, T, h,
-                     NWV * 32 * TPW);
+  if (fused)
+    hipLaunchKernelGGL((cm_prep_kernel<IO, true>), dim3(nc, B), dim3(64), 0, stream, k, v, coef, tt,
+                       yop, T, h, NWV * 32 * TPW, stride);
+  else
+    hipLaunchKernelGGL((cm_prep_kernel<IO>), dim3(nc, B), dim3(64), 0, stream, k, v, coef, tt, yop,
+                       T, h, NWV * 32 * TPW, int64_t{0});
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((cm_cols_kernel<TPW, true>), dim3((h + COLS - 1) / COLS, B, 1), dim3(NTH), 0,
@@ -903,8 +963,12 @@ hipError_t launch_scan16(const IO* q, const IO* k, const IO* v, const float* coe
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int total = B * ((T + RG - 1) / RG);
-  hipLaunchKernelGGL((cm_read_kernel<IO, TPW>), dim3(8 * ((total + 7) / 8)), dim3(NTH), 0, stream, q,
-                     static_cast<const E*>(snap), yop, tt, out, B, T, h);
+  if (fused)
+    hipLaunchKernelGGL((cm_read_kernel<IO, TPW, true>), dim3(8 * ((total + 7) / 8)), dim3(NTH), 0,
+                       stream, q, static_cast<const E*>(snap), yop, tt, out, B, T, h, stride);
+  else
+    hipLaunchKernelGGL((cm_read_kernel<IO, TPW>), dim3(8 * ((total + 7) / 8)), dim3(NTH), 0, stream,
+                       q, static_cast<const E*>(snap), yop, tt, out, B, T, h, int64_t{0});
   return hipGetLastError();
 }
 
@@ -928,6 +992,25 @@ hipError_t launch_cham_mfma_scan(const void* q, const void* k, const void* v, in
   return chamm::launch_scan16<IO, TPW>(static_cast<const IO*>(q), static_cast<const IO*>(k),      \
                                        static_cast<const IO*>(v), coef, snap, static_cast<IO*>(out), \
                                        fr, fi, B, T, h, ws, stream)
+  if (io_dtype == VMI_BF16) {
+    if (hp == 256) VMI_CS(bf16_t, 1);
+    if (hp == 512) VMI_CS(bf16_t, 2);
+    VMI_CS(bf16_t, 4);
+  }
+  if (hp == 256) VMI_CS(f16_t, 1);
+  if (hp == 512) VMI_CS(f16_t, 2);
+  VMI_CS(f16_t, 4);
+#undef VMI_CS
+}
+
+hipError_t launch_cham_mfma_scan_fused(const void* proj, int64_t stride, int io_dtype,
+                                       const float* coef, void* snap, void* out, float* fr,
+                                       float* fi, int B, int T, int h, int hp, void* ws,
+                                       hipStream_t stream) {
+#define VMI_CS(IO, TPW)                                                                          \
+  return chamm::launch_scan16<IO, TPW>(static_cast<const IO*>(proj), static_cast<const IO*>(proj), \
+                                       static_cast<const IO*>(proj), coef, snap, static_cast<IO*>(out), \
+                                       fr, fi, B, T, h, ws, stream, true, stride)
   if (io_dtype == VMI_BF16) {
     if (hp == 256) VMI_CS(bf16_t, 1);
     if (hp == 512) VMI_CS(bf16_t, 2);

@@ -72,6 +72,72 @@ __global__ __launch_bounds__(256) void wide_coef_kernel(const IO* __restrict__ k
   }
 }
 
+// Fused (the stacked projection, row b*T + t: k at h, v at 2h, the gamma logit at 3h): silu(v),
+// the norms 1/|k|, 1/|v| (F.normalize, eps 1e-12) into the two spare floats of the token's
+// coefficients (the prep kernel scales with them), the Gram entries of the normalised rows as
+// rounded to f16, gamma = 0.1 sigmoid(logit) * mask[b*T + t] (null mask: 1).  h <= 1024.
+template <typename IO>
+__global__ __launch_bounds__(256) void wide_coef_fused_kernel(const IO* __restrict__ proj,
+                                                              int64_t stride,
+                                                              const uint8_t* __restrict__ mask,
+                                                              float* __restrict__ coef, int BT,
+                                                              int h) {
+  constexpr int MAXR = 16;  // elements per lane (h <= 1024)
+  const int lane = threadIdx.x & 63;
+  const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= BT) return;  // whole wave
+  const IO* row = proj + static_cast<int64_t>(tok) * stride;
+  float xk[MAXR], xv[MAXR];
+  float kk = 0.f, vv = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXR; ++i) {
+    const int r = lane + 64 * i;
+    xk[i] = r < h ? io<IO>::load(row, h + r) : 0.f;
+    xv[i] = r < h ? cham::silu_f(io<IO>::load(row, 2 * h + r)) : 0.f;
+    kk = fmaf(xk[i], xk[i], kk);
+    vv = fmaf(xv[i], xv[i], vv);
+  }
+  kk = row_pair_sum(row16_sum(kk));
+  vv = row_pair_sum(row16_sum(vv));
+  kk += __shfl_xor(kk, 32);
+  vv += __shfl_xor(vv, 32);
+  // F.normalize's scale (an infinite norm gives 0, as x / inf does); a NaN norm gives 0 too,
+  // so the token's finite elements stay 0 in the f16 operands (1e12 would overflow them) and
+  // the NaN itself guards the token below
+  const float nk = __builtin_isnan(kk) ? 0.f : 1.f / fmaxf(sqrtf(kk), 1e-12f);
+  const float nv = __builtin_isnan(vv) ? 0.f : 1.f / fmaxf(sqrtf(vv), 1e-12f);
+  float gk = 0.f, gv = 0.f, gkv = 0.f;
+  bool fin = true;
+#pragma unroll
+  for (int i = 0; i < MAXR; ++i) {
+    fin = fin && __builtin_isfinite(xk[i]) && __builtin_isfinite(xv[i]);
+    const float af = static_cast<float>(cham::fused_f16(xk[i], nk));
+    const float cf = static_cast<float>(cham::fused_f16(xv[i], nv));
+    gk = fmaf(af, af, gk);
+    gv = fmaf(cf, cf, gv);
+    gkv = fmaf(af, cf, gkv);
+  }
+  gk = row_pair_sum(row16_sum(gk));
+  gv = row_pair_sum(row16_sum(gv));
+  gkv = row_pair_sum(row16_sum(gkv));
+  gk += __shfl_xor(gk, 32);
+  gv += __shfl_xor(gv, 32);
+  gkv += __shfl_xor(gkv, 32);
+  // a non-finite element anywhere in the token's k or v: the reference's solve is not finite
+  // and the token becomes the identity (its elements read as 0 in the rounded Gram above)
+  const bool all_fin = __all(fin);
+  if (lane == 0) {
+    const float logit = io<IO>::load(row, 3 * h);
+    const float mk = mask != nullptr ? static_cast<float>(mask[tok]) : 1.f;
+    const float gam = 0.1f / (1.f + expf(-logit)) * mk;
+    bool ok;
+    NCoef N = cham::cayley_n_guarded(all_fin ? gam : __builtin_nanf(""), gk, gv, gkv, ok);
+    float4* o = reinterpret_cast<float4*>(coef + static_cast<int64_t>(tok) * NCF);
+    o[0] = make_float4(N.n11r, N.n11i, N.n12r, N.n12i);
+    o[1] = make_float4(N.n22r, N.n22i, nk, nv);
+  }
+}
+
 // ---------------------------------------------------------------- shared column machinery
 // A column (of the state, or one token's vector) is held by LPC lanes (a wave carries
 // 64 / LPC of them); lane ll = lane % LPC holds rows 4 LPC i + 4 ll + e (i < RPL / 4,
@@ -613,7 +679,9 @@ hipError_t launch_rpl(const void* q, const void* k, const void* v, const float* 
   constexpr int io_code = std::is_same<IO, bf16_t>::value ? VMI_BF16
                         : (std::is_same<IO, f16_t>::value ? VMI_F16 : VMI_F32);
   hipError_t e;
-  const bool mm = cham_mfma_usable(io_code, h, k, v);
+  // T = 0 takes the column kernel below, which passes the start state through without reading
+  // a token (the matrix-core kernels load chunk 0's operands unconditionally)
+  const bool mm = T > 0 && cham_mfma_usable(io_code, h, k, v);
   if (mm && !h0r && (reinterpret_cast<uintptr_t>(q) & 15) == 0 &&
       (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
     // identity start: chunked carry and chunked readout on the matrix cores (f16 snapshots
@@ -683,7 +751,42 @@ hipError_t launch_io(const void* q, const void* k, const void* v, const void* ga
   return launch_typed<IO, f16_t>(q, k, v, gamma, h0r, h0i, out, hr_out, hi_out, B, T, h, ws, stream);
 }
 
+template <typename IO>
+hipError_t launch_fused_io(const void* proj, int64_t stride, const uint8_t* mask, void* out,
+                           float* hr_out, float* hi_out, int B, int T, int h, void* workspace,
+                           hipStream_t stream) {
+  if (T == 0)  // the identity passed through (no token is read)
+    return launch_io<IO>(proj, proj, proj, proj, std::is_same<IO, bf16_t>::value ? VMI_BF16 : VMI_F16,
+                         nullptr, nullptr, out, hr_out, hi_out, B, 0, h, workspace, stream);
+  const WideWs w = carve(workspace, B, T, h);
+  const int BT = B * T;
+  if (BT > 0) {
+    hipLaunchKernelGGL((wide_coef_fused_kernel<IO>), dim3((BT + 3) / 4), dim3(256), 0, stream,
+                       static_cast<const IO*>(proj), stride, mask, w.coef, BT, h);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  constexpr int io_code = std::is_same<IO, bf16_t>::value ? VMI_BF16 : VMI_F16;
+  return launch_cham_mfma_scan_fused(proj, stride, io_code, w.coef, w.snap, out, hr_out, hi_out, B,
+                                     T, h, padded(h), w.mm, stream);
+}
+
 }  // namespace chamw
+
+bool cham_fused_scan_supported(int io_dtype, int64_t h) {
+  return (io_dtype == VMI_BF16 || io_dtype == VMI_F16) && h > 128 && h <= kChamMaxDim &&
+         h % 8 == 0;
+}
+
+hipError_t launch_cham_wide_fused(const void* proj, int64_t proj_stride, int io_dtype,
+                                  const uint8_t* mask, void* out, float* hr_out, float* hi_out,
+                                  int B, int T, int h, void* workspace, hipStream_t stream) {
+  if (io_dtype == VMI_BF16)
+    return chamw::launch_fused_io<bf16_t>(proj, proj_stride, mask, out, hr_out, hi_out, B, T, h,
+                                          workspace, stream);
+  return chamw::launch_fused_io<f16_t>(proj, proj_stride, mask, out, hr_out, hi_out, B, T, h,
+                                       workspace, stream);
+}
 
 size_t cham_wide_workspace_bytes(int64_t B, int64_t T, int64_t h) {
   return chamw::carve(nullptr, B, T, h).floats * sizeof(float);

@@ -164,6 +164,16 @@ hipError_t launch_cham_wide(const void* q, const void* k, const void* v, const v
                             void* out, float* hr_out, float* hi_out, int B, int T, int h,
                             void* workspace, hipStream_t stream);
 
+// cham_wide.hip: the scan fused with the projections before it (identity start, 16-bit I/O,
+// 128 < h <= kChamMaxDim, h % 8 == 0): proj [B, T, stride] raw (x [W_q; W_k; W_v; W_gamma]^T;
+// q at 0, k at h, v at 2h, the gamma logit at 3h; stride % 8 == 0, 16-byte aligned base);
+// v = silu(v), q, k, v normalised and gamma = 0.1 sigmoid(.) * mask[b*T + t] in the kernels.
+// Workspace as cham_scan_workspace_bytes.
+bool cham_fused_scan_supported(int io_dtype, int64_t h);
+hipError_t launch_cham_wide_fused(const void* proj, int64_t proj_stride, int io_dtype,
+                                  const uint8_t* mask, void* out, float* hr_out, float* hi_out,
+                                  int B, int T, int h, void* workspace, hipStream_t stream);
+
 // cham_mfma.hip: the wide route's state carry on the matrix cores (16-bit k, v, h % 8 == 0,
 // 16-byte aligned k, v; entries of k, v below 65504 in magnitude, as L2-normalised rows are).
 bool cham_mfma_usable(int io_dtype, int h, const void* k, const void* v);
@@ -175,6 +185,12 @@ size_t cham_mfma_snap16_bytes(int64_t B, int64_t T, int64_t hp);
 hipError_t launch_cham_mfma_scan(const void* q, const void* k, const void* v, int io_dtype,
                                  const float* coef, void* snap, void* out, float* fr, float* fi,
                                  int B, int T, int h, int hp, void* ws, hipStream_t stream);
+// the same from the stacked projection [B*T, stride] (fused: silu(v), normalised q, k, v; coef
+// from the fused coefficient kernel, with the k and v norms in its floats 6 and 7)
+hipError_t launch_cham_mfma_scan_fused(const void* proj, int64_t stride, int io_dtype,
+                                       const float* coef, void* snap, void* out, float* fr,
+                                       float* fi, int B, int T, int h, int hp, void* ws,
+                                       hipStream_t stream);
 hipError_t launch_cham_mfma_cols(const void* k, const void* v, int io_dtype, const float* coef,
                                  const float* i0r, const float* i0i, const float* i1r,
                                  const float* i1i, float* snap, float* fr, float* fi, int B,

@@ -22,6 +22,7 @@ Drop-in replacements for the reference's SSSD hot path:
                                (CHAM holographic scan, holographic_dim <= 1024)
 * ``cham_step_``               -- in-place single-token CHAM step (opt-in)
 * ``cham_step_fused_``         -- the same step with silu, the normalisations and gamma fused in
+* ``launch_cham_hip_update_fused`` -- the CHAM scan from the identity with the same fusion
 * ``ContinuousHolographicMemory`` <- ``verace_v1.modules.cham_memory.ContinuousHolographicMemory``
 * ``ManifoldContinuousMoE`` / ``SiTUGLU`` <- ``verace_v1.modules.mcmoe`` / ``.activations`` (torch ops)
 * ``VeraceV1Layer`` / ``VeraceV1Model`` / ``VeraceV1Config`` / ``DecodeState``
@@ -36,7 +37,7 @@ autograd (``ops.py``), for FakeTensor / meta tracing and ``torch.compile``.
 All compute runs in ``libverace_sssd.so`` (C ABI: ``include/verace_sssd.h``).
 """
 from .hip_kernels import (HAS_HIP, SSSDScanFunction, cham_step_, cham_step_fused_,
-                          launch_cham_hip_update,
+                          launch_cham_hip_update, launch_cham_hip_update_fused,
                           launch_sssd_hip_scan, launch_sssd_hip_scan_bwd,
                           launch_sssd_hip_scan_fused,
                           newton_schulz_unitary_retraction, parallel_newton_schulz_retraction,
@@ -60,6 +61,7 @@ __all__ = [
     "launch_sssd_hip_scan",
     "launch_sssd_hip_scan_fused",
     "launch_cham_hip_update",
+    "launch_cham_hip_update_fused",
     "sssd_step_",
     "sssd_step_fused_",
     "cham_step_",

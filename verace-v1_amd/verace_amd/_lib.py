@@ -43,6 +43,7 @@ EXPORTED = (
     "vmi_state_cache_cham_step",
     "vmi_cham_scan_workspace_bytes",
     "vmi_cham_scan_fwd",
+    "vmi_cham_scan_fused",
     "vmi_sssd_scan_bwd_workspace_bytes",
     "vmi_sssd_scan_bwd",
     "vmi_cham_step_workspace_bytes",
@@ -127,6 +128,8 @@ def _declare(lib):
     lib.vmi_cham_step_inplace.restype = i32
     lib.vmi_cham_step_fused.argtypes = [vp, i64, i32, vp, vp, vp, vp, vp, vp, i64, i64, vp, sz, vp]
     lib.vmi_cham_step_fused.restype = i32
+    lib.vmi_cham_scan_fused.argtypes = [vp, i64, i32, vp, vp, vp, vp, i64, i64, i64, vp, sz, vp]
+    lib.vmi_cham_scan_fused.restype = i32
     lib.vmi_cham_ns_workspace_bytes.argtypes = [i64, i64, ctypes.POINTER(sz)]
     lib.vmi_cham_ns_workspace_bytes.restype = i32
     lib.vmi_cham_ns_retraction.argtypes = [vp, vp, vp, vp, i64, i64, i32, vp, sz, vp]

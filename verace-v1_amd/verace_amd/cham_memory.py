@@ -14,7 +14,9 @@ Newton-Schulz readout ``Re(NS_3(H_t) q_t)``), then ``norm(w_out(.))``.  The raw 
 :meth:`step_` is the opt-in in-place single-token step for callers that own the state (a
 decode loop): the reference re-runs the forward at seq_len 1 and returns a fresh state.  At
 holographic_dim 1024 it runs the projections as one GEMM on the stacked weights and lets the
-step kernel form silu(v), the normalisations and gamma (:func:`cham_step_fused_`).
+step kernel form silu(v), the normalisations and gamma (:func:`cham_step_fused_`); the forward
+does the same for a scan from the identity with 16-bit inputs and 128 < h <= 1024
+(:func:`launch_cham_hip_update_fused`).
 """
 from __future__ import annotations
 
@@ -24,7 +26,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .hip_kernels import cham_step_, cham_step_fused_, launch_cham_hip_update
+from .hip_kernels import (cham_fused_scan_supported, cham_step_, cham_step_fused_,
+                          launch_cham_hip_update, launch_cham_hip_update_fused)
 
 
 class ContinuousHolographicMemory(nn.Module):
@@ -56,6 +59,11 @@ class ContinuousHolographicMemory(nn.Module):
             self._proj_cat, self._proj_key = cat, key
         return self._proj_cat
 
+    def _fused_scan(self, x: torch.Tensor) -> bool:
+        return (self.fuse_projections and cham_fused_scan_supported(x.dtype, self.holographic_dim)
+                and all(w.dtype == x.dtype for w in (self.w_q.weight, self.w_k.weight,
+                                                      self.w_v.weight, self.w_gamma.weight)))
+
     def _fused_step(self, x: torch.Tensor) -> bool:
         return (self.fuse_projections and x.shape[1] == 1 and self.holographic_dim == 1024
                 and x.dtype in (torch.bfloat16, torch.float16, torch.float32)
@@ -86,8 +94,13 @@ class ContinuousHolographicMemory(nn.Module):
         if torch.is_grad_enabled() and x.requires_grad:
             raise RuntimeError("verace_amd.ContinuousHolographicMemory has no backward kernel "
                                "(the CHAM scan is inference-only here); run under torch.no_grad()")
-        q, k, v, gamma = self.project(x, active_mask)
-        rec, hologram = launch_cham_hip_update(q, k, v, gamma, initial_hologram)
+        if initial_hologram is None and self._fused_scan(x):
+            # one projection GEMM; silu, the normalisations and gamma in the scan's kernels
+            rec, hologram = launch_cham_hip_update_fused(F.linear(x, self._stacked_weight()),
+                                                         self.holographic_dim, active_mask)
+        else:
+            q, k, v, gamma = self.project(x, active_mask)
+            rec, hologram = launch_cham_hip_update(q, k, v, gamma, initial_hologram)
         y = self.norm(self.w_out(rec.to(self.w_out.weight.dtype)))
         return y, hologram
 

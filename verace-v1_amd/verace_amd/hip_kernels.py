@@ -431,6 +431,56 @@ def launch_cham_hip_update(
     return out, (hr, hi)
 
 
+def cham_fused_scan_supported(x_dtype: torch.dtype, holographic_dim: int) -> bool:
+    """Whether :func:`launch_cham_hip_update_fused` runs these shapes (16-bit I/O, 128 < h <= 1024,
+    h % 8 == 0); other shapes take the unfused ops and :func:`launch_cham_hip_update`."""
+    h = holographic_dim
+    return x_dtype in (torch.bfloat16, torch.float16) and 128 < h <= 1024 and h % 8 == 0
+
+
+def launch_cham_hip_update_fused(
+    proj: torch.Tensor,
+    holographic_dim: int,
+    active_mask: Optional[torch.Tensor] = None,
+):
+    """The CHAM scan from the identity with the projections' post-processing fused
+    (``cham_memory.py:128-155`` before the scan): ``proj`` [B, T, >= 3h + 1] is
+    ``x @ [W_q; W_k; W_v; W_gamma].T`` (raw); ``v = silu(.)``, q, k, v are L2-normalised and
+    ``gamma = 0.1 * sigmoid(.) * active_mask`` inside the kernels.  Returns (out [B, T, h] in
+    proj's dtype, (H_real, H_imag) the raw final state, float32), as
+    :func:`launch_cham_hip_update` without an initial hologram.  Shapes outside
+    :func:`cham_fused_scan_supported` raise."""
+    _require_device(proj, "proj")
+    if proj.dim() != 3:
+        raise RuntimeError(f"verace_amd: proj must be [B, T, N], got {tuple(proj.shape)}")
+    b, s, n = proj.shape
+    h = holographic_dim
+    if not cham_fused_scan_supported(proj.dtype, h):
+        raise RuntimeError("verace_amd: the fused CHAM scan needs bf16/fp16 and 128 < h <= 1024, h % 8 == 0")
+    if n < 3 * h + 1:
+        raise RuntimeError(f"verace_amd: proj has {n} columns, needs >= {3 * h + 1}")
+    if proj.stride(2) != 1 or proj.stride(1) % 8 != 0 or proj.stride(0) != s * proj.stride(1) \
+            or proj.data_ptr() % 16 != 0:
+        proj = _aligned(torch.nn.functional.pad(proj, (0, (-n) % 8)).contiguous())
+    mask = None
+    if active_mask is not None:
+        _require_device(active_mask, "active_mask")
+        mask = active_mask.reshape(b, s).to(torch.uint8).contiguous()
+    out = _aligned(torch.empty(b, s, h, device=proj.device, dtype=proj.dtype))
+    hr = torch.empty(b, h, h, device=proj.device, dtype=torch.float32)
+    hi = torch.empty(b, h, h, device=proj.device, dtype=torch.float32)
+    lib = _lib.load()
+    ws_bytes = ctypes.c_size_t(0)
+    _lib.check(lib.vmi_cham_scan_workspace_bytes(b, s, h, ctypes.byref(ws_bytes)),
+               "vmi_cham_scan_workspace_bytes")
+    ws = torch.empty(ws_bytes.value, device=proj.device, dtype=torch.uint8) if ws_bytes.value else None
+    _lib.check(lib.vmi_cham_scan_fused(_ptr(proj), proj.stride(1), _lib.dtype_code(proj.dtype),
+                                       _ptr(mask), _ptr(out), _ptr(hr), _ptr(hi), b, s, h, _ptr(ws),
+                                       ws_bytes.value, _lib.stream_handle(proj.device)),
+               "vmi_cham_scan_fused")
+    return out, (hr, hi)
+
+
 def cham_step_fused_(
     proj: torch.Tensor,
     holographic_dim: int,

@@ -13,6 +13,7 @@ Replaces, for tracing purposes, the reference's Triton launcher ``launch_sssd_tr
   :func:`sssd_step_fused_` (mutates state).
 * ``verace::cham_scan(q, k, v, gamma, h0_real?, h0_imag?) -> (out, h_real, h_imag)``.
 * ``verace::cham_step_(q, k, v, gamma, h_real!, h_imag!, r_real!?, r_imag!?) -> out``.
+* ``verace::cham_scan_fused(proj, h, mask?) -> (out, h_real, h_imag)`` -- :func:`launch_cham_hip_update_fused`.
 * ``verace::cham_step_fused_(proj, h, h_real!, h_imag!, r_real!?, r_imag!?, mask?) -> out`` --
   :func:`cham_step_fused_` (mutates the states).
 * ``verace::ns_retraction(h_real, h_imag, steps) -> (real, imag)``.
@@ -148,6 +149,21 @@ def cham_step_(q: Tensor, k: Tensor, v: Tensor, gamma: Tensor, h_real: Tensor, h
 def _cham_step_fake(q, k, v, gamma, h_real, h_imag, r_real, r_imag):
     B, h, _ = h_real.shape
     return q.new_empty((B, 1, h))
+
+
+@torch.library.custom_op("verace::cham_scan_fused", mutates_args=())
+def cham_scan_fused(proj: Tensor, holographic_dim: int,
+                    active_mask: Optional[Tensor]) -> Tuple[Tensor, Tensor, Tensor]:
+    out, (hr, hi) = hk.launch_cham_hip_update_fused(proj, holographic_dim, active_mask)
+    return out, hr, hi
+
+
+@cham_scan_fused.register_fake
+def _cham_scan_fused_fake(proj, holographic_dim, active_mask):
+    B, T, _ = proj.shape
+    h = holographic_dim
+    return (proj.new_empty((B, T, h)), proj.new_empty((B, h, h), dtype=torch.float32),
+            proj.new_empty((B, h, h), dtype=torch.float32))
 
 
 @torch.library.custom_op("verace::cham_step_fused_",
