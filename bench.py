@@ -828,6 +828,53 @@ MFMA_KERNELS = [  # (label, substring of the kernel name in rocprofv3's CSVs, de
 ]
 
 
+def trace_summary(trace_csv, match="vmi"):
+    """Markdown table of a rocprofv3 --kernel-trace CSV: dispatches grouped by kernel name,
+    grid and workgroup size (calls, average / min / max duration in us), this library's
+    kernels only (namespace vmi), largest total time first."""
+    import csv
+    groups = {}
+    with open(trace_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            if match not in name:
+                continue
+            wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+            grid = (int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"]),
+                    int(r["Grid_Size_Y"]) // int(r["Workgroup_Size_Y"]),
+                    int(r["Grid_Size_Z"]) // int(r["Workgroup_Size_Z"]))
+            us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+            groups.setdefault((name.split("(")[0], grid, wg), []).append(us)
+    def pretty(name):
+        # Itanium-mangled template kernels of this library: the last name component and the
+        # template arguments (bf16 / f16 / float element types, booleans as 0 / 1)
+        import re
+        m = re.match(r"_ZN((?:\d+\w+?)+?)I(.*)EEv", name)
+        if not m:
+            return name.replace("vmi::chunk::", "")
+        parts, pos, ids = m.group(1), 0, []
+        while pos < len(parts):
+            n = re.match(r"\d+", parts[pos:]).group(0)
+            pos += len(n)
+            ids.append(parts[pos:pos + int(n)])
+            pos += int(n)
+        args = m.group(2)
+        for a, b in (("NS_6bf16_tE", "bf16,"), ("NS_5f16_tE", "f16,"), ("DF16b", "bf16,"),
+                     ("DF16_", "f16,"), ("Lb1E", "1,"), ("Lb0E", "0,")):
+            args = args.replace(a, b)
+        args = re.sub(r"(?<![a-z0-9_])f(?=[A-Z,]|$)", "float,", args)
+        return f"{ids[-1]}<{args.rstrip(',')}>"
+
+    lines = ["| kernel | grid x threads | calls | avg us | min us | max us |",
+             "|---|---|---|---|---|---|"]
+    for (name, grid, wg), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        name = pretty(name)
+        g = ", ".join(str(x) for x in grid if x > 1) or "1"
+        lines.append(f"| `{name}` | ({g}) x {wg} | {len(v)} | {sum(v) / len(v):.1f} | "
+                     f"{min(v):.1f} | {max(v):.1f} |")
+    return "\n".join(lines)
+
+
 def mfma_summary(counter_csv, trace_csv, out_json):
     """Per-kernel MFMA counters from a rocprofv3 --pmc run (SQ_INSTS_VALU_MFMA_MOPS_{F16,BF16,
     F32}, SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE, SQ_INSTS_MFMA / VALU / LDS) and the kernel
@@ -907,6 +954,8 @@ def main():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc counter CSVs into "
                          "profiles/pmc_traffic_op_scan.json and exit")
+    ap.add_argument("--trace-summary", metavar="TRACE_CSV",
+                    help="group a rocprofv3 kernel trace of this library's kernels (markdown table)")
     ap.add_argument("--mfma-summary", nargs=2, metavar=("COUNTER_CSV", "TRACE_CSV"),
                     help="summarise a rocprofv3 --pmc MFMA counter run and a --kernel-trace run "
                          "of the same command into profiles/<--mfma-out> and exit")
@@ -919,6 +968,9 @@ def main():
     if args.pmc_summary:
         out = os.path.join(REPO_ROOT, "profiles", "pmc_traffic_op_scan.json")
         print(json.dumps(pmc_summary(args.pmc_summary[0], args.pmc_summary[1], out), indent=1))
+        return
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary))
         return
     if args.mfma_summary:
         out = os.path.join(REPO_ROOT, "profiles", args.mfma_out)
