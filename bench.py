@@ -825,6 +825,8 @@ MFMA_KERNELS = [  # (label, substring of the kernel name in rocprofv3's CSVs, de
     ("backward prep (bwdc_prep_kernel)", "bwdc_prep_kernel", 157.3),
     ("CHAM NS GEMM (ns_gemm2_kernel)", "ns_gemm2_kernel", 157.3),
     ("CHAM Z (wide_z_kernel)", "wide_z_kernel", 157.3),
+    ("CHAM matrix-core carry (cm_cols_kernel)", "cm_cols_kernel", MFMA_F16_PEAK_TFLOPS),
+    ("CHAM matrix-core readout (cm_read_kernel)", "cm_read_kernel", MFMA_F16_PEAK_TFLOPS),
 ]
 
 
