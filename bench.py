@@ -162,9 +162,11 @@ def check_scan(cpu_inputs, outs, B, H):
     return res
 
 
-def bench_long(device, iters=5):
+def bench_long(device, iters=10, warmup=5):
     """LONG config: B=1 T=65536 H=16 D=128 bf16 scan (delta = 0.05 sigmoid(z)) from the
-    identity, one call (the segment carry spans the whole sequence)."""
+    identity, one call (the segment carry spans the whole sequence).  After `warmup` calls,
+    `iters` calls with events around each (median: `us_median`), then `iters` calls back to back
+    between two events (`us_back_to_back`, the throughput figure)."""
     import torch
     import torch.nn.functional as F
     from verace_amd import launch_sssd_hip_scan
@@ -174,7 +176,8 @@ def bench_long(device, iters=5):
     k = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1).to(torch.bfloat16).to(device)
     v = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1).to(torch.bfloat16).to(device)
     d = (0.05 * torch.sigmoid(torch.randn(B, T, H, generator=g))).to(torch.bfloat16).to(device)
-    launch_sssd_hip_scan(q, k, v, d)
+    for _ in range(warmup):
+        launch_sssd_hip_scan(q, k, v, d)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(device)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
@@ -184,11 +187,21 @@ def bench_long(device, iters=5):
         ev[i + 1].record(stream)
     torch.cuda.synchronize()
     us = statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(iters))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(iters):
+        launch_sssd_hip_scan(q, k, v, d)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us_b2b = e0.elapsed_time(e1) * 1000.0 / iters
     nbytes = algorithmic_bytes_scan(B, T, H, D)
     nrm = psi.reshape(B * H, -1).norm(dim=-1) / D ** 0.5
     return {
         "config": "LONG: SSSD scan B=1 T=65536 H=16 D=128 bf16, identity start",
         "us_median": round(us, 1),
+        "us_back_to_back": round(us_b2b, 1),
+        "hbm_frac_back_to_back": round(algorithmic_bytes_scan(B, T, H, D) / (us_b2b * 1e-6) / 1e9
+                                       / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(B * T / (us * 1e-6), 1),
         "hbm_frac": round(nbytes / (us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
         "state_norm_drift": float((nrm - 1).abs().max()),
