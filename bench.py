@@ -489,10 +489,11 @@ def bench_cham(device, iters=5, warmup=2):
     # the reference's default holographic_dim (1024): prefill from the identity (fp32 inputs:
     # the token-sequential column route; bf16 inputs, as the model's projections give them:
     # the chunked matrix-core route), and one decode token for 64 sequences with their held
-    # holograms (R_0 = NS_3(H_0) per call)
+    # holograms through the reference's call semantics (a fresh state and R_0 = NS_3(H_0) per
+    # call); the decode path itself is the in-place step below
     for name, (Bw, Tw, init_w, dt) in (("h1024_identity_B4_T2048", (4, 2048, False, torch.float32)),
                                        ("h1024_identity_B4_T2048_bf16", (4, 2048, False, torch.bfloat16)),
-                                       ("h1024_decode_B64_T1", (64, 1, True, torch.float32))):
+                                       ("h1024_call_with_hologram_B64_T1", (64, 1, True, torch.float32))):
         hw = 1024
         qw = nrm(torch.randn(Bw, Tw, hw, generator=g), dim=-1).to(dt).to(device)
         kw = nrm(torch.randn(Bw, Tw, hw, generator=g), dim=-1).to(dt).to(device)
@@ -514,6 +515,32 @@ def bench_cham(device, iters=5, warmup=2):
         us = statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(3))
         res[name] = {"us_median": round(us, 1), "tokens_per_s": round(Bw * Tw / (us * 1e-6), 1)}
         del qw, kw, vw, gw, iw
+    # the decode path: the in-place step (cham_step_, O(h^2) per token) at B64 h1024 bf16 on
+    # unitary holograms (a sequence started from the identity: R = H), one read and one write
+    # of every state
+    from verace_amd import cham_step_
+    Bw, hw = 64, 1024
+    qw, kw, vw = (nrm(torch.randn(Bw, 1, hw, generator=g), dim=-1).to(torch.bfloat16).to(device)
+                  for _ in range(3))
+    gw = (0.1 * torch.sigmoid(torch.randn(Bw, 1, generator=g))).to(torch.bfloat16).to(device)
+    hol = (torch.eye(hw, device=device).expand(Bw, hw, hw).contiguous(),
+           torch.zeros(Bw, hw, hw, device=device))
+    for _ in range(warmup):
+        cham_step_(qw, kw, vw, gw, hol)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+    ev[0].record(stream)
+    for i in range(iters):
+        cham_step_(qw, kw, vw, gw, hol)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    us = statistics.median(ev[i].elapsed_time(ev[i + 1]) * 1000.0 for i in range(iters))
+    nbytes = 2 * 2 * Bw * hw * hw * 4
+    res["h1024_decode_step_B64"] = {"us_median": round(us, 1),
+                                    "tokens_per_s": round(Bw / (us * 1e-6), 1),
+                                    "state_bytes": nbytes,
+                                    "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del qw, kw, vw, gw, hol
     return res
 
 
