@@ -432,8 +432,10 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
   for (int w = 1; w < NT / 64; ++w) {
     kk += s_dot[w][0]; vv += s_dot[w][1]; kv += s_dot[w][2]; qq += s_dot[w][3];
   }
+  float nk = 1.f, nv = 1.f;
   if constexpr (FUSED) {  // the sums of the normalised rows: scale by the norms
-    const float nk = 1.f / fmaxf(sqrtf(kk), 1e-12f), nv = 1.f / fmaxf(sqrtf(vv), 1e-12f);
+    nk = 1.f / fmaxf(sqrtf(kk), 1e-12f);
+    nv = 1.f / fmaxf(sqrtf(vv), 1e-12f);
     const float nq = 1.f / fmaxf(sqrtf(qq), 1e-12f);
     kv = kv * nk * nv;
     kk = kk * nk * nk;
@@ -441,11 +443,6 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       A[e].x *= nk; A[e].y *= nk; A[e].z *= nv; A[e].w *= nv;
-    }
-#pragma unroll
-    for (int m = 0; m < RPT; ++m) {
-      kr[m] *= nk;
-      vr[m] *= nv;
     }
     qc.x *= nq; qc.y *= nq; qc.z *= nq; qc.w *= nq;
   }
@@ -465,6 +462,9 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
     di[e] = N.n12r * s.y + N.n12i * s.x + N.n22r * s.w + N.n22i * s.z;
     // identity token: the column sums were taken with the non-finite rows (NaN * 0 is NaN)
     if (!ok) cr[e] = ci[e] = dr[e] = di[e] = 0.f;
+    if constexpr (FUSED) {  // H' = H + k^ c + v^ d with k^ = nk k, v^ = nv v: the raw rows
+      cr[e] *= nk; ci[e] *= nk; dr[e] *= nv; di[e] *= nv;  // below, the norms folded in here
+    }
   }
   float* pp = part + (static_cast<int64_t>(b) * nblk + blk) * H;
   auto upd = [&](int m, float4 yr, float4 yi) {
