@@ -54,6 +54,7 @@
 // square spans both readout waves: each keeps its rows of chunk c in registers for one
 // iteration and stores them once both partial sums are in LDS.  With 8 producers the k/v
 // normalisation takes the otherwise empty phase.
+#include <algorithm>
 #include <type_traits>
 
 #include "vmi_common.h"
@@ -1305,8 +1306,12 @@ hipError_t run_chunked_fused(const void* proj, int64_t proj_stride, const uint8_
 size_t chunk_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int io_dtype) {
   if (!chunk_path(T, D, io_dtype)) return 0;
   const Plan p = make_plan(B * H, T);
-  if (p.nseg <= 1) return 0;
-  return static_cast<size_t>(p.nfactors + p.nseg - 1) * B * H * D * D * sizeof(float);
+  const size_t seg = p.nseg <= 1 ? 0
+                                 : static_cast<size_t>(p.nfactors + p.nseg - 1) * B * H * D * D *
+                                       sizeof(float);
+  // enough for either plan: the column-split scan is chosen at launch (use_xsplit)
+  if (use_xsplit(B, T, H, D, io_dtype)) return std::max(seg, xsplit_workspace_bytes(B, H));
+  return seg;
 }
 
 bool use_chunk_path(int64_t T, int64_t D, int io_dtype) { return chunk_path(T, D, io_dtype); }
@@ -1327,6 +1332,10 @@ hipError_t launch_sssd_chunked(const void* q, const void* k, const void* v, cons
                                int io_dtype, int delta_dtype, const float* psi_in, void* out,
                                float* psi_out, int B, int T, int H, void* workspace,
                                hipStream_t stream) {
+  if (use_xsplit(B, T, H, chunk::D, io_dtype) &&
+      (delta_dtype == VMI_F32 || (reinterpret_cast<uintptr_t>(delta) & 3) == 0))
+    return launch_sssd_xsplit(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, B, T, H,
+                              workspace, stream);
 #define VMI_RUN(E, DT) \
   return run_chunked<E, DT>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, B, T, H, workspace, \
                             stream)

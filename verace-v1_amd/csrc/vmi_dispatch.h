@@ -113,6 +113,15 @@ hipError_t launch_sssd_chunked(const void* q, const void* k, const void* v, cons
                                float* psi_out, int B, int T, int H, void* workspace,
                                hipStream_t stream);
 
+// sssd_xsplit.hip: single-pass column-split scan (bf16/fp16 I/O, head_dim 128), four
+// cooperating workgroups per sequence; taken by launch_sssd_chunked when use_xsplit holds.
+bool use_xsplit(int64_t B, int64_t T, int64_t H, int64_t D, int io_dtype);
+size_t xsplit_workspace_bytes(int64_t B, int64_t H);
+hipError_t launch_sssd_xsplit(const void* q, const void* k, const void* v, const void* delta,
+                              int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                              float* psi_out, int B, int T, int H, void* workspace,
+                              hipStream_t stream);
+
 // sssd_chunk.hip, fused projections: proj [B, T, 3HD + H] raw (x [W_q; W_k; W_v; W_delta]^T);
 // q, k, v normalised and delta = 0.1 sigmoid(.) * mask in the kernel; out = head_rmsnorm(o)
 // when rms_w is given (else o).  Needs use_chunk_path(T, 128, io_dtype).
