@@ -6,9 +6,11 @@
  * (passed as void*, it is a hipStream_t; NULL = the null stream).  Nothing
  * here allocates device memory: scratch space is passed in by the caller and
  * sized with the matching *_workspace_bytes query.  Kernels are enqueued on
- * the given stream; no entry point synchronises the host.  The library holds
- * no mutable global state, so calls from several host threads are safe as
- * long as they use disjoint output buffers.
+ * the given stream; no entry point synchronises the host.  The one piece of
+ * mutable global state is the fixed scratch array of vmi_sssd_scan_fwd_noalloc
+ * (one per GPU): calls of that entry point that overlap on one GPU race.  Every
+ * other entry point is safe from several host threads as long as the calls
+ * use disjoint output and workspace buffers.
  *
  * Math implemented (reference: verace_v1/modules/sssd_attention.py:144-182):
  *   X_t   = (delta_t / 2) * (k_t v_t^T - v_t k_t^T)
@@ -215,9 +217,11 @@ int vmi_state_cache_step(vmi_state_cache* cache, int64_t layer, const int64_t* h
  * becomes part of the cache, so a handle's (sssd_state, cham_hologram) tuple of
  * acd_engine.py:88-92 lives in one slot of each pool.  vmi_state_cache_cham_step runs the
  * in-place CHAM decode step (as vmi_cham_step_inplace) over the hologram slots with the slot
- * decisions of the layer's last vmi_state_cache_step: call it with the same handles in the
- * same order after that layer's SSSD step (the CHAM sub-layer's inputs come from the SSSD
- * sub-layer's output, backbone.py:83-93); other handle lists return VMI_ERR_INVALID_ARG.
+ * decisions of the layer's last vmi_state_cache_step: call it once, with the same handles in
+ * the same order, after that layer's SSSD step (the CHAM sub-layer's inputs come from the
+ * SSSD sub-layer's output, backbone.py:83-93).  Other handle lists, a second call for the
+ * same step, and a call after a fork, a release or another plan of the layer in between
+ * return VMI_ERR_INVALID_ARG.
  * A handle with no slot yet starts from the identity.  Every cached hologram is taken to have
  * started from the identity (unitary, so the readout NS_3(H) = H; write NS_3-retracted pairs
  * only if that holds).  q, k, v, out: [n, 1, h] io_dtype; gamma: [n] gamma_dtype; h % 4 == 0,

@@ -255,3 +255,46 @@ def test_cache_tree_search_against_oracle_with_holograms(device):
         q, k, v, d, cq, ck, cv, cg = (t.to(device) for t in toks[(0, 0)])
         cache.step(0, q, k, v, d, hs)
         cache.cham_step(0, cq[:2], ck[:2], cv[:2], cg[:2], hs[:2])
+
+
+def test_cham_step_decisions_are_spent_once(device):
+    """vmi_state_cache_cham_step replays the slot decisions of the layer's last SSSD step: only
+    once, and not after a fork, a release or another plan of the layer (each can free or share
+    the recorded slots, so a replay would copy into a slot that is now in place or reused)."""
+    from verace_amd import SSSDStateCache
+    print("[case] cham_step decisions are spent once", flush=True)
+    H, D, h = 2, 128, 64
+    cache = SSSDStateCache(2, 16, H, D, device=device, hologram_dim=h)
+    g = torch.Generator().manual_seed(3)
+
+    def cham_tok(n):
+        return (F.normalize(torch.randn(n, 1, h, generator=g), dim=-1).bfloat16().to(device),
+                F.normalize(torch.randn(n, 1, h, generator=g), dim=-1).bfloat16().to(device),
+                F.normalize(torch.randn(n, 1, h, generator=g), dim=-1).bfloat16().to(device),
+                (0.1 * torch.sigmoid(torch.randn(n, generator=g))).bfloat16().to(device))
+    hs = cache.new(2)
+
+    def sssd_step():
+        q, k, v, d = (t.to(device) for t in _tokens(2, H, D, seed=int(torch.randint(1 << 20, (1,), generator=g))))
+        cache.step(0, q, k, v, d, hs)
+    sssd_step()
+    cache.cham_step(0, *cham_tok(2), hs)
+    with pytest.raises(ValueError):            # the same step's decisions a second time
+        cache.cham_step(0, *cham_tok(2), hs)
+    sssd_step()
+    (child,) = cache.fork(hs[0], 1)
+    with pytest.raises(ValueError):            # a fork in between
+        cache.cham_step(0, *cham_tok(2), hs)
+    sssd_step()
+    cache.release([child])
+    with pytest.raises(ValueError):            # a release in between
+        cache.cham_step(0, *cham_tok(2), hs)
+    sssd_step()
+    cache.table.plan_step(0, hs)
+    with pytest.raises(ValueError):            # another plan of the layer in between
+        cache.cham_step(0, *cham_tok(2), hs)
+    # a plan of another layer leaves layer 0's decisions standing
+    sssd_step()
+    cache.table.plan_step(1, hs)
+    cache.cham_step(0, *cham_tok(2), hs)
+    torch.cuda.synchronize()

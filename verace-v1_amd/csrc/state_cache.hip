@@ -68,6 +68,12 @@ int64_t new_handle(vmi_state_cache* c) {
   return h;
 }
 
+// Slot decisions recorded for the CHAM half hold only until the table changes: a fork
+// adds holders to slots, a release frees them for reuse.
+void forget_cham_decisions(vmi_state_cache* c) {
+  for (auto& lh : c->last_handles) lh.clear();
+}
+
 void unref(vmi_state_cache* c, int64_t l, int32_t s) {
   int32_t& r = c->refs[l * c->N + s];
   if (--r == 0) c->free[l].push_back(s);
@@ -89,6 +95,7 @@ bool check_handles(vmi_state_cache* c, const int64_t* handles, int64_t n) {
 // c->dst and updates the table as if it had run.
 int plan(vmi_state_cache* c, int64_t l, const int64_t* handles, int64_t n) {
   if (l < 0 || l >= c->L || n < 0) return VMI_ERR_INVALID_ARG;
+  c->last_handles[l].clear();  // any new plan of the layer voids the recorded CHAM decisions
   if (!check_handles(c, handles, n)) return VMI_ERR_INVALID_ARG;
   c->src.resize(n);
   c->dst.resize(n);
@@ -162,6 +169,7 @@ int vmi_state_cache_new(vmi_state_cache* c, int64_t n, int64_t* handles) {
 int vmi_state_cache_fork(vmi_state_cache* c, int64_t parent, int64_t n, int64_t* handles) {
   if (c == nullptr || n < 0 || (n > 0 && handles == nullptr)) return VMI_ERR_INVALID_ARG;
   if (!valid_handle(c, parent)) return VMI_ERR_INVALID_ARG;
+  if (n > 0) forget_cham_decisions(c);
   for (int64_t i = 0; i < n; ++i) {
     const int64_t h = new_handle(c);  // may grow phys: index the parent afresh
     c->phys[h] = c->phys[parent];
@@ -174,6 +182,7 @@ int vmi_state_cache_fork(vmi_state_cache* c, int64_t parent, int64_t n, int64_t*
 
 int vmi_state_cache_release(vmi_state_cache* c, const int64_t* handles, int64_t n) {
   if (c == nullptr || n < 0 || !check_handles(c, handles, n)) return VMI_ERR_INVALID_ARG;
+  if (n > 0) forget_cham_decisions(c);
   for (int64_t i = 0; i < n; ++i) {
     const int64_t h = handles[i];
     for (int64_t l = 0; l < c->L; ++l)
@@ -285,12 +294,16 @@ int vmi_state_cache_cham_step(vmi_state_cache* c, int64_t layer, const int64_t* 
   if (io_dtype != VMI_F32 && io_dtype != VMI_BF16 && io_dtype != VMI_F16) return VMI_ERR_INVALID_ARG;
   if (gamma_dtype != VMI_F32 && gamma_dtype != VMI_BF16 && gamma_dtype != VMI_F16)
     return VMI_ERR_INVALID_ARG;
-  // the same handles, in the same order, as this layer's last SSSD step
-  const auto& lh = c->last_handles[layer];
+  // the same handles, in the same order, as this layer's last SSSD step, once, with no
+  // fork, release or other plan of the layer in between
+  auto& lh = c->last_handles[layer];
   if (static_cast<int64_t>(lh.size()) != n) return VMI_ERR_INVALID_ARG;
   for (int64_t b = 0; b < n; ++b)
     if (handles == nullptr || lh[b] != handles[b]) return VMI_ERR_INVALID_ARG;
-  if (n == 0) return VMI_OK;
+  if (n == 0) {
+    lh.clear();
+    return VMI_OK;
+  }
   if (q == nullptr || k == nullptr || v == nullptr || gamma == nullptr || out == nullptr)
     return VMI_ERR_INVALID_ARG;
   size_t need = 0;
@@ -309,8 +322,12 @@ int vmi_state_cache_cham_step(vmi_state_cache* c, int64_t layer, const int64_t* 
         static_cast<const char*>(v) + tok, static_cast<const char*>(gamma) + b0 * g_bytes, io_dtype,
         gamma_dtype, pool, c->last_src[layer].data() + b0, c->last_dst[layer].data() + b0,
         static_cast<char*>(out) + tok, nb, static_cast<int>(h), workspace, s);
-    if (e != hipSuccess) return vmi::hip_status(e);
+    if (e != hipSuccess) {
+      lh.clear();
+      return vmi::hip_status(e);
+    }
   }
+  lh.clear();  // the decisions are spent: a second call would copy into in-place slots
   return VMI_OK;
 }
 

@@ -208,7 +208,9 @@ class SSSDStateCache:
                   gamma: torch.Tensor, handles) -> torch.Tensor:
         """The in-place CHAM decode step of ``layer`` for the same ``handles`` (same order) as
         the preceding :meth:`step` of that layer: each hologram moves with its SSSD state's
-        slot (copy-on-write included).  q, k, v: [B, 1, h] or [B, h]; gamma: [B] or [B, 1].
+        slot (copy-on-write included).  Once per step: a second call, or one after a fork, a
+        release or another plan of the layer, raises ValueError.
+        q, k, v: [B, 1, h] or [B, h]; gamma: [B] or [B, 1].
         Returns Re(NS_3(H') q) [B, 1, h] in q's dtype."""
         if self.holograms is None:
             raise RuntimeError("verace_amd: this cache holds no holograms (hologram_dim=None)")
