@@ -8,7 +8,8 @@ beside it and reported in `decode`.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 
-Prints ONE JSON line.  Timing: W untimed steps, then K steps bracketed by
+Prints ONE JSON line.  Timing: W untimed steps (and at least --min-warmup-ms of them, default
+300 ms, so a short --warmup still reaches the steady state), then K steps bracketed by
 torch.cuda.synchronize(); each step is bracketed by HIP events recorded on the stream
 the kernels are launched on.  Two input sets are rotated so a step never finds its
 inputs in the 256 MB MALL left over from the previous step.
@@ -125,8 +126,7 @@ def bench_scan(args, device):
         if st != 0:
             raise RuntimeError(f"vmi_sssd_scan_fwd failed: {st}")
 
-    for i in range(args.warmup):
-        capi_step(i)
+    warm = steady_warmup(capi_step, stream, args.warmup, args.min_warmup_ms)
     total, wall = back_to_back(capi_step, args.steps)
     per, _ = timed(capi_step, args.steps)
     outs = bufs[(args.steps - 1) % 2][:2]
@@ -135,7 +135,37 @@ def bench_scan(args, device):
     for i in range(2):
         launch_sssd_hip_scan(*sets[i % 2][1])
     api, _ = timed(lambda i: launch_sssd_hip_scan(*sets[i % 2][1]), args.steps)
-    return total, per, wall, parity, api
+    return total, per, wall, parity, api, warm
+
+
+def steady_warmup(step, stream, n_min, min_ms):
+    """Untimed calls before the timed ones: at least `n_min` and at least `min_ms` of wall
+    time, synchronising every 16 calls so the wall time follows the device.  A GPU fresh from
+    process start runs its first few milliseconds of scans slower (clocks and caches ramping
+    up); a warm-up counted in calls alone (the driver's --warmup 5 is ~1 ms of scans) times
+    that ramp.  Every warm-up call is bracketed by events on the kernels' stream, and the
+    returned record shows the ramp: per-call times of the first calls against the median of
+    the last ones."""
+    import torch
+    evs = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    i = 0
+    while i < n_min or (time.perf_counter() - t0) * 1e3 < min_ms:
+        e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        e[0].record(stream)
+        step(i)
+        e[1].record(stream)
+        evs.append(e)
+        i += 1
+        if i % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    per = [a.elapsed_time(b) for a, b in evs]
+    return {"calls": i, "wall_ms": round(wall_ms, 1), "min_ms": min_ms,
+            "first_calls_ms": [round(x, 4) for x in per[:8]],
+            "median_last_calls_ms": round(statistics.median(per[-64:]), 4)}
 
 
 def check_scan(cpu_inputs, outs, B, H):
@@ -986,6 +1016,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--min-warmup-ms", type=float, default=300.0,
+                    help="OP warm-up runs at least this much wall time, whatever --warmup says")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-long", action="store_true", help="skip the LONG (T=65536) scan timing")
@@ -1025,7 +1057,7 @@ def main():
 
     import torch
     device = torch.device("cuda:0")
-    total_ms, per, wall, parity, api = bench_scan(args, device)
+    total_ms, per, wall, parity, api, warm = bench_scan(args, device)
     B, T, H, D = OP["B"], OP["T"], OP["H"], OP["D"]
     tokens = B * T
     ms = total_ms / args.steps
@@ -1081,10 +1113,13 @@ def main():
         # accumulation; every MFMA accumulates in fp32); measured drift in "parity"
         "state_operand_precision": "f16 per 16-token chunk, fp32 accumulate",
         "wall_s_timed_region": round(wall, 3),
+        # untimed steady-state warm-up: max(--warmup calls, --min-warmup-ms of scans)
+        "warmup_run": warm,
         # the same K scans through the torch-facing launch_sssd_hip_scan (argument checks and
         # output / workspace allocation per call): host time included where it exceeds the scan
         "torch_api_ms_per_step": round(sum(api) / len(api), 4),
-        "timing": "C-ABI vmi_sssd_scan_fwd calls with prebuilt arguments: K calls back to back "
+        "timing": "C-ABI vmi_sssd_scan_fwd calls with prebuilt arguments, after a warm-up of "
+                  "at least --warmup calls and --min-warmup-ms of wall time: K calls back to back "
                   "between two events (value, ms_per_step, roofline); then K calls with events "
                   "around each (ms_per_step_median)",
     }
