@@ -146,3 +146,56 @@ def test_chunk_scan_full_layer_shape(device):
     psi0 = torch.linalg.qr(torch.randn(B, H, D, D, generator=g))[0].contiguous()
     o, psi = _gpu(q, k, v, delta, psi0, device)
     _check(o, psi, q, k, v, delta, psi0, "FULL shape orthogonal start")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dmax", [0.5, 2.0, 8.0])
+@pytest.mark.parametrize("knorm,vnorm", [(0.1, 0.1), (10.0, 10.0), (10.0, 0.1)])
+def test_chunk_scan_input_envelope(device, dtype, dmax, knorm, vnorm):
+    """Inputs away from the model's operating point (unit k, v and delta <= 0.1): delta in
+    [dmax / 2, dmax] and k, v of norm 0.1 or 10, from an orthogonal start, against the fp64
+    closed form with the chunk path's bars (2e-2 per slice, norm drift 1e-4)."""
+    B, T, H, D = 2, 300, 2, 128
+    print(f"[case] envelope {dtype} delta<={dmax} |k|={knorm} |v|={vnorm}", flush=True)
+    g = torch.Generator().manual_seed(int(dmax * 10 + knorm * 3 + vnorm))
+    q = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1).to(dtype)
+    k = (knorm * F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1)).to(dtype)
+    v = (vnorm * F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1)).to(dtype)
+    delta = (dmax * (0.5 + 0.5 * torch.rand(B, T, H, generator=g))).to(dtype)
+    psi0 = torch.linalg.qr(torch.randn(B, H, D, D, generator=g))[0].contiguous()
+    o, psi = _gpu(q, k, v, delta, psi0, device)
+    _check(o, psi, q, k, v, delta, psi0, f"envelope {dtype} d{dmax} k{knorm} v{vnorm}")
+
+
+def test_chunk_scan_wide_rotations_take_fp32(device):
+    """Heads whose tokens rotate the state by more than the f16-operand chunk scan's envelope
+    allows (m = (delta / 2) |k ^ v| > 0.25) are recomputed by the fp32 token-sequential kernel:
+    their final states equal, bit for bit, those of the fp32 scan of the same values, while the
+    heads inside the envelope keep the chunk result.  Every head holds the bars against the fp64
+    closed form."""
+    B, T, H, D = 1, 4096, 8, 128
+    ms = [0.05, 0.2, 0.3, 1.0, 2.0, 5.0, 25.0, 400.0]
+    print(f"[case] wide rotations m={ms} T={T}", flush=True)
+    g = torch.Generator().manual_seed(12)
+    q = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1)
+    k = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1)
+    v = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1)
+    # unit k, v with delta = 0.4 rotate by m <= 0.2; head h reaches m = ms[h] on token T / 2
+    # (a single token puts a head out) and stays at min(ms[h], 0.2) elsewhere
+    delta = torch.full((B, T, H), 0.4)
+    for h, m in enumerate(ms):
+        s = math.sqrt(m / 0.2)
+        k[:, T // 2:T // 2 + 1, h] *= s
+        v[:, T // 2:T // 2 + 1, h] *= s
+        k[:, :T // 2, h] *= min(s, 1.0)
+        v[:, :T // 2, h] *= min(s, 1.0)
+    q, k, v, delta = (t.to(torch.bfloat16) for t in (q, k, v, delta))
+    o, psi = _gpu(q, k, v, delta, None, device)
+    o32, p32 = _gpu(q.float(), k.float(), v.float(), delta.float(), None, device)
+    _check(o, psi, q, k, v, delta, None, "wide rotations")
+    for h, m in enumerate(ms):
+        same = torch.equal(psi[:, h], p32[:, h])
+        assert same == (m > 0.25), (h, m, same)
+    # the recomputed heads' outputs are the fp32 scan's, rounded once to bf16
+    wide = [h for h, m in enumerate(ms) if m > 0.25]
+    assert torch.equal(o[:, :, wide], o32[:, :, wide].to(torch.bfloat16).float())

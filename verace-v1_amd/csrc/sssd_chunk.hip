@@ -55,6 +55,7 @@
 // iteration and stores them once both partial sums are in LDS.  With 8 producers the k/v
 // normalisation takes the otherwise empty phase.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "vmi_common.h"
@@ -168,6 +169,10 @@ struct Args {
   const uint8_t* mask;
   const float* rms_w;
   float rms_eps;
+  // pass C of the unfused scan: flags[bh] = tag when a token of sequence bh lies outside the
+  // accuracy envelope (rotation_outside_chunk_envelope); null: no check
+  uint32_t* flags;
+  uint32_t tag;
 };
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also waits for every
@@ -498,7 +503,7 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
       *reinterpret_cast<float4*>(&P.gram[l32 * T_LD + 8 * q4 + 4 * g]) =
           make_float4(gacc[4 * q4], gacc[4 * q4 + 1], gacc[4 * q4 + 2], gacc[4 * q4 + 3]);
     wave_sync();
-    bool ok = true;
+    bool ok = true, wide = false;
     if (lane < C) {
       const int t = lane;
       const float kk = P.gram[(2 * t) * T_LD + 2 * t];
@@ -509,6 +514,11 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
         dl = (r.mk && t0 + t < a.T) ? 0.1f / (1.f + __expf(-dl)) : 0.f;
       const cayley2 M = cayley_guarded(dl, kk, vv, kv, ok);
       P.mcoef[t] = make_float4(M.m00, M.m01, M.m10, M.m11);
+      if constexpr (READOUT && !FUSED) wide = ok && rotation_outside_chunk_envelope(dl, kk, vv, kv);
+    }
+    if constexpr (READOUT && !FUSED) {
+      // hand the sequence to the fp32 recompute (a plain store: every writer stores the tag)
+      if (__ballot(wide) != 0 && lane == 0 && a.flags != nullptr) a.flags[bh] = a.tag;
     }
     // Tokens with a non-finite Cayley factor act as R = I (cayley_guarded): their U rows
     // are zeroed and the Gram matrix is recomputed, so no NaN/Inf reaches T~ or the
@@ -1272,11 +1282,14 @@ hipError_t run_chunked_args(chunk::Args a, const float* psi_in, void* out, float
 template <typename IO, typename DT>
 hipError_t run_chunked(const void* q, const void* k, const void* v, const void* delta,
                        int delta_dtype, const float* psi_in, void* out, float* psi_out, int B,
-                       int T, int H, void* workspace, hipStream_t stream) {
+                       int T, int H, void* workspace, uint32_t* flags, uint32_t tag,
+                       hipStream_t stream) {
   chunk::Args a{};
   a.q = q; a.k = k; a.v = v; a.delta = delta; a.delta_dtype = delta_dtype;
   a.in_stride = static_cast<int64_t>(H) * chunk::D;
   a.dl_stride = H;
+  a.flags = flags;
+  a.tag = tag;
   return run_chunked_args<IO, DT, false>(a, psi_in, out, psi_out, B, T, H, workspace, stream);
 }
 
@@ -1303,15 +1316,34 @@ hipError_t run_chunked_fused(const void* proj, int64_t proj_stride, const uint8_
 
 }  // namespace
 
+namespace {
+
+// Workspace of the unfused scan: the plan's own buffers (pass A factors and segment starts, or
+// the column-split scan's rings), then one flag word per sequence at this offset.
+size_t flags_offset(int64_t B, int64_t T, int64_t H, int64_t D, int io_dtype) {
+  const Plan p = make_plan(B * H, T);
+  size_t plan = p.nseg <= 1 ? 0
+                            : static_cast<size_t>(p.nfactors + p.nseg - 1) * B * H * D * D *
+                                  sizeof(float);
+  // enough for either plan: the column-split scan is chosen at launch (use_xsplit)
+  if (use_xsplit(B, T, H, D, io_dtype)) plan = std::max(plan, xsplit_workspace_bytes(B, H));
+  return (plan + 255) & ~size_t(255);
+}
+
+// Tags of the envelope flags: a fresh nonzero value per scan, so flag words left in a reused
+// workspace by earlier scans (or never written) do not match.
+std::atomic<uint32_t> g_flag_tag{0x6a09e667u};
+uint32_t next_flag_tag() {
+  uint32_t t = ++g_flag_tag;
+  if (t == 0) t = ++g_flag_tag;
+  return t;
+}
+
+}  // namespace
+
 size_t chunk_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t D, int io_dtype) {
   if (!chunk_path(T, D, io_dtype)) return 0;
-  const Plan p = make_plan(B * H, T);
-  const size_t seg = p.nseg <= 1 ? 0
-                                 : static_cast<size_t>(p.nfactors + p.nseg - 1) * B * H * D * D *
-                                       sizeof(float);
-  // enough for either plan: the column-split scan is chosen at launch (use_xsplit)
-  if (use_xsplit(B, T, H, D, io_dtype)) return std::max(seg, xsplit_workspace_bytes(B, H));
-  return seg;
+  return flags_offset(B, T, H, D, io_dtype) + static_cast<size_t>(B * H) * sizeof(uint32_t);
 }
 
 bool use_chunk_path(int64_t T, int64_t D, int io_dtype) { return chunk_path(T, D, io_dtype); }
@@ -1332,22 +1364,36 @@ hipError_t launch_sssd_chunked(const void* q, const void* k, const void* v, cons
                                int io_dtype, int delta_dtype, const float* psi_in, void* out,
                                float* psi_out, int B, int T, int H, void* workspace,
                                hipStream_t stream) {
+  // The f16-operand scan flags every sequence with a token outside its accuracy envelope
+  // (rotation_outside_chunk_envelope); a second launch recomputes exactly those sequences in
+  // fp32, token by token, from psi_in (which the scan leaves intact: it may not alias psi_out),
+  // overwriting their outputs and final states.  Its other workgroups exit at once.
+  uint32_t* flags = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) +
+                                                flags_offset(B, T, H, chunk::D, io_dtype));
+  const uint32_t tag = next_flag_tag();
+  hipError_t e;
   if (use_xsplit(B, T, H, chunk::D, io_dtype) &&
-      (delta_dtype == VMI_F32 || (reinterpret_cast<uintptr_t>(delta) & 3) == 0))
-    return launch_sssd_xsplit(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, B, T, H,
-                              workspace, stream);
+      (delta_dtype == VMI_F32 || (reinterpret_cast<uintptr_t>(delta) & 3) == 0)) {
+    e = launch_sssd_xsplit(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, B, T, H,
+                           workspace, flags, tag, stream);
+  } else {
 #define VMI_RUN(E, DT) \
-  return run_chunked<E, DT>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, B, T, H, workspace, \
-                            stream)
-  if (io_dtype == VMI_BF16) {
-    if (delta_dtype == VMI_F32) VMI_RUN(__bf16, float);
-    if (delta_dtype == VMI_BF16) VMI_RUN(__bf16, bf16_t);
-    VMI_RUN(__bf16, f16_t);
-  }
-  if (delta_dtype == VMI_F32) VMI_RUN(_Float16, float);
-  if (delta_dtype == VMI_BF16) VMI_RUN(_Float16, bf16_t);
-  VMI_RUN(_Float16, f16_t);
+  e = run_chunked<E, DT>(q, k, v, delta, delta_dtype, psi_in, out, psi_out, B, T, H, workspace, \
+                         flags, tag, stream)
+    if (io_dtype == VMI_BF16) {
+      if (delta_dtype == VMI_F32) VMI_RUN(__bf16, float);
+      else if (delta_dtype == VMI_BF16) VMI_RUN(__bf16, bf16_t);
+      else VMI_RUN(__bf16, f16_t);
+    } else {
+      if (delta_dtype == VMI_F32) VMI_RUN(_Float16, float);
+      else if (delta_dtype == VMI_BF16) VMI_RUN(_Float16, bf16_t);
+      else VMI_RUN(_Float16, f16_t);
+    }
 #undef VMI_RUN
+  }
+  if (e != hipSuccess) return e;
+  return launch_sssd_seq(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, B, T, H,
+                         chunk::D, stream, FlaggedStates{flags, tag});
 }
 
 }  // namespace vmi

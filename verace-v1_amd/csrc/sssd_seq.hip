@@ -42,6 +42,7 @@ __global__ __launch_bounds__(seq_cfg<DMAX>::NT) void sssd_seq_kernel(
   const int cg = tid % CG;
   const int rg = tid / CG;
   const int bh = blockIdx.x;          // b * H + h
+  if (map.skip(bh)) return;           // uniform over the workgroup
   const int b = bh / H;
   const int h = bh - b * H;
   const int64_t DD = static_cast<int64_t>(D) * D;
@@ -300,6 +301,14 @@ hipError_t launch_sssd_seq(const void* q, const void* k, const void* v, const vo
                            int io_dtype, int delta_dtype, const float* psi_in, void* out,
                            float* psi_out, int B, int T, int H, int D, hipStream_t stream,
                            const SlotArgs& map) {
+  return launch_seq_map(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, B, T, H, D,
+                        stream, map);
+}
+
+hipError_t launch_sssd_seq(const void* q, const void* k, const void* v, const void* delta,
+                           int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                           float* psi_out, int B, int T, int H, int D, hipStream_t stream,
+                           const FlaggedStates& map) {
   return launch_seq_map(q, k, v, delta, io_dtype, delta_dtype, psi_in, out, psi_out, B, T, H, D,
                         stream, map);
 }

@@ -160,6 +160,8 @@ struct Args {
   unsigned char* ws;  // workspace (layout())
   int T, H, BH, nch;
   unsigned tag;
+  unsigned* flags;    // flags[bh] = ftag when a token lies outside the chunk envelope
+  unsigned ftag;
 };
 
 // ------------------------------------------------------------------ small helpers
@@ -768,7 +770,7 @@ __global__ __launch_bounds__(NT) void sssd_xsplit_kernel(Args a) {
         *reinterpret_cast<float4*>(&P.gram[l32 * T_LD + 8 * q4 + 4 * g2]) =
             make_float4(ra.gacc[4 * q4], ra.gacc[4 * q4 + 1], ra.gacc[4 * q4 + 2], ra.gacc[4 * q4 + 3]);
       wave_sync();
-      bool ok = true;
+      bool ok = true, wide = false;
       if (lane < C) {
         const int t = lane;
         const float kk = P.gram[(2 * t) * T_LD + 2 * t];
@@ -777,7 +779,10 @@ __global__ __launch_bounds__(NT) void sssd_xsplit_kernel(Args a) {
         const float dl = n * C + t >= a.T ? 0.f : ra.d;
         const cayley2 M = cayley_guarded(dl, kk, vv, kv, ok);
         P.mcoef[t] = make_float4(M.m00, M.m01, M.m10, M.m11);
+        wide = ok && rotation_outside_chunk_envelope(dl, kk, vv, kv);
       }
+      // hand the sequence to the fp32 recompute (a plain store: every writer stores the tag)
+      if (__builtin_amdgcn_ballot_w64(wide) != 0 && lane == 0) a.flags[bh] = a.ftag;
       // a token whose factor is not finite acts as R = I: its rows are zeroed and the Gram
       // matrix recomputed (uniform branch, taken only for such chunks)
       const unsigned long long badm = __builtin_amdgcn_ballot_w64(!ok);
@@ -1002,8 +1007,10 @@ size_t xsplit_workspace_bytes(int64_t B, int64_t H) {
 template <typename IO, typename DT>
 static hipError_t run_xsplit(const void* q, const void* k, const void* v, const void* delta,
                              const float* psi_in, void* out, float* psi_out, int B, int T, int H,
-                             void* workspace, hipStream_t stream) {
+                             void* workspace, uint32_t* flags, uint32_t ftag, hipStream_t stream) {
   xs::Args a{};
+  a.flags = flags;
+  a.ftag = ftag;
   a.q = q; a.k = k; a.v = v; a.delta = delta;
   a.in_stride = static_cast<int64_t>(H) * xs::D;
   a.dl_stride = H;
@@ -1025,9 +1032,10 @@ static hipError_t run_xsplit(const void* q, const void* k, const void* v, const 
 hipError_t launch_sssd_xsplit(const void* q, const void* k, const void* v, const void* delta,
                               int io_dtype, int delta_dtype, const float* psi_in, void* out,
                               float* psi_out, int B, int T, int H, void* workspace,
-                              hipStream_t stream) {
+                              uint32_t* flags, uint32_t ftag, hipStream_t stream) {
 #define VMI_RUN(E, DT) \
-  return run_xsplit<E, DT>(q, k, v, delta, psi_in, out, psi_out, B, T, H, workspace, stream)
+  return run_xsplit<E, DT>(q, k, v, delta, psi_in, out, psi_out, B, T, H, workspace, flags, ftag, \
+                           stream)
   if (io_dtype == VMI_BF16) {
     if (delta_dtype == VMI_F32) VMI_RUN(__bf16, float);
     if (delta_dtype == VMI_BF16) VMI_RUN(__bf16, bf16_t);

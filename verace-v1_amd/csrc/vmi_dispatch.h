@@ -28,6 +28,19 @@ struct DenseStates {
   static constexpr bool kSlotted = false;  // every index valid: no guard on the writes
   __device__ __forceinline__ int64_t in_index(int bh, int) const { return bh; }
   __device__ __forceinline__ int64_t out_index(int bh, int) const { return bh; }
+  __device__ __forceinline__ bool skip(int) const { return false; }
+};
+
+// Dense states, and only the sequences whose flag word holds `tag` run (the others leave
+// their outputs and states untouched): the fp32 recompute of the sequences a chunk scan
+// found outside its accuracy envelope (rotation_outside_chunk_envelope).
+struct FlaggedStates {
+  static constexpr bool kSlotted = false;
+  const uint32_t* flags;  // [B * H]
+  uint32_t tag;
+  __device__ __forceinline__ int64_t in_index(int bh, int) const { return bh; }
+  __device__ __forceinline__ int64_t out_index(int bh, int) const { return bh; }
+  __device__ __forceinline__ bool skip(int bh) const { return flags[bh] != tag; }
 };
 
 __device__ __forceinline__ int64_t slot_index(int s, int nslots, int bh, int H) {
@@ -45,6 +58,7 @@ struct StateMap {
   __device__ __forceinline__ int64_t out_index(int bh, int H) const {
     return slot_index(out_slot[bh / H], nslots, bh, H);
   }
+  __device__ __forceinline__ bool skip(int) const { return false; }
 };
 
 constexpr int kMaxSlotArgs = 256;
@@ -59,6 +73,7 @@ struct SlotArgs {
   __device__ __forceinline__ int64_t out_index(int bh, int H) const {
     return slot_index(out_slot[bh / H], nslots, bh, H);
   }
+  __device__ __forceinline__ bool skip(int) const { return false; }
 };
 
 // sssd_seq.hip: token-sequential fp32 scan, one workgroup per (b, h).
@@ -73,6 +88,10 @@ hipError_t launch_sssd_seq(const void* q, const void* k, const void* v, const vo
                            int io_dtype, int delta_dtype, const float* psi_in, void* out,
                            float* psi_out, int B, int T, int H, int D, hipStream_t stream,
                            const SlotArgs& map);
+hipError_t launch_sssd_seq(const void* q, const void* k, const void* v, const void* delta,
+                           int io_dtype, int delta_dtype, const float* psi_in, void* out,
+                           float* psi_out, int B, int T, int H, int D, hipStream_t stream,
+                           const FlaggedStates& map);
 
 // sssd_step.hip: single-token step for head_dim 128 (persistent, two workgroups per CU,
 // heads in units of 64 columns whose loads run one unit ahead of the update and store).
@@ -120,7 +139,7 @@ size_t xsplit_workspace_bytes(int64_t B, int64_t H);
 hipError_t launch_sssd_xsplit(const void* q, const void* k, const void* v, const void* delta,
                               int io_dtype, int delta_dtype, const float* psi_in, void* out,
                               float* psi_out, int B, int T, int H, void* workspace,
-                              hipStream_t stream);
+                              uint32_t* flags, uint32_t ftag, hipStream_t stream);
 
 // sssd_chunk.hip, fused projections: proj [B, T, 3HD + H] raw (x [W_q; W_k; W_v; W_delta]^T);
 // q, k, v normalised and delta = 0.1 sigmoid(.) * mask in the kernel; out = head_rmsnorm(o)
