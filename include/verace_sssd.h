@@ -276,7 +276,13 @@ int vmi_sssd_scan_bwd(const void* q, const void* k, const void* v, const void* d
  *   q, k, v, out : [B, T, h] io_dtype;  gamma : [B, T] gamma_dtype;
  *   h0_*, h_*_out : [B, h, h] float32 (outputs must not overlap the inputs).
  * h > 1024: VMI_ERR_UNSUPPORTED.  Workspace from vmi_cham_scan_workspace_bytes (for
- * h > 128 it holds a state snapshot per 64 tokens: about 2 B T h^2 / 64 floats). */
+ * h > 128 it holds a state snapshot per 64 tokens: about 2 B T h^2 / 64 floats).
+ * Precondition of the 16-bit route for 128 < h <= 1024 (io_dtype BF16 or F16): every element
+ * of k and v is below 65504 in magnitude, because the matrix-core carry converts them to f16
+ * (exactly, inside that range).  A token with a larger element (bf16 values from 65536 up) is
+ * taken as the identity, as a token with a non-finite element is.  The module's L2-normalised
+ * k, v are at most 1; other callers with larger elements pass io_dtype F32, whose route takes
+ * any finite value. */
 int vmi_cham_scan_workspace_bytes(int64_t B, int64_t T, int64_t h, size_t* bytes);
 int vmi_cham_scan_fwd(const void* q, const void* k, const void* v, const void* gamma,
                       int io_dtype, int gamma_dtype, const float* h0_real,

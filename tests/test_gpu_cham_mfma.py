@@ -126,3 +126,26 @@ def test_cham_mfma_route_nonfinite_tokens(device):
     eo, es = _rel(out, ref), max(_rel(hr, rr), _rel(hi, ri))
     print(f"  rel out={eo:.2e} state={es:.2e}", flush=True)
     assert eo <= 1e-2 and es <= 1e-5
+
+
+def test_cham_mfma_elements_beyond_f16_are_identity_tokens(device):
+    """The 16-bit route's documented precondition (every k, v element below 65504, the f16
+    range): a token with a finite bf16 element above it is taken as the identity, exactly as
+    the same token with gamma = 0, and the fp32 route takes the same values as they are
+    (against the fp64 oracle)."""
+    B, T, h = 1, 40, 256
+    print(f"[case] cham mfma element beyond f16 range B{B} T{T} h{h}", flush=True)
+    q, k, v, gam = _inputs(B, T, h, seed=77, dtype=torch.bfloat16)
+    big = k.clone()
+    big[0, 17, 5] = 1.0e5          # finite in bf16 (99840), above f16's 65504
+    gz = gam.clone()
+    gz[0, 17] = 0.0
+    ob, hrb, hib = _run(device, q, big, v, gam, None)
+    oz, hrz, hiz = _run(device, q, k, v, gz, None)
+    assert torch.isfinite(hrb).all() and torch.isfinite(ob).all()
+    assert torch.equal(hrb, hrz) and torch.equal(hib, hiz) and torch.equal(ob, oz)
+    # the fp32 route on the same values: the large element counts
+    of, hrf, hif = _run(device, q.float(), big.float(), v.float(), gam.float(), None)
+    rec, (sr, si) = cham_scan.cham_scan_closed(q.double().numpy(), big.double().numpy(),
+                                               v.double().numpy(), gam.double().numpy())
+    assert _rel(np.concatenate([hrf.numpy(), hif.numpy()], 1), np.concatenate([sr, si], 1)) <= 1e-5

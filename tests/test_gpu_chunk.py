@@ -199,3 +199,20 @@ def test_chunk_scan_wide_rotations_take_fp32(device):
     # the recomputed heads' outputs are the fp32 scan's, rounded once to bf16
     wide = [h for h, m in enumerate(ms) if m > 0.25]
     assert torch.equal(o[:, :, wide], o32[:, :, wide].to(torch.bfloat16).float())
+
+
+def test_chunk_scan_unrepresentable_tokens_take_fp32(device):
+    """Tokens whose f16 operands cannot hold them -- a finite bf16 element of k above the f16
+    range, a NaN in v -- put their sequence on the fp32 recompute: its state then equals the fp32
+    scan's bit for bit (which takes the large element as it is and applies the reference's
+    identity guard to the NaN token), and the other heads keep the chunk result."""
+    B, T, H, D = 1, 256, 3, 128
+    print(f"[case] unrepresentable tokens T={T}", flush=True)
+    q, k, v, delta = _inputs(B, T, H, D, seed=21, dtype=torch.bfloat16)
+    k[0, 100, 0, 7] = 7.0e4      # finite in bf16, Inf in f16
+    v[0, 50, 1, 3] = float("nan")
+    o, psi = _gpu(q, k, v, delta, None, device)
+    o32, p32 = _gpu(q.float(), k.float(), v.float(), delta.float(), None, device)
+    assert torch.equal(psi[:, 0], p32[:, 0]) and torch.equal(psi[:, 1], p32[:, 1])
+    assert not torch.equal(psi[:, 2], p32[:, 2])
+    assert torch.isfinite(psi).all() and torch.isfinite(o).all()

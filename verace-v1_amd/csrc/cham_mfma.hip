@@ -25,7 +25,9 @@
 //      (16x16x32, hi/lo products), H += Y Z with Y read back through transposing LDS reads.
 //
 // Precision: k, v from bf16 / f16 are exact in f16 (bf16 values below 2^-14 round to f16
-// subnormals, an absolute change below 2^-25); H and W enter the products as f16 hi + lo
+// subnormals, an absolute change below 2^-25; bf16 values from 2^16 up have no f16 value: their
+// token is taken as the identity, like a token with a non-finite element, and the entry point
+// documents |k|, |v| elements below 65504 as this route's precondition); H and W enter the products as f16 hi + lo
 // pairs and T as an f16 hi + lo pair, so every product is fp32-faithful (~2^-21 relative)
 // and the fp32 accumulators carry the state.  The state is carried scaled (TSCALE, SMAX
 // below) so that the lo parts stay normal f16 numbers: measured against the fp64 closed form
@@ -63,16 +65,19 @@ __host__ __device__ constexpr int rho_slot(int rho) {
   return ((rho & 1) << 3) | ((rho & 2) << 3) | (rho & 4) | ((rho & 8) >> 2) | ((rho & 16) >> 4);
 }
 
-// Non-finite 16-bit values are recognised by their bit patterns (all-ones exponent field).
+// 16-bit values that have no finite f16 value, recognised by their magnitude bits: f16 Inf /
+// NaN (0x7c00 and up), and for bf16 also the finite values from 2^16 (0x4780) up, which round
+// to f16 Inf.  Such an element reads as zero, and its token is the identity (its coefficients
+// are zeroed by wide_coef_kernel's matching test).
 template <typename IO> struct bits16;
-template <> struct bits16<f16_t> { static constexpr uint32_t EXP = 0x7c00u; };
-template <> struct bits16<bf16_t> { static constexpr uint32_t EXP = 0x7f80u; };
+template <> struct bits16<f16_t> { static constexpr uint32_t LIMIT = 0x7c00u; };
+template <> struct bits16<bf16_t> { static constexpr uint32_t LIMIT = 0x4780u; };
 
-// mask with 0xffff in each 16-bit half of `w` that holds a finite value, 0 elsewhere
+// mask with 0xffff in each 16-bit half of `w` that holds an f16-representable value, 0 elsewhere
 template <typename IO> __device__ __forceinline__ uint32_t finite_mask(uint32_t w) {
-  constexpr uint32_t X = bits16<IO>::EXP;
-  const uint32_t lo = (w & X) == X ? 0u : 0x0000ffffu;
-  const uint32_t hi = ((w >> 16) & X) == X ? 0u : 0xffff0000u;
+  constexpr uint32_t L = bits16<IO>::LIMIT;
+  const uint32_t lo = (w & 0x7fffu) >= L ? 0u : 0x0000ffffu;
+  const uint32_t hi = ((w >> 16) & 0x7fffu) >= L ? 0u : 0xffff0000u;
   return lo | hi;
 }
 

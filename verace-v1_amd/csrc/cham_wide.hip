@@ -51,12 +51,15 @@ __global__ __launch_bounds__(256) void wide_coef_kernel(const IO* __restrict__ k
   if (tok >= BT) return;  // whole wave
   const int64_t base = static_cast<int64_t>(tok) * h;
   float kk = 0.f, vv = 0.f, kv = 0.f;
+  bool wide = false;  // a bf16 element beyond the f16 range (the matrix-core carry's operands)
   for (int r = lane; r < h; r += 64) {
     const float x = io<IO>::load(k, base + r), y = io<IO>::load(v, base + r);
     kk = fmaf(x, x, kk);
     vv = fmaf(y, y, vv);
     kv = fmaf(x, y, kv);
+    if constexpr (std::is_same<IO, bf16_t>::value) wide |= fabsf(x) >= 65536.f || fabsf(y) >= 65536.f;
   }
+  const bool f16_ok = __ballot(wide) == 0;
   kk = row_pair_sum(row16_sum(kk));
   vv = row_pair_sum(row16_sum(vv));
   kv = row_pair_sum(row16_sum(kv));
@@ -65,7 +68,8 @@ __global__ __launch_bounds__(256) void wide_coef_kernel(const IO* __restrict__ k
   kv += __shfl_xor(kv, 32);
   if (lane == 0) {
     bool ok;  // identity token: N = 0 (its k, v are read as zero where staged)
-    const NCoef N = cham::cayley_n_guarded(io<GT>::load(gamma, tok), kk, vv, kv, ok);
+    NCoef N = cham::cayley_n_guarded(io<GT>::load(gamma, tok), kk, vv, kv, ok);
+    if (!f16_ok) N = NCoef{};
     float4* o = reinterpret_cast<float4*>(coef + static_cast<int64_t>(tok) * NCF);
     o[0] = make_float4(N.n11r, N.n11i, N.n12r, N.n12i);
     o[1] = make_float4(N.n22r, N.n22i, 0.f, 0.f);

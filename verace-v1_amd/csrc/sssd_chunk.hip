@@ -514,7 +514,10 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
         dl = (r.mk && t0 + t < a.T) ? 0.1f / (1.f + __expf(-dl)) : 0.f;
       const cayley2 M = cayley_guarded(dl, kk, vv, kv, ok);
       P.mcoef[t] = make_float4(M.m00, M.m01, M.m10, M.m11);
-      if constexpr (READOUT && !FUSED) wide = ok && rotation_outside_chunk_envelope(dl, kk, vv, kv);
+      // also every token the f16 operands cannot hold: a non-finite Gram entry comes from a
+      // non-finite input (the fp32 kernel applies the same identity guard) or from a finite
+      // 16-bit element above the f16 range (65504), which the fp32 kernel takes as it is
+      if constexpr (READOUT && !FUSED) wide = !ok || rotation_outside_chunk_envelope(dl, kk, vv, kv);
     }
     if constexpr (READOUT && !FUSED) {
       // hand the sequence to the fp32 recompute (a plain store: every writer stores the tag)

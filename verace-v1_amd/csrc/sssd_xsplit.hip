@@ -779,7 +779,7 @@ __global__ __launch_bounds__(NT) void sssd_xsplit_kernel(Args a) {
         const float dl = n * C + t >= a.T ? 0.f : ra.d;
         const cayley2 M = cayley_guarded(dl, kk, vv, kv, ok);
         P.mcoef[t] = make_float4(M.m00, M.m01, M.m10, M.m11);
-        wide = ok && rotation_outside_chunk_envelope(dl, kk, vv, kv);
+        wide = !ok || rotation_outside_chunk_envelope(dl, kk, vv, kv);  // as the segment scan
       }
       // hand the sequence to the fp32 recompute (a plain store: every writer stores the tag)
       if (__builtin_amdgcn_ballot_w64(wide) != 0 && lane == 0) a.flags[bh] = a.ftag;
