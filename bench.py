@@ -31,6 +31,7 @@ for _p in (REPO_ROOT, PKG_DIR):
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E spec-sheet peak, GB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 / f16 MFMA spec-sheet peak, TFLOP/s
+MFMA_F32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA spec-sheet peak, TFLOP/s
 OP = dict(B=8, T=4096, H=8, D=128)
 DEC = dict(B=64, H=8, D=128, layers=12, steps=256, prefill=512)
 
@@ -574,6 +575,57 @@ def bench_cham(device, iters=5, warmup=2):
     return res
 
 
+def bench_ns(device, n=1024, batches=(4, 64), steps=3, iters=3, warmup=1):
+    """CHAM Newton-Schulz retraction (vmi_cham_ns_retraction, reference cham_memory.py:21-51 /
+    :296-315) at the reference's default holographic_dim n = 1024, `steps` iterations, batch 4
+    and 64 near-unitary matrices (I + N(0, 0.1 / sqrt(n)) real and imaginary perturbations).
+    Algorithmic work per iteration: H^H H and H (3I - H^H H) / 2, two complex n x n products =
+    16 n^3 real flops, so 48 n^3 per matrix at 3 steps.  C-ABI calls with preallocated outputs
+    and workspace, events around every call."""
+    import ctypes
+    import torch
+    from verace_amd import _lib
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(device)
+    res = {"config": f"NS retraction n={n}, {steps} steps, fp32 in/out",
+           "algorithmic_flops_per_matrix": 16 * steps * n ** 3}
+    for batch in batches:
+        g = torch.Generator().manual_seed(batch)
+        scale = 0.1 / n ** 0.5  # singular values within ~[0.8, 1.2]: 3 steps converge
+        hr = (torch.randn(batch, n, n, generator=g) * scale + torch.eye(n)).to(device)
+        hi = (torch.randn(batch, n, n, generator=g) * scale).to(device)
+        out_r, out_i = torch.empty_like(hr), torch.empty_like(hi)
+        ws_bytes = ctypes.c_size_t(0)
+        _lib.check(lib.vmi_cham_ns_workspace_bytes(batch, n, ctypes.byref(ws_bytes)),
+                   "vmi_cham_ns_workspace_bytes")
+        ws = torch.empty(max(ws_bytes.value, 1), device=device, dtype=torch.uint8)
+        vp = ctypes.c_void_p
+        args = (vp(hr.data_ptr()), vp(hi.data_ptr()), vp(out_r.data_ptr()), vp(out_i.data_ptr()),
+                batch, n, steps, vp(ws.data_ptr()), ws_bytes.value, _lib.stream_handle(device))
+        for _ in range(warmup):
+            _lib.check(lib.vmi_cham_ns_retraction(*args), "vmi_cham_ns_retraction")
+        per = []
+        for _ in range(iters):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            _lib.check(lib.vmi_cham_ns_retraction(*args), "vmi_cham_ns_retraction")
+            b.record(stream)
+            torch.cuda.synchronize()
+            per.append(a.elapsed_time(b))
+        ms = statistics.median(per)
+        tf = 16 * steps * n ** 3 * batch / (ms * 1e-3) / 1e12
+        # unitarity of the result (first matrix), as a sanity check of the timed output
+        H = torch.complex(out_r[0].double(), out_i[0].double())
+        unit = float((H.conj().t() @ H - torch.eye(n, dtype=torch.complex128, device=device)).abs().max())
+        res[f"batch{batch}"] = {"ms_median": round(ms, 3), "tflops": round(tf, 2),
+                                "frac_fp32_mfma_peak": round(tf / MFMA_F32_PEAK_TFLOPS, 4),
+                                "frac_f16_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                                "unitarity_err": unit}
+        del hr, hi, out_r, out_i, ws
+        torch.cuda.empty_cache()
+    return res
+
+
 def bench_backward(device, iters=5, warmup=2):
     """Backward of the scan (row f4) at the FULL training shape B=4 T=2048 H=8 D=128, bf16:
     launch_sssd_hip_scan_bwd (dq, dk, dv, ddelta from dOut, states rebuilt from the final
@@ -893,7 +945,9 @@ MFMA_KERNELS = [  # (label, substring of the kernel name in rocprofv3's CSVs, de
     ("fused scan pass C", "sssd_chunk_kernelIDF16bNS_6bf16_tELb1ELb1E", MFMA_F16_PEAK_TFLOPS),
     ("backward columns (bwdc_cols_kernel)", "bwdc_cols_kernel", MFMA_F16_PEAK_TFLOPS),
     ("backward prep (bwdc_prep_kernel)", "bwdc_prep_kernel", 157.3),
-    ("CHAM NS GEMM (ns_gemm2_kernel)", "ns_gemm2_kernel", 157.3),
+    ("CHAM NS GEMM (ns_gemm2_kernel, fp32 MFMA, n not a multiple of 128)", "ns_gemm2_kernel", 157.3),
+    ("CHAM NS Gram (ns16_gemm_kernel<GRAM>, f16 hi + lo)", "ns16_gemm_kernel<true|ns16_gemm_kernelILb1E", MFMA_F16_PEAK_TFLOPS),
+    ("CHAM NS update (ns16_gemm_kernel<update>, f16 hi + lo)", "ns16_gemm_kernel<false|ns16_gemm_kernelILb0E", MFMA_F16_PEAK_TFLOPS),
     ("CHAM Z (wide_z_kernel)", "wide_z_kernel", 157.3),
     ("CHAM matrix-core carry (cm_cols_kernel)", "cm_cols_kernel", MFMA_F16_PEAK_TFLOPS),
     ("CHAM matrix-core readout (cm_read_kernel)", "cm_read_kernel", MFMA_F16_PEAK_TFLOPS),
@@ -965,15 +1019,16 @@ def mfma_summary(counter_csv, trace_csv, out_json):
         durs.setdefault(r["Kernel_Name"], []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
     res = {}
     for label, sub, peak in MFMA_KERNELS:
-        names = [n for n in counts if sub in n]
+        alts = sub.split("|")  # demangled or mangled forms of the same kernel
+        hit = lambda name: any(x in name for x in alts)
+        names = [n for n in counts if hit(n)]
         if not names:
             continue
-        n = names[0]
-        c = counts[n]
-        get = lambda cn: sums.get((n, cn), 0.0) / c
+        c = sum(counts[n] for n in names)
+        get = lambda cn: sum(sums.get((n, cn), 0.0) for n in names) / c
         flops = 512 * (get("SQ_INSTS_VALU_MFMA_MOPS_F16") + get("SQ_INSTS_VALU_MFMA_MOPS_BF16")
                        + get("SQ_INSTS_VALU_MFMA_MOPS_F32"))
-        tr = [d for k, v in durs.items() if sub in k for d in v]
+        tr = [d for k, v in durs.items() if hit(k) for d in v]
         mean_ns = statistics.mean(tr) if tr else None
         util = 100 * get("SQ_VALU_MFMA_BUSY_CYCLES") / max(get("GRBM_GUI_ACTIVE") * 1024, 1)
         res[label] = {
@@ -1023,6 +1078,10 @@ def main():
     ap.add_argument("--no-long", action="store_true", help="skip the LONG (T=65536) scan timing")
     ap.add_argument("--no-module", action="store_true",
                     help="skip the FULL SSSD sub-layer (fused vs unfused projections) timing")
+    ap.add_argument("--ns-only", action="store_true",
+                    help="time only the NS retraction leg (for profiling runs)")
+    ap.add_argument("--ns-batches", default="4,64",
+                    help="comma-separated batch sizes of the NS leg (default 4,64)")
     ap.add_argument("--no-model", action="store_true",
                     help="skip the model-level FULL prefill and DEC decode timings")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -1057,6 +1116,10 @@ def main():
 
     import torch
     device = torch.device("cuda:0")
+    ns_batches = tuple(int(x) for x in args.ns_batches.split(","))
+    if args.ns_only:
+        print(json.dumps({"ns": bench_ns(device, batches=ns_batches)}), flush=True)
+        return
     total_ms, per, wall, parity, api, warm = bench_scan(args, device)
     B, T, H, D = OP["B"], OP["T"], OP["H"], OP["D"]
     tokens = B * T
@@ -1138,6 +1201,7 @@ def main():
     if not args.no_module:
         result["module_full"] = bench_module_full(device)
         result["cham"] = bench_cham(device)
+        result["ns"] = bench_ns(device, batches=ns_batches)
         result["scan_backward"] = bench_backward(device)
     if not args.no_model:
         model = _build_model(device)

@@ -76,3 +76,24 @@ def test_ns_retraction_default_size(device):
                 / torch.sqrt((ref_r ** 2).sum() + (ref_i ** 2).sum()))
     print(f"  max abs err real={er:.2e} imag={ei:.2e} rel={rel:.2e}", flush=True)
     assert er < 1e-5 and ei < 1e-5 and rel < 1e-5
+
+
+@pytest.mark.parametrize("batch,n,steps", [(3, 128, 3), (2, 256, 1), (1, 384, 5), (2, 512, 3)])
+def test_ns_matrix_core_route(device, batch, n, steps):
+    """n a multiple of 128 runs the 16-bit matrix-core route (f16 hi + lo operands, two complex
+    GEMM launches per iteration, the Gram's mirror-written tiles): against the fp64 oracle at
+    the fp32 bar (1e-5), with perturbations that exercise every tile and the off-diagonal
+    (mirrored) Gram tiles, and an imaginary part of the same size as the real perturbation."""
+    from verace_amd import newton_schulz_unitary_retraction
+    print(f"[case] ns16 batch={batch} n={n} steps={steps}", flush=True)
+    g = torch.Generator().manual_seed(n + steps)
+    scale = 0.4 / n ** 0.5
+    hr = torch.randn(batch, n, n, generator=g) * scale + torch.eye(n)
+    hi = torch.randn(batch, n, n, generator=g) * scale
+    got_r, got_i = newton_schulz_unitary_retraction(hr.to(device), hi.to(device), steps=steps)
+    torch.cuda.synchronize()
+    ref_r, ref_i = cham_ns.newton_schulz_retraction(hr.double(), hi.double(), steps=steps)
+    er = float((got_r.cpu().double() - ref_r).abs().max())
+    ei = float((got_i.cpu().double() - ref_i).abs().max())
+    print(f"  max abs err real={er:.2e} imag={ei:.2e}", flush=True)
+    assert er < 1e-5 and ei < 1e-5

@@ -121,6 +121,7 @@ hipError_t gemm2(const float* A0, const float* B0, const float* A1, const float*
 }  // namespace
 
 size_t ns_workspace_bytes(int64_t batch, int64_t n) {
+  if (ns16_usable(n)) return ns16_workspace_bytes(batch, n);
   return static_cast<size_t>(6) * batch * n * n * sizeof(float);
 }
 
@@ -136,6 +137,9 @@ hipError_t launch_ns_retraction(const float* h_real, const float* h_imag, float*
       e = hipMemcpyAsync(out_imag, h_imag, bytes, hipMemcpyDeviceToDevice, stream);
     return e;
   }
+  if (ns16_usable(n))  // 16-bit matrix cores, two launches per iteration (cham_ns16.hip)
+    return launch_ns16_retraction(h_real, h_imag, out_real, out_imag, batch, n, steps, workspace,
+                                  stream);
   float* ws = static_cast<float*>(workspace);
   float* Dr = ws;
   float* Di = ws + mat;

@@ -548,8 +548,8 @@ size_t cham_scan_workspace_bytes(int64_t B, int64_t T, int64_t h) {
   // chunk-start states, plus R_0 and the retraction's scratch for calls of RTOK+ tokens
   // (sized for them whether or not an initial hologram is given)
   const int64_t states = nch > 1 ? 2 * B * (nch - 1) * h * h : 0;
-  const int64_t rpart = T >= cham::RTOK ? 8 * B * h * h : 0;
-  return static_cast<size_t>(states + rpart) * sizeof(float);
+  const size_t rpart = T >= cham::RTOK ? 2 * B * h * h * sizeof(float) + ns_workspace_bytes(B, h) : 0;
+  return static_cast<size_t>(states) * sizeof(float) + rpart;
 }
 
 bool cham_scan_supported(int64_t h) { return h >= 1 && h <= kChamMaxDim; }

@@ -622,7 +622,9 @@ WideWs carve(void* base, int64_t B, int64_t T, int64_t h) {
   const int64_t HP = padded(static_cast<int>(h));
   const int64_t nch = (T + C2 - 1) / C2;
   const int64_t sizes[8] = {B * T * NCF, B * nch * 2 * h * HP, B * nch * 2 * C2 * HP,
-                            B * h * h, B * h * h, 6 * B * h * h, 4 * B * MVT * 2 * HP,
+                            B * h * h, B * h * h,
+                            static_cast<int64_t>((ns_workspace_bytes(B, h) + 3) / 4),
+                            4 * B * MVT * 2 * HP,
                             static_cast<int64_t>((cham_mfma_workspace_bytes(B, T, HP) + 3) / 4)};
   WideWs w;
   float* p = static_cast<float*>(base);

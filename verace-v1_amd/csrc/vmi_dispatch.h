@@ -250,6 +250,13 @@ hipError_t launch_sssd_bwd_chunk(const void* q, const void* k, const void* v, co
 
 // cham_ns.hip: Newton-Schulz unitary retraction.
 size_t ns_workspace_bytes(int64_t batch, int64_t n);
+// cham_ns16.hip: the same retraction on the 16-bit matrix cores (f16 hi + lo operands) for
+// n a multiple of 128; launch_ns_retraction takes it whenever ns16_usable(n).
+bool ns16_usable(int64_t n);
+size_t ns16_workspace_bytes(int64_t batch, int64_t n);
+hipError_t launch_ns16_retraction(const float* h_real, const float* h_imag, float* out_real,
+                                  float* out_imag, int batch, int n, int steps, void* workspace,
+                                  hipStream_t stream);
 hipError_t launch_ns_retraction(const float* h_real, const float* h_imag, float* out_real,
                                 float* out_imag, int batch, int n, int steps, void* workspace,
                                 hipStream_t stream);
