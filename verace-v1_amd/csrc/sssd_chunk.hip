@@ -700,6 +700,12 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
       if (n >= 0 && n < nch) {  // uniform across the wave
         PScratch& P = sm.pscr[NPW == 8 ? p : (n & 1)];
         if constexpr (NPW == 4) {
+          // The two long phases run at a raised issue priority: a producer in one of them
+          // sets the iteration period (it shares its SIMD with a consumer and, on SIMDs 0
+          // and 1, a readout wave, both of which have slack).  Measured at OP: 174.6 ->
+          // 165.8 us per scan; all four phases raised, or phase 2 with them, is slower.
+          if (phase == 1 || phase == 3) __builtin_amdgcn_s_setprio(2);
+          else __builtin_amdgcn_s_setprio(0);
           if (phase == 0) {
             p_load(r, n);
           } else if (phase == 1) {
