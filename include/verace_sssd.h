@@ -5,7 +5,8 @@
  * Every entry point takes plain device pointers, sizes and a HIP stream
  * (passed as void*, it is a hipStream_t; NULL = the null stream).  Nothing
  * here allocates device memory: scratch space is passed in by the caller and
- * sized with the matching *_workspace_bytes query.  Kernels are enqueued on
+ * sized with the matching *_workspace_bytes query and 16-byte aligned (as every
+ * device allocation is; some kernels read it 16 bytes at a time).  Kernels are enqueued on
  * the given stream; no entry point synchronises the host.  The one piece of
  * mutable global state is the fixed scratch array of vmi_sssd_scan_fwd_noalloc
  * (one per GPU): calls of that entry point that overlap on one GPU race.  Every

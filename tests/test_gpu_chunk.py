@@ -167,36 +167,40 @@ def test_chunk_scan_input_envelope(device, dtype, dmax, knorm, vnorm):
     _check(o, psi, q, k, v, delta, psi0, f"envelope {dtype} d{dmax} k{knorm} v{vnorm}")
 
 
-def test_chunk_scan_wide_rotations_take_fp32(device):
+@pytest.mark.parametrize("where", ["first", "middle", "last"])
+def test_chunk_scan_wide_rotations_take_fp32(device, where):
     """Heads whose tokens rotate the state by more than the f16-operand chunk scan's envelope
-    allows (m = (delta / 2) |k ^ v| > 0.25) are recomputed by the fp32 token-sequential kernel:
-    their final states equal, bit for bit, those of the fp32 scan of the same values, while the
-    heads inside the envelope keep the chunk result.  Every head holds the bars against the fp64
-    closed form."""
+    allows (m = (delta / 2) |k ^ v| > 0.25) are recomputed by the fp32 token-sequential kernel
+    from psi_0: their final states equal, bit for bit, those of the fp32 scan of the same values,
+    and their outputs are the fp32 scan's rounded once to bf16, while the heads inside the
+    envelope keep the chunk result.  The wide token sits in the first, a middle or the last of
+    the scan's segments (at B 1, H 8, T 4096: 32 segments of 128 tokens; the last one is not
+    part of the first pass).  Every head holds the bars against the fp64 closed form."""
     B, T, H, D = 1, 4096, 8, 128
+    pos = {"first": 40, "middle": T // 2 + 37, "last": T - 5}[where]
     ms = [0.05, 0.2, 0.3, 1.0, 2.0, 5.0, 25.0, 400.0]
-    print(f"[case] wide rotations m={ms} T={T}", flush=True)
+    print(f"[case] wide rotations m={ms} T={T} wide token {pos} ({where} segment)", flush=True)
     g = torch.Generator().manual_seed(12)
     q = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1)
     k = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1)
     v = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1)
-    # unit k, v with delta = 0.4 rotate by m <= 0.2; head h reaches m = ms[h] on token T / 2
-    # (a single token puts a head out) and stays at min(ms[h], 0.2) elsewhere
+    # unit k, v with delta = 0.4 rotate by m <= 0.2; head h reaches m = ms[h] on token pos (a
+    # single token puts a head out) and stays at min(ms[h], 0.2) elsewhere
     delta = torch.full((B, T, H), 0.4)
     for h, m in enumerate(ms):
         s = math.sqrt(m / 0.2)
-        k[:, T // 2:T // 2 + 1, h] *= s
-        v[:, T // 2:T // 2 + 1, h] *= s
-        k[:, :T // 2, h] *= min(s, 1.0)
-        v[:, :T // 2, h] *= min(s, 1.0)
+        k[:, pos:pos + 1, h] *= s
+        v[:, pos:pos + 1, h] *= s
+        k[:, :pos, h] *= min(s, 1.0)
+        v[:, :pos, h] *= min(s, 1.0)
+    psi0 = torch.linalg.qr(torch.randn(B, H, D, D, generator=g))[0].contiguous()
     q, k, v, delta = (t.to(torch.bfloat16) for t in (q, k, v, delta))
-    o, psi = _gpu(q, k, v, delta, None, device)
-    o32, p32 = _gpu(q.float(), k.float(), v.float(), delta.float(), None, device)
-    _check(o, psi, q, k, v, delta, None, "wide rotations")
+    o, psi = _gpu(q, k, v, delta, psi0, device)
+    o32, p32 = _gpu(q.float(), k.float(), v.float(), delta.float(), psi0, device)
+    _check(o, psi, q, k, v, delta, psi0, f"wide rotations, {where} segment")
     for h, m in enumerate(ms):
         same = torch.equal(psi[:, h], p32[:, h])
         assert same == (m > 0.25), (h, m, same)
-    # the recomputed heads' outputs are the fp32 scan's, rounded once to bf16
     wide = [h for h, m in enumerate(ms) if m > 0.25]
     assert torch.equal(o[:, :, wide], o32[:, :, wide].to(torch.bfloat16).float())
 
