@@ -264,10 +264,10 @@ int vmi_sssd_scan_bwd(const void* q, const void* k, const void* v, const void* d
                       void* d_delta, float* d_psi0, int64_t B, int64_t T, int64_t H, int64_t D,
                       void* workspace, size_t workspace_bytes, void* stream);
 
-/* CHAM holographic scan, holographic_dim h <= 1024: replaces launch_cham_triton_update
- * with its single-program kernel for h <= 128 (cham_holographic_scan_kernel,
- * triton_kernels.py:151-306, :639-685) and its tiled route for larger h
- * (launch_cham_triton_tiled, :477-597), and the eager path of
+/* CHAM holographic scan, holographic_dim h <= 1024, or h a multiple of 4 up to 4096:
+ * replaces launch_cham_triton_update with its single-program kernel for h <= 128
+ * (cham_holographic_scan_kernel, triton_kernels.py:151-306, :639-685) and its tiled route for
+ * larger h (launch_cham_triton_tiled, :477-597), and the eager path of
  * ContinuousHolographicMemory.forward (cham_memory.py:167-238).
  *   H_t = U_t H_{t-1},  U_t = (I - i G_t/2)^-1 (I + i G_t/2),
  *   G_t = gamma_t (k_t v_t^T + v_t k_t^T)       (exact Cayley, closed rank-2 form)
@@ -276,8 +276,12 @@ int vmi_sssd_scan_bwd(const void* q, const void* k, const void* v, const void* d
  * is written to (h_real_out, h_imag_out).
  *   q, k, v, out : [B, T, h] io_dtype;  gamma : [B, T] gamma_dtype;
  *   h0_*, h_*_out : [B, h, h] float32 (outputs must not overlap the inputs).
- * h > 1024: VMI_ERR_UNSUPPORTED.  Workspace from vmi_cham_scan_workspace_bytes (for
- * h > 128 it holds a state snapshot per 64 tokens: about 2 B T h^2 / 64 floats).
+ * Above h = 1024 the scan runs one in-place step per token (the kernels of
+ * vmi_cham_step_inplace on H and, when H_0 is given, on R = NS_3(H_0) held in the workspace):
+ * O(T h^2) memory traffic, B <= 65535 and B h^2 <= 2^31 - 1; h > 4096 or h % 4 != 0 there:
+ * VMI_ERR_UNSUPPORTED.  Workspace from vmi_cham_scan_workspace_bytes (for 128 < h <= 1024 it
+ * holds a state snapshot per 64 tokens: about 2 B T h^2 / 64 floats; above 1024 the readout
+ * state, the retraction's scratch and the step's partials).
  * Precondition of the 16-bit route for 128 < h <= 1024 (io_dtype BF16 or F16): every element
  * of k and v is below 65504 in magnitude, because the matrix-core carry converts them to f16
  * (exactly, inside that range).  A token with a larger element (bf16 values from 65536 up) is
@@ -303,8 +307,9 @@ int vmi_cham_scan_fwd(const void* q, const void* k, const void* v, const void* g
  * the in-place form is opt-in for callers that own the state (as vmi_sssd_step_inplace).
  *   q, k, v, out : [B, 1, h] io_dtype;  gamma : [B] gamma_dtype;
  *   h_real, h_imag (and r_real, r_imag) : [B, h, h] float32, read and written, distinct.
- * h % 4 == 0 and h <= 1024 (otherwise VMI_ERR_UNSUPPORTED).  Workspace from
- * vmi_cham_step_workspace_bytes (per-block readout partials: B (h/32) h floats). */
+ * h % 4 == 0 and h <= 4096 (otherwise VMI_ERR_UNSUPPORTED).  Workspace from
+ * vmi_cham_step_workspace_bytes (per-block readout partials: B (h/16) h floats up to h = 1024,
+ * B (h/4) h above). */
 int vmi_cham_step_workspace_bytes(int64_t B, int64_t h, size_t* bytes);
 int vmi_cham_step_inplace(const void* q, const void* k, const void* v, const void* gamma,
                           int io_dtype, int gamma_dtype, float* h_real, float* h_imag,

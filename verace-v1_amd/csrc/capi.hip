@@ -253,6 +253,8 @@ int vmi_cham_scan_fwd(const void* q, const void* k, const void* v, const void* g
   if (!valid_dtype(io_dtype) || !valid_dtype(gamma_dtype)) return VMI_ERR_INVALID_ARG;
   if (B < 0 || T < 0 || h < 1 || B * T > INT32_MAX) return VMI_ERR_INVALID_ARG;
   if (!vmi::cham_scan_supported(h)) return VMI_ERR_UNSUPPORTED;
+  // the per-token route above h = 1024: one item per grid row, 32-bit retraction indices
+  if (h > vmi::kChamMaxDim && (B > 65535 || B * h * h > INT32_MAX)) return VMI_ERR_INVALID_ARG;
   if ((h0_real == nullptr) != (h0_imag == nullptr)) return VMI_ERR_INVALID_ARG;
   if (h_real_out == nullptr || h_imag_out == nullptr) return VMI_ERR_INVALID_ARG;
   if (T > 0 && (q == nullptr || k == nullptr || v == nullptr || gamma == nullptr || out == nullptr))
@@ -300,7 +302,7 @@ int vmi_cham_scan_fused(const void* proj, int64_t proj_stride, int io_dtype, con
 
 int vmi_cham_step_workspace_bytes(int64_t B, int64_t h, size_t* bytes) {
   if (bytes == nullptr || B < 0 || h < 1) return VMI_ERR_INVALID_ARG;
-  if (h > 1024 || h % 4 != 0) return VMI_ERR_UNSUPPORTED;
+  if (!vmi::cham_step_supported(h)) return VMI_ERR_UNSUPPORTED;
   *bytes = vmi::cham_step_workspace_bytes(B, h);
   return VMI_OK;
 }
@@ -311,7 +313,7 @@ int vmi_cham_step_inplace(const void* q, const void* k, const void* v, const voi
                           void* workspace, size_t workspace_bytes, void* stream) {
   if (!valid_dtype(io_dtype) || !valid_dtype(gamma_dtype)) return VMI_ERR_INVALID_ARG;
   if (B < 0 || h < 1 || B > 65535) return VMI_ERR_INVALID_ARG;
-  if (h > 1024 || h % 4 != 0) return VMI_ERR_UNSUPPORTED;
+  if (!vmi::cham_step_supported(h)) return VMI_ERR_UNSUPPORTED;
   if ((r_real == nullptr) != (r_imag == nullptr)) return VMI_ERR_INVALID_ARG;
   if (B > 0 && (q == nullptr || k == nullptr || v == nullptr || gamma == nullptr ||
                 out == nullptr || h_real == nullptr || h_imag == nullptr))

@@ -543,6 +543,7 @@ hipError_t launch_io(const void* q, const void* k, const void* v, const void* ga
 }  // namespace cham
 
 size_t cham_scan_workspace_bytes(int64_t B, int64_t T, int64_t h) {
+  if (h > kChamMaxDim) return cham_step_scan_workspace_bytes(B, h);
   if (h > cham::HP) return cham_wide_workspace_bytes(B, T, h);
   const int64_t nch = (T + cham::CH - 1) / cham::CH;
   // chunk-start states, plus R_0 and the retraction's scratch for calls of RTOK+ tokens
@@ -552,12 +553,17 @@ size_t cham_scan_workspace_bytes(int64_t B, int64_t T, int64_t h) {
   return static_cast<size_t>(states) * sizeof(float) + rpart;
 }
 
-bool cham_scan_supported(int64_t h) { return h >= 1 && h <= kChamMaxDim; }
+bool cham_scan_supported(int64_t h) {
+  return (h >= 1 && h <= kChamMaxDim) || cham_step_supported(h);
+}
 
 hipError_t launch_cham_scan(const void* q, const void* k, const void* v, const void* gamma,
                             int io_dtype, int gamma_dtype, const float* h0r, const float* h0i,
                             void* out, float* hr_out, float* hi_out, int B, int T, int h,
                             void* workspace, hipStream_t stream) {
+  if (h > kChamMaxDim)
+    return launch_cham_step_scan(q, k, v, gamma, io_dtype, gamma_dtype, h0r, h0i, out, hr_out,
+                                 hi_out, B, T, h, workspace, stream);
   if (h > cham::HP)
     return launch_cham_wide(q, k, v, gamma, io_dtype, gamma_dtype, h0r, h0i, out, hr_out, hi_out,
                             B, T, h, workspace, stream);

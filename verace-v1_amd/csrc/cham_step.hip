@@ -20,9 +20,12 @@
 // one state of one item (512 threads): thread (rg, cg) holds rows rg + (512 / (CB/4)) m and
 // columns 4 cg .. 4 cg + 3 (float4; CB / 4 lanes cover a row piece of the block).  CB = 32
 // (128-byte row pieces) up to h = 512, CB = 16 above (8 rows of both parts per thread: 64
-// floats; 32 columns would need 128 and spill).  The readout sums over columns, so the
-// readout-state workgroups write per-block partial sums of Rr' q; cham_step_finish_kernel
-// adds them.
+// floats; 32 columns would need 128 and spill), and CB = 4 for 1024 < h <= 4096 (one float4
+// column group, 512 row groups of 4 or 8 rows: the same 64 floats per thread, in 16-byte row
+// pieces).  The readout sums over columns, so the readout-state workgroups write per-block
+// partial sums of Rr' q; cham_step_finish_kernel adds them.  Token rows and gamma are read
+// at item strides (ios, gs), so the holographic scan above h = 1024 runs this kernel once
+// per token on the rows of its [B, T, h] inputs.
 #include "cham_common.h"
 #include "vmi_dispatch.h"
 
@@ -31,7 +34,9 @@ namespace chams {
 
 using cham::NCoef;
 
-constexpr int CB_MIN = 16;      // smallest column block (sizes the readout partials)
+constexpr int CB_MIN = 16;      // smallest column block up to h = 1024 (sizes the partials)
+constexpr int CB_BIG = 4;       // column block above h = 2048 (8 from 1024 to 2048)
+constexpr int H_BIG = 4096;     // largest h of the step kernels
 
 // Where item b's state lives.  DenseItems: plane arrays [B, h, h] (real and imaginary
 // separate).  SlotItems: the per-layer hologram pool of a decode state cache, slot s at
@@ -86,17 +91,20 @@ template <typename IO, typename GT, int NT, int CB, int RPT, bool EXACT, typenam
 __global__ __launch_bounds__(NT) void cham_step_kernel(
     const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
     const GT* __restrict__ gamma, float* hr0, float* hi0, float* hr1, float* hi1,
-    float* __restrict__ part, int h_arg, int nstates, const Map map) {
+    float* __restrict__ part, int h_arg, int nstates, const Map map, int64_t ios, int64_t gs) {
   constexpr int CGN = CB / 4;        // column groups of 4 columns (float4)
   const int h = EXACT ? NT / CGN * RPT : h_arg;
   constexpr int NRG = NT / CGN;  // row groups
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cg = tid & (CGN - 1), rg = tid / CGN;
-  // With 16-column blocks two blocks share each 128-byte line of a row.  Workgroups go to the
-  // 8 XCDs round robin by linear id, so blocks x and x + 8 land on the same XCD (and L2):
-  // they take the two halves of the same lines (column blocks 2c and 2c + 1).
+  // Below 32 columns, LG = 32 / CB blocks share each 128-byte line of a row.  Workgroups go to
+  // the 8 XCDs round robin by linear id, so blocks x, x + 8, .. land on the same XCD (and L2):
+  // they take the LG pieces of the same lines (column blocks LG c .. LG c + LG - 1).
+  constexpr int LG = 32 / CB;
   const int bx = blockIdx.x;
-  const int blk = (CB == 16 && (gridDim.x & 15) == 0) ? ((bx & ~15) | ((bx & 7) << 1) | ((bx >> 3) & 1)) : bx;
+  const int blk = (LG > 1 && gridDim.x % (8 * LG) == 0)
+                      ? ((bx / (8 * LG)) * 8 + (bx & 7)) * LG + ((bx >> 3) % LG)
+                      : bx;
   const int b = blockIdx.y, z = blockIdx.z;
   const int nblk = gridDim.x;
   const int c0 = blk * CB + 4 * cg;
@@ -104,7 +112,7 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
   float* __restrict__ sr = z == 0 ? hr0 : hr1;
   float* __restrict__ si = z == 0 ? hi0 : hi1;
   const int64_t hh = static_cast<int64_t>(h) * h;
-  const int64_t tb = static_cast<int64_t>(b) * h;  // this item's token row
+  const int64_t tb = static_cast<int64_t>(b) * ios;  // this item's token row
 
   __shared__ float4 s_red[NT / 64][CB];  // per wave: (ar, ai, br, bi) of each column
   __shared__ float s_dot[NT / 64][3];
@@ -145,7 +153,7 @@ __global__ __launch_bounds__(NT) void cham_step_kernel(
       }
     }
   }
-  const float g = io<GT>::load(gamma, b);
+  const float g = io<GT>::load(gamma, static_cast<int64_t>(b) * gs);
   float4 qc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (readout && colok)
     qc = make_float4(io<IO>::load(q, tb + c0), io<IO>::load(q, tb + c0 + 1),
@@ -493,7 +501,7 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
   for (int m = RR; m < RPT; ++m) upd(m, s_hold[m - RR][0][tid], s_hold[m - RR][1][tid]);
 }
 
-// out[b][i] = sum over the column blocks of the readout partials (io dtype), in block order.
+// out[b][i] = sum over the NB column blocks of the readout partials (io dtype), in block order.
 // Four outputs per thread (16-byte loads; h % 4 == 0), 64 threads per workgroup; with NB
 // (the block count, 32 at h = 1024) known, all NB loads of a thread are issued before the
 // first add, so the partials cost one memory round trip (a runtime-length loop waited on
@@ -501,48 +509,98 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
 template <typename IO, int NB>
 __global__ __launch_bounds__(64) void cham_step_finish_kernel(const float* __restrict__ part,
                                                               IO* __restrict__ out, int h,
-                                                              int nblk) {
+                                                              int nblk, int64_t os) {
   const int b = blockIdx.y;
   const int i = (blockIdx.x * 64 + threadIdx.x) * 4;
   if (i >= h) return;
   const float* pp = part + static_cast<int64_t>(b) * nblk * h + i;
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
   auto add = [&](const float4& x) { s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w; };
-  if constexpr (NB > 0) {
-    float4 x[NB];
+  (void)nblk;
+  float4 x[NB];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) x[j] = *reinterpret_cast<const float4*>(pp + static_cast<int64_t>(j) * h);
+  for (int j = 0; j < NB; ++j) x[j] = *reinterpret_cast<const float4*>(pp + static_cast<int64_t>(j) * h);
 #pragma unroll
-    for (int j = 0; j < NB; ++j) add(x[j]);
-  } else {
-    for (int j = 0; j < nblk; ++j) add(*reinterpret_cast<const float4*>(pp + static_cast<int64_t>(j) * h));
-  }
-  IO* o = out + static_cast<int64_t>(b) * h + i;
+  for (int j = 0; j < NB; ++j) add(x[j]);
+  IO* o = out + static_cast<int64_t>(b) * os + i;  // os: item stride of out (elements)
   io<IO>::store(o, 0, s.x);
   io<IO>::store(o, 1, s.y);
   io<IO>::store(o, 2, s.z);
   io<IO>::store(o, 3, s.w);
 }
 
+// The same for any block count: 1024 threads per 256 outputs, each of 16 thread slices sums
+// its share of the blocks (16-byte loads, 8 in flight), then the slices are added in order
+// through LDS (above h = 1024 there are up to 1024 blocks per output).
 template <typename IO>
-hipError_t launch_finish(const float* part, void* out, int B, int h, int nblk, hipStream_t stream) {
+__global__ __launch_bounds__(1024) void cham_step_finish_sliced_kernel(
+    const float* __restrict__ part, IO* __restrict__ out, int h, int nblk, int64_t os) {
+  constexpr int NS = 16;
+  __shared__ float4 acc[NS][64];
+  const int b = blockIdx.y;
+  const int og = threadIdx.x & 63, sl = threadIdx.x >> 6;
+  const int i = (blockIdx.x * 64 + og) * 4;
+  const int j0 = static_cast<int>(static_cast<int64_t>(nblk) * sl / NS);
+  const int j1 = static_cast<int>(static_cast<int64_t>(nblk) * (sl + 1) / NS);
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (i < h) {
+    const float* pp = part + static_cast<int64_t>(b) * nblk * h + i;
+    int j = j0;
+    for (; j + 8 <= j1; j += 8) {
+      float4 x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = *reinterpret_cast<const float4*>(pp + static_cast<int64_t>(j + u) * h);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) { s.x += x[u].x; s.y += x[u].y; s.z += x[u].z; s.w += x[u].w; }
+    }
+    for (; j < j1; ++j) {
+      const float4 x = *reinterpret_cast<const float4*>(pp + static_cast<int64_t>(j) * h);
+      s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
+    }
+  }
+  acc[sl][og] = s;
+  __syncthreads();
+  if (sl == 0 && i < h) {
+    for (int u = 1; u < NS; ++u) {
+      const float4 x = acc[u][og];
+      s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
+    }
+    IO* o = out + static_cast<int64_t>(b) * os + i;
+    io<IO>::store(o, 0, s.x);
+    io<IO>::store(o, 1, s.y);
+    io<IO>::store(o, 2, s.z);
+    io<IO>::store(o, 3, s.w);
+  }
+}
+
+template <typename IO>
+hipError_t launch_finish(const float* part, void* out, int B, int h, int nblk, int64_t os,
+                         hipStream_t stream) {
   const dim3 grid((h / 4 + 63) / 64, B);
   if (nblk == 32)
     hipLaunchKernelGGL((cham_step_finish_kernel<IO, 32>), grid, dim3(64), 0, stream, part,
-                       static_cast<IO*>(out), h, nblk);
+                       static_cast<IO*>(out), h, nblk, os);
   else
-    hipLaunchKernelGGL((cham_step_finish_kernel<IO, 0>), grid, dim3(64), 0, stream, part,
-                       static_cast<IO*>(out), h, nblk);
+    hipLaunchKernelGGL((cham_step_finish_sliced_kernel<IO>), grid, dim3(1024), 0, stream, part,
+                       static_cast<IO*>(out), h, nblk, os);
   return hipGetLastError();
 }
 
+int step_block_cols(int h) {
+  return h > 2048 ? CB_BIG : h > 1024 ? 8 : (h > 512 && h != 1024) ? 16 : 32;
+}
+
+// One step of B items.  Item b's q, k, v rows start at element b * ios of q, k, v, its gamma
+// at b * gs, its output row at b * os of out (a single decode step: ios = os = h, gs = 1; a
+// token of a [B, T, h] scan: ios = os = T h, gs = T, pointers offset to the token).
 template <typename IO, typename GT, typename Map>
 hipError_t launch_t(const void* q, const void* k, const void* v, const void* gamma, float* hr,
                     float* hi, float* rr, float* ri, void* out, int B, int h, float* part,
-                    const Map& map, hipStream_t stream) {
-  // h = 1024: the LDS-holding kernel with 32-column blocks; other h above 512: 16-column
-  // blocks of 512 threads, 8 rows each (32 columns would need 16 rows per thread and spill)
-  const int cb = (h > 512 && h != 1024) ? 16 : 32;
+                    const Map& map, hipStream_t stream, int64_t ios, int64_t gs, int64_t os) {
+  // h = 1024: the LDS-holding kernel with 32-column blocks (item strides h and 1 only); other h
+  // above 512: 16-column blocks of 512 threads, 8 rows each (32 columns would need 16 rows per
+  // thread and spill); above 1024: 4-column blocks, 4 or 8 rows per thread
+  const int cb = step_block_cols(h);
   const int nblk = (h + cb - 1) / cb;
   const int nstates = rr ? 2 : 1;
   const dim3 grid(nblk, B, nstates);
@@ -552,21 +610,27 @@ hipError_t launch_t(const void* q, const void* k, const void* v, const void* gam
   const GT* gg = static_cast<const GT*>(gamma);
 #define VMI_CS(CB_, RPT_, EX_) \
   hipLaunchKernelGGL((cham_step_kernel<IO, GT, 512, CB_, RPT_, EX_, Map>), grid, dim3(512), 0, \
-                     stream, qq, kq, vq, gg, hr, hi, rr, ri, part, h, nstates, map)
+                     stream, qq, kq, vq, gg, hr, hi, rr, ri, part, h, nstates, map, ios, gs)
+
   if (h == 128) VMI_CS(32, 2, true);
   else if (h < 128) VMI_CS(32, 2, false);
   else if (h == 256) VMI_CS(32, 4, true);
   else if (h < 256) VMI_CS(32, 4, false);
   else if (h == 512) VMI_CS(32, 8, true);
   else if (h < 512) VMI_CS(32, 8, false);
-  else if (h == 1024)
+  else if (h == 1024) {
+    if (ios != h || gs != 1) return hipErrorInvalidValue;
     hipLaunchKernelGGL((cham_step1024_kernel<IO, GT, Map>), grid, dim3(512), 0, stream, qq, kq, vq,
                        gg, hr, hi, rr, ri, part, nstates, map, ChamFused{});
-  else VMI_CS(16, 8, false);
+  } else if (h < 1024) VMI_CS(16, 8, false);
+  else if (h == 2048) VMI_CS(8, 8, true);
+  else if (h < 2048) VMI_CS(8, 8, false);
+  else if (h == H_BIG) VMI_CS(CB_BIG, 8, true);
+  else VMI_CS(CB_BIG, 8, false);
 #undef VMI_CS
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_finish<IO>(part, out, B, h, nblk, stream);
+  return launch_finish<IO>(part, out, B, h, nblk, os, stream);
 }
 
 template <typename IO>
@@ -581,7 +645,7 @@ hipError_t launch_fused_t(const void* proj, int64_t stride, const uint8_t* mask,
                      DenseItems{}, ChamFused{stride, mask});
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_finish<IO>(part, out, B, h, nblk, stream);
+  return launch_finish<IO>(part, out, B, h, nblk, h, stream);
 }
 
 }  // namespace chams
@@ -603,24 +667,29 @@ hipError_t launch_cham_step_fused(const void* proj, int64_t proj_stride, int io_
 }
 
 size_t cham_step_workspace_bytes(int64_t B, int64_t h) {
-  return static_cast<size_t>(B) * ((h + chams::CB_MIN - 1) / chams::CB_MIN) * h * sizeof(float);
+  const int64_t cb = h > 2048 ? chams::CB_BIG : h > kChamMaxDim ? 8 : chams::CB_MIN;
+  return static_cast<size_t>(B) * ((h + cb - 1) / cb) * h * sizeof(float);
+}
+
+bool cham_step_supported(int64_t h) {
+  return h >= 1 && h % 4 == 0 && h <= chams::H_BIG;
 }
 
 template <typename Map>
 hipError_t launch_cham_step_map(const void* q, const void* k, const void* v, const void* gamma,
                                 int io_dtype, int gamma_dtype, float* hr, float* hi, float* rr,
                                 float* ri, void* out, int B, int h, void* workspace, const Map& map,
-                                hipStream_t stream) {
+                                hipStream_t stream, int64_t ios, int64_t gs, int64_t os) {
   float* part = static_cast<float*>(workspace);
 #define VMI_GT(IO_)                                                                              \
   if (gamma_dtype == VMI_F32)                                                                  \
     return chams::launch_t<IO_, float, Map>(q, k, v, gamma, hr, hi, rr, ri, out, B, h, part, map, \
-                                            stream);                                           \
+                                            stream, ios, gs, os);                              \
   if (gamma_dtype == VMI_BF16)                                                                 \
     return chams::launch_t<IO_, bf16_t, Map>(q, k, v, gamma, hr, hi, rr, ri, out, B, h, part, map, \
-                                             stream);                                          \
+                                             stream, ios, gs, os);                             \
   return chams::launch_t<IO_, f16_t, Map>(q, k, v, gamma, hr, hi, rr, ri, out, B, h, part, map,   \
-                                          stream);
+                                          stream, ios, gs, os);
   if (io_dtype == VMI_F32) { VMI_GT(float) }
   if (io_dtype == VMI_BF16) { VMI_GT(bf16_t) }
   VMI_GT(f16_t)
@@ -632,7 +701,7 @@ hipError_t launch_cham_step(const void* q, const void* k, const void* v, const v
                             float* ri, void* out, int B, int h, void* workspace,
                             hipStream_t stream) {
   return launch_cham_step_map(q, k, v, gamma, io_dtype, gamma_dtype, hr, hi, rr, ri, out, B, h,
-                              workspace, chams::DenseItems{}, stream);
+                              workspace, chams::DenseItems{}, stream, h, 1, h);
 }
 
 hipError_t launch_cham_step_slots(const void* q, const void* k, const void* v, const void* gamma,
@@ -645,7 +714,71 @@ hipError_t launch_cham_step_slots(const void* q, const void* k, const void* v, c
     map.out_slot[i] = out_slot[i];
   }
   return launch_cham_step_map(q, k, v, gamma, io_dtype, gamma_dtype, pool, pool, nullptr, nullptr,
-                              out, B, h, workspace, map, stream);
+                              out, B, h, workspace, map, stream, h, 1, h);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The holographic scan above h = 1024 (up to 4096, h % 4 == 0), where the chunked routes'
+// register and LDS tiles end: the state starts as H_0 (or I) in the output buffers, the readout
+// state R_0 = NS_3(H_0) (when H_0 is given) in the workspace, and every token is one step
+// (the kernels above, one read and one write of each state per token) on its rows of the
+// [B, T, h] inputs.  O(T h^2) memory traffic instead of the chunked routes' matrix-core
+// products: a route for sizes the reference's own tiled fallback covers
+// (launch_cham_triton_tiled, triton_kernels.py:477-597), not a fast path.
+namespace chams {
+__global__ __launch_bounds__(256) void eye_kernel(float* __restrict__ hr, float* __restrict__ hi,
+                                                  int64_t n, int h) {
+  const int64_t hh = static_cast<int64_t>(h) * h;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t e = i % hh;
+    hr[i] = e / h == e % h ? 1.f : 0.f;
+    hi[i] = 0.f;
+  }
+}
+size_t elem_bytes(int dtype) { return dtype == VMI_F32 ? 4 : 2; }
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+}  // namespace chams
+
+size_t cham_step_scan_workspace_bytes(int64_t B, int64_t h) {
+  return chams::align256(cham_step_workspace_bytes(B, h)) +
+         chams::align256(2 * static_cast<size_t>(B) * h * h * sizeof(float)) + ns_workspace_bytes(B, h);
+}
+
+hipError_t launch_cham_step_scan(const void* q, const void* k, const void* v, const void* gamma,
+                                 int io_dtype, int gamma_dtype, const float* h0r,
+                                 const float* h0i, void* out, float* hr_out, float* hi_out, int B,
+                                 int T, int h, void* workspace, hipStream_t stream) {
+  char* ws = static_cast<char*>(workspace);
+  float* part = reinterpret_cast<float*>(ws);
+  const int64_t hh = static_cast<int64_t>(h) * h;
+  float* rr = reinterpret_cast<float*>(ws + chams::align256(cham_step_workspace_bytes(B, h)));
+  float* ri = rr + B * hh;
+  void* nsws = reinterpret_cast<char*>(rr) + chams::align256(2 * static_cast<size_t>(B) * hh * sizeof(float));
+  const size_t sb = static_cast<size_t>(B) * hh * sizeof(float);
+  hipError_t e;
+  if (h0r != nullptr) {
+    e = hipMemcpyAsync(hr_out, h0r, sb, hipMemcpyDeviceToDevice, stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(hi_out, h0i, sb, hipMemcpyDeviceToDevice, stream);
+    if (e == hipSuccess) e = launch_ns_retraction(h0r, h0i, rr, ri, B, h, 3, nsws, stream);
+  } else {
+    hipLaunchKernelGGL(chams::eye_kernel, dim3(1024), dim3(256), 0, stream, hr_out, hi_out, B * hh, h);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
+  const size_t ie = chams::elem_bytes(io_dtype), ge = chams::elem_bytes(gamma_dtype);
+  const int64_t ts = static_cast<int64_t>(T) * h;  // item stride of q, k, v, out
+  for (int t = 0; t < T; ++t) {
+    const size_t o = static_cast<size_t>(t) * h * ie;
+    e = launch_cham_step_map(static_cast<const char*>(q) + o, static_cast<const char*>(k) + o,
+                             static_cast<const char*>(v) + o,
+                             static_cast<const char*>(gamma) + static_cast<size_t>(t) * ge,
+                             io_dtype, gamma_dtype, hr_out, hi_out, h0r ? rr : nullptr,
+                             h0r ? ri : nullptr, static_cast<char*>(out) + o, B, h, part,
+                             chams::DenseItems{}, stream, ts, T, ts);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace vmi

@@ -150,8 +150,9 @@ hipError_t launch_sssd_chunked_fused(const void* proj, int64_t proj_stride, int 
                                      void* out, float* psi_out, int B, int T, int H,
                                      void* workspace, hipStream_t stream);
 
-// cham_scan.hip: CHAM holographic scan (h <= 128 there, larger h routed to cham_wide.hip):
-// raw complex state with exact Cayley rank-2 updates, readout Re(NS_3(H_t) q_t).
+// cham_scan.hip: CHAM holographic scan (h <= 128 there, 128 < h <= kChamMaxDim routed to
+// cham_wide.hip, larger h to the per-token steps of cham_step.hip): raw complex state with
+// exact Cayley rank-2 updates, readout Re(NS_3(H_t) q_t).
 constexpr int64_t kChamMaxDim = 1024;
 bool cham_scan_supported(int64_t h);
 size_t cham_scan_workspace_bytes(int64_t B, int64_t T, int64_t h);
@@ -160,8 +161,9 @@ hipError_t launch_cham_scan(const void* q, const void* k, const void* v, const v
                             void* out, float* hr_out, float* hi_out, int B, int T, int h,
                             void* workspace, hipStream_t stream);
 
-// cham_step.hip: single-token CHAM step, states updated in place (h % 4 == 0, h <= 1024);
-// rr/ri (the readout state) may be null (then the readout uses H).
+// cham_step.hip: single-token CHAM step, states updated in place (cham_step_supported: h % 4
+// == 0, h <= 4096); rr/ri (the readout state) may be null (then the readout uses H).
+bool cham_step_supported(int64_t h);
 size_t cham_step_workspace_bytes(int64_t B, int64_t h);
 hipError_t launch_cham_step(const void* q, const void* k, const void* v, const void* gamma,
                             int io_dtype, int gamma_dtype, float* hr, float* hi, float* rr,
@@ -184,6 +186,14 @@ hipError_t launch_cham_step_slots(const void* q, const void* k, const void* v, c
                                   int io_dtype, int gamma_dtype, float* pool, const int32_t* in_slot,
                                   const int32_t* out_slot, void* out, int B, int h, void* workspace,
                                   hipStream_t stream);
+
+// cham_step.hip: the holographic scan for kChamMaxDim < h (cham_step_supported), one step per
+// token (H_0 copied to the outputs, R_0 = NS_3(H_0) in the workspace when H_0 is given).
+size_t cham_step_scan_workspace_bytes(int64_t B, int64_t h);
+hipError_t launch_cham_step_scan(const void* q, const void* k, const void* v, const void* gamma,
+                                 int io_dtype, int gamma_dtype, const float* h0r,
+                                 const float* h0i, void* out, float* hr_out, float* hi_out, int B,
+                                 int T, int h, void* workspace, hipStream_t stream);
 
 // cham_wide.hip: the same scan for 128 < h <= kChamMaxDim.
 size_t cham_wide_workspace_bytes(int64_t B, int64_t T, int64_t h);

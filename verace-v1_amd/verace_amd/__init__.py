@@ -19,7 +19,7 @@ Drop-in replacements for the reference's SSSD hot path:
 * ``newton_schulz_unitary_retraction`` / ``parallel_newton_schulz_retraction``
                                <- ``verace_v1.modules.cham_memory`` (same names)
 * ``launch_cham_hip_update``   <- ``verace_v1.serving.triton_kernels.launch_cham_triton_update``
-                               (CHAM holographic scan, holographic_dim <= 1024)
+                               (CHAM holographic scan, holographic_dim <= 4096)
 * ``cham_step_``               -- in-place single-token CHAM step (opt-in)
 * ``cham_step_fused_``         -- the same step with silu, the normalisations and gamma fused in
 * ``launch_cham_hip_update_fused`` -- the CHAM scan from the identity with the same fusion

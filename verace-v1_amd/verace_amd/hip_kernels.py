@@ -383,7 +383,8 @@ def launch_cham_hip_update(
     """CHAM holographic scan on the GPU (replaces ``launch_cham_triton_update``,
     ``triton_kernels.py:639-685``; parity target ``cham_memory.py:167-238``).
 
-    q, k, v: [batch, seq_len, holographic_dim] (h <= 1024); gamma: [batch, seq_len];
+    q, k, v: [batch, seq_len, holographic_dim] (h <= 1024, or a multiple of 4 up to 4096: one
+    in-place step per token there); gamma: [batch, seq_len];
     initial_hologram: optional (H_real, H_imag) [batch, h, h], identity when None (never
     modified).  Returns (out [batch, seq_len, h] in q's dtype = Re(NS_3(H_t) q_t),
     (H_real, H_imag) the raw final state, float32).
@@ -555,7 +556,8 @@ def cham_step_(
     callers that own the state: the reference never mutates ``initial_hologram`` (the
     generator's branches share it), so pass copies where it is shared.  Reference: the CHAM
     forward at seq_len 1 (``cham_memory.py:117-238``) that the decode loop re-runs per token.
-    h must be a multiple of 4 (<= 1024); other h take the general scan and a retraction.
+    h must be a multiple of 4 (<= 4096); other h up to 1024 take the general scan and a
+    retraction.
     """
     hr, hi = hologram
     for name, t in (("q", q), ("H_real", hr), ("H_imag", hi)):
@@ -577,7 +579,7 @@ def cham_step_(
     g_c = gamma.reshape(B).contiguous()
     for name, t in (("k", k_c), ("v", v_c), ("gamma", g_c)):
         _require_device(t, name)
-    if h % 4 != 0 or h > 1024:
+    if h % 4 != 0:
         # general route: the scan from the current state (it retracts for the readout), then
         # the new raw state (and its retraction) written back in place
         out, (nr, ni) = launch_cham_hip_update(q_c, k_c, v_c, g_c.reshape(B, 1), (hr, hi))
