@@ -50,6 +50,51 @@ __device__ __forceinline__ short to_bf16(float x) {  // round to nearest even
 
 enum { kStore = 0, kAdd = 1, kMaskStore = 2 };
 
+// N consecutive elements of a row as raw 32-bit words (one 8- or 16-byte load, two for 8
+// fp32), and element j of them as a float.  The row must be aligned to its byte size.
+template <typename T, int N> struct RowRaw {
+  static constexpr int W = N * static_cast<int>(sizeof(T)) / 4;
+  uint32_t w[W];
+};
+template <typename T, int N>
+__device__ __forceinline__ RowRaw<T, N> load_raw(const T* p) {
+  RowRaw<T, N> r;
+  constexpr int W = RowRaw<T, N>::W;
+  static_assert(W == 2 || W % 4 == 0, "8-byte or whole 16-byte pieces");
+  if constexpr (W == 2) {
+    const uint2 x = *reinterpret_cast<const uint2*>(p);
+    r.w[0] = x.x; r.w[1] = x.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i) {
+      const uint4 x = reinterpret_cast<const uint4*>(p)[i];
+      r.w[4 * i] = x.x; r.w[4 * i + 1] = x.y; r.w[4 * i + 2] = x.z; r.w[4 * i + 3] = x.w;
+    }
+  }
+  return r;
+}
+template <typename T, int N>
+__device__ __forceinline__ float raw_elem(const RowRaw<T, N>& r, int j) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(r.w[j]);
+  } else {
+    const uint16_t hbits = static_cast<uint16_t>(r.w[j >> 1] >> (16 * (j & 1)));
+    if constexpr (std::is_same<T, bf16_t>::value) return bf16_to_f32(hbits);
+    else return static_cast<float>(__builtin_bit_cast(f16_t, hbits));
+  }
+}
+
+// Workgroup barrier that orders LDS accesses only: it waits for this wave's LDS operations,
+// not for its global loads and stores (which __syncthreads() also waits for).  The columns
+// kernel's global loads fill registers for the next chunk and its global stores are read by
+// the next kernel, so neither needs ordering at the chunk's barriers.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt(63) expcnt(7) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // LDS row strides (64 banks of 4 B): with 19 and 37 every MFMA operand read is at most 2-way
 // bank conflicted across the wave, in both orientations and for both lane layouts (fp32:
 // lane (m, kq) reads element k0 + kq of row m, or row k0 + kq of column m; bf16: elements
@@ -278,86 +323,87 @@ __global__ __launch_bounds__(NT) void bwdc_cols_kernel(
     Ps[i * L16 + jj] = psi_T[o];
     Lm[i * L16 + jj] = dpsi_T ? dpsi_T[o] : 0.f;
   }
-  // chunk n's inputs: registers first (the next chunk's arrive while this one runs)
+  // chunk n's inputs: registers first (the next chunk's arrive while this one runs).  Thread
+  // (t = tid / 16, j0 = EU (tid % 16)) holds elements j0 .. j0 + EU - 1 of token t's k, v and
+  // dO rows as raw words (one 8- or 16-byte load each per row and thread; converted at the
+  // commit), its q element, and four consecutive words of the chunk record's T~.
   constexpr int EU = D * C / NT;  // elements of k (and of v, dO) per thread
-  float rk[EU], rv[EU], rd[EU], rq, rt[R * R / NT];
+  static_assert(NT == 16 * C && D == 16 * EU, "16 threads per token row");
+  RowRaw<IO, EU> rk, rv;
+  RowRaw<GO, EU> rd;
+  float rq;
+  float4 rt;
   int rbad = 0;  // tokens of the chunk that are the identity (non-finite Cayley factor)
   auto tok = [&](int tg) { return (static_cast<int64_t>(b) * T + tg) * H + hd; };
+  const int ft = tid >> 4, fj = EU * (tid & 15);
   auto fetch = [&](int n) {
-#pragma unroll
-    for (int m = 0; m < EU; ++m) {
-      const int e = tid + NT * m, t = e / D, i = e % D, tg = n * C + t;
-      const int64_t o = tok(tg < T ? tg : 0) * D + i;
-      rk[m] = io<IO>::load(k, o);
-      rv[m] = io<IO>::load(v, o);
-      rd[m] = io<GO>::load(dout, o);
-    }
+    const int tg = n * C + ft;
+    const int64_t o = tok(tg < T ? tg : 0) * D + fj;
+    rk = load_raw<IO, EU>(k + o);
+    rv = load_raw<IO, EU>(v + o);
+    rd = load_raw<GO, EU>(dout + o);
     {
-      const int t = tid / CB, jj = tid % CB, tg = n * C + t;  // CB * C == NT
-      rq = io<IO>::load(q, tok(tg < T ? tg : 0) * D + blk * CB + jj);
+      const int t = tid / CB, jj = tid % CB, tq = n * C + t;  // CB * C == NT
+      rq = io<IO>::load(q, tok(tq < T ? tq : 0) * D + blk * CB + jj);
     }
-#pragma unroll
-    for (int m = 0; m < R * R / NT; ++m)
-      rt[m] = tt[(static_cast<int64_t>(bh) * nch + n) * REC + tid + NT * m];
-    rbad = __float_as_int(tt[(static_cast<int64_t>(bh) * nch + n) * REC + REC_BAD]);
+    const float* rec = tt + (static_cast<int64_t>(bh) * nch + n) * REC;
+    rt = *reinterpret_cast<const float4*>(rec + 4 * tid);  // R * R == 4 NT
+    rbad = __float_as_int(rec[REC_BAD]);
   };
   auto commit = [&](int n) {
+    const bool ok = n * C + ft < T;
+    const bool uk = ok && !((rbad >> ft) & 1);
 #pragma unroll
-    for (int m = 0; m < EU; ++m) {
-      const int e = tid + NT * m, t = e / D, i = e % D;
-      const bool ok = n * C + t < T;
-      const bool uk = ok && !((rbad >> t) & 1);
-      U[i * L32 + 2 * t] = uk ? rk[m] : 0.f;
-      U[i * L32 + 2 * t + 1] = uk ? rv[m] : 0.f;
-      dO[i * L16 + t] = ok ? rd[m] : 0.f;
+    for (int j = 0; j < EU; ++j) {
+      const int i = fj + j;
+      U[i * L32 + 2 * ft] = uk ? raw_elem<IO, EU>(rk, j) : 0.f;
+      U[i * L32 + 2 * ft + 1] = uk ? raw_elem<IO, EU>(rv, j) : 0.f;
+      dO[i * L16 + ft] = ok ? raw_elem<GO, EU>(rd, j) : 0.f;
     }
     {
       const int t = tid / CB, jj = tid % CB;
       Qb[jj * L16 + t] = n * C + t < T ? rq : 0.f;
     }
-#pragma unroll
-    for (int m = 0; m < R * R / NT; ++m) {
-      const int e = tid + NT * m;
-      Tt[(e / R) * L32 + e % R] = rt[m];
-    }
+    float* trow = &Tt[((4 * tid) / R) * L32 + (4 * tid) % R];  // row pitch 37: 4-byte stores
+    trow[0] = rt.x; trow[1] = rt.y; trow[2] = rt.z; trow[3] = rt.w;
   };
 
   if (nch > 0) {
     fetch(nch - 1);
     commit(nch - 1);
   }
-  __syncthreads();
+  lds_barrier();
   for (int n = nch - 1; n >= 0; --n) {
     if (n > 0) fetch(n - 1);
     // Psi_s = Psi_e + U (T~^T (U^T Psi_e))
     lgemm<R, CB, D, true, false, kStore>(U, L32, Ps, L16, S1, L16, wave, lane);
-    __syncthreads();
+    lds_barrier();
     lgemm<R, CB, R, true, false, kStore>(Tt, L32, S1, L16, Wm, L16, wave, lane);
-    __syncthreads();
+    lds_barrier();
     lgemm<D, CB, R, false, false, kAdd>(U, L32, Wm, L16, Ps, L16, wave, lane);
-    __syncthreads();
+    lds_barrier();
     // W = U^T Psi_s (waves 0-1);  dX = mask o (U^T dO) (waves 2-3)
     lgemm<R, CB, D, true, false, kStore, 0, 2, LP>(U, L32, Ps, L16, Wm, L16, wave, lane);
     lgemm<R, C, D, true, false, kMaskStore, 2, 2, LP>(U, L32, dO, L16, dXm, L16, wave, lane);
-    __syncthreads();
+    lds_barrier();
     // Z = T~ W (waves 0-1), Psi_s^T dO (wave 0, first term of dQ);
     // dZ = U^T Lam_e + dX Q^T (waves 2-3)
     lgemm<R, CB, R, false, false, kStore, 0, 2, LP>(Tt, L32, Wm, L16, Zm, L16, wave, lane);
     lgemm<CB, C, D, true, false, kStore, 1, 1, LP>(Ps, L16, dO, L16, QD, L16, wave, lane);
     lgemm<R, CB, D, true, false, kStore, 2, 2, LP>(U, L32, Lm, L16, dZm, L16, wave, lane);
     lgemm<R, CB, C, false, true, kAdd, 2, 2, LP>(dXm, L16, Qb, L16, dZm, L16, wave, lane);
-    __syncthreads();
+    lds_barrier();
     // X = mask o (Z Q) (wave 0);  dW = T~^T dZ (wave 1);  dT~ partial = dZ W^T (waves 2-3);
     // dQ = Z^T dX + Psi_s^T dO (wave 0)
     lgemm<R, C, CB, false, false, kMaskStore, 0, 1, LP>(Zm, L16, Qb, L16, Xm, L16, wave, lane);
     lgemm<R, CB, R, true, false, kStore, 1, 1, LP>(Tt, L32, dZm, L16, dWm, L16, wave, lane);
     lgemm<R, R, CB, false, true, kStore, 2, 2, LP>(dZm, L16, Wm, L16, dTp, L32, wave, lane);
     lgemm<CB, C, R, true, false, kStore, 0, 1, LP>(Zm, L16, dXm, L16, dQm, L16, wave, lane);
-    __syncthreads();
+    lds_barrier();
     // dU partial = Lam_e Z^T + dO X^T + Psi_s dW^T, straight to the workspace
     float* pp = part + ((static_cast<int64_t>(bh) * nch + n) * NBLK + blk) * PS;
     lgemm3_nt_global<D, LP>(Lm, Zm, dO, Xm, Ps, dWm, pp + R * R, wave, lane);
-    __syncthreads();
+    lds_barrier();
     // outputs of the chunk, then Lam_s = Lam_e + dO Q^T + U dW
     {
       for (int e = tid; e < R * R; e += NT) pp[e] = dTp[(e / R) * L32 + e % R];
@@ -366,9 +412,9 @@ __global__ __launch_bounds__(NT) void bwdc_cols_kernel(
     }
     lgemm<D, CB, C, false, true, kAdd>(dO, L16, Qb, L16, Lm, L16, wave, lane);
     lgemm<D, CB, R, false, false, kAdd>(U, L32, dWm, L16, Lm, L16, wave, lane);
-    __syncthreads();
+    lds_barrier();
     if (n > 0) commit(n - 1);
-    __syncthreads();
+    lds_barrier();
   }
   if (dpsi0) {
     for (int e = tid; e < D * CB; e += NT) {
