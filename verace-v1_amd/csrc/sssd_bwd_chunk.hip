@@ -74,6 +74,35 @@ __device__ __forceinline__ RowRaw<T, N> load_raw(const T* p) {
   return r;
 }
 template <typename T, int N>
+__device__ __forceinline__ void store_row(T* p, const float (&x)[N]) {
+  RowRaw<T, N> r;
+  constexpr int W = RowRaw<T, N>::W;
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) r.w[j] = __float_as_uint(x[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; j += 2) {
+      uint32_t lo, hi;
+      if constexpr (std::is_same<T, bf16_t>::value) {
+        lo = f32_to_bf16(x[j]);
+        hi = f32_to_bf16(x[j + 1]);
+      } else {
+        lo = __builtin_bit_cast(uint16_t, static_cast<f16_t>(x[j]));
+        hi = __builtin_bit_cast(uint16_t, static_cast<f16_t>(x[j + 1]));
+      }
+      r.w[j >> 1] = lo | (hi << 16);
+    }
+  }
+  if constexpr (W == 2) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(r.w[0], r.w[1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i)
+      reinterpret_cast<uint4*>(p)[i] = make_uint4(r.w[4 * i], r.w[4 * i + 1], r.w[4 * i + 2], r.w[4 * i + 3]);
+  }
+}
+template <typename T, int N>
 __device__ __forceinline__ float raw_elem(const RowRaw<T, N>& r, int j) {
   if constexpr (sizeof(T) == 4) {
     return __uint_as_float(r.w[j]);
@@ -267,12 +296,17 @@ __global__ __launch_bounds__(NT) void bwdc_prep_kernel(const IO* __restrict__ k,
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, hd = bh % H;
   const int nch = gridDim.x;
-  for (int e = tid; e < D * C; e += NT) {
-    const int t = e / D, i = e % D, tg = n * C + t;
+  {  // thread (t, EU consecutive features): one 8- or 16-byte load per row
+    constexpr int EU = D * C / NT;
+    const int t = tid >> 4, i0 = EU * (tid & 15), tg = n * C + t;
     const bool ok = tg < T;
-    const int64_t o = ((static_cast<int64_t>(b) * T + (ok ? tg : 0)) * H + hd) * D + i;
-    U[i * L32 + 2 * t] = ok ? io<IO>::load(k, o) : 0.f;
-    U[i * L32 + 2 * t + 1] = ok ? io<IO>::load(v, o) : 0.f;
+    const int64_t o = ((static_cast<int64_t>(b) * T + (ok ? tg : 0)) * H + hd) * D + i0;
+    const RowRaw<IO, EU> rk = load_raw<IO, EU>(k + o), rv = load_raw<IO, EU>(v + o);
+#pragma unroll
+    for (int j = 0; j < EU; ++j) {
+      U[(i0 + j) * L32 + 2 * t] = ok ? raw_elem<IO, EU>(rk, j) : 0.f;
+      U[(i0 + j) * L32 + 2 * t + 1] = ok ? raw_elem<IO, EU>(rv, j) : 0.f;
+    }
   }
   if (tid < C) {
     const int tg = n * C + tid;
@@ -466,14 +500,10 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
     }
     if (tid < 4 * C) rm = rec[3 * R * R + tid];
   }
-  float rk[NK], rv[NK];
-#pragma unroll
-  for (int u = 0; u < NK; ++u) {
-    const int e = tid + NT * u, t = e / D, i = e % D, tg = n * C + t;
-    const int64_t o = tok(tg < T ? tg : 0) * D + i;
-    rk[u] = io<IO>::load(k, o);
-    rv[u] = io<IO>::load(v, o);
-  }
+  // thread (t, NK consecutive features) of the chunk's k, v rows: one 8- or 16-byte load each
+  const int ft = tid >> 4, fi = NK * (tid & 15);
+  const int64_t fo = tok(n * C + ft < T ? n * C + ft : 0) * D + fi;
+  const RowRaw<IO, NK> rk = load_raw<IO, NK>(k + fo), rv = load_raw<IO, NK>(v + fo);
   if (tid < C) {
     const int tg = n * C + tid;
     rd = tg < T ? load_scalar(delta, delta_dtype, tok(tg)) : 0.f;
@@ -486,12 +516,13 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
   }
   if (tid < 4 * C) Mb[tid] = rm;
   if (tid < C) dl[tid] = rd;
+  {
+    const bool ok = n * C + ft < T && !((bad >> ft) & 1);
 #pragma unroll
-  for (int u = 0; u < NK; ++u) {
-    const int e = tid + NT * u, t = e / D, i = e % D;
-    const bool ok = n * C + t < T && !((bad >> t) & 1);
-    U[i * L32 + 2 * t] = ok ? rk[u] : 0.f;
-    U[i * L32 + 2 * t + 1] = ok ? rv[u] : 0.f;
+    for (int j = 0; j < NK; ++j) {
+      U[(fi + j) * L32 + 2 * ft] = ok ? raw_elem<IO, NK>(rk, j) : 0.f;
+      U[(fi + j) * L32 + 2 * ft + 1] = ok ? raw_elem<IO, NK>(rv, j) : 0.f;
+    }
   }
 #pragma unroll
   for (int u = 0; u < NE; ++u) {
@@ -570,14 +601,16 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
   __syncthreads();
   lgemm<D, R, R, false, false, kAdd>(U, L32, tmp, L32, dU, R, wave, lane);
   __syncthreads();
-  for (int e = tid; e < D * C; e += NT) {
-    const int t = e / D, i = e % D, tg = n * C + t;
-    if (tg < T) {
-      const int64_t o = tok(tg) * D + i;
-      const bool z = (bad >> t) & 1;
-      io<IO>::store(dk, o, z ? 0.f : dU[i * R + 2 * t]);
-      io<IO>::store(dv, o, z ? 0.f : dU[i * R + 2 * t + 1]);
+  if (n * C + ft < T) {  // the same (token, features) split: one 8- or 16-byte store per row
+    const bool z = (bad >> ft) & 1;
+    float xk[NK], xv[NK];
+#pragma unroll
+    for (int j = 0; j < NK; ++j) {
+      xk[j] = z ? 0.f : dU[(fi + j) * R + 2 * ft];
+      xv[j] = z ? 0.f : dU[(fi + j) * R + 2 * ft + 1];
     }
+    store_row<IO, NK>(dk + fo, xk);
+    store_row<IO, NK>(dv + fo, xv);
   }
 }
 
