@@ -196,13 +196,13 @@ __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, i
 // dst (global, M x 32, row stride 32) = A1 B1^T + A2 B2^T + A3 B3^T with A_i [M][16] and
 // B_i [32][16] in LDS (row stride L16): the three products of one tile share one
 // accumulator, so the sum goes to memory once.
-template <int M, bool LP>
+template <int M, bool LP, int NWAVES>
 __device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B1, const float* A2,
                                                  const float* B2, const float* A3, const float* B3,
                                                  float* dst, int wave, int lane) {
   constexpr int NTILE = (M / 16) * 2;
   const int l16 = lane & 15, kq = lane >> 4;
-  for (int tile = wave; tile < NTILE; tile += NT / 64) {
+  for (int tile = wave; tile < NTILE; tile += NWAVES) {
     const int tm = tile >> 1, tn = tile & 1;
     const int am = 16 * tm + l16, bn = 16 * tn + l16;
     f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
@@ -329,8 +329,11 @@ __global__ __launch_bounds__(NT) void bwdc_prep_kernel(const IO* __restrict__ k,
 // part layout per (bh, chunk, column block): dT~ partial [R][R], then dU partial [D][R].
 template <int D> struct PartC { static constexpr int size = R * R + D * R; };
 
+constexpr int NTC = 512;         // threads of the columns kernel: 8 waves, two per SIMD
+constexpr int NWC = NTC / 64;
+
 template <typename IO, typename GO, int D>
-__global__ __launch_bounds__(NT) void bwdc_cols_kernel(
+__global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
     const float* __restrict__ tt, const float* __restrict__ psi_T, const GO* __restrict__ dout,
     const float* __restrict__ dpsi_T, IO* __restrict__ dq, float* __restrict__ dpsi0,
@@ -341,9 +344,9 @@ __global__ __launch_bounds__(NT) void bwdc_cols_kernel(
   // the state reconstruction and the adjoint update, carried across chunks, stay fp32
   constexpr bool LP = !std::is_same<IO, float>::value;
   // row strides: L32 for the 32-wide (rank index) matrices, L16 for the 16-wide ones
-  __shared__ float U[D * L32], Tt[R * L32], Qb[CB * L16], dO[D * L16];
+  __shared__ float U[D * L32], Tt[R * L32], Gm[R * L32], Qb[CB * L16], dO[D * L16];
   __shared__ float Ps[D * L16], Lm[D * L16];
-  __shared__ float S1[R * L16], Wm[R * L16], Zm[R * L16], Xm[R * L16], dXm[R * L16],
+  __shared__ float S1[R * L16], Wm[R * L16], Wt[R * L16], Zm[R * L16], Xm[R * L16], dXm[R * L16],
       dZm[R * L16], dWm[R * L16], QD[CB * L16];
   __shared__ float dTp[R * L32], dQm[CB * L16];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -351,40 +354,46 @@ __global__ __launch_bounds__(NT) void bwdc_cols_kernel(
   const int nch = (T + C - 1) / C;
   const int64_t DD = static_cast<int64_t>(D) * D;
 
-  for (int e = tid; e < D * CB; e += NT) {
+  for (int e = tid; e < D * CB; e += NTC) {
     const int i = e / CB, jj = e % CB;
     const int64_t o = bh * DD + static_cast<int64_t>(i) * D + blk * CB + jj;
     Ps[i * L16 + jj] = psi_T[o];
     Lm[i * L16 + jj] = dpsi_T ? dpsi_T[o] : 0.f;
   }
-  // chunk n's inputs: registers first (the next chunk's arrive while this one runs).  Thread
-  // (t = tid / 16, j0 = EU (tid % 16)) holds elements j0 .. j0 + EU - 1 of token t's k, v and
-  // dO rows as raw words (one 8- or 16-byte load each per row and thread; converted at the
-  // commit), its q element, and four consecutive words of the chunk record's T~.
-  constexpr int EU = D * C / NT;  // elements of k (and of v, dO) per thread
-  static_assert(NT == 16 * C && D == 16 * EU, "16 threads per token row");
+  // chunk n's inputs: registers first (the next chunk's arrive while this one runs), loaded by
+  // the first 256 threads.  Thread (t = tid / 16, j0 = EU (tid % 16)) holds elements
+  // j0 .. j0 + EU - 1 of token t's k, v and dO rows as raw words (one 8- or 16-byte load each
+  // per row; converted at the commit), its q element, and four consecutive words of the chunk
+  // record's T~ and of its Gram matrix G.
+  constexpr int NL = 16 * C;      // loading threads
+  constexpr int EU = D * C / NL;  // elements of k (and of v, dO) per loading thread
+  static_assert(D == 16 * EU && CB * C == NL && R * R == 4 * NL, "16 threads per token row");
+  const bool loader = tid < NL;
   RowRaw<IO, EU> rk, rv;
   RowRaw<GO, EU> rd;
-  float rq;
-  float4 rt;
+  float rq = 0.f;
+  float4 rt, rg;
   int rbad = 0;  // tokens of the chunk that are the identity (non-finite Cayley factor)
   auto tok = [&](int tg) { return (static_cast<int64_t>(b) * T + tg) * H + hd; };
-  const int ft = tid >> 4, fj = EU * (tid & 15);
+  const int ft = (tid >> 4) & (C - 1), fj = EU * (tid & 15);
   auto fetch = [&](int n) {
+    if (!loader) return;
     const int tg = n * C + ft;
     const int64_t o = tok(tg < T ? tg : 0) * D + fj;
     rk = load_raw<IO, EU>(k + o);
     rv = load_raw<IO, EU>(v + o);
     rd = load_raw<GO, EU>(dout + o);
     {
-      const int t = tid / CB, jj = tid % CB, tq = n * C + t;  // CB * C == NT
+      const int t = tid / CB, jj = tid % CB, tq = n * C + t;
       rq = io<IO>::load(q, tok(tq < T ? tq : 0) * D + blk * CB + jj);
     }
     const float* rec = tt + (static_cast<int64_t>(bh) * nch + n) * REC;
-    rt = *reinterpret_cast<const float4*>(rec + 4 * tid);  // R * R == 4 NT
+    rt = *reinterpret_cast<const float4*>(rec + 4 * tid);
+    rg = *reinterpret_cast<const float4*>(rec + 2 * R * R + 4 * tid);
     rbad = __float_as_int(rec[REC_BAD]);
   };
   auto commit = [&](int n) {
+    if (!loader) return;
     const bool ok = n * C + ft < T;
     const bool uk = ok && !((rbad >> ft) & 1);
 #pragma unroll
@@ -398,8 +407,9 @@ __global__ __launch_bounds__(NT) void bwdc_cols_kernel(
       const int t = tid / CB, jj = tid % CB;
       Qb[jj * L16 + t] = n * C + t < T ? rq : 0.f;
     }
-    float* trow = &Tt[((4 * tid) / R) * L32 + (4 * tid) % R];  // row pitch 37: 4-byte stores
-    trow[0] = rt.x; trow[1] = rt.y; trow[2] = rt.z; trow[3] = rt.w;
+    const int e = (4 * tid) / R * L32 + (4 * tid) % R;  // row pitch 37: 4-byte stores
+    Tt[e] = rt.x; Tt[e + 1] = rt.y; Tt[e + 2] = rt.z; Tt[e + 3] = rt.w;
+    Gm[e] = rg.x; Gm[e + 1] = rg.y; Gm[e + 2] = rg.z; Gm[e + 3] = rg.w;
   };
 
   if (nch > 0) {
@@ -407,51 +417,59 @@ __global__ __launch_bounds__(NT) void bwdc_cols_kernel(
     commit(nch - 1);
   }
   lds_barrier();
+  // Per chunk, seven phases between LDS barriers, independent products of a phase on disjoint
+  // waves.  W = U^T Psi_s is formed as S1 + G Wm (U^T Psi_s = U^T Psi_e + U^T U T~^T S1), so it
+  // needs no product over the state rows after the reconstruction.
   for (int n = nch - 1; n >= 0; --n) {
     if (n > 0) fetch(n - 1);
-    // Psi_s = Psi_e + U (T~^T (U^T Psi_e))
-    lgemm<R, CB, D, true, false, kStore>(U, L32, Ps, L16, S1, L16, wave, lane);
-    lds_barrier();
-    lgemm<R, CB, R, true, false, kStore>(Tt, L32, S1, L16, Wm, L16, wave, lane);
-    lds_barrier();
-    lgemm<D, CB, R, false, false, kAdd>(U, L32, Wm, L16, Ps, L16, wave, lane);
-    lds_barrier();
-    // W = U^T Psi_s (waves 0-1);  dX = mask o (U^T dO) (waves 2-3)
-    lgemm<R, CB, D, true, false, kStore, 0, 2, LP>(U, L32, Ps, L16, Wm, L16, wave, lane);
+    // (1) S1 = U^T Psi_e (waves 0-1); dX = mask o (U^T dO) (waves 2-3); dZ = U^T Lam_e (4-5)
+    lgemm<R, CB, D, true, false, kStore, 0, 2>(U, L32, Ps, L16, S1, L16, wave, lane);
     lgemm<R, C, D, true, false, kMaskStore, 2, 2, LP>(U, L32, dO, L16, dXm, L16, wave, lane);
+    lgemm<R, CB, D, true, false, kStore, 4, 2, LP>(U, L32, Lm, L16, dZm, L16, wave, lane);
     lds_barrier();
-    // Z = T~ W (waves 0-1), Psi_s^T dO (wave 0, first term of dQ);
-    // dZ = U^T Lam_e + dX Q^T (waves 2-3)
-    lgemm<R, CB, R, false, false, kStore, 0, 2, LP>(Tt, L32, Wm, L16, Zm, L16, wave, lane);
-    lgemm<CB, C, D, true, false, kStore, 1, 1, LP>(Ps, L16, dO, L16, QD, L16, wave, lane);
-    lgemm<R, CB, D, true, false, kStore, 2, 2, LP>(U, L32, Lm, L16, dZm, L16, wave, lane);
-    lgemm<R, CB, C, false, true, kAdd, 2, 2, LP>(dXm, L16, Qb, L16, dZm, L16, wave, lane);
+    // (2) Wm = T~^T S1 (waves 0-1); dZ += dX Q^T (waves 4-5, the tiles they stored);
+    //     W starts as S1 (every thread one element)
+    lgemm<R, CB, R, true, false, kStore, 0, 2>(Tt, L32, S1, L16, Wm, L16, wave, lane);
+    lgemm<R, CB, C, false, true, kAdd, 4, 2, LP>(dXm, L16, Qb, L16, dZm, L16, wave, lane);
+    for (int e = tid; e < R * CB; e += NTC) Wt[(e / CB) * L16 + e % CB] = S1[(e / CB) * L16 + e % CB];
     lds_barrier();
-    // X = mask o (Z Q) (wave 0);  dW = T~^T dZ (wave 1);  dT~ partial = dZ W^T (waves 2-3);
-    // dQ = Z^T dX + Psi_s^T dO (wave 0)
-    lgemm<R, C, CB, false, false, kMaskStore, 0, 1, LP>(Zm, L16, Qb, L16, Xm, L16, wave, lane);
-    lgemm<R, CB, R, true, false, kStore, 1, 1, LP>(Tt, L32, dZm, L16, dWm, L16, wave, lane);
-    lgemm<R, R, CB, false, true, kStore, 2, 2, LP>(dZm, L16, Wm, L16, dTp, L32, wave, lane);
-    lgemm<CB, C, R, true, false, kStore, 0, 1, LP>(Zm, L16, dXm, L16, dQm, L16, wave, lane);
+    // (3) Psi_s = Psi_e + U Wm (8 waves); W += G Wm (waves 0-1, after their Psi tile);
+    //     dW = T~^T dZ (waves 2-3)
+    lgemm<D, CB, R, false, false, kAdd, 0, NWC>(U, L32, Wm, L16, Ps, L16, wave, lane);
+    lgemm<R, CB, R, false, false, kAdd, 0, 2>(Gm, L32, Wm, L16, Wt, L16, wave, lane);
+    lgemm<R, CB, R, true, false, kStore, 2, 2, LP>(Tt, L32, dZm, L16, dWm, L16, wave, lane);
     lds_barrier();
-    // dU partial = Lam_e Z^T + dO X^T + Psi_s dW^T, straight to the workspace
+    // (4) Z = T~ W (waves 0-1); Psi_s^T dO (wave 2, first term of dQ); dT~ partial = dZ W^T
+    //     (waves 4-7)
+    lgemm<R, CB, R, false, false, kStore, 0, 2, LP>(Tt, L32, Wt, L16, Zm, L16, wave, lane);
+    lgemm<CB, C, D, true, false, kStore, 2, 1, LP>(Ps, L16, dO, L16, QD, L16, wave, lane);
+    lgemm<R, R, CB, false, true, kStore, 4, 4, LP>(dZm, L16, Wt, L16, dTp, L32, wave, lane);
+    lds_barrier();
+    // (5) X = mask o (Z Q) (waves 0-1); dQ second term Z^T dX (wave 2)
+    lgemm<R, C, CB, false, false, kMaskStore, 0, 2, LP>(Zm, L16, Qb, L16, Xm, L16, wave, lane);
+    lgemm<CB, C, R, true, false, kStore, 2, 1, LP>(Zm, L16, dXm, L16, dQm, L16, wave, lane);
+    lds_barrier();
+    // (6) dU partial = Lam_e Z^T + dO X^T + Psi_s dW^T straight to the workspace; dT~ partial
+    //     and dq out
     float* pp = part + ((static_cast<int64_t>(bh) * nch + n) * NBLK + blk) * PS;
-    lgemm3_nt_global<D, LP>(Lm, Zm, dO, Xm, Ps, dWm, pp + R * R, wave, lane);
-    lds_barrier();
-    // outputs of the chunk, then Lam_s = Lam_e + dO Q^T + U dW
+    lgemm3_nt_global<D, LP, NWC>(Lm, Zm, dO, Xm, Ps, dWm, pp + R * R, wave, lane);
     {
-      for (int e = tid; e < R * R; e += NT) pp[e] = dTp[(e / R) * L32 + e % R];
-      const int jj = tid / C, t = tid % C, tg = n * C + t;  // CB * C == NT
-      if (tg < T) io<IO>::store(dq, tok(tg) * D + blk * CB + jj, dQm[jj * L16 + t] + QD[jj * L16 + t]);
+      for (int e = tid; e < R * R; e += NTC) pp[e] = dTp[(e / R) * L32 + e % R];
+      if (loader) {
+        const int jj = tid / C, t = tid % C, tg = n * C + t;  // CB * C == NL
+        if (tg < T) io<IO>::store(dq, tok(tg) * D + blk * CB + jj, dQm[jj * L16 + t] + QD[jj * L16 + t]);
+      }
     }
-    lgemm<D, CB, C, false, true, kAdd>(dO, L16, Qb, L16, Lm, L16, wave, lane);
-    lgemm<D, CB, R, false, false, kAdd>(U, L32, dWm, L16, Lm, L16, wave, lane);
+    lds_barrier();
+    // (7) Lam_s = Lam_e + dO Q^T + U dW (8 waves, one tile each, both terms)
+    lgemm<D, CB, C, false, true, kAdd, 0, NWC>(dO, L16, Qb, L16, Lm, L16, wave, lane);
+    lgemm<D, CB, R, false, false, kAdd, 0, NWC>(U, L32, dWm, L16, Lm, L16, wave, lane);
     lds_barrier();
     if (n > 0) commit(n - 1);
     lds_barrier();
   }
   if (dpsi0) {
-    for (int e = tid; e < D * CB; e += NT) {
+    for (int e = tid; e < D * CB; e += NTC) {
       const int i = e / CB, jj = e % CB;
       dpsi0[bh * DD + static_cast<int64_t>(i) * D + blk * CB + jj] = Lm[i * L16 + jj];
     }
@@ -630,7 +648,7 @@ hipError_t launch_d(const void* q, const void* k, const void* v, const void* del
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((bwdc_cols_kernel<IO, GO, D>), dim3(D / CB, BH), dim3(NT), 0, stream,
+  hipLaunchKernelGGL((bwdc_cols_kernel<IO, GO, D>), dim3(D / CB, BH), dim3(NTC), 0, stream,
                      static_cast<const IO*>(q), static_cast<const IO*>(k),
                      static_cast<const IO*>(v), tt, psi_T, static_cast<const GO*>(dout), dpsi_T,
                      static_cast<IO*>(dq), dpsi0, part, T, H);
