@@ -73,6 +73,14 @@ __device__ __forceinline__ RowRaw<T, N> load_raw(const T* p) {
   }
   return r;
 }
+// One element as raw bits in word 0 (RowRaw<T, 2>, low half for 16-bit types).
+template <typename T>
+__device__ __forceinline__ RowRaw<T, 2> load_raw1(const T* p) {
+  RowRaw<T, 2> r = {};
+  if constexpr (sizeof(T) == 4) r.w[0] = *reinterpret_cast<const uint32_t*>(p);
+  else r.w[0] = *reinterpret_cast<const uint16_t*>(p);
+  return r;
+}
 template <typename T, int N>
 __device__ __forceinline__ void store_row(T* p, const float (&x)[N]) {
   RowRaw<T, N> r;
@@ -361,21 +369,26 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     Lm[i * L16 + jj] = dpsi_T ? dpsi_T[o] : 0.f;
   }
   // chunk n's inputs: registers first (the next chunk's arrive while this one runs), loaded by
-  // the first 256 threads.  Thread (t = tid / 16, j0 = EU (tid % 16)) holds elements
+  // waves 4-7, which are idle in the phase that issues the loads.  Thread (t = tid / 16, j0 = EU (tid % 16)) holds elements
   // j0 .. j0 + EU - 1 of token t's k, v and dO rows as raw words (one 8- or 16-byte load each
   // per row; converted at the commit), its q element, and four consecutive words of the chunk
   // record's T~ and of its Gram matrix G.
   constexpr int NL = 16 * C;      // loading threads
   constexpr int EU = D * C / NL;  // elements of k (and of v, dO) per loading thread
   static_assert(D == 16 * EU && CB * C == NL && R * R == 4 * NL, "16 threads per token row");
-  const bool loader = tid < NL;
+  const bool loader = tid >= NTC - NL;
+  const int lt = tid - (NTC - NL);  // loader thread index (meaningful for loaders)
+  // Nothing loaded here is converted or moved before the commit, so no wait for the loads is
+  // placed in the phase that issues them (q is kept as raw bits, and the bad-token mask comes
+  // through a vector load: a scalar load would be waited for at the next LDS barrier, which
+  // counts both).
   RowRaw<IO, EU> rk, rv;
   RowRaw<GO, EU> rd;
-  float rq = 0.f;
+  RowRaw<IO, 2> rq;
   float4 rt, rg;
   int rbad = 0;  // tokens of the chunk that are the identity (non-finite Cayley factor)
   auto tok = [&](int tg) { return (static_cast<int64_t>(b) * T + tg) * H + hd; };
-  const int ft = (tid >> 4) & (C - 1), fj = EU * (tid & 15);
+  const int ft = (lt >> 4) & (C - 1), fj = EU * (lt & 15);
   auto fetch = [&](int n) {
     if (!loader) return;
     const int tg = n * C + ft;
@@ -384,13 +397,15 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     rv = load_raw<IO, EU>(v + o);
     rd = load_raw<GO, EU>(dout + o);
     {
-      const int t = tid / CB, jj = tid % CB, tq = n * C + t;
-      rq = io<IO>::load(q, tok(tq < T ? tq : 0) * D + blk * CB + jj);
+      const int t = lt / CB, jj = lt % CB, tq = n * C + t;
+      rq = load_raw1<IO>(q + tok(tq < T ? tq : 0) * D + blk * CB + jj);
     }
     const float* rec = tt + (static_cast<int64_t>(bh) * nch + n) * REC;
-    rt = *reinterpret_cast<const float4*>(rec + 4 * tid);
-    rg = *reinterpret_cast<const float4*>(rec + 2 * R * R + 4 * tid);
-    rbad = __float_as_int(rec[REC_BAD]);
+    rt = *reinterpret_cast<const float4*>(rec + 4 * lt);
+    rg = *reinterpret_cast<const float4*>(rec + 2 * R * R + 4 * lt);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(rec), (short)0, REC * static_cast<int>(sizeof(float)), 0x00020000);
+    rbad = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(rs, REC_BAD * 4, 0, 0));
   };
   auto commit = [&](int n) {
     if (!loader) return;
@@ -404,10 +419,10 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
       dO[i * L16 + ft] = ok ? raw_elem<GO, EU>(rd, j) : 0.f;
     }
     {
-      const int t = tid / CB, jj = tid % CB;
-      Qb[jj * L16 + t] = n * C + t < T ? rq : 0.f;
+      const int t = lt / CB, jj = lt % CB;
+      Qb[jj * L16 + t] = n * C + t < T ? raw_elem<IO, 2>(rq, 0) : 0.f;
     }
-    const int e = (4 * tid) / R * L32 + (4 * tid) % R;  // row pitch 37: 4-byte stores
+    const int e = (4 * lt) / R * L32 + (4 * lt) % R;  // row pitch 37: 4-byte stores
     Tt[e] = rt.x; Tt[e + 1] = rt.y; Tt[e + 2] = rt.z; Tt[e + 3] = rt.w;
     Gm[e] = rg.x; Gm[e + 1] = rg.y; Gm[e + 2] = rg.z; Gm[e + 3] = rg.w;
   };
@@ -421,7 +436,6 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
   // waves.  W = U^T Psi_s is formed as S1 + G Wm (U^T Psi_s = U^T Psi_e + U^T U T~^T S1), so it
   // needs no product over the state rows after the reconstruction.
   for (int n = nch - 1; n >= 0; --n) {
-    if (n > 0) fetch(n - 1);
     // (1) S1 = U^T Psi_e (waves 0-1); dX = mask o (U^T dO) (waves 2-3); dZ = U^T Lam_e (4-5)
     lgemm<R, CB, D, true, false, kStore, 0, 2>(U, L32, Ps, L16, S1, L16, wave, lane);
     lgemm<R, C, D, true, false, kMaskStore, 2, 2, LP>(U, L32, dO, L16, dXm, L16, wave, lane);
@@ -445,9 +459,11 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     lgemm<CB, C, D, true, false, kStore, 2, 1, LP>(Ps, L16, dO, L16, QD, L16, wave, lane);
     lgemm<R, R, CB, false, true, kStore, 4, 4, LP>(dZm, L16, Wt, L16, dTp, L32, wave, lane);
     lds_barrier();
-    // (5) X = mask o (Z Q) (waves 0-1); dQ second term Z^T dX (wave 2)
+    // (5) X = mask o (Z Q) (waves 0-1); dQ second term Z^T dX (wave 2); the next chunk's loads
+    //     (waves 4-7: issued here, before this chunk's stores, and committed after phase 7)
     lgemm<R, C, CB, false, false, kMaskStore, 0, 2, LP>(Zm, L16, Qb, L16, Xm, L16, wave, lane);
     lgemm<CB, C, R, true, false, kStore, 2, 1, LP>(Zm, L16, dXm, L16, dQm, L16, wave, lane);
+    if (n > 0) fetch(n - 1);
     lds_barrier();
     // (6) dU partial = Lam_e Z^T + dO X^T + Psi_s dW^T straight to the workspace; dT~ partial
     //     and dq out
@@ -455,8 +471,8 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     lgemm3_nt_global<D, LP, NWC>(Lm, Zm, dO, Xm, Ps, dWm, pp + R * R, wave, lane);
     {
       for (int e = tid; e < R * R; e += NTC) pp[e] = dTp[(e / R) * L32 + e % R];
-      if (loader) {
-        const int jj = tid / C, t = tid % C, tg = n * C + t;  // CB * C == NL
+      if (tid < CB * C) {
+        const int jj = tid / C, t = tid % C, tg = n * C + t;
         if (tg < T) io<IO>::store(dq, tok(tg) * D + blk * CB + jj, dQm[jj * L16 + t] + QD[jj * L16 + t]);
       }
     }
