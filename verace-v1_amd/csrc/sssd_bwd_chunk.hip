@@ -201,9 +201,10 @@ __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, i
   }
 }
 
-// dst (global, M x 32, row stride 32) = A1 B1^T + A2 B2^T + A3 B3^T with A_i [M][16] and
-// B_i [32][16] in LDS (row stride L16): the three products of one tile share one
-// accumulator, so the sum goes to memory once.
+// dst (global) = (A1 B1^T + A2 B2^T + A3 B3^T)^T, 32 x M with row stride M, with A_i [M][16]
+// and B_i [32][16] in LDS (row stride L16): the three products of one tile share one
+// accumulator, so the sum goes to memory once, four consecutive elements (one 16-byte store)
+// per lane.
 template <int M, bool LP, int NWAVES>
 __device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B1, const float* A2,
                                                  const float* B2, const float* A3, const float* B3,
@@ -236,8 +237,8 @@ __device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B
         }
       }
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) dst[(16 * tm + 4 * kq + r) * R + bn] = acc0[r] + acc1[r];
+    *reinterpret_cast<float4*>(dst + bn * M + 16 * tm + 4 * kq) =
+        make_float4(acc0[0] + acc1[0], acc0[1] + acc1[1], acc0[2] + acc1[2], acc0[3] + acc1[3]);
   }
 }
 
@@ -334,7 +335,8 @@ __global__ __launch_bounds__(NT) void bwdc_prep_kernel(const IO* __restrict__ k,
 }
 
 // ---------------------------------------------------------------- state columns, in reverse
-// part layout per (bh, chunk, column block): dT~ partial [R][R], then dU partial [D][R].
+// part layout per (bh, chunk, column block): dT~ partial [R][R], then dU partial transposed,
+// [R][D].
 template <int D> struct PartC { static constexpr int size = R * R + D * R; };
 
 constexpr int NTC = 512;         // threads of the columns kernel: 8 waves, two per SIMD
@@ -633,15 +635,16 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
     tmp[r * L32 + c] = L[r * R + c] + L[c * R + r];
   }
   __syncthreads();
-  lgemm<D, R, R, false, false, kAdd>(U, L32, tmp, L32, dU, R, wave, lane);
+  // dU^T += (dG + dG^T) U^T (the partials hold dU transposed, [R][D])
+  lgemm<R, D, R, false, true, kAdd>(tmp, L32, U, L32, dU, D, wave, lane);
   __syncthreads();
   if (n * C + ft < T) {  // the same (token, features) split: one 8- or 16-byte store per row
     const bool z = (bad >> ft) & 1;
     float xk[NK], xv[NK];
 #pragma unroll
     for (int j = 0; j < NK; ++j) {
-      xk[j] = z ? 0.f : dU[(fi + j) * R + 2 * ft];
-      xv[j] = z ? 0.f : dU[(fi + j) * R + 2 * ft + 1];
+      xk[j] = z ? 0.f : dU[(2 * ft) * D + fi + j];
+      xv[j] = z ? 0.f : dU[(2 * ft + 1) * D + fi + j];
     }
     store_row<IO, NK>(dk + fo, xk);
     store_row<IO, NK>(dv + fo, xv);
