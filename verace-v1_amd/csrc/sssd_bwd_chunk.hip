@@ -357,7 +357,7 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
   __shared__ float U[D * L32], Tt[R * L32], Gm[R * L32], Qb[CB * L16], dO[D * L16];
   __shared__ float Ps[D * L16], Lm[D * L16];
   __shared__ float S1[R * L16], Wm[R * L16], Wt[R * L16], Zm[R * L16], Xm[R * L16], dXm[R * L16],
-      dZm[R * L16], dWm[R * L16], QD[CB * L16];
+      dZm[R * L16], dWm[R * L16], QD[2][CB * L16];
   __shared__ float dTp[R * L32], dQm[CB * L16];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int blk = blockIdx.x, bh = blockIdx.y, b = bh / H, hd = bh % H;
@@ -455,10 +455,12 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     lgemm<R, CB, R, false, false, kAdd, 0, 2>(Gm, L32, Wm, L16, Wt, L16, wave, lane);
     lgemm<R, CB, R, true, false, kStore, 2, 2, LP>(Tt, L32, dZm, L16, dWm, L16, wave, lane);
     lds_barrier();
-    // (4) Z = T~ W (waves 0-1); Psi_s^T dO (wave 2, first term of dQ); dT~ partial = dZ W^T
-    //     (waves 4-7)
+    // (4) Z = T~ W (waves 0-1); Psi_s^T dO (first term of dQ) over two halves of the state rows
+    //     (waves 2-3); dT~ partial = dZ W^T (waves 4-7)
     lgemm<R, CB, R, false, false, kStore, 0, 2, LP>(Tt, L32, Wt, L16, Zm, L16, wave, lane);
-    lgemm<CB, C, D, true, false, kStore, 2, 1, LP>(Ps, L16, dO, L16, QD, L16, wave, lane);
+    lgemm<CB, C, D / 2, true, false, kStore, 2, 1, LP>(Ps, L16, dO, L16, QD[0], L16, wave, lane);
+    lgemm<CB, C, D / 2, true, false, kStore, 3, 1, LP>(Ps + (D / 2) * L16, L16, dO + (D / 2) * L16,
+                                                       L16, QD[1], L16, wave, lane);
     lgemm<R, R, CB, false, true, kStore, 4, 4, LP>(dZm, L16, Wt, L16, dTp, L32, wave, lane);
     lds_barrier();
     // (5) X = mask o (Z Q) (waves 0-1); dQ second term Z^T dX (wave 2); the next chunk's loads
@@ -475,7 +477,8 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
       for (int e = tid; e < R * R; e += NTC) pp[e] = dTp[(e / R) * L32 + e % R];
       if (tid < CB * C) {
         const int jj = tid / C, t = tid % C, tg = n * C + t;
-        if (tg < T) io<IO>::store(dq, tok(tg) * D + blk * CB + jj, dQm[jj * L16 + t] + QD[jj * L16 + t]);
+        const int e = jj * L16 + t;
+        if (tg < T) io<IO>::store(dq, tok(tg) * D + blk * CB + jj, dQm[e] + QD[0][e] + QD[1][e]);
       }
     }
     lds_barrier();
