@@ -201,14 +201,24 @@ __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, i
   }
 }
 
+// Partials of the column blocks in the workspace: fp32 for fp32 inputs; bf16 (rounded to
+// nearest even) for bf16 / fp16 inputs, whose gradient products already take bf16 operands.
+// The reduce kernel sums them in fp32.  put4 stores four consecutive elements.
+__device__ __forceinline__ void put4(float* p, float a, float b, float c, float d) {
+  *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+}
+__device__ __forceinline__ void put4(uint16_t* p, float a, float b, float c, float d) {
+  *reinterpret_cast<uint2*>(p) = make_uint2(f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16),
+                                            f32_to_bf16(c) | (static_cast<uint32_t>(f32_to_bf16(d)) << 16));
+}
+
 // dst (global) = (A1 B1^T + A2 B2^T + A3 B3^T)^T, 32 x M with row stride M, with A_i [M][16]
 // and B_i [32][16] in LDS (row stride L16): the three products of one tile share one
-// accumulator, so the sum goes to memory once, four consecutive elements (one 16-byte store)
-// per lane.
-template <int M, bool LP, int NWAVES>
+// accumulator, so the sum goes to memory once, four consecutive elements (one store) per lane.
+template <int M, bool LP, int NWAVES, typename PT>
 __device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B1, const float* A2,
                                                  const float* B2, const float* A3, const float* B3,
-                                                 float* dst, int wave, int lane) {
+                                                 PT* dst, int wave, int lane) {
   constexpr int NTILE = (M / 16) * 2;
   const int l16 = lane & 15, kq = lane >> 4;
   for (int tile = wave; tile < NTILE; tile += NWAVES) {
@@ -237,8 +247,8 @@ __device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B
         }
       }
     }
-    *reinterpret_cast<float4*>(dst + bn * M + 16 * tm + 4 * kq) =
-        make_float4(acc0[0] + acc1[0], acc0[1] + acc1[1], acc0[2] + acc1[2], acc0[3] + acc1[3]);
+    put4(dst + bn * M + 16 * tm + 4 * kq, acc0[0] + acc1[0], acc0[1] + acc1[1], acc0[2] + acc1[2],
+         acc0[3] + acc1[3]);
   }
 }
 
@@ -347,12 +357,14 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     const IO* __restrict__ q, const IO* __restrict__ k, const IO* __restrict__ v,
     const float* __restrict__ tt, const float* __restrict__ psi_T, const GO* __restrict__ dout,
     const float* __restrict__ dpsi_T, IO* __restrict__ dq, float* __restrict__ dpsi0,
-    float* __restrict__ part, int T, int H) {
+    void* __restrict__ part_v, int T, int H) {
   constexpr int PS = PartC<D>::size;
   constexpr int NBLK = D / CB;
   // bf16 / fp16 inputs: the per-chunk gradient products take bf16 operands (their 2e-2 bar);
   // the state reconstruction and the adjoint update, carried across chunks, stay fp32
   constexpr bool LP = !std::is_same<IO, float>::value;
+  typedef typename std::conditional<LP, uint16_t, float>::type PT;  // partials (see put4)
+  PT* __restrict__ part = static_cast<PT*>(part_v);
   // row strides: L32 for the 32-wide (rank index) matrices, L16 for the 16-wide ones
   __shared__ float U[D * L32], Tt[R * L32], Gm[R * L32], Qb[CB * L16], dO[D * L16];
   __shared__ float Ps[D * L16], Lm[D * L16];
@@ -471,10 +483,13 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     lds_barrier();
     // (6) dU partial = Lam_e Z^T + dO X^T + Psi_s dW^T straight to the workspace; dT~ partial
     //     and dq out
-    float* pp = part + ((static_cast<int64_t>(bh) * nch + n) * NBLK + blk) * PS;
+    PT* pp = part + ((static_cast<int64_t>(bh) * nch + n) * NBLK + blk) * PS;
     lgemm3_nt_global<D, LP, NWC>(Lm, Zm, dO, Xm, Ps, dWm, pp + R * R, wave, lane);
     {
-      for (int e = tid; e < R * R; e += NTC) pp[e] = dTp[(e / R) * L32 + e % R];
+      for (int e = 4 * tid; e < R * R; e += 4 * NTC) {
+        const float* d = &dTp[(e / R) * L32 + e % R];
+        put4(pp + e, d[0], d[1], d[2], d[3]);
+      }
       if (tid < CB * C) {
         const int jj = tid / C, t = tid % C, tg = n * C + t;
         const int e = jj * L16 + t;
@@ -501,7 +516,7 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
 template <typename IO, int D>
 __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
     const IO* __restrict__ k, const IO* __restrict__ v, const void* __restrict__ delta,
-    int delta_dtype, const float* __restrict__ tt, const float* __restrict__ part,
+    int delta_dtype, const float* __restrict__ tt, const void* __restrict__ part,
     IO* __restrict__ dk, IO* __restrict__ dv, void* __restrict__ ddelta, int T, int H) {
   constexpr int PS = PartC<D>::size;
   constexpr int NBLK = D / CB;
@@ -517,14 +532,23 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
   // column blocks (16-byte loads), the chunk record (A, G, M) and the chunk's k, v, delta
   static_assert(PS % (4 * NT) == 0, "partials split evenly over the threads");
   constexpr int NE = PS / (4 * NT);
-  float4 x[NE][NBLK];
+  constexpr bool LP = !std::is_same<IO, float>::value;  // bf16 partials (see put4)
+  typedef typename std::conditional<LP, uint2, float4>::type PV;  // four partial elements
+  PV x[NE][NBLK];
   {
-    const float4* pp = reinterpret_cast<const float4*>(part + (static_cast<int64_t>(bh) * nch + n) * NBLK * PS);
+    const PV* pp = reinterpret_cast<const PV*>(part) + (static_cast<int64_t>(bh) * nch + n) * NBLK * (PS / 4);
 #pragma unroll
     for (int u = 0; u < NE; ++u)
 #pragma unroll
       for (int j = 0; j < NBLK; ++j) x[u][j] = pp[j * (PS / 4) + tid + NT * u];
   }
+  auto f4 = [](const PV& y) {
+    if constexpr (LP)
+      return make_float4(bf16_to_f32(y.x & 0xffffu), bf16_to_f32(y.x >> 16),
+                         bf16_to_f32(y.y & 0xffffu), bf16_to_f32(y.y >> 16));
+    else
+      return y;
+  };
   static_assert(R * R % NT == 0 && D * C % NT == 0 && 4 * C <= NT, "record and tokens split evenly");
   constexpr int NR = R * R / NT, NK = D * C / NT;
   float ra[NR], rg[NR], rm = 0.f, rd = 0.f;
@@ -565,9 +589,12 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
   }
 #pragma unroll
   for (int u = 0; u < NE; ++u) {
-    float4 s = x[u][0];
+    float4 s = f4(x[u][0]);
 #pragma unroll
-    for (int j = 1; j < NBLK; ++j) { s.x += x[u][j].x; s.y += x[u][j].y; s.z += x[u][j].z; s.w += x[u][j].w; }
+    for (int j = 1; j < NBLK; ++j) {
+      const float4 y = f4(x[u][j]);
+      s.x += y.x; s.y += y.y; s.z += y.z; s.w += y.w;
+    }
     const int e = 4 * (tid + NT * u);
     float* dst = e < R * R ? dT + e : dU + (e - R * R);
     *reinterpret_cast<float4*>(dst) = s;
