@@ -20,7 +20,7 @@
 // state norm drifts as a random walk (~1e-6 over 65536 tokens, against 1e-4 allowed)
 // and the state stays within ~3e-4 of the exact recurrence at that length.
 //
-// Workgroup = 10 (pass C) or 12 (pass A) waves for one (batch*head, segment):
+// Workgroup = 12 waves for one (batch*head, segment):
 //   waves 0-3 (consumers) each own a 32-column slab of the fp32 state, held in
 //     MFMA accumulators for the whole segment; columns evolve independently, so
 //     W, Z and the update need no cross-wave traffic.  With the readout every wave
@@ -28,7 +28,7 @@
 //   waves 4-5 (readout, pass C only) compute, from the stashes of chunk c-1, 64
 //     complete output rows each (transposing LDS loads, no reduction) while the
 //     consumers work on chunk c.
-//   the remaining 4 (pass C) or 8 (pass A) producer waves take chunks round-robin
+//   the remaining 6 (pass C) or 8 (pass A) producer waves take chunks round-robin
 //     (producer p owns chunks n = p mod NPW) and run each through NPW phases, one per
 //     iteration, ahead of the consumers: loads of k/v/q/delta; Gram matrix on MFMA and
 //     Cayley blocks; diagonal and off-diagonal 8x8 blocks of T~; the write of U, q
@@ -52,8 +52,8 @@
 // rounding) and the q rows (sum of squares over a DPP row), and form delta = 0.1
 // sigmoid(logit) * mask; the readout waves apply head RMSNorm, whose per-token mean
 // square spans both readout waves: each keeps its rows of chunk c in registers for one
-// iteration and stores them once both partial sums are in LDS.  With 8 producers the k/v
-// normalisation takes the otherwise empty phase.
+// iteration and stores them once both partial sums are in LDS.  The k/v normalisation
+// takes the phase that otherwise converts k, v to f16.
 #include <algorithm>
 #include <atomic>
 #include <type_traits>
@@ -69,15 +69,15 @@ constexpr int D = 128;
 constexpr int C = 16;           // tokens per chunk
 constexpr int R = 2 * C;        // rank rows per chunk
 constexpr int NCW = 4;          // consumer waves
-// Up to 3 waves per SIMD (at most 168 VGPRs each).  Pass C: 4 consumers (the state),
-// 2 readout waves and 4 producers; two readout waves of 64 rows each compute Z Q half
-// as often as four of 32 rows and measured fastest.  Pass A (no readout): 4 consumers
-// and 8 producers, whose latency-bound phases are then split over a deeper pipeline.
+// 3 waves per SIMD (at most 168 VGPRs each).  Pass C: 4 consumers (the state), 2 readout
+// waves and 6 producers; two readout waves of 64 rows each compute Z Q half as often as
+// four of 32 rows and measured fastest.  Pass A (no readout): 4 consumers and 8
+// producers, whose latency-bound phases are then split over a deeper pipeline.
 template <bool READOUT> struct Cfg {
-  static constexpr int NPW = READOUT ? 4 : 8;
+  static constexpr int NPW = READOUT ? 6 : 8;
   static constexpr int NRW = READOUT ? 2 : 0;  // readout waves (64 output rows each)
   static constexpr int NT = (NCW + NRW + NPW) * 64;
-  static constexpr int NSCR = READOUT ? 2 : 8;  // producer scratch slots
+  static constexpr int NSCR = READOUT ? 3 : 8;  // producer scratch slots (chunk n % 3 / producer)
 };
 // LDS bank model (measured on gfx950): 64 banks of 4 B; a 64-bit access (also the
 // transposing ds_read_b64_tr_b16 and each half of read2/write2_b64) is served in
@@ -113,7 +113,7 @@ __host__ __device__ constexpr int j_slot(int j) {  // bits 0,1,2,3,4 -> 2,3,0,1,
   return ((j & 1) << 2) | ((j & 2) << 2) | ((j & 4) >> 2) | ((j & 8) >> 2) | (j & 16);
 }
 
-// Scratch of a producer wave during phases 1-2 of one chunk (two slots, by chunk parity).
+// Scratch of a producer wave from the Gram matrix to the off-diagonal blocks of one chunk.
 struct PScratch {
   float gram[R * T_LD];         // Gram matrix G = U^T U (symmetric)
   float4 mcoef[C];              // (m00, m01, m10, m11) per token
@@ -388,19 +388,20 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   // Every wave runs iterations it = -NPW .. last with the same barriers.  Consumers
   // process chunk it in iteration it (and read out chunk it-1).  Producer p owns the
   // chunks n = p (mod NPW) and spends NPW iterations on each, one phase per iteration.
-  // With 4 producers:
-  //   it = n-4  phase 0: global loads of k, v, q, delta into registers
-  //   it = n-3  phase 1: Gram matrix (MFMA), Cayley blocks, diagonal blocks of T~
-  //   it = n-2  phase 2: off-diagonal blocks of T~ (kept in registers; the 16x16 block on MFMA)
-  //   it = n-1  phase 3: k, v, q rows -> tok[n % 3], T~ (hi + lo) -> tt[n & 1]
-  // with 8 the same steps run as load, f16 conversion (fused: k, v normalisation), Gram +
-  // Cayley blocks, diagonal blocks, three off-diagonal steps and the write (it = n-8 .. n-1).
-  // tok[n % 3] last held chunk n-3, whose readout ended in iteration n-2, and tt[n & 1]
-  // last held chunk n-2, so the write overwrites nothing still in use.  The scratch of
-  // a chunk is pscr[n & 1] with 4 producers (chunk n+2, the next one to use it, starts
-  // its Gram in iteration n-1, after chunk n's off-diagonal blocks) and the producer's
-  // own slot with 8.  Each phase is a short dependent chain, and NPW of them are in
-  // flight per workgroup, so their latency stays off the consumers' critical path.
+  // With 6 producers (pass C):
+  //   it = n-6  phase 0: global loads of k, v, q, delta into registers
+  //   it = n-5  phase 1: k, v to f16 (fused: normalised)
+  //   it = n-4  phase 2: Gram matrix (MFMA), Cayley blocks
+  //   it = n-3  phase 3: diagonal 8x8 blocks of T~, first off-diagonal step
+  //   it = n-2  phase 4: the other off-diagonal blocks (the 16x16 block on MFMA)
+  //   it = n-1  phase 5: k, v, q rows -> tok[n % 3], T~ (hi + lo) -> tt[n & 1]
+  // with 8 (pass A) the diagonal blocks and the three off-diagonal steps take a phase each
+  // (it = n-8 .. n-1).  tok[n % 3] last held chunk n-3, whose readout ended in iteration
+  // n-2, and tt[n & 1] last held chunk n-2, so the write overwrites nothing still in use.
+  // The scratch of a chunk is pscr[n % 3] with 6 producers (used in iterations n-4 .. n-2;
+  // chunk n+3, the next one to use it, starts its Gram in iteration n-1) and the
+  // producer's own slot with 8.  Each phase is a short dependent chain, and NPW of them
+  // are in flight per workgroup, so their latency stays off the consumers' critical path.
   struct Regs {
     uint4 kv[8];  // k/v in Gram-operand order: rho = l32, features 16ks + 8g + 0..7
     uint4 q[4];   // q: e = lane + 64m -> token e>>4, features 8*(e&15) + 0..7
@@ -441,10 +442,10 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   };
 
   // zero the tokens past the end; fused mode: normalise the k, v rows (to f16)
-  auto p_prep = [&](Regs& r, int n, PScratch& P) {
+  auto p_prep = [&](Regs& r, int n) {
     const int t0 = (chunk0 + n) * C;
-    if constexpr (!FUSED && NPW == 8) {  // the 8-phase schedule converts here, a phase
-#pragma unroll                          // before the Gram matrix
+    if constexpr (!FUSED) {  // a phase before the Gram matrix
+#pragma unroll
       for (int ks = 0; ks < 8; ++ks) r.kv[ks] = to_f16x8<IO>(r.kv[ks]);
     }
     if (t0 + C > a.T) {  // last, partial chunk
@@ -471,13 +472,16 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
         const typename MR::v8 x = __builtin_bit_cast(typename MR::v8, r.kv[ks]);
         racc = MR::mma32(x, x, racc);
       }
+      // lane (l32, g) holds G[8(r/4) + 4g + r%4][l32]: the diagonal entry G[l32][l32] is
+      // element r = 4(l32 >> 3) + (l32 & 3) of the half g = (l32 >> 2) & 1, and the other
+      // half takes it from lane ^ 32
+      const int ri = 4 * (l32 >> 3) + (l32 & 3);
+      float dg = racc[0];
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4)
-        *reinterpret_cast<float4*>(&P.gram[l32 * T_LD + 8 * q4 + 4 * g]) =
-            make_float4(racc[4 * q4], racc[4 * q4 + 1], racc[4 * q4 + 2], racc[4 * q4 + 3]);
-      wave_sync();
-      const float inv = rsqrtf(fmaxf(P.gram[l32 * T_LD + l32], 1e-24f));  // 1 / max(|row|, 1e-12)
-      wave_sync();  // every lane has read its diagonal entry before the Gram below lands
+      for (int r2 = 1; r2 < 16; ++r2) dg = ri == r2 ? racc[r2] : dg;
+      const float dx = __shfl_xor(dg, 32);
+      const float nn = g == ((l32 >> 2) & 1) ? dg : dx;
+      const float inv = rsqrtf(fmaxf(nn, 1e-24f));  // 1 / max(|row|, 1e-12)
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) r.kv[ks] = to_f16x8_scaled<IO>(r.kv[ks], inv);
     }
@@ -487,10 +491,6 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   // factor I + U T~ U^T stays exactly consistent with its Gram matrix; Cayley blocks
   auto p_gram = [&](Regs& r, int n, PScratch& P) {
     const int t0 = (chunk0 + n) * C;
-    if constexpr (!FUSED && NPW != 8) {
-#pragma unroll
-      for (int ks = 0; ks < 8; ++ks) r.kv[ks] = to_f16x8<IO>(r.kv[ks]);
-    }
     f32x16 gacc = {};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
@@ -550,7 +550,9 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   // diagonal 8x8 blocks of T~ (4 tokens) by forward substitution, lane = (block gb, column c)
   auto p_diag = [&](PScratch& P) {
     if (lane < 32) {
-      const int gb = lane >> 3, c = lane & 7;
+      int ln = lane;
+      asm volatile("" : "+v"(ln));  // lane constants recomputed here, not held across the loop
+      const int gb = ln >> 3, c = ln & 7;
       float gblk[8][8];
 #pragma unroll
       for (int rr = 0; rr < 8; ++rr) {
@@ -634,17 +636,24 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   };
 
   // the write: U and q rows, T~ (f16 hi + lo) for the consumers
-  auto p_write = [&](Regs& r, int n, const float* tv, const float* cv) {
-    E* tb = sm.tok[n % 3];
-    if constexpr (FUSED && READOUT) {
-      // q rows normalised here (the lightest phase): token (lane + 64m) >> 4 spans 16
-      // consecutive lanes
+  // q rows to f16; fused mode: normalised (token (lane + 64m) >> 4 spans 16 consecutive
+  // lanes, one DPP row)
+  auto p_qprep = [&](Regs& r) {
+    if constexpr (READOUT) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        const float s2 = row16_sum(sumsq8<IO>(r.q[m]));
-        r.q[m] = to_f16x8_scaled<IO>(r.q[m], rsqrtf(fmaxf(s2, 1e-24f)));
+        if constexpr (FUSED) {
+          const float s2 = row16_sum(sumsq8<IO>(r.q[m]));
+          r.q[m] = to_f16x8_scaled<IO>(r.q[m], rsqrtf(fmaxf(s2, 1e-24f)));
+        } else {
+          r.q[m] = to_f16x8<IO>(r.q[m]);
+        }
       }
     }
+  };
+
+  auto p_write = [&](Regs& r, int n, const float* tv, const float* cv) {
+    E* tb = sm.tok[n % 3];
     // Each 16-byte piece as two ds_write_b64: rows are 8-byte aligned (264-byte pitch), and a
     // ds_write_b128 of this pattern measured 5x the LDS cycles of the two 8-byte writes.
     E* tdst = tb + rho_slot(l32) * U_LD;
@@ -659,8 +668,14 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const int e = lane + 64 * m;
-        *reinterpret_cast<uint4*>(tb + Q_OFF + (e >> 4) * Q_LD + 8 * (e & 15)) =
-            FUSED ? r.q[m] : to_f16x8<IO>(r.q[m]);  // fused: already normalised f16
+        uint4 qh;
+        if constexpr (FUSED) {
+          const float s2 = row16_sum(sumsq8<IO>(r.q[m]));
+          qh = to_f16x8_scaled<IO>(r.q[m], rsqrtf(fmaxf(s2, 1e-24f)));
+        } else {
+          qh = to_f16x8<IO>(r.q[m]);
+        }
+        *reinterpret_cast<uint4*>(tb + Q_OFF + (e >> 4) * Q_LD + 8 * (e & 15)) = qh;
       }
     }
     // T~ as f16 hi + lo.  Lanes pair up (lane, lane ^ 1) on adjacent columns: the even
@@ -669,6 +684,10 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
     const bool odd = lane & 1;
     uint32_t* const tw = reinterpret_cast<uint32_t*>(odd ? sm.ttl[n & 1] : sm.tth[n & 1]);
     auto put_pair = [&](float x, int row, int col_even) {
+      // hi is the f16 rounding of the fp32 value x: the empty asm keeps the compiler from
+      // folding the conversion into the FMA that produced x (one f16 rounding of the exact
+      // product, which differs from this one in rare ties)
+      asm("" : "+v"(x));
       const E hpart = static_cast<E>(x);
       const E lpart = static_cast<E>(x - static_cast<float>(hpart));
       const uint32_t hb = __builtin_bit_cast(uint16_t, hpart), lb = __builtin_bit_cast(uint16_t, lpart);
@@ -694,47 +713,59 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
     const int p = wave - NCW - NRW;
     Regs r;
     float tv[6], cv[4];
-    for (int it = -NPW; it <= last; ++it) {
-      const int phase = (it - p + 2 * NPW) & (NPW - 1);
-      const int n = it + NPW - phase;
-      if (n >= 0 && n < nch) {  // uniform across the wave
-        PScratch& P = sm.pscr[NPW == 8 ? p : (n & 1)];
-        if constexpr (NPW == 4) {
-          // The two long phases run at a raised issue priority: a producer in one of them
-          // sets the iteration period (it shares its SIMD with a consumer and, on SIMDs 0
-          // and 1, a readout wave, both of which have slack).  Measured at OP: 174.6 ->
-          // 165.8 us per scan; all four phases raised, or phase 2 with them, is slower.
-          if (phase == 1 || phase == 3) __builtin_amdgcn_s_setprio(2);
-          else __builtin_amdgcn_s_setprio(0);
-          if (phase == 0) {
-            p_load(r, n);
-          } else if (phase == 1) {
-            p_prep(r, n, P);
-            p_gram(r, n, P);
-            wave_sync();
-            p_diag(P);
-          } else if (phase == 2) {
-            od_1a(P, tv);
-            wave_sync();
-            od_1b(P, tv);
-            wave_sync();
-            od_c(P, cv);
-          } else {
-            p_write(r, n, tv, cv);
-          }
-        } else {  // 8 phases: the f16 conversion (fused: the k, v normalisation) has its own
-          if (phase == 0) p_load(r, n);
-          else if (phase == 1) p_prep(r, n, P);
-          else if (phase == 2) p_gram(r, n, P);
-          else if (phase == 3) p_diag(P);
-          else if (phase == 4) od_1a(P, tv);
-          else if (phase == 5) od_1b(P, tv);
-          else if (phase == 6) od_c(P, cv);
-          else p_write(r, n, tv, cv);
-        }
+    // Chunk-major: producer p runs the phases of its chunks n = p, p + NPW, ... as
+    // straight-line code, phase k of chunk n in iteration n - NPW + k; bare barriers
+    // before its first chunk and after its last keep the count at one per iteration.
+    int it = -NPW;
+    for (; it < p - NPW; ++it) lds_barrier();  // (A)
+    for (int n = p; n < nch; n += NPW) {
+      PScratch& P = sm.pscr[NPW == 8 ? p : n % 3];
+      if constexpr (NPW == 6) {
+        // The diagonal-block and write phases run at a raised issue priority (they share
+        // SIMDs with consumer and readout waves, which have slack).  Measured at OP against
+        // no raised phase, and against raising the Gram phase or the 16x16 block's phase
+        // as well: 1-3 % faster.
+        p_load(r, n);
+        lds_barrier();  // (A)
+        p_prep(r, n);
+        lds_barrier();  // (A)
+        p_gram(r, n, P);
+        lds_barrier();  // (A)
+        __builtin_amdgcn_s_setprio(2);
+        p_diag(P);
+        wave_sync();
+        od_1a(P, tv);
+        __builtin_amdgcn_s_setprio(0);
+        lds_barrier();  // (A)
+        od_1b(P, tv);
+        wave_sync();
+        od_c(P, cv);
+        lds_barrier();  // (A)
+        __builtin_amdgcn_s_setprio(2);
+        p_write(r, n, tv, cv);
+        __builtin_amdgcn_s_setprio(0);
+        lds_barrier();  // (A)
+      } else {
+        p_load(r, n);
+        lds_barrier();  // (A)
+        p_prep(r, n);
+        lds_barrier();  // (A)
+        p_gram(r, n, P);
+        lds_barrier();  // (A)
+        p_diag(P);
+        lds_barrier();  // (A)
+        od_1a(P, tv);
+        lds_barrier();  // (A)
+        od_1b(P, tv);
+        lds_barrier();  // (A)
+        od_c(P, cv);
+        lds_barrier();  // (A)
+        p_write(r, n, tv, cv);
+        lds_barrier();  // (A)
       }
-      lds_barrier();  // (A)
+      it = n;
     }
+    for (; it <= last; ++it) lds_barrier();  // (A)
     return;
   }
 
@@ -1199,7 +1230,7 @@ __global__ __launch_bounds__(CARRY_NT) void sssd_carry_kernel(const float* psi0,
 // ------------------------------------------------------------------ host side
 namespace {
 
-constexpr int kTargetWorkgroups = 256;  // one 5-wave workgroup per CU (LDS-limited)
+constexpr int kTargetWorkgroups = 256;  // one workgroup per CU (LDS-limited)
 
 struct Plan {
   int nchunks, seg_chunks, nseg;
