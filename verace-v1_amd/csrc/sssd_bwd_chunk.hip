@@ -257,8 +257,9 @@ __device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B
 // Tokens with a non-finite Cayley factor (vmi::cayley_guarded) get M = 0 and their U columns
 // zeroed, G is recomputed, and their bits are left in *badm.
 template <int D>
-__device__ void chunk_prep(float* U, const float* dl, float* G, float* Mb, float* L,
-                           float* A, int* badm, int tid, int wave, int lane) {
+__device__ __forceinline__ void chunk_prep(float* U, const float* dl, float* G, float* Mb,
+                                           float* L, float* A, int* badm, int tid, int wave,
+                                           int lane, int solver) {
   lgemm<R, R, D, true, false, kStore>(U, L32, U, L32, G, R, wave, lane);
   __syncthreads();
   bool ok = true;
@@ -286,21 +287,51 @@ __device__ void chunk_prep(float* U, const float* dl, float* G, float* Mb, float
     float x = 0.f;
     if (i < t) x = Mb[4 * t + 2 * a] * G[(2 * t) * R + 2 * i + b] + Mb[4 * t + 2 * a + 1] * G[(2 * t + 1) * R + 2 * i + b];
     L[e] = x;
-    A[e] = r == c ? 1.f : 0.f;
   }
   __syncthreads();
-  // A = I + L A, block row t from the rows of the earlier blocks
-  for (int t = 1; t < C; ++t) {
-    if (tid < 2 * R) {
-      const int r = 2 * t + (tid >> 5), c = tid & 31;
-      if ((c >> 1) < t) {
-        float x = 0.f;
-        for (int m = 2 * (c >> 1); m < 2 * t; ++m) x = fmaf(L[r * R + m], A[m * R + c], x);
-        A[r * R + c] = x;
+  // A = I + L A, block row t from the rows of the earlier blocks, in one wave without barriers:
+  // lane (a, c) = (lane >> 5, lane & 31) holds column c of A in registers, computes row 2t + a
+  // of it (the two rows of a block do not depend on each other: L is zero inside the diagonal
+  // blocks) from the row of L (16-byte reads, the same address across the half-wave) and takes
+  // the other row from lane ^ 32 (v_permlane32_swap).  Column c is zero above its own block, so
+  // every lane sums from m = 0 in the same order (the extra terms add exact zeros to a zero sum).
+  // The solving wave rotates with the chunk, so the workgroups on a CU spread their solves.
+  if (wave == (solver & 3)) {
+    const int c = lane & 31, a = lane >> 5;
+    float col[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) col[r] = r == c ? 1.f : 0.f;
+#pragma unroll
+    for (int t = 1; t < C; ++t) {
+      const float* lr = L + (2 * t + a) * R;
+      float x = 0.f;
+#pragma unroll
+      for (int m = 0; m + 4 <= 2 * t; m += 4) {
+        const float4 l4 = *reinterpret_cast<const float4*>(lr + m);
+        x = fmaf(l4.x, col[m], x);
+        x = fmaf(l4.y, col[m + 1], x);
+        x = fmaf(l4.z, col[m + 2], x);
+        x = fmaf(l4.w, col[m + 3], x);
       }
+      if ((2 * t) % 4 != 0) {
+        const float2 l2 = *reinterpret_cast<const float2*>(lr + 2 * t - 2);
+        x = fmaf(l2.x, col[2 * t - 2], x);
+        x = fmaf(l2.y, col[2 * t - 1], x);
+      }
+      const float mine = (c >> 1) < t ? x : (a ? col[2 * t + 1] : col[2 * t]);
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mine), __float_as_uint(mine),
+                                                       false, false);
+      // lanes 32-63 receive lanes 0-31 in the first result, lanes 0-31 lanes 32-63 in the second
+      const float other = __uint_as_float(a ? sw[0] : sw[1]);
+      col[2 * t] = a ? other : mine;
+      col[2 * t + 1] = a ? mine : other;
     }
-    __syncthreads();
+    if (a == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) A[r * R + c] = col[r];
+    }
   }
+  __syncthreads();
 }
 
 // ---------------------------------------------------------------- T~ of every chunk
@@ -310,7 +341,8 @@ __global__ __launch_bounds__(NT) void bwdc_prep_kernel(const IO* __restrict__ k,
                                                        const void* __restrict__ delta,
                                                        int delta_dtype, float* __restrict__ tt,
                                                        int T, int H) {
-  __shared__ float U[D * L32], G[R * R], L[R * R], A[R * R], Mb[4 * C], dl[C];
+  __shared__ float U[D * L32], G[R * R], A[R * R], Mb[4 * C], dl[C];
+  __shared__ __attribute__((aligned(16))) float L[R * R];  // rows read 16 bytes at a time
   __shared__ int badm;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, hd = bh % H;
@@ -332,7 +364,7 @@ __global__ __launch_bounds__(NT) void bwdc_prep_kernel(const IO* __restrict__ k,
     dl[tid] = tg < T ? load_scalar(delta, delta_dtype, (static_cast<int64_t>(b) * T + tg) * H + hd) : 0.f;
   }
   __syncthreads();
-  chunk_prep<D>(U, dl, G, Mb, L, A, &badm, tid, wave, lane);
+  chunk_prep<D>(U, dl, G, Mb, L, A, &badm, tid, wave, lane, n + bh);
   float* o = tt + (static_cast<int64_t>(bh) * nch + n) * REC;
   for (int e = tid; e < R * R; e += NT) {  // T~ = A blockdiag(M), then A, G, M
     const int r = e / R, c = e % R, s = c >> 1, cb = c & 1;
