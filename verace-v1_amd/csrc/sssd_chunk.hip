@@ -396,8 +396,10 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
   //   it = n-2  phase 4: the other off-diagonal blocks (the 16x16 block on MFMA)
   //   it = n-1  phase 5: k, v, q rows -> tok[n % 3], T~ (hi + lo) -> tt[n & 1]
   // with 8 (pass A) the diagonal blocks and the three off-diagonal steps take a phase each
-  // (it = n-8 .. n-1).  tok[n % 3] last held chunk n-3, whose readout ended in iteration
-  // n-2, and tt[n & 1] last held chunk n-2, so the write overwrites nothing still in use.
+  // (it = n-8 .. n-1), and the U rows go out with the 16x16 block (it = n-2: no readout
+  // waves hold tok[n % 3] then).  tok[n % 3] last held chunk n-3, whose readout ended in
+  // iteration n-2, and tt[n & 1] last held chunk n-2, so the write overwrites nothing still
+  // in use.
   // The scratch of a chunk is pscr[n % 3] with 6 producers (used in iterations n-4 .. n-2;
   // chunk n+3, the next one to use it, starts its Gram in iteration n-1) and the
   // producer's own slot with 8.  Each phase is a short dependent chain, and NPW of them
@@ -652,7 +654,8 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
     }
   };
 
-  auto p_write = [&](Regs& r, int n, const float* tv, const float* cv) {
+  // the write: U and q rows (p_write_rows), T~ as f16 hi + lo (p_write_tt) for the consumers
+  auto p_write_rows = [&](Regs& r, int n) {
     E* tb = sm.tok[n % 3];
     // Each 16-byte piece as two ds_write_b64: rows are 8-byte aligned (264-byte pitch), and a
     // ds_write_b128 of this pattern measured 5x the LDS cycles of the two 8-byte writes.
@@ -678,6 +681,8 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
         *reinterpret_cast<uint4*>(tb + Q_OFF + (e >> 4) * Q_LD + 8 * (e & 15)) = qh;
       }
     }
+  };
+  auto p_write_tt = [&](int n, const float* tv, const float* cv) {
     // T~ as f16 hi + lo.  Lanes pair up (lane, lane ^ 1) on adjacent columns: the even
     // lane writes the two hi parts, the odd lane the two lo parts, as one 32-bit store
     // each (DPP quad_perm(1, 0, 3, 2) swaps the parts between the two lanes).
@@ -704,6 +709,10 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
     // T~[16:32, 0:16]: rows 16 + 4 g4 + r of column l16
 #pragma unroll
     for (int r = 0; r < 4; ++r) put_pair(cv[r], 16 + 4 * g4 + r, l16 & ~1);
+  };
+  auto p_write = [&](Regs& r, int n, const float* tv, const float* cv) {
+    p_write_rows(r, n);
+    p_write_tt(n, tv, cv);
   };
 
   // Every iteration ends with one workgroup barrier (A).
@@ -759,8 +768,11 @@ __global__ __launch_bounds__(Cfg<READOUT>::NT) void sssd_chunk_kernel(Args a) {
         od_1b(P, tv);
         lds_barrier();  // (A)
         od_c(P, cv);
+        // no readout waves in this pass: tok[n % 3] (last used by the consumers of chunk n-3 in
+        // iteration n-3) is free a phase early, which takes the U rows off the T~ write
+        p_write_rows(r, n);
         lds_barrier();  // (A)
-        p_write(r, n, tv, cv);
+        p_write_tt(n, tv, cv);
         lds_barrier();  // (A)
       }
       it = n;
