@@ -339,7 +339,6 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
   for (int m = 0; m < RPT; ++m) {
     kr[m] = io<IO>::load(kb, rg + NRG * m);
     vr[m] = io<IO>::load(vb, rg + NRG * m);
-    if constexpr (FUSED) vr[m] = vr[m] / (1.f + expf(-vr[m]));  // silu
   }
   float g;
   float qq = 0.f;  // fused: this thread's share of |q|^2 (entries tid and tid + 512)
@@ -378,6 +377,10 @@ __global__ __launch_bounds__(512) void cham_step1024_kernel(
         tr[m - RR] = ld_stream4(sr + off0 + m * NRG * H);
         ti[m - RR] = ld_stream4(si + off0 + m * NRG * H);
       }
+    }
+    if constexpr (FUSED) {  // silu, after the second batch of state loads is in flight
+#pragma unroll
+      for (int m = 0; m < RPT; ++m) vr[m] = vr[m] / (1.f + expf(-vr[m]));
     }
 #pragma unroll
     for (int m = 0; m < RR; ++m) acc(kr[m], vr[m], xr[m], xi[m]);
