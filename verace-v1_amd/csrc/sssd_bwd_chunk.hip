@@ -149,10 +149,11 @@ constexpr int L32 = 37;  // 32-wide matrices
 // LP: operands rounded to bf16 (v_mfma_f32_16x16x16_bf16, lane (m, kq) supplies
 // A[m][4 kq .. 4 kq + 3] of a 16-wide k step), fp32 accumulation; for the bf16 / fp16
 // inputs' per-chunk gradient products only.
+// With B2, the B operand is B + B2 (same layout and stride), summed as it is read.
 template <int M, int N, int K, bool TA, bool TB, int MODE, int W0 = 0, int NW = 4,
-          bool LP = false>
+          bool LP = false, bool SUMB = false>
 __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, int ldb, float* Cm,
-                                      int ldc, int wave, int lane) {
+                                      int ldc, int wave, int lane, const float* B2 = nullptr) {
   constexpr int TN = N / 16, NTILE = (M / 16) * TN;
   if (wave < W0 || wave >= W0 + NW) return;
   const int l16 = lane & 15, kq = lane >> 4;
@@ -179,12 +180,14 @@ __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, i
     for (int k0 = 0; k0 < K; k0 += 8) {
       const int k = k0 + kq;
       const float a0 = TA ? A[k * lda + am] : A[am * lda + k];
-      const float b0 = TB ? B[bn * ldb + k] : B[k * ldb + bn];
+      float b0 = TB ? B[bn * ldb + k] : B[k * ldb + bn];
+      if constexpr (SUMB) b0 += TB ? B2[bn * ldb + k] : B2[k * ldb + bn];
       acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc0, 0, 0, 0);
       if (k0 + 4 < K) {
         const int k1 = k + 4;
         const float a1 = TA ? A[k1 * lda + am] : A[am * lda + k1];
-        const float b1 = TB ? B[bn * ldb + k1] : B[k1 * ldb + bn];
+        float b1 = TB ? B[bn * ldb + k1] : B[k1 * ldb + bn];
+        if constexpr (SUMB) b1 += TB ? B2[bn * ldb + k1] : B2[k1 * ldb + bn];
         acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc1, 0, 0, 0);
       }
     }
@@ -400,7 +403,7 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
   // row strides: L32 for the 32-wide (rank index) matrices, L16 for the 16-wide ones
   __shared__ float U[D * L32], Tt[R * L32], Gm[R * L32], Qb[CB * L16], dO[D * L16];
   __shared__ float Ps[D * L16], Lm[D * L16];
-  __shared__ float S1[R * L16], Wm[R * L16], Wt[R * L16], Zm[R * L16], Xm[R * L16], dXm[R * L16],
+  __shared__ float S1[R * L16], S1b[R * L16], Wm[R * L16], Wt[R * L16], Zm[R * L16], Xm[R * L16], dXm[R * L16],
       dZm[R * L16], dWm[R * L16], QD[2][CB * L16];
   __shared__ float dTp[R * L32], dQm[CB * L16];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -482,16 +485,22 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
   // waves.  W = U^T Psi_s is formed as S1 + G Wm (U^T Psi_s = U^T Psi_e + U^T U T~^T S1), so it
   // needs no product over the state rows after the reconstruction.
   for (int n = nch - 1; n >= 0; --n) {
-    // (1) S1 = U^T Psi_e (waves 0-1); dX = mask o (U^T dO) (waves 2-3); dZ = U^T Lam_e (4-5)
-    lgemm<R, CB, D, true, false, kStore, 0, 2>(U, L32, Ps, L16, S1, L16, wave, lane);
+    // (1) S1 = U^T Psi_e as two halves of the state rows, S1 (waves 0-1) + S1b (waves 6-7);
+    //     dX = mask o (U^T dO) (waves 2-3); dZ = U^T Lam_e (4-5)
+    lgemm<R, CB, D / 2, true, false, kStore, 0, 2>(U, L32, Ps, L16, S1, L16, wave, lane);
+    lgemm<R, CB, D / 2, true, false, kStore, 6, 2>(U + (D / 2) * L32, L32, Ps + (D / 2) * L16, L16,
+                                                   S1b, L16, wave, lane);
     lgemm<R, C, D, true, false, kMaskStore, 2, 2, LP>(U, L32, dO, L16, dXm, L16, wave, lane);
     lgemm<R, CB, D, true, false, kStore, 4, 2, LP>(U, L32, Lm, L16, dZm, L16, wave, lane);
     lds_barrier();
     // (2) Wm = T~^T S1 (waves 0-1); dZ += dX Q^T (waves 4-5, the tiles they stored);
     //     W starts as S1 (every thread one element)
-    lgemm<R, CB, R, true, false, kStore, 0, 2>(Tt, L32, S1, L16, Wm, L16, wave, lane);
+    lgemm<R, CB, R, true, false, kStore, 0, 2, false, true>(Tt, L32, S1, L16, Wm, L16, wave, lane, S1b);
     lgemm<R, CB, C, false, true, kAdd, 4, 2, LP>(dXm, L16, Qb, L16, dZm, L16, wave, lane);
-    for (int e = tid; e < R * CB; e += NTC) Wt[(e / CB) * L16 + e % CB] = S1[(e / CB) * L16 + e % CB];
+    for (int e = tid; e < R * CB; e += NTC) {
+      const int o = (e / CB) * L16 + e % CB;
+      Wt[o] = S1[o] + S1b[o];
+    }
     lds_barrier();
     // (3) Psi_s = Psi_e + U Wm (8 waves); W += G Wm (waves 0-1, after their Psi tile);
     //     dW = T~^T dZ (waves 2-3)
