@@ -47,6 +47,13 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ short to_bf16(float x) {  // round to nearest even
   return __builtin_bit_cast(short, static_cast<__bf16>(x));
 }
+// two values as one word of bf16 (v_cvt_pk_bf16_f32: round to nearest even, the same bits as
+// f32_to_bf16 for every non-NaN value, without its branch per element)
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
 
 enum { kStore = 0, kAdd = 1, kMaskStore = 2 };
 
@@ -93,8 +100,9 @@ __device__ __forceinline__ void store_row(T* p, const float (&x)[N]) {
     for (int j = 0; j < N; j += 2) {
       uint32_t lo, hi;
       if constexpr (std::is_same<T, bf16_t>::value) {
-        lo = f32_to_bf16(x[j]);
-        hi = f32_to_bf16(x[j + 1]);
+        const uint32_t w = pack_bf16x2(x[j], x[j + 1]);
+        lo = w & 0xffffu;
+        hi = w >> 16;
       } else {
         lo = __builtin_bit_cast(uint16_t, static_cast<f16_t>(x[j]));
         hi = __builtin_bit_cast(uint16_t, static_cast<f16_t>(x[j + 1]));
@@ -211,8 +219,7 @@ __device__ __forceinline__ void put4(float* p, float a, float b, float c, float 
   *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
 }
 __device__ __forceinline__ void put4(uint16_t* p, float a, float b, float c, float d) {
-  *reinterpret_cast<uint2*>(p) = make_uint2(f32_to_bf16(a) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16),
-                                            f32_to_bf16(c) | (static_cast<uint32_t>(f32_to_bf16(d)) << 16));
+  *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(a, b), pack_bf16x2(c, d));
 }
 
 // dst (global) = (A1 B1^T + A2 B2^T + A3 B3^T)^T, 32 x M with row stride M, with A_i [M][16]
