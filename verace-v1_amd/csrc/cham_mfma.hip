@@ -659,7 +659,10 @@ template <> __device__ __forceinline__ void unpack8<f16_t>(uint4 r, float* f) {
   }
 }
 template <typename IO> __device__ __forceinline__ uint16_t pack_io(float x);
-template <> __device__ __forceinline__ uint16_t pack_io<bf16_t>(float x) { return f32_to_bf16(x); }
+template <> __device__ __forceinline__ uint16_t pack_io<bf16_t>(float x) {
+  // v_cvt_pk_bf16_f32: round to nearest even like f32_to_bf16, without its branch
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+}
 template <> __device__ __forceinline__ uint16_t pack_io<f16_t>(float x) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
 }
