@@ -55,7 +55,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-enum { kStore = 0, kAdd = 1, kMaskStore = 2 };
+enum { kStore = 0, kAdd = 1, kMaskStore = 2, kAddFrom = 3 };  // kAddFrom: C = Cs + A B
 
 // N consecutive elements of a row as raw 32-bit words (one 8- or 16-byte load, two for 8
 // fp32), and element j of them as a float.  The row must be aligned to its byte size.
@@ -161,7 +161,8 @@ constexpr int L32 = 37;  // 32-wide matrices
 template <int M, int N, int K, bool TA, bool TB, int MODE, int W0 = 0, int NW = 4,
           bool LP = false, bool SUMB = false>
 __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, int ldb, float* Cm,
-                                      int ldc, int wave, int lane, const float* B2 = nullptr) {
+                                      int ldc, int wave, int lane, const float* B2 = nullptr,
+                                      const float* Cs = nullptr) {
   constexpr int TN = N / 16, NTILE = (M / 16) * TN;
   if (wave < W0 || wave >= W0 + NW) return;
   const int l16 = lane & 15, kq = lane >> 4;
@@ -207,6 +208,7 @@ __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, i
       float* p = Cm + row * ldc + col;
       if (MODE == kStore) *p = x;
       else if (MODE == kAdd) *p += x;
+      else if (MODE == kAddFrom) *p = Cs[row * ldc + col] + x;
       else *p = (row >> 1) <= col ? x : 0.f;
     }
   }
@@ -409,7 +411,7 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
   PT* __restrict__ part = static_cast<PT*>(part_v);
   // row strides: L32 for the 32-wide (rank index) matrices, L16 for the 16-wide ones
   __shared__ float U[D * L32], Tt[R * L32], Gm[R * L32], Qb[CB * L16], dO[D * L16];
-  __shared__ float Ps[D * L16], Lm[D * L16];
+  __shared__ float Ps[D * L16], Lmb[2][D * L16];  // Lam: the chunk's Lam_e and the next one's
   __shared__ float S1[R * L16], S1b[R * L16], Wm[R * L16], Wt[R * L16], Zm[R * L16], Xm[R * L16], dXm[R * L16],
       dZm[R * L16], dWm[R * L16], QD[2][CB * L16];
   __shared__ float dTp[R * L32], dQm[CB * L16];
@@ -422,7 +424,7 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     const int i = e / CB, jj = e % CB;
     const int64_t o = bh * DD + static_cast<int64_t>(i) * D + blk * CB + jj;
     Ps[i * L16 + jj] = psi_T[o];
-    Lm[i * L16 + jj] = dpsi_T ? dpsi_T[o] : 0.f;
+    Lmb[0][i * L16 + jj] = dpsi_T ? dpsi_T[o] : 0.f;
   }
   // chunk n's inputs: registers first (the next chunk's arrive while this one runs), loaded by
   // waves 4-7, which are idle in the phase that issues the loads.  Thread (t = tid / 16, j0 = EU (tid % 16)) holds elements
@@ -491,7 +493,10 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
   // Per chunk, seven phases between LDS barriers, independent products of a phase on disjoint
   // waves.  W = U^T Psi_s is formed as S1 + G Wm (U^T Psi_s = U^T Psi_e + U^T U T~^T S1), so it
   // needs no product over the state rows after the reconstruction.
+  int lc = 0;  // Lmb[lc] holds Lam_e of chunk n
   for (int n = nch - 1; n >= 0; --n) {
+    const float* Lm = Lmb[lc];
+    float* Ln = Lmb[lc ^ 1];
     // (1) S1 = U^T Psi_e as two halves of the state rows, S1 (waves 0-1) + S1b (waves 6-7);
     //     dX = mask o (U^T dO) (waves 2-3); dZ = U^T Lam_e (4-5)
     lgemm<R, CB, D / 2, true, false, kStore, 0, 2>(U, L32, Ps, L16, S1, L16, wave, lane);
@@ -544,10 +549,11 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
         if (tg < T) io<IO>::store(dq, tok(tg) * D + blk * CB + jj, dQm[e] + QD[0][e] + QD[1][e]);
       }
     }
-    lds_barrier();
-    // (7) Lam_s = Lam_e + dO Q^T + U dW (8 waves, one tile each, both terms)
-    lgemm<D, CB, C, false, true, kAdd, 0, NWC>(dO, L16, Qb, L16, Lm, L16, wave, lane);
-    lgemm<D, CB, R, false, false, kAdd, 0, NWC>(U, L32, dWm, L16, Lm, L16, wave, lane);
+    // (7, same phase) Lam_s = Lam_e + dO Q^T + U dW into the other buffer (8 waves, one tile
+    // each, both terms): the dU partial above still reads Lam_e
+    lgemm<D, CB, C, false, true, kAddFrom, 0, NWC>(dO, L16, Qb, L16, Ln, L16, wave, lane, nullptr, Lm);
+    lgemm<D, CB, R, false, false, kAdd, 0, NWC>(U, L32, dWm, L16, Ln, L16, wave, lane);
+    lc ^= 1;
     lds_barrier();
     if (n > 0) commit(n - 1);
     lds_barrier();
@@ -555,7 +561,7 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
   if (dpsi0) {
     for (int e = tid; e < D * CB; e += NTC) {
       const int i = e / CB, jj = e % CB;
-      dpsi0[bh * DD + static_cast<int64_t>(i) * D + blk * CB + jj] = Lm[i * L16 + jj];
+      dpsi0[bh * DD + static_cast<int64_t>(i) * D + blk * CB + jj] = Lmb[lc][i * L16 + jj];
     }
   }
 }
