@@ -174,13 +174,16 @@ __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, i
       static_assert(K % 16 == 0, "bf16 steps of 16");
 #pragma unroll 4
       for (int k0 = 0; k0 < K; k0 += 16) {
-        s16x4 a, b;
+        float af[4], bf[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int k = k0 + 4 * kq + i;
-          a[i] = to_bf16(TA ? A[k * lda + am] : A[am * lda + k]);
-          b[i] = to_bf16(TB ? B[bn * ldb + k] : B[k * ldb + bn]);
+          af[i] = TA ? A[k * lda + am] : A[am * lda + k];
+          bf[i] = TB ? B[bn * ldb + k] : B[k * ldb + bn];
         }
+        // two elements per v_cvt_pk_bf16_f32
+        const s16x4 a = __builtin_bit_cast(s16x4, make_uint2(pack_bf16x2(af[0], af[1]), pack_bf16x2(af[2], af[3])));
+        const s16x4 b = __builtin_bit_cast(s16x4, make_uint2(pack_bf16x2(bf[0], bf[1]), pack_bf16x2(bf[2], bf[3])));
         if ((k0 >> 4) & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc1, 0, 0, 0);
         else acc0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc0, 0, 0, 0);
       }
@@ -242,12 +245,10 @@ __device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B
 #pragma unroll
     for (int u = 0; u < 3; ++u) {
       if constexpr (LP) {
-        s16x4 a, b;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          a[i] = to_bf16(As[u][am * L16 + 4 * kq + i]);
-          b[i] = to_bf16(Bs[u][bn * L16 + 4 * kq + i]);
-        }
+        const float* pa = As[u] + am * L16 + 4 * kq;
+        const float* pb = Bs[u] + bn * L16 + 4 * kq;
+        const s16x4 a = __builtin_bit_cast(s16x4, make_uint2(pack_bf16x2(pa[0], pa[1]), pack_bf16x2(pa[2], pa[3])));
+        const s16x4 b = __builtin_bit_cast(s16x4, make_uint2(pack_bf16x2(pb[0], pb[1]), pack_bf16x2(pb[2], pb[3])));
         if (u & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc1, 0, 0, 0);
         else acc0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc0, 0, 0, 0);
       } else {
@@ -568,33 +569,54 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
 
 // ---------------------------------------------------------------- per chunk: dT~ -> dk, dv, ddelta
 template <typename IO, int D>
-__global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void bwdc_reduce_kernel(
     const IO* __restrict__ k, const IO* __restrict__ v, const void* __restrict__ delta,
     int delta_dtype, const float* __restrict__ tt, const void* __restrict__ part,
     IO* __restrict__ dk, IO* __restrict__ dv, void* __restrict__ ddelta, int T, int H) {
   constexpr int PS = PartC<D>::size;
   constexpr int NBLK = D / CB;
-  // U, A and tmp are read along rows by the MFMA operand loads: stride 33 (conflict-free)
-  __shared__ float U[D * L32], A[R * L32], tmp[R * L32];
-  __shared__ float G[R * R], L[R * R], Mb[4 * C], dl[C];
-  __shared__ float dT[R * R], dA[R * R], dG[R * R], dU[D * R];
+  static_assert(R * R % NT == 0 && D * C % NT == 0 && 4 * C <= NT, "record and tokens split evenly");
+  constexpr int NR = R * R / NT, NK = D * C / NT;
+  // 40 KB of LDS (four workgroups per CU): U (row stride 37), tmp and A (row stride 33), and a
+  // pool whose buffers are dead by the last product, which writes its R x D result over them.
+  // The dU partial sums stay in registers.  dT and G share a buffer (G is stored once dT is
+  // consumed), and so do dG and L (the new dG, written once dG is consumed).
+  constexpr int LA = 33;
+  constexpr int POOL = 3 * R * R + R * LA + 4 * C + C;
+  static_assert(POOL >= R * D, "the last product's output fits the pool");
+  __shared__ float U[D * L32], tmp[R * LA], pool[POOL];
+  float* const dT = pool;           // then G
+  float* const dA = pool + R * R;
+  float* const dG = pool + 2 * R * R;  // then L
+  float* const A = pool + 3 * R * R;
+  float* const Mb = A + R * LA;
+  float* const dl = Mb + 4 * C;
+  float* const G = dT;
+  float* const L = dG;
+  float* const dU = pool;           // the last product's output, R x D
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n = blockIdx.x, bh = blockIdx.y, b = bh / H, hd = bh % H;
   const int nch = gridDim.x;
   auto tok = [&](int tg) { return (static_cast<int64_t>(b) * T + tg) * H + hd; };
   // every global load of the workgroup is issued before the first wait: the partials of all
-  // column blocks (16-byte loads), the chunk record (A, G, M) and the chunk's k, v, delta
-  static_assert(PS % (4 * NT) == 0, "partials split evenly over the threads");
-  constexpr int NE = PS / (4 * NT);
+  // column blocks, the chunk record (A, G, M) and the chunk's k, v, delta.  Thread (ft = tid /
+  // 16, fi = NK (tid % 16)) loads elements fi .. fi + NK - 1 of rows 2 ft and 2 ft + 1 of each
+  // dU partial (the elements of dk, dv it stores at the end) and four consecutive dT~ elements.
   constexpr bool LP = !std::is_same<IO, float>::value;  // bf16 partials (see put4)
+  typedef typename std::conditional<LP, bf16_t, float>::type PE;  // partial element type
   typedef typename std::conditional<LP, uint2, float4>::type PV;  // four partial elements
-  PV x[NE][NBLK];
+  static_assert(R * R == 4 * NT, "four dT~ elements per thread");
+  const int ft = tid >> 4, fi = NK * (tid & 15);
+  PV xt[NBLK];
+  RowRaw<PE, NK> xk[NBLK], xv[NBLK];
   {
-    const PV* pp = reinterpret_cast<const PV*>(part) + (static_cast<int64_t>(bh) * nch + n) * NBLK * (PS / 4);
+    const PE* pp = static_cast<const PE*>(part) + (static_cast<int64_t>(bh) * nch + n) * NBLK * PS;
 #pragma unroll
-    for (int u = 0; u < NE; ++u)
-#pragma unroll
-      for (int j = 0; j < NBLK; ++j) x[u][j] = pp[j * (PS / 4) + tid + NT * u];
+    for (int j = 0; j < NBLK; ++j) {
+      xt[j] = reinterpret_cast<const PV*>(pp + j * PS)[tid];
+      xk[j] = load_raw<PE, NK>(pp + j * PS + R * R + (2 * ft) * D + fi);
+      xv[j] = load_raw<PE, NK>(pp + j * PS + R * R + (2 * ft + 1) * D + fi);
+    }
   }
   auto f4 = [](const PV& y) {
     if constexpr (LP)
@@ -603,8 +625,6 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
     else
       return y;
   };
-  static_assert(R * R % NT == 0 && D * C % NT == 0 && 4 * C <= NT, "record and tokens split evenly");
-  constexpr int NR = R * R / NT, NK = D * C / NT;
   float ra[NR], rg[NR], rm = 0.f, rd = 0.f;
   int bad;  // tokens of the chunk that are the identity (non-finite Cayley factor): no gradient
   {
@@ -617,8 +637,7 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
     }
     if (tid < 4 * C) rm = rec[3 * R * R + tid];
   }
-  // thread (t, NK consecutive features) of the chunk's k, v rows: one 8- or 16-byte load each
-  const int ft = tid >> 4, fi = NK * (tid & 15);
+  // the same (token, features) split of the chunk's k, v rows: one 8- or 16-byte load each
   const int64_t fo = tok(n * C + ft < T ? n * C + ft : 0) * D + fi;
   const RowRaw<IO, NK> rk = load_raw<IO, NK>(k + fo), rv = load_raw<IO, NK>(v + fo);
   if (tid < C) {
@@ -628,8 +647,7 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
 #pragma unroll
   for (int u = 0; u < NR; ++u) {
     const int e = tid + NT * u;
-    A[(e / R) * L32 + e % R] = ra[u];
-    G[e] = rg[u];
+    A[(e / R) * LA + e % R] = ra[u];
   }
   if (tid < 4 * C) Mb[tid] = rm;
   if (tid < C) dl[tid] = rd;
@@ -641,17 +659,25 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
       U[(fi + j) * L32 + 2 * ft + 1] = ok ? raw_elem<IO, NK>(rv, j) : 0.f;
     }
   }
-#pragma unroll
-  for (int u = 0; u < NE; ++u) {
-    float4 s = f4(x[u][0]);
+  {
+    float4 s = f4(xt[0]);
 #pragma unroll
     for (int j = 1; j < NBLK; ++j) {
-      const float4 y = f4(x[u][j]);
+      const float4 y = f4(xt[j]);
       s.x += y.x; s.y += y.y; s.z += y.z; s.w += y.w;
     }
-    const int e = 4 * (tid + NT * u);
-    float* dst = e < R * R ? dT + e : dU + (e - R * R);
-    *reinterpret_cast<float4*>(dst) = s;
+    *reinterpret_cast<float4*>(dT + 4 * tid) = s;
+  }
+  float sk[NK], sv[NK];  // dU partial sums, rows 2 ft and 2 ft + 1
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    sk[i] = raw_elem<PE, NK>(xk[0], i);
+    sv[i] = raw_elem<PE, NK>(xv[0], i);
+#pragma unroll
+    for (int j = 1; j < NBLK; ++j) {
+      sk[i] += raw_elem<PE, NK>(xk[j], i);
+      sv[i] += raw_elem<PE, NK>(xv[j], i);
+    }
   }
   __syncthreads();
   // B = blockdiag(M); dA = dT~ B^T (block structure: dA[r][2s + a] = sum_b dT[r][2s + b] M_s[a][b])
@@ -661,11 +687,13 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
   }
   __syncthreads();
   // tmp = A^T dA; dB = A^T dT~ (its diagonal blocks used) into dG
-  lgemm<R, R, R, true, false, kStore>(A, L32, dA, R, tmp, L32, wave, lane);
-  lgemm<R, R, R, true, false, kStore>(A, L32, dT, R, dG, R, wave, lane);
+  lgemm<R, R, R, true, false, kStore>(A, LA, dA, R, tmp, LA, wave, lane);
+  lgemm<R, R, R, true, false, kStore>(A, LA, dT, R, dG, R, wave, lane);
   __syncthreads();
-  // dL = tmp A^T  (into dA)
-  lgemm<R, R, R, false, true, kStore>(tmp, L32, A, L32, dA, R, wave, lane);
+  // dL = tmp A^T  (into dA); G over dT, which is consumed
+  lgemm<R, R, R, false, true, kStore>(tmp, LA, A, LA, dA, R, wave, lane);
+#pragma unroll
+  for (int u = 0; u < NR; ++u) G[tid + NT * u] = rg[u];
   __syncthreads();
   // dM_t = dB_tt + sum_{i<t} dL_ti G_ti^T; then the M chain; dG_ti = M_t^T dL_ti (i < t)
   if (tid < 4 * C) {
@@ -682,7 +710,7 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
     float y = 0.f;
     if (i < t)  // (M_t^T dL_ti)[a][cb] = sum_m M_t[m][a] dL_ti[m][cb]
       y = Mb[4 * t + a] * dA[(2 * t) * R + c] + Mb[4 * t + 2 + a] * dA[(2 * t + 1) * R + c];
-    L[e] = y;  // L is free now: the new dG
+    L[e] = y;  // the new dG, over dG (consumed above)
   }
   __syncthreads();
   if (tid < C) {  // M chain (vmi::cayley_coeffs) -> ddelta and the diagonal Gram entries
@@ -716,22 +744,23 @@ __global__ __launch_bounds__(NT) void bwdc_reduce_kernel(
   __syncthreads();
   for (int e = tid; e < R * R; e += NT) {  // symmetrise: dG + dG^T
     const int r = e / R, c = e % R;
-    tmp[r * L32 + c] = L[r * R + c] + L[c * R + r];
+    tmp[r * LA + c] = L[r * R + c] + L[c * R + r];
   }
   __syncthreads();
-  // dU^T += (dG + dG^T) U^T (the partials hold dU transposed, [R][D])
-  lgemm<R, D, R, false, true, kAdd>(tmp, L32, U, L32, dU, D, wave, lane);
+  // dU^T = partial sums + (dG + dG^T) U^T (the partials hold dU transposed, [R][D]); the
+  // product goes over the pool, whose buffers are all consumed
+  lgemm<R, D, R, false, true, kStore>(tmp, LA, U, L32, dU, D, wave, lane);
   __syncthreads();
   if (n * C + ft < T) {  // the same (token, features) split: one 8- or 16-byte store per row
     const bool z = (bad >> ft) & 1;
-    float xk[NK], xv[NK];
+    float yk[NK], yv[NK];
 #pragma unroll
     for (int j = 0; j < NK; ++j) {
-      xk[j] = z ? 0.f : dU[(2 * ft) * D + fi + j];
-      xv[j] = z ? 0.f : dU[(2 * ft + 1) * D + fi + j];
+      yk[j] = z ? 0.f : sk[j] + dU[(2 * ft) * D + fi + j];
+      yv[j] = z ? 0.f : sv[j] + dU[(2 * ft + 1) * D + fi + j];
     }
-    store_row<IO, NK>(dk + fo, xk);
-    store_row<IO, NK>(dv + fo, xv);
+    store_row<IO, NK>(dk + fo, yk);
+    store_row<IO, NK>(dv + fo, yv);
   }
 }
 
