@@ -235,8 +235,13 @@ __device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B
                                                  const float* B2, const float* A3, const float* B3,
                                                  PT* dst, int wave, int lane) {
   constexpr int NTILE = (M / 16) * 2;
+  static_assert(NTILE % NWAVES == 0, "whole tiles per wave");
   const int l16 = lane & 15, kq = lane >> 4;
-  for (int tile = wave; tile < NTILE; tile += NWAVES) {
+  // a static number of stores per wave, so that a later wait for global loads issued before
+  // them is counted past them instead of waiting for the stores as well
+#pragma unroll
+  for (int it = 0; it < NTILE / NWAVES; ++it) {
+    const int tile = wave + NWAVES * it;
     const int tm = tile >> 1, tn = tile & 1;
     const int am = 16 * tm + l16, bn = 16 * tn + l16;
     f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
