@@ -55,7 +55,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-enum { kStore = 0, kAdd = 1, kMaskStore = 2, kAddFrom = 3 };  // kAddFrom: C = Cs + A B
+enum { kStore = 0, kAdd = 1, kMaskStore = 2 };
 
 // N consecutive elements of a row as raw 32-bit words (one 8- or 16-byte load, two for 8
 // fp32), and element j of them as a float.  The row must be aligned to its byte size.
@@ -161,8 +161,7 @@ constexpr int L32 = 37;  // 32-wide matrices
 template <int M, int N, int K, bool TA, bool TB, int MODE, int W0 = 0, int NW = 4,
           bool LP = false, bool SUMB = false>
 __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, int ldb, float* Cm,
-                                      int ldc, int wave, int lane, const float* B2 = nullptr,
-                                      const float* Cs = nullptr) {
+                                      int ldc, int wave, int lane, const float* B2 = nullptr) {
   constexpr int TN = N / 16, NTILE = (M / 16) * TN;
   if (wave < W0 || wave >= W0 + NW) return;
   const int l16 = lane & 15, kq = lane >> 4;
@@ -211,8 +210,42 @@ __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, i
       float* p = Cm + row * ldc + col;
       if (MODE == kStore) *p = x;
       else if (MODE == kAdd) *p += x;
-      else if (MODE == kAddFrom) *p = Cs[row * ldc + col] + x;
       else *p = (row >> 1) <= col ? x : 0.f;
+    }
+  }
+}
+
+// Cm = Cs + A1 B1^T + A2 B2 (fp32, all in LDS; A1 [M][K1], B1 [N][K1], A2 [M][K2], B2 [K2][N]):
+// both products in one pair of accumulators, so the sum is stored once.  16 x 16 output tiles
+// round robin over NW waves, lane layout as in lgemm.
+template <int M, int N, int K1, int K2, int NW>
+__device__ __forceinline__ void lgemm2_addfrom(const float* A1, int lda1, const float* B1, int ldb1,
+                                               const float* A2, int lda2, const float* B2, int ldb2,
+                                               const float* Cs, float* Cm, int ldc, int wave,
+                                               int lane) {
+  constexpr int TN = N / 16, NTILE = (M / 16) * TN;
+  static_assert(K1 % 4 == 0 && K2 % 4 == 0, "k steps of 4");
+  const int l16 = lane & 15, kq = lane >> 4;
+  for (int tile = wave; tile < NTILE; tile += NW) {
+    const int tm = tile / TN, tn = tile % TN;
+    const int am = 16 * tm + l16, bn = 16 * tn + l16;
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k0 = 0; k0 < K1; k0 += 4) {
+      const float a = A1[am * lda1 + k0 + kq], b = B1[bn * ldb1 + k0 + kq];
+      if ((k0 >> 2) & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc1, 0, 0, 0);
+      else acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int k0 = 0; k0 < K2; k0 += 4) {
+      const float a = A2[am * lda2 + k0 + kq], b = B2[(k0 + kq) * ldb2 + bn];
+      if ((k0 >> 2) & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc1, 0, 0, 0);
+      else acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int o = (16 * tm + 4 * kq + r) * ldc + bn;
+      Cm[o] = Cs[o] + (acc0[r] + acc1[r]);
     }
   }
 }
@@ -556,9 +589,8 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
       }
     }
     // (7, same phase) Lam_s = Lam_e + dO Q^T + U dW into the other buffer (8 waves, one tile
-    // each, both terms): the dU partial above still reads Lam_e
-    lgemm<D, CB, C, false, true, kAddFrom, 0, NWC>(dO, L16, Qb, L16, Ln, L16, wave, lane, nullptr, Lm);
-    lgemm<D, CB, R, false, false, kAdd, 0, NWC>(U, L32, dWm, L16, Ln, L16, wave, lane);
+    // each, both terms in one accumulation): the dU partial above still reads Lam_e
+    lgemm2_addfrom<D, CB, C, R, NWC>(dO, L16, Qb, L16, U, L32, dWm, L16, Lm, Ln, L16, wave, lane);
     lc ^= 1;
     lds_barrier();
     if (n > 0) commit(n - 1);
