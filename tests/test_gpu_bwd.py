@@ -55,6 +55,9 @@ def _oracle(q, k, v, d, psi0, w_o, w_s, with_state_grad):
     (1, 1, 1, 128, torch.float32, True, False),
     (2, 33, 3, 128, torch.float16, False, False),
     (1, 50, 2, 64, torch.bfloat16, True, True),
+    # B * H past a multiple of 8: whole groups of 8 heads share an XCD, the rest go in order
+    (3, 40, 4, 128, torch.bfloat16, True, True),
+    (2, 24, 5, 64, torch.float32, False, True),
     # head dims other than 64 / 128 (the per-token reverse pass at any T, padded inside)
     (2, 40, 2, 96, torch.float32, True, True),
     (1, 20, 3, 48, torch.float32, False, True),

@@ -455,7 +455,22 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
       dZm[R * L16], dWm[R * L16], QD[2][CB * L16];
   __shared__ float dTp[R * L32], dQm[CB * L16];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int blk = blockIdx.x, bh = blockIdx.y, b = bh / H, hd = bh % H;
+  // Workgroups go to the 8 XCDs round robin by linear index.  The column blocks of one (b, h)
+  // read the same k, v, dO rows and chunk records, so they get linear indices of one residue
+  // mod 8 (one XCD, one L2); a last group of fewer than 8 (b, h) keeps the plain order.
+  int blk, bh;
+  {
+    const int L = blockIdx.x + NBLK * blockIdx.y;  // gridDim.x == NBLK
+    const int full = (static_cast<int>(gridDim.y) / 8) * 8 * NBLK;
+    if (L < full) {
+      blk = (L / 8) % NBLK;
+      bh = (L / (8 * NBLK)) * 8 + L % 8;
+    } else {
+      blk = (L - full) % NBLK;
+      bh = full / NBLK + (L - full) / NBLK;
+    }
+  }
+  const int b = bh / H, hd = bh % H;
   const int nch = (T + C - 1) / C;
   const int64_t DD = static_cast<int64_t>(D) * D;
 
