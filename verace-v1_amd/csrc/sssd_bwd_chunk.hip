@@ -129,6 +129,22 @@ __device__ __forceinline__ float raw_elem(const RowRaw<T, N>& r, int j) {
   }
 }
 
+// N elements of a raw row as N / 2 words of bf16 pairs (round to nearest even; bf16 rows as they
+// are), or zeros; stored with one 8- or 16-byte LDS write at p (aligned to that size).
+template <typename T, int N>
+__device__ __forceinline__ void put_bf16_row(uint16_t* p, const RowRaw<T, N>& r, bool keep) {
+  static_assert(N == 4 || N == 8, "8 or 16 bytes");
+  uint32_t w[N / 2];
+#pragma unroll
+  for (int j = 0; j < N / 2; ++j) {
+    if constexpr (std::is_same<T, bf16_t>::value) w[j] = r.w[j];
+    else w[j] = pack_bf16x2(raw_elem<T, N>(r, 2 * j), raw_elem<T, N>(r, 2 * j + 1));
+    w[j] = keep ? w[j] : 0u;
+  }
+  if constexpr (N == 4) *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+  else *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // Workgroup barrier that orders LDS accesses only: it waits for this wave's LDS operations,
 // not for its global loads and stores (which __syncthreads() also waits for).  The columns
 // kernel's global loads fill registers for the next chunk and its global stores are read by
@@ -158,10 +174,19 @@ constexpr int L32 = 37;  // 32-wide matrices
 // A[m][4 kq .. 4 kq + 3] of a 16-wide k step), fp32 accumulation; for the bf16 / fp16
 // inputs' per-chunk gradient products only.
 // With B2, the B operand is B + B2 (same layout and stride), summed as it is read.
+// ABF / BBF (LP only): that operand is read from a bf16 copy instead, Ab [M][ldab] / Bb [N][ldbb]
+// with k contiguous (opA(m, k) = Ab[m ldab + k], opB(k, n) = Bb[n ldbb + k]): one 8-byte read per
+// lane and k step, the same bits as rounding the fp32 operand (A / B and TA / TB unused).
+// With Ct, the result is also written transposed in bf16 (Ct [N][ldct]), the operand layout of a
+// later product that reads it transposed.
 template <int M, int N, int K, bool TA, bool TB, int MODE, int W0 = 0, int NW = 4,
-          bool LP = false, bool SUMB = false>
+          bool LP = false, bool SUMB = false, bool ABF = false, bool BBF = false>
 __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, int ldb, float* Cm,
-                                      int ldc, int wave, int lane, const float* B2 = nullptr) {
+                                      int ldc, int wave, int lane, const float* B2 = nullptr,
+                                      const uint16_t* Ab = nullptr, int ldab = 0,
+                                      const uint16_t* Bb = nullptr, int ldbb = 0,
+                                      uint16_t* Ct = nullptr, int ldct = 0) {
+  static_assert(LP || !(ABF || BBF), "bf16 copies feed the bf16 products only");
   constexpr int TN = N / 16, NTILE = (M / 16) * TN;
   if (wave < W0 || wave >= W0 + NW) return;
   const int l16 = lane & 15, kq = lane >> 4;
@@ -173,16 +198,30 @@ __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, i
       static_assert(K % 16 == 0, "bf16 steps of 16");
 #pragma unroll 4
       for (int k0 = 0; k0 < K; k0 += 16) {
-        float af[4], bf[4];
+        s16x4 a, b;
+        if constexpr (ABF) {
+          a = *reinterpret_cast<const s16x4*>(Ab + am * ldab + k0 + 4 * kq);
+        } else {
+          float af[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int k = k0 + 4 * kq + i;
-          af[i] = TA ? A[k * lda + am] : A[am * lda + k];
-          bf[i] = TB ? B[bn * ldb + k] : B[k * ldb + bn];
+          for (int i = 0; i < 4; ++i) {
+            const int k = k0 + 4 * kq + i;
+            af[i] = TA ? A[k * lda + am] : A[am * lda + k];
+          }
+          // two elements per v_cvt_pk_bf16_f32
+          a = __builtin_bit_cast(s16x4, make_uint2(pack_bf16x2(af[0], af[1]), pack_bf16x2(af[2], af[3])));
         }
-        // two elements per v_cvt_pk_bf16_f32
-        const s16x4 a = __builtin_bit_cast(s16x4, make_uint2(pack_bf16x2(af[0], af[1]), pack_bf16x2(af[2], af[3])));
-        const s16x4 b = __builtin_bit_cast(s16x4, make_uint2(pack_bf16x2(bf[0], bf[1]), pack_bf16x2(bf[2], bf[3])));
+        if constexpr (BBF) {
+          b = *reinterpret_cast<const s16x4*>(Bb + bn * ldbb + k0 + 4 * kq);
+        } else {
+          float bf[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int k = k0 + 4 * kq + i;
+            bf[i] = TB ? B[bn * ldb + k] : B[k * ldb + bn];
+          }
+          b = __builtin_bit_cast(s16x4, make_uint2(pack_bf16x2(bf[0], bf[1]), pack_bf16x2(bf[2], bf[3])));
+        }
         if ((k0 >> 4) & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc1, 0, 0, 0);
         else acc0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc0, 0, 0, 0);
       }
@@ -203,15 +242,21 @@ __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, i
       }
     }
     }
+    float y[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * tm + 4 * kq + r, col = bn;
       const float x = acc0[r] + acc1[r];
       float* p = Cm + row * ldc + col;
-      if (MODE == kStore) *p = x;
-      else if (MODE == kAdd) *p += x;
-      else *p = (row >> 1) <= col ? x : 0.f;
+      if (MODE == kStore) y[r] = x;
+      else if (MODE == kAdd) y[r] = *p + x;
+      else y[r] = (row >> 1) <= col ? x : 0.f;
+      *p = y[r];
     }
+    // Ct: the result transposed in bf16 ([N][ldct], this lane's four rows one 8-byte write)
+    if (Ct != nullptr)
+      *reinterpret_cast<uint2*>(Ct + bn * ldct + 16 * tm + 4 * kq) =
+          make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
   }
 }
 
@@ -222,7 +267,7 @@ template <int M, int N, int K1, int K2, int NW>
 __device__ __forceinline__ void lgemm2_addfrom(const float* A1, int lda1, const float* B1, int ldb1,
                                                const float* A2, int lda2, const float* B2, int ldb2,
                                                const float* Cs, float* Cm, int ldc, int wave,
-                                               int lane) {
+                                               int lane, uint16_t* Ct = nullptr, int ldct = 0) {
   constexpr int TN = N / 16, NTILE = (M / 16) * TN;
   static_assert(K1 % 4 == 0 && K2 % 4 == 0, "k steps of 4");
   const int l16 = lane & 15, kq = lane >> 4;
@@ -242,11 +287,16 @@ __device__ __forceinline__ void lgemm2_addfrom(const float* A1, int lda1, const 
       if ((k0 >> 2) & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc1, 0, 0, 0);
       else acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc0, 0, 0, 0);
     }
+    float y[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int o = (16 * tm + 4 * kq + r) * ldc + bn;
-      Cm[o] = Cs[o] + (acc0[r] + acc1[r]);
+      y[r] = Cs[o] + (acc0[r] + acc1[r]);
+      Cm[o] = y[r];
     }
+    if (Ct != nullptr)  // the result transposed in bf16, as in lgemm
+      *reinterpret_cast<uint2*>(Ct + bn * ldct + 16 * tm + 4 * kq) =
+          make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
   }
 }
 
@@ -454,6 +504,14 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
   __shared__ float S1[R * L16], S1b[R * L16], Wm[R * L16], Wt[R * L16], Zm[R * L16], Xm[R * L16], dXm[R * L16],
       dZm[R * L16], dWm[R * L16], QD[2][CB * L16];
   __shared__ float dTp[R * L32], dQm[CB * L16];
+  // bf16 inputs' copies of U^T ([R][D], k and v rows) and dO^T ([C][D], token rows), features
+  // contiguous: the A operand of dX and dZ and the B operand of dX and Psi_s^T dO, one 8-byte
+  // read per lane and k step.  Row pitch D + 8: 16-byte rows, conflict-free 8-byte reads.
+  constexpr int LUT = D + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t UTb[LP ? R * LUT : 8], dOTb[LP ? C * LUT : 8];
+  // and of Lam_e^T and Psi_s^T ([CB][D]): the B operand of dZ and the A operand of Psi_s^T dO,
+  // written by the products that update Lam and Psi
+  __shared__ __attribute__((aligned(16))) uint16_t LTb[LP ? CB * LUT : 8], PTb[LP ? CB * LUT : 8];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // Workgroups go to the 8 XCDs round robin by linear index.  The column blocks of one (b, h)
   // read the same k, v, dO rows and chunk records, so they get linear indices of one residue
@@ -479,6 +537,7 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     const int64_t o = bh * DD + static_cast<int64_t>(i) * D + blk * CB + jj;
     Ps[i * L16 + jj] = psi_T[o];
     Lmb[0][i * L16 + jj] = dpsi_T ? dpsi_T[o] : 0.f;
+    if constexpr (LP) LTb[jj * LUT + i] = static_cast<uint16_t>(to_bf16(Lmb[0][i * L16 + jj]));
   }
   // chunk n's inputs: registers first (the next chunk's arrive while this one runs), loaded by
   // waves 4-7, which are idle in the phase that issues the loads.  Thread (t = tid / 16, j0 = EU (tid % 16)) holds elements
@@ -530,6 +589,11 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
       U[i * L32 + 2 * ft + 1] = uk ? raw_elem<IO, EU>(rv, j) : 0.f;
       dO[i * L16 + ft] = ok ? raw_elem<GO, EU>(rd, j) : 0.f;
     }
+    if constexpr (LP) {
+      put_bf16_row<IO, EU>(UTb + (2 * ft) * LUT + fj, rk, uk);
+      put_bf16_row<IO, EU>(UTb + (2 * ft + 1) * LUT + fj, rv, uk);
+      put_bf16_row<GO, EU>(dOTb + ft * LUT + fj, rd, ok);
+    }
     {
       const int t = lt / CB, jj = lt % CB;
       Qb[jj * L16 + t] = n * C + t < T ? raw_elem<IO, 2>(rq, 0) : 0.f;
@@ -556,8 +620,15 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     lgemm<R, CB, D / 2, true, false, kStore, 0, 2>(U, L32, Ps, L16, S1, L16, wave, lane);
     lgemm<R, CB, D / 2, true, false, kStore, 6, 2>(U + (D / 2) * L32, L32, Ps + (D / 2) * L16, L16,
                                                    S1b, L16, wave, lane);
-    lgemm<R, C, D, true, false, kMaskStore, 2, 2, LP>(U, L32, dO, L16, dXm, L16, wave, lane);
-    lgemm<R, CB, D, true, false, kStore, 4, 2, LP>(U, L32, Lm, L16, dZm, L16, wave, lane);
+    if constexpr (LP) {
+      lgemm<R, C, D, true, false, kMaskStore, 2, 2, true, false, true, true>(
+          U, L32, dO, L16, dXm, L16, wave, lane, nullptr, UTb, LUT, dOTb, LUT);
+      lgemm<R, CB, D, true, false, kStore, 4, 2, true, false, true, true>(
+          U, L32, Lm, L16, dZm, L16, wave, lane, nullptr, UTb, LUT, LTb, LUT);
+    } else {
+      lgemm<R, C, D, true, false, kMaskStore, 2, 2>(U, L32, dO, L16, dXm, L16, wave, lane);
+      lgemm<R, CB, D, true, false, kStore, 4, 2>(U, L32, Lm, L16, dZm, L16, wave, lane);
+    }
     lds_barrier();
     // (2) Wm = T~^T S1 (waves 0-1); dZ += dX Q^T (waves 4-5, the tiles they stored);
     //     W starts as S1 (every thread one element)
@@ -570,16 +641,25 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     lds_barrier();
     // (3) Psi_s = Psi_e + U Wm (8 waves); W += G Wm (waves 0-1, after their Psi tile);
     //     dW = T~^T dZ (waves 2-3)
-    lgemm<D, CB, R, false, false, kAdd, 0, NWC>(U, L32, Wm, L16, Ps, L16, wave, lane);
+    lgemm<D, CB, R, false, false, kAdd, 0, NWC>(U, L32, Wm, L16, Ps, L16, wave, lane, nullptr,
+                                               nullptr, 0, nullptr, 0, LP ? PTb : nullptr, LUT);
     lgemm<R, CB, R, false, false, kAdd, 0, 2>(Gm, L32, Wm, L16, Wt, L16, wave, lane);
     lgemm<R, CB, R, true, false, kStore, 2, 2, LP>(Tt, L32, dZm, L16, dWm, L16, wave, lane);
     lds_barrier();
     // (4) Z = T~ W (waves 0-1); Psi_s^T dO (first term of dQ) over two halves of the state rows
     //     (waves 2-3); dT~ partial = dZ W^T (waves 4-7)
     lgemm<R, CB, R, false, false, kStore, 0, 2, LP>(Tt, L32, Wt, L16, Zm, L16, wave, lane);
-    lgemm<CB, C, D / 2, true, false, kStore, 2, 1, LP>(Ps, L16, dO, L16, QD[0], L16, wave, lane);
-    lgemm<CB, C, D / 2, true, false, kStore, 3, 1, LP>(Ps + (D / 2) * L16, L16, dO + (D / 2) * L16,
-                                                       L16, QD[1], L16, wave, lane);
+    if constexpr (LP) {
+      lgemm<CB, C, D / 2, true, false, kStore, 2, 1, true, false, true, true>(
+          Ps, L16, dO, L16, QD[0], L16, wave, lane, nullptr, PTb, LUT, dOTb, LUT);
+      lgemm<CB, C, D / 2, true, false, kStore, 3, 1, true, false, true, true>(
+          Ps + (D / 2) * L16, L16, dO + (D / 2) * L16, L16, QD[1], L16, wave, lane, nullptr,
+          PTb + D / 2, LUT, dOTb + D / 2, LUT);
+    } else {
+      lgemm<CB, C, D / 2, true, false, kStore, 2, 1>(Ps, L16, dO, L16, QD[0], L16, wave, lane);
+      lgemm<CB, C, D / 2, true, false, kStore, 3, 1>(Ps + (D / 2) * L16, L16, dO + (D / 2) * L16,
+                                                     L16, QD[1], L16, wave, lane);
+    }
     lgemm<R, R, CB, false, true, kStore, 4, 4, LP>(dZm, L16, Wt, L16, dTp, L32, wave, lane);
     lds_barrier();
     // (5) X = mask o (Z Q) (waves 0-1); dQ second term Z^T dX (wave 2); the next chunk's loads
@@ -605,7 +685,8 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     }
     // (7, same phase) Lam_s = Lam_e + dO Q^T + U dW into the other buffer (8 waves, one tile
     // each, both terms in one accumulation): the dU partial above still reads Lam_e
-    lgemm2_addfrom<D, CB, C, R, NWC>(dO, L16, Qb, L16, U, L32, dWm, L16, Lm, Ln, L16, wave, lane);
+    lgemm2_addfrom<D, CB, C, R, NWC>(dO, L16, Qb, L16, U, L32, dWm, L16, Lm, Ln, L16, wave, lane,
+                                     LP ? LTb : nullptr, LUT);
     lc ^= 1;
     lds_barrier();
     if (n > 0) commit(n - 1);
