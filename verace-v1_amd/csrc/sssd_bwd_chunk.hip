@@ -178,14 +178,15 @@ constexpr int L32 = 37;  // 32-wide matrices
 // with k contiguous (opA(m, k) = Ab[m ldab + k], opB(k, n) = Bb[n ldbb + k]): one 8-byte read per
 // lane and k step, the same bits as rounding the fp32 operand (A / B and TA / TB unused).
 // With Ct, the result is also written transposed in bf16 (Ct [N][ldct]), the operand layout of a
-// later product that reads it transposed.
+// later product that reads it transposed; with Cb, in bf16 as it is laid out (Cb [M][ldcb]).
 template <int M, int N, int K, bool TA, bool TB, int MODE, int W0 = 0, int NW = 4,
           bool LP = false, bool SUMB = false, bool ABF = false, bool BBF = false>
 __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, int ldb, float* Cm,
                                       int ldc, int wave, int lane, const float* B2 = nullptr,
                                       const uint16_t* Ab = nullptr, int ldab = 0,
                                       const uint16_t* Bb = nullptr, int ldbb = 0,
-                                      uint16_t* Ct = nullptr, int ldct = 0) {
+                                      uint16_t* Ct = nullptr, int ldct = 0,
+                                      uint16_t* Cb = nullptr, int ldcb = 0) {
   static_assert(LP || !(ABF || BBF), "bf16 copies feed the bf16 products only");
   constexpr int TN = N / 16, NTILE = (M / 16) * TN;
   if (wave < W0 || wave >= W0 + NW) return;
@@ -253,10 +254,19 @@ __device__ __forceinline__ void lgemm(const float* A, int lda, const float* B, i
       else y[r] = (row >> 1) <= col ? x : 0.f;
       *p = y[r];
     }
-    // Ct: the result transposed in bf16 ([N][ldct], this lane's four rows one 8-byte write)
+    // Ct: the result transposed in bf16 ([N][ldct], this lane's four rows one 8-byte write);
+    // Cb: the result in bf16 as it is laid out ([M][ldcb])
     if (Ct != nullptr)
       *reinterpret_cast<uint2*>(Ct + bn * ldct + 16 * tm + 4 * kq) =
           make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+    if (Cb != nullptr) {
+      const uint32_t w0 = pack_bf16x2(y[0], y[1]), w1 = pack_bf16x2(y[2], y[3]);
+      uint16_t* q = Cb + (16 * tm + 4 * kq) * ldcb + bn;
+      q[0] = static_cast<uint16_t>(w0);
+      q[ldcb] = static_cast<uint16_t>(w0 >> 16);
+      q[2 * ldcb] = static_cast<uint16_t>(w1);
+      q[3 * ldcb] = static_cast<uint16_t>(w1 >> 16);
+    }
   }
 }
 
@@ -347,6 +357,39 @@ __device__ __forceinline__ void lgemm3_nt_global(const float* A1, const float* B
           acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(As[u][am * L16 + k + 4], Bs[u][bn * L16 + k + 4], acc1, 0, 0, 0);
         }
       }
+    }
+    put4(dst + bn * M + 16 * tm + 4 * kq, acc0[0] + acc1[0], acc0[1] + acc1[1], acc0[2] + acc1[2],
+         acc0[3] + acc1[3]);
+  }
+}
+
+// lgemm3_nt_global (LP) with the B operands read from bf16 copies (B_i [32][ldb], 16 values of k
+// per row): one 8-byte read per B operand and lane, the same bits as rounding the fp32 values.
+// The A operands are fp32 as in lgemm3_nt_global.  (bf16 copies of the A operands too, written by
+// their producers as 2-byte scattered stores, made the columns kernel 21 us slower.)
+template <int M, int NWAVES, typename PT>
+__device__ __forceinline__ void lgemm3_nt_global_b16(const float* A1, const uint16_t* B1,
+                                                     const float* A2, const uint16_t* B2,
+                                                     const float* A3, const uint16_t* B3,
+                                                     int ldb, PT* dst, int wave, int lane) {
+  constexpr int NTILE = (M / 16) * 2;
+  static_assert(NTILE % NWAVES == 0, "whole tiles per wave");
+  const int l16 = lane & 15, kq = lane >> 4;
+#pragma unroll
+  for (int it = 0; it < NTILE / NWAVES; ++it) {  // a static store count, as in lgemm3_nt_global
+    const int tile = wave + NWAVES * it;
+    const int tm = tile >> 1, tn = tile & 1;
+    const int am = 16 * tm + l16, bn = 16 * tn + l16;
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    const float* As[3] = {A1, A2, A3};
+    const uint16_t* Bs[3] = {B1, B2, B3};
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      const float* pa = As[u] + am * L16 + 4 * kq;
+      const s16x4 a = __builtin_bit_cast(s16x4, make_uint2(pack_bf16x2(pa[0], pa[1]), pack_bf16x2(pa[2], pa[3])));
+      const s16x4 b = *reinterpret_cast<const s16x4*>(Bs[u] + bn * ldb + 4 * kq);
+      if (u & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc1, 0, 0, 0);
+      else acc0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, acc0, 0, 0, 0);
     }
     put4(dst + bn * M + 16 * tm + 4 * kq, acc0[0] + acc1[0], acc0[1] + acc1[1], acc0[2] + acc1[2],
          acc0[3] + acc1[3]);
@@ -512,6 +555,12 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
   // and of Lam_e^T and Psi_s^T ([CB][D]): the B operand of dZ and the A operand of Psi_s^T dO,
   // written by the products that update Lam and Psi
   __shared__ __attribute__((aligned(16))) uint16_t LTb[LP ? CB * LUT : 8], PTb[LP ? CB * LUT : 8];
+  // and of the dU partial's B operands Z, X, dW as they are laid out ([R][16], pitch LB),
+  // written by the products that form them
+  constexpr int LB = 20;
+  constexpr int NB = LP ? 1 : 0;
+  __shared__ __attribute__((aligned(16))) uint16_t Zb[NB * R * LB + 8], Xb[NB * R * LB + 8],
+      dWb[NB * R * LB + 8];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // Workgroups go to the 8 XCDs round robin by linear index.  The column blocks of one (b, h)
   // read the same k, v, dO rows and chunk records, so they get linear indices of one residue
@@ -644,11 +693,15 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     lgemm<D, CB, R, false, false, kAdd, 0, NWC>(U, L32, Wm, L16, Ps, L16, wave, lane, nullptr,
                                                nullptr, 0, nullptr, 0, LP ? PTb : nullptr, LUT);
     lgemm<R, CB, R, false, false, kAdd, 0, 2>(Gm, L32, Wm, L16, Wt, L16, wave, lane);
-    lgemm<R, CB, R, true, false, kStore, 2, 2, LP>(Tt, L32, dZm, L16, dWm, L16, wave, lane);
+    lgemm<R, CB, R, true, false, kStore, 2, 2, LP>(Tt, L32, dZm, L16, dWm, L16, wave, lane, nullptr,
+                                                   nullptr, 0, nullptr, 0, nullptr, 0,
+                                                   LP ? dWb : nullptr, LB);
     lds_barrier();
     // (4) Z = T~ W (waves 0-1); Psi_s^T dO (first term of dQ) over two halves of the state rows
     //     (waves 2-3); dT~ partial = dZ W^T (waves 4-7)
-    lgemm<R, CB, R, false, false, kStore, 0, 2, LP>(Tt, L32, Wt, L16, Zm, L16, wave, lane);
+    lgemm<R, CB, R, false, false, kStore, 0, 2, LP>(Tt, L32, Wt, L16, Zm, L16, wave, lane, nullptr,
+                                                    nullptr, 0, nullptr, 0, nullptr, 0,
+                                                    LP ? Zb : nullptr, LB);
     if constexpr (LP) {
       lgemm<CB, C, D / 2, true, false, kStore, 2, 1, true, false, true, true>(
           Ps, L16, dO, L16, QD[0], L16, wave, lane, nullptr, PTb, LUT, dOTb, LUT);
@@ -664,14 +717,19 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     lds_barrier();
     // (5) X = mask o (Z Q) (waves 0-1); dQ second term Z^T dX (wave 2); the next chunk's loads
     //     (waves 4-7: issued here, before this chunk's stores, and committed after phase 7)
-    lgemm<R, C, CB, false, false, kMaskStore, 0, 2, LP>(Zm, L16, Qb, L16, Xm, L16, wave, lane);
+    lgemm<R, C, CB, false, false, kMaskStore, 0, 2, LP>(Zm, L16, Qb, L16, Xm, L16, wave, lane,
+                                                        nullptr, nullptr, 0, nullptr, 0, nullptr,
+                                                        0, LP ? Xb : nullptr, LB);
     lgemm<CB, C, R, true, false, kStore, 2, 1, LP>(Zm, L16, dXm, L16, dQm, L16, wave, lane);
     if (n > 0) fetch(n - 1);
     lds_barrier();
     // (6) dU partial = Lam_e Z^T + dO X^T + Psi_s dW^T straight to the workspace; dT~ partial
     //     and dq out
     PT* pp = part + ((static_cast<int64_t>(bh) * nch + n) * NBLK + blk) * PS;
-    lgemm3_nt_global<D, LP, NWC>(Lm, Zm, dO, Xm, Ps, dWm, pp + R * R, wave, lane);
+    if constexpr (LP)
+      lgemm3_nt_global_b16<D, NWC>(Lm, Zb, dO, Xb, Ps, dWb, LB, pp + R * R, wave, lane);
+    else
+      lgemm3_nt_global<D, LP, NWC>(Lm, Zm, dO, Xm, Ps, dWm, pp + R * R, wave, lane);
     {
       for (int e = 4 * tid; e < R * R; e += 4 * NTC) {
         const float* d = &dTp[(e / R) * L32 + e % R];
