@@ -561,6 +561,10 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
   constexpr int NB = LP ? 1 : 0;
   __shared__ __attribute__((aligned(16))) uint16_t Zb[NB * R * LB + 8], Xb[NB * R * LB + 8],
       dWb[NB * R * LB + 8];
+  // and T~ ([R][R], from the commit) and W^T ([CB][R], from W's last product): the operands of
+  // Z = T~ W
+  constexpr int LT = R + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t Ttb[NB * R * LT + 8], WTb[NB * CB * LT + 8];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // Workgroups go to the 8 XCDs round robin by linear index.  The column blocks of one (b, h)
   // read the same k, v, dO rows and chunk records, so they get linear indices of one residue
@@ -649,6 +653,9 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     }
     const int e = (4 * lt) / R * L32 + (4 * lt) % R;  // row pitch 37: 4-byte stores
     Tt[e] = rt.x; Tt[e + 1] = rt.y; Tt[e + 2] = rt.z; Tt[e + 3] = rt.w;
+    if constexpr (LP)
+      *reinterpret_cast<uint2*>(Ttb + (4 * lt) / R * LT + (4 * lt) % R) =
+          make_uint2(pack_bf16x2(rt.x, rt.y), pack_bf16x2(rt.z, rt.w));
     Gm[e] = rg.x; Gm[e + 1] = rg.y; Gm[e + 2] = rg.z; Gm[e + 3] = rg.w;
   };
 
@@ -692,16 +699,19 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     //     dW = T~^T dZ (waves 2-3)
     lgemm<D, CB, R, false, false, kAdd, 0, NWC>(U, L32, Wm, L16, Ps, L16, wave, lane, nullptr,
                                                nullptr, 0, nullptr, 0, LP ? PTb : nullptr, LUT);
-    lgemm<R, CB, R, false, false, kAdd, 0, 2>(Gm, L32, Wm, L16, Wt, L16, wave, lane);
+    lgemm<R, CB, R, false, false, kAdd, 0, 2>(Gm, L32, Wm, L16, Wt, L16, wave, lane, nullptr,
+                                              nullptr, 0, nullptr, 0, LP ? WTb : nullptr, LT);
     lgemm<R, CB, R, true, false, kStore, 2, 2, LP>(Tt, L32, dZm, L16, dWm, L16, wave, lane, nullptr,
                                                    nullptr, 0, nullptr, 0, nullptr, 0,
                                                    LP ? dWb : nullptr, LB);
     lds_barrier();
     // (4) Z = T~ W (waves 0-1); Psi_s^T dO (first term of dQ) over two halves of the state rows
     //     (waves 2-3); dT~ partial = dZ W^T (waves 4-7)
-    lgemm<R, CB, R, false, false, kStore, 0, 2, LP>(Tt, L32, Wt, L16, Zm, L16, wave, lane, nullptr,
-                                                    nullptr, 0, nullptr, 0, nullptr, 0,
-                                                    LP ? Zb : nullptr, LB);
+    if constexpr (LP)
+      lgemm<R, CB, R, false, false, kStore, 0, 2, true, false, true, true>(
+          Tt, L32, Wt, L16, Zm, L16, wave, lane, nullptr, Ttb, LT, WTb, LT, nullptr, 0, Zb, LB);
+    else
+      lgemm<R, CB, R, false, false, kStore, 0, 2>(Tt, L32, Wt, L16, Zm, L16, wave, lane);
     if constexpr (LP) {
       lgemm<CB, C, D / 2, true, false, kStore, 2, 1, true, false, true, true>(
           Ps, L16, dO, L16, QD[0], L16, wave, lane, nullptr, PTb, LUT, dOTb, LUT);
