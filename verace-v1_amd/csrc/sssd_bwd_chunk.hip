@@ -684,9 +684,9 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     commit(nch - 1);
   }
   lds_barrier();
-  // Per chunk, seven phases between LDS barriers, independent products of a phase on disjoint
-  // waves.  W = U^T Psi_s is formed as S1 + G Wm (U^T Psi_s = U^T Psi_e + U^T U T~^T S1), so it
-  // needs no product over the state rows after the reconstruction.
+  // Per chunk, six phases and the commit between LDS barriers, independent products of a phase
+  // on disjoint waves.  W = U^T Psi_s is formed as S1 + G Wm (U^T Psi_s = U^T Psi_e + U^T U T~^T
+  // S1), so it needs no product over the state rows after the reconstruction.
   int lc = 0;  // Lmb[lc] holds Lam_e of chunk n
   for (int n = nch - 1; n >= 0; --n) {
     const float* Lm = Lmb[lc];
@@ -746,7 +746,7 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
     lgemm<R, R, CB, false, true, kStore, 4, 4, LP>(dZm, L16, Wt, L16, dTp, L32, wave, lane);
     lds_barrier();
     // (5) X = mask o (Z Q) (waves 0-1); dQ second term Z^T dX (wave 2); the next chunk's loads
-    //     (waves 4-7: issued here, before this chunk's stores, and committed after phase 7)
+    //     (waves 4-7: issued here, before this chunk's stores, and committed after phase 6)
     lgemm<R, C, CB, false, false, kMaskStore, 0, 2, LP>(Zm, L16, Qb, L16, Xm, L16, wave, lane,
                                                         nullptr, nullptr, 0, nullptr, 0, nullptr,
                                                         0, LP ? Xb : nullptr, LB);
@@ -771,7 +771,7 @@ __global__ __launch_bounds__(NTC) void bwdc_cols_kernel(
         if (tg < T) io<IO>::store(dq, tok(tg) * D + blk * CB + jj, dQm[e] + QD[0][e] + QD[1][e]);
       }
     }
-    // (7, same phase) Lam_s = Lam_e + dO Q^T + U dW into the other buffer (8 waves, one tile
+    // (6, continued) Lam_s = Lam_e + dO Q^T + U dW into the other buffer (8 waves, one tile
     // each, both terms in one accumulation): the dU partial above still reads Lam_e
     lgemm2_addfrom<D, CB, C, R, NWC>(dO, L16, Qb, L16, U, L32, dWm, L16, Lm, Ln, L16, wave, lane,
                                      LP ? LTb : nullptr, LUT);
